@@ -1,0 +1,184 @@
+/*
+ * oscar_hip.h -- C ABI of the MI355X (gfx950) OSCAR INT2 KV-cache hot path.
+ *
+ * Every entry point replaces one Python entry point of the reference plugin
+ * (jpl123123/Oscar_new, package oscar_ascend, file kernels.py) and keeps its
+ * argument meaning. Conventions:
+ *   - device pointers are plain addresses; bf16 data is passed as 16-bit words;
+ *   - strides are in ELEMENTS of the pointed-to type;
+ *   - `stream` is a hipStream_t (NULL = default stream); launches are asynchronous,
+ *     nothing synchronizes the host and nothing is read back to it;
+ *   - no entry point allocates device memory (callers own every buffer), so all of
+ *     them can be captured in a HIP graph;
+ *   - return value: 0 on success, a negative OSCAR_E* code for an argument error
+ *     detected on the host (nothing launched), or a positive hipError_t from the launch.
+ * Device-side metadata (counts, task tables, block tables, slots) is trusted for
+ * semantics but every history/window/table access is bounds-checked against the sizes
+ * passed here; out-of-range entries are skipped, never dereferenced.
+ */
+#ifndef OSCAR_HIP_H_
+#define OSCAR_HIP_H_
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define OSCAR_ABI_VERSION 1
+
+enum oscar_status {
+  OSCAR_OK = 0,
+  OSCAR_E_NULL = -1,        /* a required pointer is NULL */
+  OSCAR_E_SHAPE = -2,       /* sizes/strides inconsistent or unsupported */
+  OSCAR_E_LAYOUT = -3,      /* cache geometry invalid */
+  OSCAR_E_ALIGN = -4,       /* pointer or stride alignment not supported */
+  OSCAR_E_UNSUPPORTED = -5  /* valid request outside this build's coverage */
+};
+
+/* Cache geometry (reference: oscar_ascend/layout.py:9-44, config.py:45-63). */
+typedef struct oscar_layout {
+  int32_t head_dim;              /* D; must be 256 */
+  int32_t kv_heads;              /* H */
+  int32_t physical_block_tokens; /* Bp, tokens per physical page */
+  int32_t kernel_block_tokens;   /* BK, tokens per block-table entry (power of two) */
+  int32_t slot_bytes;            /* 160 */
+  int32_t vector_bytes;          /* 68 */
+  int32_t sink_tokens;           /* S */
+  int32_t recent_tokens;         /* R */
+  int32_t ring_tokens;           /* C = R + speculative + 1 */
+  int32_t reserved;              /* 0 */
+  int64_t stripe_page_bytes;     /* Bp * H * D * 2 */
+} oscar_layout;
+
+/* Clip configuration (reference: config.py:14-19; kernels.py:69-101). */
+enum oscar_clip_mode {
+  OSCAR_CLIP_PERCENTILE = 0, /* torch.quantile(|x|, ratio) threshold; ratio 0 = off */
+  OSCAR_CLIP_FACTOR = 1,     /* max|x| * factor */
+  OSCAR_CLIP_SEARCH = 2      /* argmin-MSE over factors 0.6 + 0.4*i/7, i = 0..7 */
+};
+
+typedef struct oscar_clip {
+  int32_t mode;
+  float k_ratio, v_ratio;   /* percentile mode */
+  float k_factor, v_factor; /* factor mode */
+} oscar_clip;
+
+int oscar_abi_version(void);
+const char* oscar_status_string(int status);
+
+/*
+ * rotate -- replaces kernels.py:51-66 `rotate(x, rotation)`.
+ * out[t, h, :] = bf16( x[t, h, :] @ R ), fp32 accumulation on bf16 MFMA.
+ * x: bf16 [n, h, d] with strides (x_s0, x_s1, x_s2); R: bf16 [d, d] with strides
+ * (r_s0, r_s1) -- a transposed view (r_s0 = 1) is allowed; out: contiguous bf16 [n, h, d].
+ * d must be 256.
+ */
+int oscar_rotate(const void* x, int64_t n, int64_t h, int64_t d, int64_t x_s0, int64_t x_s1,
+                 int64_t x_s2, const void* rotation, int64_t r_s0, int64_t r_s1, void* out,
+                 void* stream);
+
+/*
+ * store_int2 -- replaces kernels.py:175-202 `store_int2(key_rot, value_rot, history,
+ * slots, counts, layout)`.
+ * For every token t < counts[1] with slots[t] >= 0 and head h: clip, INT2-quantize and
+ * pack key_rot[t, h] to bytes [0, 68) and value_rot[t, h] to bytes [68, 136) of the
+ * 160-byte slot at layout slot_offset(slots[t], h). Bytes 136..159 are never written.
+ * key_rot/value_rot: contiguous bf16 [n, H, 256]; history: K stripe bytes.
+ */
+int oscar_store_int2(const void* key_rot, const void* value_rot, int64_t n, void* history,
+                     int64_t history_bytes, const int64_t* slots, const int32_t* counts,
+                     const oscar_layout* layout, const oscar_clip* clip, void* stream);
+
+/*
+ * prepare_tasks -- replaces kernels.py:262-287 `prepare_tasks(qstarts, counts, tasks,
+ * task_count, max_reqs, query_tile, num_reqs, source_table, table, copy_columns)`.
+ * Writes tasks[i] = (req, q_offset) for every query tile of every request < counts[0]
+ * (requests in order, tiles of query_tile tokens clipped to counts[1]) and
+ * task_count[0] = number of tasks. `programs` is the reference grid size
+ * (num_reqs, or max_reqs when num_reqs is None). If source_table != NULL the first
+ * copy_columns columns of each live request row are copied into table.
+ * task_capacity bounds the rows written to tasks.
+ */
+int oscar_prepare_tasks(const int32_t* qstarts, const int32_t* counts, int32_t* tasks,
+                        int32_t* task_count, int64_t task_capacity, int64_t max_reqs,
+                        int32_t query_tile, int64_t programs, const int32_t* source_table,
+                        int64_t source_stride, int32_t* table, int64_t table_stride,
+                        int64_t copy_columns, void* stream);
+
+/*
+ * attention_partials -- replaces kernels.py:439-482 `attention_partials(query, key,
+ * value, history, window, meta, layout, scale, splits, raw)`.
+ * Grid (programs, H, splits): program i serves task i if i < task_count[0].
+ * raw == 0: INT2 history positions [min(S, prefix), max(sink_len, prefix - R)) read from
+ *           `history` through `block_tables` (query must be the ROTATED query);
+ * raw != 0: BF16 sink/ring window positions plus the causal current tokens (key/value).
+ * partials: fp32 [n, hq, splits, 256]; lse: fp32 [n, hq, splits] (natural log).
+ * Live rows of an empty split get 0 / -inf; rows of inactive programs are not written.
+ * Split boundaries follow kernels.py:368-370 with block_n tokens per tile.
+ * max_query_len: host upper bound on query tokens per request (0 = unknown). Only
+ * min(query_tile, max_query_len) * (hq / H) rows per task are computed, so a decode step
+ * (max_query_len 1) does not pay for the query_tile padding; it must not undercount.
+ */
+int oscar_attention_partials(const void* query, int64_t q_s0, int64_t q_s1, int64_t q_s2,
+                             const void* key, int64_t k_s0, int64_t k_s1, int64_t k_s2,
+                             const void* value, int64_t v_s0, int64_t v_s1, int64_t v_s2,
+                             const void* history, int64_t history_bytes, const void* window,
+                             int64_t window_elems, const int32_t* qstarts,
+                             const int32_t* seq_lens, const int32_t* block_tables,
+                             int64_t table_stride, int64_t table_columns, const int32_t* counts,
+                             const int32_t* tasks, const int32_t* task_count, int64_t n,
+                             int64_t hq, int64_t programs, int32_t splits, int32_t block_n,
+                             int32_t query_tile, int32_t max_query_len, float scale, int32_t raw,
+                             const oscar_layout* layout, float* partials, float* lse,
+                             void* stream);
+
+/*
+ * merge_splits -- replaces kernels.py:506-511 `merge_splits(partials, lse, counts)`.
+ * out[t, q, :] = sum_s e^{lse_s - M} P_s / sum_s e^{lse_s - M} (bf16) and
+ * logsum[t, q] = M + log(sum) or -inf; rows t >= counts[1] become 0 / -inf.
+ */
+int oscar_merge_splits(const float* partials, const float* lse, const int32_t* counts, int64_t n,
+                       int64_t hq, int32_t splits, int32_t d, void* out, float* logsum,
+                       void* stream);
+
+/*
+ * merge_paths -- replaces kernels.py:530-541 `merge_paths(history_out, history_lse,
+ * raw_partials, raw_lse, counts, output)`.
+ * output[t, q*256:(q+1)*256] = (wa*a + wb*b) / (wa + wb), wa = e^{la-M}, wb = e^{lb-M}.
+ * history_out: bf16 [n, hq, 256]; raw_partials: fp32 [n, hq, 1, 256]; output: bf16
+ * [n, hq*256]. merged_lse (optional, fp32 [n, hq]) = M + log(wa + wb) -- an addition of
+ * this library; the reference stores no merged LSE.
+ */
+int oscar_merge_paths(const void* history_out, const float* history_lse,
+                      const float* raw_partials, const float* raw_lse, const int32_t* counts,
+                      int64_t n, int64_t hq, int32_t d, void* output, float* merged_lse,
+                      void* stream);
+
+/*
+ * store_windows -- replaces kernels.py:598-620 `store_windows(key, value, window, meta,
+ * layout)`. Writes the current BF16 K/V of each request < counts[0] into its sink
+ * slots (position < S) and ring slots (S + position % C, latest writer only) of the
+ * owner page (block_tables[req, 0] / (Bp / BK)). Must run after both attention
+ * branches of the step. Reference grid: min(n, max_reqs) requests.
+ */
+int oscar_store_windows(const void* key, int64_t k_s0, int64_t k_s1, int64_t k_s2,
+                        const void* value, int64_t v_s0, int64_t v_s1, int64_t v_s2, int64_t n,
+                        void* window, int64_t window_elems, const int32_t* qstarts,
+                        const int32_t* seq_lens, const int32_t* block_tables,
+                        int64_t table_stride, const int32_t* counts, int64_t max_reqs,
+                        const oscar_layout* layout, void* stream);
+
+/*
+ * unpack -- the dequant half of kernels.py:651-672 `dequant_inverse_rotate(history, slots,
+ * rk, rv, layout)` (kernels.py:623-648). key_out/value_out: contiguous bf16 [n, H, 256]
+ * with bf16(code * scale + zero); rows with slot < 0 become zeros. n <= 4096.
+ */
+int oscar_unpack(const void* history, int64_t history_bytes, const int64_t* slots, int64_t n,
+                 const oscar_layout* layout, void* key_out, void* value_out, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* OSCAR_HIP_H_ */

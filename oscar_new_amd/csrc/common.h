@@ -1,0 +1,127 @@
+// Shared device helpers for the gfx950 OSCAR INT2 KV-cache kernels.
+//
+// Conventions used by every kernel in this library:
+//   * bf16 tensors are passed as uint16_t bit patterns;
+//   * one wavefront = 64 lanes; workgroups are 256 threads (4 wavefronts);
+//   * no kernel allocates, synchronizes the host or reads anything back to it.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/oscar_hip.h"
+
+namespace oscar {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kWave = 64;
+constexpr int kThreads = 256;
+constexpr int kHeadDim = 256;
+
+// ---------------------------------------------------------------- number formats
+
+__device__ __forceinline__ float bf16_to_float(uint32_t bits16) {
+  return __uint_as_float(bits16 << 16);
+}
+
+// float -> bf16 bits, round to nearest even, NaN kept quiet (matches torch's .bfloat16()).
+__device__ __forceinline__ uint32_t float_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return ((u >> 16) & 0x8000u) | 0x7fc0u;
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return u >> 16;
+}
+
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  return float_to_bf16(lo) | (float_to_bf16(hi) << 16);
+}
+
+// IEEE fp16 <-> fp32 (hardware conversion, round to nearest even, subnormals kept).
+__device__ __forceinline__ float f16_bits_to_float(uint32_t bits16) {
+  return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(bits16)));
+}
+__device__ __forceinline__ uint32_t float_to_f16_bits(float f) {
+  return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f));
+}
+__device__ __forceinline__ float half_lo_to_float(uint32_t packed) {
+  return f16_bits_to_float(packed & 0xffffu);
+}
+__device__ __forceinline__ float half_hi_to_float(uint32_t packed) {
+  return f16_bits_to_float(packed >> 16);
+}
+
+__device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
+
+__device__ __forceinline__ f32x4 mfma16x16x32(u32x4 a, u32x4 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a), as_bf16x8(b), c, 0, 0, 0);
+}
+
+// ---------------------------------------------------------------- integer helpers
+
+// Exact unsigned division by a runtime constant (Granlund-Montgomery round-up method).
+struct FastDiv {
+  uint32_t divisor;
+  uint32_t mul;
+  uint32_t shift;  // ceil(log2(divisor)); 0 means divisor == 1
+};
+
+inline FastDiv make_fastdiv(uint32_t d) {
+  FastDiv f{d, 0u, 0u};
+  uint32_t l = 0;
+  while ((1ull << l) < d) ++l;
+  f.shift = l;
+  if (l) f.mul = static_cast<uint32_t>(((1ull << 32) * ((1ull << l) - d)) / d + 1);
+  return f;
+}
+
+__device__ __forceinline__ uint32_t fastdiv(uint32_t n, FastDiv f) {
+  if (f.shift == 0) return n;
+  uint32_t t = __umulhi(n, f.mul);
+  return (t + ((n - t) >> 1)) >> (f.shift - 1);
+}
+
+__host__ __device__ __forceinline__ int cdiv(int a, int b) { return (a + b - 1) / b; }
+
+__device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
+
+// ---------------------------------------------------------------- wave reductions
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, kWave));
+  return v;
+}
+__device__ __forceinline__ float wave_min(float v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v = fminf(v, __shfl_xor(v, m, kWave));
+  return v;
+}
+// Butterfly sum: every lane ends with the pairwise tree sum whose level k adds lane blocks
+// (2j, 2j+1) of size 2^k, i.e. the canonical left-to-right pairwise order.
+__device__ __forceinline__ float wave_tree_sum(float v) {
+#pragma unroll
+  for (int m = 1; m <= 32; m <<= 1) {
+    float other = __shfl_xor(v, m, kWave);
+    v = (threadIdx.x & m) ? other + v : v + other;
+  }
+  return v;
+}
+
+// ---------------------------------------------------------------- layout (device copy)
+
+struct Layout {
+  int64_t page_bytes;  // stripe_page_bytes
+  int32_t head_dim, kv_heads, bp, bk, bk_shift, bpp;
+  int32_t slot_bytes, vector_bytes, sink, recent, ring;
+  FastDiv bpp_div;
+};
+
+// Returns OSCAR_OK or an argument error code.
+int make_layout(const oscar_layout* in, Layout* out);
+
+hipStream_t as_stream(void* s);
+
+}  // namespace oscar

@@ -1,0 +1,297 @@
+"""OSCAR INT2 KV-cache kernels for MI355X, behind the reference's Python entry points.
+
+Same names, signatures, return values and error behaviour as ``oscar_ascend/kernels.py``
+(reference), so the backend glue and tests can import either module. Every function
+launches hand-written gfx950 HIP kernels through the C ABI of ``liboscar_hip.so`` on the
+current HIP stream; there is no CPU execution path, no host read-back and no
+synchronization. Output tensors are allocated with ``torch.empty`` on the input's device,
+as in the reference.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import _ext
+from .config import CLIP_MODES, attention_programs
+
+__all__ = [
+    "rotate",
+    "store_int2",
+    "prepare_tasks",
+    "attention_partials",
+    "merge_splits",
+    "merge_paths",
+    "store_windows",
+    "dequant_inverse_rotate",
+    "layout_struct",
+    "clip_struct",
+]
+
+
+# --------------------------------------------------------------------------- helpers
+
+
+def _device_check(*tensors):
+    for t in tensors:
+        if t is not None and t.device.type != "cuda":
+            raise RuntimeError("OSCAR kernels run on a ROCm GPU; got a tensor on " + str(t.device))
+
+
+def _ptr(t):
+    return None if t is None else t.data_ptr()
+
+
+def _stream(t):
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def _bf16(t):
+    """The reference kernels cast their inputs to bf16 on load; do the same up front."""
+    return t if t.dtype == torch.bfloat16 else t.to(torch.bfloat16)
+
+
+def _rows_contiguous(t):
+    """bf16 [n, h, d] view with unit last stride and 16-byte aligned rows, copying if needed."""
+    t = _bf16(t)
+    s0, s1, s2 = t.stride()
+    if s2 != 1 or s0 % 8 or s1 % 8 or t.data_ptr() % 16:
+        t = t.contiguous()
+    return t
+
+
+def layout_struct(layout):
+    """``CacheLayout`` -> C ``oscar_layout``."""
+    cfg = layout.config
+    return _ext.OscarLayout(
+        cfg.head_dim,
+        layout.kv_heads,
+        layout.physical_block_tokens,
+        layout.kernel_block_tokens,
+        cfg.slot_bytes,
+        cfg.vector_bytes,
+        cfg.sink_tokens,
+        cfg.recent_tokens,
+        cfg.ring_tokens,
+        0,
+        layout.stripe_page_bytes,
+    )
+
+
+def clip_struct(cfg):
+    """``OscarConfig`` -> C ``oscar_clip``."""
+    return _ext.OscarClip(
+        CLIP_MODES[cfg.clip_mode],
+        cfg.k_clip_ratio,
+        cfg.v_clip_ratio,
+        cfg.k_clip_factor,
+        cfg.v_clip_factor,
+    )
+
+
+def _int32(t, name):
+    if t.dtype != torch.int32:
+        raise ValueError(f"{name} must be int32, got {t.dtype}")
+    return t
+
+
+# --------------------------------------------------------------------------- entry points
+
+
+def rotate(x, rotation):
+    """``x @ rotation`` per (token, head) row, bf16 out (reference kernels.py:51-66).
+
+    x: [n, h, 256] any strides; rotation: [256, 256] (a transposed view is fine).
+    """
+    _device_check(x, rotation)
+    n, h, d = x.shape
+    out = torch.empty((n, h, d), device=x.device, dtype=torch.bfloat16)
+    if n:
+        x = _bf16(x)
+        rotation = _bf16(rotation)
+        _ext.check(
+            _ext.library().oscar_rotate(
+                _ptr(x), n, h, d, *x.stride(), _ptr(rotation), *rotation.stride(), _ptr(out),
+                _stream(x),
+            ),
+            "rotate",
+        )
+    return out
+
+
+def store_int2(key_rot, value_rot, history, slots, counts, layout):
+    """Clip + INT2 pack rotated K/V into 160-byte slots (reference kernels.py:175-202)."""
+    _device_check(key_rot, value_rot, history, slots, counts)
+    n = key_rot.shape[0]
+    key_rot = _bf16(key_rot).contiguous()
+    value_rot = _bf16(value_rot).contiguous()
+    if slots.dtype != torch.int64:
+        raise ValueError("slot mapping must be int64")
+    _int32(counts, "counts")
+    lay = layout_struct(layout)
+    clip = clip_struct(layout.config)
+    _ext.check(
+        _ext.library().oscar_store_int2(
+            _ptr(key_rot), _ptr(value_rot), n, _ptr(history), history.numel() * history.element_size(),
+            _ptr(slots), _ptr(counts), lay, clip, _stream(key_rot),
+        ),
+        "store_int2",
+    )
+
+
+def prepare_tasks(qstarts, counts, tasks, task_count, max_reqs, query_tile, num_reqs=None,
+                  source_table=None, table=None, copy_columns=0):
+    """Compact (request, query offset) task table on device (reference kernels.py:262-287)."""
+    _device_check(qstarts, counts, tasks, task_count, source_table, table)
+    _int32(qstarts, "qstarts")
+    _int32(counts, "counts")
+    _int32(tasks, "tasks")
+    _int32(task_count, "task_count")
+    programs = max(1, max_reqs if num_reqs is None else num_reqs)
+    src_stride = table_stride = 0
+    if source_table is not None:
+        if table is None:
+            raise ValueError("prepare_tasks: source_table given without a destination table")
+        source_table = _int32(source_table.as_subclass(torch.Tensor), "source_table")
+        _int32(table, "table")
+        src_stride = source_table.stride(0)
+        table_stride = table.stride(0)
+    _ext.check(
+        _ext.library().oscar_prepare_tasks(
+            _ptr(qstarts), _ptr(counts), _ptr(tasks), _ptr(task_count), tasks.shape[0],
+            max_reqs, query_tile, programs, _ptr(source_table), src_stride,
+            _ptr(table) if source_table is not None else None, table_stride,
+            int(copy_columns) if source_table is not None else 0, _stream(qstarts),
+        ),
+        "prepare_tasks",
+    )
+
+
+def attention_partials(query, key, value, history, window, meta, layout, scale, splits, raw):
+    """Per-split partial attention and LSE of one branch (reference kernels.py:439-482).
+
+    raw=False: INT2 history (``query`` must be the rotated query). raw=True: BF16 sink /
+    recent window plus causal current tokens (unrotated query/key/value).
+    Returns ``(partials float32 [n, hq, splits, 256], lse float32 [n, hq, splits])``.
+    ``meta.max_query_len``, when present, lets decode steps skip query-tile padding rows.
+    """
+    _device_check(query, key, value, history, window)
+    n, hq, d = query.shape
+    cfg = layout.config
+    partials = torch.empty((n, hq, splits, d), dtype=torch.float32, device=query.device)
+    lse = torch.empty((n, hq, splits), dtype=torch.float32, device=query.device)
+    if n == 0:
+        return partials, lse
+    programs = attention_programs(n, meta.max_num_reqs, cfg.queries_per_tile)
+    if meta.tasks.shape[0] < programs:
+        raise ValueError(f"task table holds {meta.tasks.shape[0]} rows; the grid needs {programs}")
+    query = _rows_contiguous(query)
+    if raw:
+        key = _rows_contiguous(key)
+        value = _rows_contiguous(value)
+    table = _int32(meta.block_tables, "block_tables")
+    max_query_len = getattr(meta, "max_query_len", None)
+    max_query_len = int(max_query_len) if isinstance(max_query_len, int) else 0
+    kq = key if raw else None
+    vq = value if raw else None
+    _ext.check(
+        _ext.library().oscar_attention_partials(
+            _ptr(query), *query.stride(),
+            _ptr(kq), *(kq.stride() if raw else (0, 0, 1)),
+            _ptr(vq), *(vq.stride() if raw else (0, 0, 1)),
+            _ptr(history), history.numel() * history.element_size(),
+            _ptr(window), window.numel(),
+            _ptr(_int32(meta.query_start_loc, "query_start_loc")),
+            _ptr(_int32(meta.seq_lens, "seq_lens")),
+            _ptr(table), table.stride(0), table.shape[1],
+            _ptr(_int32(meta.counts, "counts")), _ptr(_int32(meta.tasks, "tasks")),
+            _ptr(_int32(meta.task_count, "task_count")),
+            n, hq, programs, splits, cfg.block_n, cfg.queries_per_tile, max_query_len,
+            float(scale), 1 if raw else 0, layout_struct(layout), _ptr(partials), _ptr(lse),
+            _stream(query),
+        ),
+        "attention_partials",
+    )
+    return partials, lse
+
+
+def merge_splits(partials, lse, counts):
+    """LSE merge of split partials (reference kernels.py:506-511) -> (bf16 out, logsum)."""
+    _device_check(partials, lse, counts)
+    n, hq, splits, d = partials.shape
+    out = torch.empty((n, hq, d), dtype=torch.bfloat16, device=partials.device)
+    logsum = torch.empty((n, hq), dtype=torch.float32, device=partials.device)
+    if n:
+        partials = partials.contiguous()
+        lse = lse.contiguous()
+        _ext.check(
+            _ext.library().oscar_merge_splits(
+                _ptr(partials), _ptr(lse), _ptr(_int32(counts, "counts")), n, hq, splits, d,
+                _ptr(out), _ptr(logsum), _stream(partials),
+            ),
+            "merge_splits",
+        )
+    return out, logsum
+
+
+def merge_paths(history_out, history_lse, raw_partials, raw_lse, counts, output, merged_lse=None):
+    """History/raw LSE merge into ``output`` (reference kernels.py:530-541).
+
+    ``merged_lse`` (optional float32 [n, hq]) additionally receives the merged LSE, which
+    the reference does not produce.
+    """
+    _device_check(history_out, history_lse, raw_partials, raw_lse, counts, output, merged_lse)
+    n, hq, d = history_out.shape
+    if not output.is_contiguous():
+        raise ValueError("Attention output must be contiguous")
+    if n == 0:
+        return
+    history_out = _bf16(history_out).contiguous()
+    raw_partials = raw_partials.contiguous()
+    _ext.check(
+        _ext.library().oscar_merge_paths(
+            _ptr(history_out), _ptr(history_lse.contiguous()), _ptr(raw_partials),
+            _ptr(raw_lse.contiguous()), _ptr(_int32(counts, "counts")), n, hq, d, _ptr(output),
+            _ptr(merged_lse), _stream(history_out),
+        ),
+        "merge_paths",
+    )
+
+
+def store_windows(key, value, window, meta, layout):
+    """Write current BF16 K/V into sink/ring windows (reference kernels.py:598-620)."""
+    _device_check(key, value, window)
+    n = key.shape[0]
+    key = _bf16(key)
+    value = _bf16(value)
+    table = _int32(meta.block_tables, "block_tables")
+    _ext.check(
+        _ext.library().oscar_store_windows(
+            _ptr(key), *key.stride(), _ptr(value), *value.stride(), n, _ptr(window),
+            window.numel(), _ptr(_int32(meta.query_start_loc, "query_start_loc")),
+            _ptr(_int32(meta.seq_lens, "seq_lens")), _ptr(table), table.stride(0),
+            _ptr(_int32(meta.counts, "counts")), meta.max_num_reqs, layout_struct(layout),
+            _stream(key),
+        ),
+        "store_windows",
+    )
+
+
+def dequant_inverse_rotate(history, slots, rk, rv, layout):
+    """Diagnostic unpack + inverse rotation of <= 4096 slots (reference kernels.py:651-672)."""
+    _device_check(history, slots, rk, rv)
+    n, h, d = slots.numel(), layout.kv_heads, layout.config.head_dim
+    if n > 4096:
+        raise ValueError("Diagnostic dequant is limited to 4096 tokens; use fused attention")
+    k = torch.empty((n, h, d), device=history.device, dtype=torch.bfloat16)
+    v = torch.empty_like(k)
+    if n:
+        slots = slots.to(torch.int64).contiguous()
+        _ext.check(
+            _ext.library().oscar_unpack(
+                _ptr(history), history.numel() * history.element_size(), _ptr(slots), n,
+                layout_struct(layout), _ptr(k), _ptr(v), _stream(history),
+            ),
+            "dequant_inverse_rotate",
+        )
+    return rotate(k, rk.T), rotate(v, rv.T)

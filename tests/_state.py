@@ -1,0 +1,117 @@
+"""Shared GPU test state: sentinel-filled native cache stripes, paged requests, launch order.
+
+Mirrors the harness of the reference device tests (tests/test_npu_kernels.py:27-163):
+exact three-stripe raw buffer (conv | K | V) filled with 0x5A, non-monotonic page
+ownership with page zero untouched, prefixes written through the real store kernels.
+"""
+
+from types import SimpleNamespace
+
+import numpy as np
+import torch
+
+from oscar_new_amd import kernels
+from oscar_new_amd.config import OscarConfig, task_capacity
+from oscar_new_amd.layout import CacheLayout
+
+CONV_BYTES_PER_PAGE = 15360
+
+
+def bits(t):
+    """bf16 tensor -> numpy uint16 bit patterns (CPU copy)."""
+    return t.detach().to("cpu").contiguous().view(torch.int16).numpy().view(np.uint16)
+
+
+def from_bits(a, device="cuda"):
+    return torch.from_numpy(np.ascontiguousarray(a).view(np.int16)).view(torch.bfloat16).to(device)
+
+
+def oracle_geometry(layout):
+    import oracle as O
+
+    cfg = layout.config
+    return O.Geometry(layout.physical_block_tokens, layout.kv_heads, layout.kernel_block_tokens,
+                      cfg.head_dim, cfg.sink_tokens, cfg.recent_tokens, cfg.speculative_tokens)
+
+
+def make_state(lengths, prefix_lengths, cfg=None, pages=20, max_reqs=8, device="cuda"):
+    layout = CacheLayout(768, config=cfg or OscarConfig())
+    conv = pages * CONV_BYTES_PER_PAGE
+    stripe = pages * layout.stripe_page_bytes
+    raw = torch.full((conv + 2 * stripe,), 0x5A, device=device, dtype=torch.uint8)
+    k = raw[conv : conv + stripe].view(torch.bfloat16).view(-1, 128, 1, 256)
+    v = raw[conv + stripe :].view(torch.bfloat16).view(-1, 128, 1, 256)
+    history, window = layout.tensor_views((k, v))
+    free = list(range(1, pages))
+    free = free[::2] + free[1::2]  # non-monotonic physical pages; page 0 never owned
+    bpp = layout.blocks_per_page
+    tables = torch.zeros((max_reqs, bpp * pages), dtype=torch.int32)
+    qstarts, slots = [0], []
+    for i, (length, prefix) in enumerate(zip(lengths, prefix_lengths)):
+        need = -(-length // layout.physical_block_tokens)
+        owned, free = free[:need], free[need:]
+        blocks = [p * bpp + j for p in owned for j in range(bpp)]
+        tables[i, : len(blocks)] = torch.tensor(blocks, dtype=torch.int32)
+        slots.extend(blocks[t // 128] * 128 + t % 128 for t in range(prefix, length))
+        qstarts.append(qstarts[-1] + length - prefix)
+    qbuf = torch.zeros(max_reqs + 1, dtype=torch.int32)
+    qbuf[: len(qstarts)] = torch.tensor(qstarts, dtype=torch.int32)
+    sbuf = torch.zeros(max_reqs, dtype=torch.int32)
+    sbuf[: len(lengths)] = torch.tensor(list(lengths), dtype=torch.int32)
+    meta = SimpleNamespace(
+        query_start_loc=qbuf.to(device),
+        seq_lens=sbuf.to(device),
+        block_tables=tables.to(device),
+        counts=torch.tensor([len(lengths), len(slots)], device=device, dtype=torch.int32),
+        slot_mapping=torch.tensor(slots, device=device, dtype=torch.int64),
+        num_reqs=len(lengths),
+        max_num_reqs=max_reqs,
+        max_query_len=max((l - p for l, p in zip(lengths, prefix_lengths)), default=0),
+        tasks=torch.empty(
+            (task_capacity(max(1, len(slots)), max_reqs, layout.config.queries_per_tile), 2),
+            device=device, dtype=torch.int32,
+        ),
+        task_count=torch.zeros(1, device=device, dtype=torch.int32),
+    )
+    return layout, raw, history, window, meta, tables
+
+
+def prepare_prefix(k, v, rk, rv, history, window, meta, tables, layout, prefixes, device="cuda"):
+    """Write earlier steps of every request through the real store kernels."""
+    for req, prefix in enumerate(prefixes):
+        if prefix == 0:
+            continue
+        old = SimpleNamespace(
+            query_start_loc=torch.tensor([0, prefix], device=device, dtype=torch.int32),
+            seq_lens=torch.tensor([prefix], device=device, dtype=torch.int32),
+            block_tables=meta.block_tables[req : req + 1],
+            counts=torch.tensor([1, prefix], device=device, dtype=torch.int32),
+            slot_mapping=torch.tensor(
+                [int(tables[req, t // 128]) * 128 + t % 128 for t in range(prefix)],
+                device=device, dtype=torch.int64,
+            ),
+            num_reqs=1,
+            max_num_reqs=1,
+        )
+        pk, pv = k[req][:prefix].to(device), v[req][:prefix].to(device)
+        kernels.store_int2(kernels.rotate(pk, rk), kernels.rotate(pv, rv), history,
+                           old.slot_mapping, old.counts, layout)
+        kernels.store_windows(pk, pv, window, old, layout)
+
+
+def run_attention(q, k, v, rk, rv, history, window, meta, layout, splits, merged_lse=None):
+    """The reference launch order (backend.py:171-226) through the kernel entry points."""
+    kernels.prepare_tasks(meta.query_start_loc, meta.counts, meta.tasks, meta.task_count,
+                          meta.max_num_reqs, layout.config.queries_per_tile)
+    kr, vr = kernels.rotate(k, rk), kernels.rotate(v, rv)
+    kernels.store_int2(kr, vr, history, meta.slot_mapping, meta.counts, layout)
+    qp = kernels.rotate(q, rk)
+    hp, hl = kernels.attention_partials(qp, k, v, history, window, meta, layout, 1 / 16, splits,
+                                        False)
+    hr, hls = kernels.merge_splits(hp, hl, meta.counts)
+    ho = kernels.rotate(hr, rv.T)
+    rp, rl = kernels.attention_partials(q, k, v, history, window, meta, layout, 1 / 16, 1, True)
+    out = torch.empty_like(q)
+    kernels.merge_paths(ho, hls, rp, rl, meta.counts, out, merged_lse)
+    kernels.store_windows(k, v, window, meta, layout)
+    return out

@@ -1,0 +1,50 @@
+"""The C-ABI library loads, exports every symbol declared in include/oscar_hip.h and
+rejects invalid arguments on the host (no GPU needed: nothing is launched)."""
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from oscar_new_amd import _ext
+
+ROOT = Path(__file__).resolve().parents[1]
+
+
+def declared_symbols():
+    text = (ROOT / "include" / "oscar_hip.h").read_text()
+    return sorted(set(re.findall(r"^\s*(?:int|const char\*)\s+(oscar_\w+)\s*\(", text, re.M)))
+
+
+def test_header_and_binding_agree():
+    assert declared_symbols() == _ext.exported_symbols()
+
+
+def test_library_exports_every_declared_symbol():
+    lib = ctypes.CDLL(str(_ext.LIBRARY_PATH))
+    for name in declared_symbols():
+        assert hasattr(lib, name), name
+    assert _ext.library().oscar_abi_version() == 1
+
+
+def test_host_side_argument_errors():
+    lib = _ext.library()
+    assert lib.oscar_rotate(None, 4, 1, 128, 0, 0, 1, None, 0, 0, None, None) == -5
+    assert lib.oscar_rotate(None, 4, 1, 256, 0, 0, 1, None, 0, 0, None, None) == -1
+    assert lib.oscar_rotate(None, 0, 1, 256, 0, 0, 1, None, 0, 0, None, None) == 0
+    bad = _ext.OscarLayout(256, 1, 768, 100, 160, 68, 4, 128, 132, 0, 393216)
+    clip = _ext.OscarClip(0, 0.96, 0.92, 1.0, 1.0)
+    assert lib.oscar_store_int2(None, None, 4, None, 0, None, None, bad, clip, None) == -3
+    good = _ext.OscarLayout(256, 1, 768, 128, 160, 68, 4, 128, 132, 0, 393216)
+    assert lib.oscar_store_int2(None, None, 4, None, 0, None, None, good, clip, None) == -1
+    assert lib.oscar_merge_splits(None, None, None, 3, 6, 4, 128, None, None, None) == -5
+    assert lib.oscar_unpack(None, 0, None, 5000, good, None, None, None) == -2
+    with pytest.raises(ValueError):
+        _ext.check(-2, "probe")
+
+
+def test_status_strings():
+    lib = _ext.library()
+    assert lib.oscar_status_string(0) == b"ok"
+    assert b"layout" in lib.oscar_status_string(-3)
