@@ -1,0 +1,456 @@
+#!/usr/bin/env python3
+"""OSCAR INT2 decode-attention benchmark on one MI355X.
+
+One step = one FULL-attention layer forward of a decode batch (BASELINE config 3 by
+default): rotate K/V/q, INT2 store of the current token, split-KV history attention,
+split merge, inverse V rotation, BF16 sink/recent/current attention, LSE path merge,
+window store. Each layer step is captured once as a HIP graph and replayed; steps cycle
+over ``--layers`` independent KV caches (each > 1 GB) so the 256 MB Infinity Cache cannot
+serve a step from the previous step's reads.
+
+Printed JSON (one line): ``value`` is the whole step's algorithmic HBM GB/s; also the
+per-layer-step microseconds, the dominant (history) kernel's roofline from HIP events, the
+store throughput, the CPU oracle baseline and a full-size parity sample.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+from types import SimpleNamespace
+
+ROOT = Path(__file__).resolve().parent
+if str(ROOT) not in sys.path:
+    sys.path.insert(0, str(ROOT))
+
+METRIC = "INT2 decode-attn µs/layer-step + achieved HBM GB/s at 32k ctx; store tokens/s"
+PEAK_HBM_GBPS = 8000.0
+
+CONFIGS = {
+    "c3": dict(batch=32, context=32768, qlen=1, ragged=False, splits="reference",
+               desc="one TP rank of a Qwen3.5-27B-class layer: B32 x 32768 ctx, GQA 6:1, D256, "
+                    "INT2 history + 4 sink + 128 recent BF16, 16 splits"),
+    "c4": dict(batch=64, context=131072, qlen=4, ragged=True, splits="mi355x",
+               desc="ragged MTP: B64, ctx log-uniform [256, 131072], 4 query tokens each"),
+    "c5": dict(batch=4, context=262144, qlen=1, ragged=False, splits="mi355x",
+               desc="long context: B4 x 262144 ctx, adaptive splits"),
+}
+
+
+def parse_args(argv=None):
+    p = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=200)
+    p.add_argument("--warmup", type=int, default=20)
+    p.add_argument("--config", default="c3", choices=sorted(CONFIGS))
+    p.add_argument("--layers", type=int, default=4, help="independent KV caches cycled per step")
+    p.add_argument("--seed", type=int, default=1234)
+    p.add_argument("--cpu-sample", type=int, default=2, help="requests timed on the CPU oracle")
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--no-graph", action="store_true", help="eager launches instead of HIP graphs")
+    return p.parse_args(argv)
+
+
+# ------------------------------------------------------------------ workload
+
+
+def context_lengths(cfg, gen):
+    import torch
+
+    b, ctx = cfg["batch"], cfg["context"]
+    if not cfg["ragged"]:
+        return [ctx] * b
+    lo, hi = math.log(256), math.log(ctx)
+    u = torch.rand(b, generator=gen, dtype=torch.float64)
+    return [int(round(math.exp(lo + (hi - lo) * float(x)))) for x in u]
+
+
+def build_workload(args, cfg, device):
+    """Paged INT2 cache of every request written through the product kernels."""
+    import torch
+
+    from oscar_new_amd import kernels
+    from oscar_new_amd.config import OscarConfig, task_capacity
+    from oscar_new_amd.layout import CacheLayout
+
+    ocfg = OscarConfig(sink_tokens=4, recent_tokens=128, speculative_tokens=3)
+    layout = CacheLayout(768, config=ocfg)
+    gen = torch.Generator().manual_seed(args.seed)
+    seqs = context_lengths(cfg, gen)
+    qlen = cfg["qlen"]
+    b = len(seqs)
+    bpp = layout.blocks_per_page
+    pages_per_req = [-(-s // layout.physical_block_tokens) for s in seqs]
+    pool = sum(pages_per_req) + 1  # page 0 never owned
+    order = (torch.randperm(pool - 1, generator=gen) + 1).tolist()
+    columns = max(pages_per_req) * bpp
+    table = torch.zeros((b, columns), dtype=torch.int32)
+    cursor = 0
+    for r, npg in enumerate(pages_per_req):
+        pages = order[cursor : cursor + npg]
+        cursor += npg
+        table[r, : npg * bpp] = torch.tensor([p * bpp + j for p in pages for j in range(bpp)],
+                                             dtype=torch.int32)
+    table_d = table.to(device)
+    rk = torch.linalg.qr(torch.randn(256, 256, generator=gen))[0].bfloat16().to(device)
+    rv = torch.linalg.qr(torch.randn(256, 256, generator=gen))[0].bfloat16().to(device)
+
+    k_cache = torch.zeros(pool * bpp, 128, 1, 256, dtype=torch.bfloat16, device=device)
+    v_cache = torch.zeros_like(k_cache)
+    history, window = layout.tensor_views((k_cache, v_cache))
+    dgen = torch.Generator(device=device).manual_seed(args.seed + 1)
+    prefixes = [s - qlen for s in seqs]
+    chunk = 65536
+    for r, prefix in enumerate(prefixes):  # earlier steps, written by the real kernels
+        for start in range(0, prefix, chunk):
+            stop = min(prefix, start + chunk)
+            t = stop - start
+            k = torch.randn(t, 1, 256, generator=dgen, device=device).bfloat16()
+            v = torch.randn(t, 1, 256, generator=dgen, device=device).bfloat16()
+            pos = torch.arange(start, stop, device=device)
+            slots = (table_d[r, pos // 128].to(torch.int64) * 128 + pos % 128)
+            counts = torch.tensor([1, t], dtype=torch.int32, device=device)
+            kernels.store_int2(kernels.rotate(k, rk), kernels.rotate(v, rv), history, slots,
+                               counts, layout)
+            # Window: sink positions and, per ring slot, the latest position (later chunks
+            # overwrite earlier ones, exactly as successive decode steps would).
+            meta = SimpleNamespace(
+                query_start_loc=torch.tensor([0, t], dtype=torch.int32, device=device),
+                seq_lens=torch.tensor([stop], dtype=torch.int32, device=device),
+                block_tables=table_d[r : r + 1], counts=counts, max_num_reqs=1)
+            kernels.store_windows(k, v, window, meta, layout)
+    torch.cuda.synchronize()
+
+    ntok = sum(qlen for _ in seqs)
+    q = torch.randn(ntok, 6, 256, generator=dgen, device=device).bfloat16()
+    kc = torch.randn(ntok, 1, 256, generator=dgen, device=device).bfloat16()
+    vc = torch.randn(ntok, 1, 256, generator=dgen, device=device).bfloat16()
+    slot_list = []
+    for r, s in enumerate(seqs):
+        for p in range(s - qlen, s):
+            slot_list.append(int(table[r, p // 128]) * 128 + p % 128)
+    meta = SimpleNamespace(
+        query_start_loc=torch.arange(0, ntok + 1, qlen, dtype=torch.int32, device=device),
+        seq_lens=torch.tensor(seqs, dtype=torch.int32, device=device),
+        block_tables=table_d,
+        slot_mapping=torch.tensor(slot_list, dtype=torch.int64, device=device),
+        counts=torch.tensor([b, ntok], dtype=torch.int32, device=device),
+        num_reqs=b, num_actual_tokens=ntok, max_query_len=qlen, max_num_reqs=b,
+        max_seq_len=max(seqs), layout=layout,
+        tasks=torch.zeros((task_capacity(ntok, b, ocfg.queries_per_tile), 2), dtype=torch.int32,
+                          device=device),
+        task_count=torch.zeros(1, dtype=torch.int32, device=device),
+        merged_lse=torch.empty(ntok, 6, dtype=torch.float32, device=device),
+    )
+    kernels.prepare_tasks(meta.query_start_loc, meta.counts, meta.tasks, meta.task_count, b,
+                          ocfg.queries_per_tile)
+    return SimpleNamespace(layout=layout, cfg=ocfg, seqs=seqs, prefixes=prefixes, qlen=qlen,
+                           table=table, k_cache=k_cache, v_cache=v_cache, rk=rk, rv=rv, q=q,
+                           k=kc, v=vc, meta=meta)
+
+
+def algorithmic_bytes(w):
+    """Bytes a step must move: 136 B per INT2 history token-head, 1024 B per BF16
+    sink/recent/current token-head, q + output + used block-table entries."""
+    cfg = w.cfg
+    hist = bf16 = cols = 0
+    for s, prefix in zip(w.seqs, w.prefixes):
+        sink = min(cfg.sink_tokens, prefix)
+        recent_begin = max(sink, prefix - cfg.recent_tokens)
+        hist += recent_begin - sink
+        bf16 += sink + (prefix - recent_begin) + w.qlen
+        cols += -(-s // 128)
+    ntok = w.q.shape[0]
+    q_out = 2 * ntok * 6 * 256 * 2
+    return SimpleNamespace(history_tokens=hist, int2=136 * hist, bf16=1024 * bf16,
+                           q_out=q_out, table=4 * cols, total=136 * hist + 1024 * bf16 + q_out + 4 * cols)
+
+
+# ------------------------------------------------------------------ measurements
+
+
+def time_store(device, args, steps):
+    """rotate + clip-search + INT2 pack of 4096 tokens into permuted pages."""
+    import torch
+
+    from oscar_new_amd import kernels
+    from oscar_new_amd.config import OscarConfig
+    from oscar_new_amd.layout import CacheLayout
+
+    n = 4096
+    cfg = OscarConfig(sink_tokens=4, recent_tokens=128, clip_mode="search")
+    layout = CacheLayout(768, config=cfg)
+    gen = torch.Generator().manual_seed(args.seed + 2)
+    k = torch.randn(n, 1, 256, generator=gen)
+    v = torch.randn(n, 1, 256, generator=gen)
+    chans = torch.randperm(256, generator=gen)[:5]
+    k[..., chans] *= 10
+    v[..., chans] *= 10
+    k, v = k.bfloat16().to(device), v.bfloat16().to(device)
+    rk = torch.linalg.qr(torch.randn(256, 256, generator=gen))[0].bfloat16().to(device)
+    rv = torch.linalg.qr(torch.randn(256, 256, generator=gen))[0].bfloat16().to(device)
+    pages = 64
+    history = torch.zeros(pages * layout.stripe_page_bytes, dtype=torch.uint8, device=device)
+    blocks = torch.randperm(pages * 6, generator=gen)[: n // 128]
+    slots = (blocks[:, None] * 128 + torch.arange(128)[None]).reshape(-1).to(torch.int64).to(device)
+    counts = torch.tensor([1, n], dtype=torch.int32, device=device)
+
+    def once():
+        kernels.store_int2(kernels.rotate(k, rk), kernels.rotate(v, rv), history, slots, counts,
+                           layout)
+
+    for _ in range(5):
+        once()
+    kr, vr = kernels.rotate(k, rk), kernels.rotate(v, rv)
+    torch.cuda.synchronize()
+    full = []
+    for _ in range(steps):
+        e = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+        e[0].record()
+        once()
+        e[1].record()
+        kernels.store_int2(kr, vr, history, slots, counts, layout)
+        e[2].record()
+        full.append(e)
+    torch.cuda.synchronize()
+    t_full = statistics.median(x[0].elapsed_time(x[1]) for x in full) * 1e3
+    t_store = statistics.median(x[1].elapsed_time(x[2]) for x in full) * 1e3
+    alg = n * (2 * 512) + 2 * 256 * 256 * 2 + n * 136 + n * 8
+    return {
+        "workload": "c2: 4096 tokens x 1 kv head, D256, 2% outlier channels x10, seeded QR "
+                    "rotation, 8-factor MSE clip search, 128-token pages on permuted slots",
+        "tokens_per_s": n / (t_full * 1e-6),
+        "us_per_call": t_full,
+        "store_kernel_us": t_store,
+        "store_kernel_tokens_per_s": n / (t_store * 1e-6),
+        "algorithmic_bytes": alg,
+        "store_kernel_GBps": alg / (t_store * 1e-6) / 1e9,
+    }
+
+
+def cpu_baseline(w, args, outputs):
+    """CPU oracle (numpy) on a bounded sample of requests of layer 0, plus parity."""
+    import numpy as np
+    import torch
+
+    import oracle as O
+
+    geo = O.Geometry(w.layout.physical_block_tokens, 1, 128, 256, w.cfg.sink_tokens,
+                     w.cfg.recent_tokens, w.cfg.speculative_tokens)
+    history = w.k_cache.view(torch.uint8).view(-1).cpu().numpy()
+    window = w.v_cache.view(torch.int16).view(-1).cpu().numpy().view(np.uint16)
+
+    def bits(t):
+        return t.detach().cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
+
+    rk, rv = bits(w.rk), bits(w.rv)
+    sample = list(range(min(args.cpu_sample, len(w.seqs))))
+    got = outputs.float().cpu().numpy().reshape(-1, 6, 256)
+    got_lse = w.meta.merged_lse.cpu().numpy()
+    errs, lse_errs, times = [], [], []
+    for rep in range(3):
+        t0 = time.perf_counter()
+        for r in sample:
+            rows = slice(r * w.qlen, (r + 1) * w.qlen)
+            out, lse = O.cached_decode_reference(history, window, w.table[r].numpy(), w.seqs[r],
+                                                 bits(w.q[rows]), bits(w.k[rows]), bits(w.v[rows]),
+                                                 rk, rv, geo, scale=1 / 16)
+            if rep == 0:
+                errs.append(np.abs(got[rows] - out))
+                lse_errs.append(np.abs(got_lse[rows] - lse))
+        times.append(time.perf_counter() - t0)
+    per_req = statistics.median(times) / len(sample)
+    try:
+        from threadpoolctl import threadpool_info
+
+        cores = max((i.get("num_threads", 1) for i in threadpool_info()), default=1)
+    except Exception:  # pragma: no cover
+        cores = os.cpu_count() or 1
+    err = np.concatenate([e.reshape(-1) for e in errs])
+    lerr = np.concatenate([e.reshape(-1) for e in lse_errs])
+    cpu = {
+        "value": per_req * len(w.seqs) * 1e6,
+        "unit": "us/layer-step",
+        "cores": int(cores),
+        "kind": "port",
+        "sample": f"{len(sample)} of {len(w.seqs)} requests of layer 0 (numpy oracle "
+                  f"cached_decode_reference: INT2 dequant + inverse rotation + dense fp64 "
+                  f"attention), median of 3, scaled x{len(w.seqs) / len(sample):g}",
+    }
+    parity = {"requests": len(sample), "max_abs": float(err.max()), "mean_abs": float(err.mean()),
+              "lse_max_abs": float(lerr.max())}
+    return cpu, parity
+
+
+def read_traffic():
+    """HBM bytes per history-kernel launch from the committed rocprof PMC summary, if any."""
+    path = ROOT / "profiles" / "history_kernel_c3_traffic.txt"
+    if not path.exists():
+        return None
+    for line in path.read_text().splitlines():
+        if line.startswith("traffic_bytes_per_launch:"):
+            return float(line.split(":", 1)[1])
+    return None
+
+
+def main(argv=None):
+    args = parse_args(argv)
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one MI355X; --gpus {args.gpus} is not supported "
+              "(no multi-GPU path exists; run with --gpus 1)", file=sys.stderr)
+        return 2
+    import torch
+
+    from oscar_new_amd import kernels
+    from oscar_new_amd.backend import OscarAttentionImpl
+
+    if not torch.cuda.is_available():
+        print("bench.py: no ROCm GPU visible", file=sys.stderr)
+        return 1
+    device = torch.device("cuda:0")
+    torch.cuda.set_device(device)
+    cfg = CONFIGS[args.config]
+    print(f"[bench] building {args.config} workload ({args.layers} layers)", file=sys.stderr, flush=True)
+    w = build_workload(args, cfg, device)
+    layers = [(w.k_cache, w.v_cache)]
+    for _ in range(args.layers - 1):
+        layers.append((w.k_cache.clone(), w.v_cache.clone()))
+    impls = []
+    for _ in layers:
+        impl = OscarAttentionImpl(6, 256, 1 / 16, 1, w.cfg, split_policy=cfg["splits"])
+        impl.initialize_layer(w.rk, w.rv)
+        impls.append(impl)
+    ntok = w.q.shape[0]
+    outputs = [torch.empty(ntok, 6 * 256, dtype=torch.bfloat16, device=device) for _ in layers]
+    splits = impls[0].splits_for(w.meta)
+
+    def step(i):
+        impls[i].forward(None, w.q, w.k, w.v, layers[i], w.meta, outputs[i])
+
+    for i in range(len(layers)):  # eager warm-up (also builds the tensor views)
+        step(i)
+    torch.cuda.synchronize()
+    graphs = None
+    if not args.no_graph:
+        graphs = []
+        stream = torch.cuda.Stream()
+        stream.wait_stream(torch.cuda.current_stream())
+        pool = None
+        for i in range(len(layers)):
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=stream, pool=pool):
+                step(i)
+            pool = g.pool()
+            graphs.append(g)
+        torch.cuda.synchronize()
+
+    def run(i):
+        if graphs is not None:
+            graphs[i % len(layers)].replay()
+        else:
+            step(i % len(layers))
+
+    print(f"[bench] warmup {args.warmup}, timed {args.steps}", file=sys.stderr, flush=True)
+    for i in range(args.warmup):
+        run(i)
+    torch.cuda.synchronize()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    ev0.record()
+    for i in range(args.steps):
+        run(i)
+    ev1.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    gpu_ms = ev0.elapsed_time(ev1)
+    us_step = wall / args.steps * 1e6
+
+    # Dominant kernel alone: history attention, HIP events around each launch.
+    qrot = kernels.rotate(w.q, w.rk)
+    hist_views = [w.layout.tensor_views(c) for c in layers]
+    for i in range(len(layers)):
+        kernels.attention_partials(qrot, w.k, w.v, hist_views[i][0], hist_views[i][1], w.meta,
+                                   w.layout, 1 / 16, splits, False)
+    torch.cuda.synchronize()
+    evs = []
+    for i in range(args.steps):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        h, win = hist_views[i % len(layers)]
+        a.record()
+        kernels.attention_partials(qrot, w.k, w.v, h, win, w.meta, w.layout, 1 / 16, splits,
+                                   False)
+        b.record()
+        evs.append((a, b))
+    torch.cuda.synchronize()
+    hist_us = statistics.mean(a.elapsed_time(b) for a, b in evs) * 1e3
+    alg = algorithmic_bytes(w)
+    partial_bytes = ntok * 6 * splits * (256 * 4 + 4)
+    hist_alg = alg.int2 + ntok * 6 * 256 * 2 + alg.table + partial_bytes
+    print(f"[bench] step {us_step:.1f} us, history kernel {hist_us:.1f} us", file=sys.stderr,
+          flush=True)
+
+    store = time_store(device, args, max(20, args.steps // 2))
+    result = {
+        "metric": METRIC,
+        "value": alg.total / (us_step * 1e-6) / 1e9,
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": us_step / 1e3,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": f"{args.config}: {cfg['desc']}",
+            "batch": len(w.seqs),
+            "context": cfg["context"],
+            "query_tokens_per_request": w.qlen,
+            "q_heads": 6, "kv_heads": 1, "head_dim": 256,
+            "page_tokens": 768, "kernel_block_tokens": 128,
+            "splits": splits, "layers_cycled": len(layers),
+            "hip_graph": graphs is not None, "seed": args.seed,
+        },
+        "us_per_layer_step": us_step,
+        "gpu_us_per_layer_step": gpu_ms / args.steps * 1e3,
+        "algorithmic_bytes_per_step": alg.total,
+        "history_kernel": {
+            "us": hist_us,
+            "history_tokens": alg.history_tokens,
+            "algorithmic_bytes": hist_alg,
+            "GBps": hist_alg / (hist_us * 1e-6) / 1e9,
+            "int2_GBps": alg.int2 / (hist_us * 1e-6) / 1e9,
+        },
+        "store": store,
+        "roofline": {
+            "bound": "hbm",
+            "achieved": hist_alg / (hist_us * 1e-6) / 1e9,
+            "peak": PEAK_HBM_GBPS,
+            "unit": "GB/s",
+            "frac": hist_alg / (hist_us * 1e-6) / 1e9 / PEAK_HBM_GBPS,
+            "traffic": read_traffic(),
+        },
+    }
+    if not args.no_cpu_baseline:
+        print("[bench] CPU oracle baseline", file=sys.stderr, flush=True)
+        graphs[0].replay() if graphs is not None else step(0)
+        torch.cuda.synchronize()
+        cpu, parity = cpu_baseline(SimpleNamespace(**{**vars(w), "k_cache": layers[0][0],
+                                                      "v_cache": layers[0][1]}),
+                                   args, outputs[0])
+        result["cpu_baseline"] = cpu
+        result["parity_sample"] = parity
+    print(json.dumps(result))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

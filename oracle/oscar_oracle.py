@@ -51,6 +51,8 @@ __all__ = [
     "dense_attention",
     "hybrid_reference",
     "unpack",
+    "dequant_rows",
+    "cached_decode_reference",
 ]
 
 NEG_INF = np.float32(-np.inf)
@@ -646,3 +648,63 @@ def hybrid_reference(q_bits, k_bits, v_bits, prefix, rk_bits, rv_bits, cfg):
         keys[s_tok:end] = bf16_to_f32(kd[s_tok:end]).astype(np.float64) @ rk.T
         values[s_tok:end] = bf16_to_f32(vd[s_tok:end]).astype(np.float64) @ rv.T
     return dense_attention(bf16_to_f32(q_bits), keys, values, prefix)
+
+
+# --------------------------------------------------------------------------- bulk decode
+
+
+def dequant_rows(history, offsets, d=256):
+    """Vectorized ``load_vec`` (kernels.py:205-219) of many vectors: bf16 bits [N, d]."""
+    offsets = np.asarray(offsets, np.int64)
+    data = history[offsets[:, None] + np.arange(d // 4)[None, :]].astype(np.int32)
+    codes = ((data[:, :, None] >> (2 * np.arange(4))[None, None, :]) & 3).reshape(len(offsets), d)
+    sz = history[offsets[:, None] + d // 4 + np.arange(4)[None, :]]
+    scale = np.ascontiguousarray(sz[:, :2]).view(np.float16)[:, 0].astype(np.float32)
+    zero = np.ascontiguousarray(sz[:, 2:]).view(np.float16)[:, 0].astype(np.float32)
+    value = (codes.astype(np.float32) * scale[:, None]).astype(np.float32) + zero[:, None]
+    return f32_to_bf16(value.astype(np.float32))
+
+
+def cached_decode_reference(history, window, table_row, seq, q_bits, k_bits, v_bits, rk_bits,
+                            rv_bits, geometry: Geometry, scale=None, head=0):
+    """Hybrid attention of tests/oracle.py:55-65, read back from a quantized paged cache.
+
+    Positions [0, sink_len) and [recent_begin, prefix) come from the BF16 window, history
+    positions [sink_len, recent_begin) are dequantized from their INT2 slots and
+    inverse-rotated (``kd @ R.T``), current positions [prefix, seq) come from k/v.
+    One request, one kv head. Returns ``(out float32 [T, Hq, D], lse float32 [T, Hq])``.
+    """
+    t, hq, d = q_bits.shape
+    prefix = seq - t
+    s_tok, recent = geometry.sink_tokens, geometry.recent_tokens
+    sink_len = min(s_tok, prefix)
+    recent_begin = max(sink_len, prefix - recent)
+    bk = geometry.kernel_block_tokens
+    pos = np.arange(sink_len, recent_begin)
+    slots = np.asarray(table_row, np.int64)[pos // bk] * bk + pos % bk
+    pages, within = np.divmod(slots, geometry.physical_block_tokens)
+    offs = pages * geometry.stripe_page_bytes + (within * geometry.kv_heads + head) * geometry.slot_bytes
+    rk = bf16_to_f32(rk_bits)
+    rv = bf16_to_f32(rv_bits)
+    keys = np.empty((seq, d), np.float32)
+    values = np.empty((seq, d), np.float32)
+    keys[sink_len:recent_begin] = bf16_to_f32(dequant_rows(history, offs, d)) @ rk.T
+    values[sink_len:recent_begin] = bf16_to_f32(dequant_rows(history, offs + geometry.vector_bytes, d)) @ rv.T
+    first = int(table_row[0])
+    for p in list(range(0, sink_len)) + list(range(recent_begin, prefix)):
+        kb = geometry.window_element(first, p, 0, head)
+        vb = geometry.window_element(first, p, 1, head)
+        keys[p] = bf16_to_f32(window[kb : kb + d])
+        values[p] = bf16_to_f32(window[vb : vb + d])
+    keys[prefix:] = bf16_to_f32(k_bits[:, head])
+    values[prefix:] = bf16_to_f32(v_bits[:, head])
+    q = bf16_to_f32(q_bits).astype(np.float64).reshape(t * hq, d)
+    sc = (q @ keys.astype(np.float64).T) * (d ** -0.5 if scale is None else float(scale))
+    qi = np.repeat(np.arange(t), hq)[:, None] + prefix
+    sc = np.where(np.arange(seq)[None, :] > qi, -np.inf, sc)
+    m = sc.max(-1, keepdims=True)
+    p = np.exp(sc - m)
+    den = p.sum(-1, keepdims=True)
+    out = (p / den) @ values.astype(np.float64)
+    lse = (m + np.log(den))[:, 0]
+    return out.reshape(t, hq, d).astype(np.float32), lse.reshape(t, hq).astype(np.float32)

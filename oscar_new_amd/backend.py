@@ -1,0 +1,100 @@
+"""Per-layer launch order of the OSCAR INT2 attention path (vLLM-free).
+
+Reference: oscar_ascend/backend.py:67-227 (``OscarAttentionImpl``). The vLLM class plumbing
+(AttentionBackend registration, vllm_config validation) is out of scope; what is kept is the
+forward contract: same arguments, same kernel order, no host reads, the window store last
+(it must follow both attention branches because a long current chunk wraps the ring).
+Initial prefill without history (the reference's Ascend FIA call) is not provided: the
+INT2 path below also serves it, with one split.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import kernels
+from .config import OscarConfig, choose_splits, choose_splits_mi355x
+
+
+class OscarAttentionImpl:
+    """Reference: backend.py:132-227. ``split_policy`` "reference" keeps config.py:84-89,
+    "mi355x" fills the 256 CUs (config.choose_splits_mi355x)."""
+
+    def __init__(self, num_heads, head_size, scale, num_kv_heads, cfg=None,
+                 split_policy="reference"):
+        if head_size != 256:
+            raise ValueError("OSCAR requires FULL decoder attention with D256")
+        if num_kv_heads <= 0 or num_heads % num_kv_heads:
+            raise ValueError("query heads must be a multiple of kv heads")
+        if split_policy not in ("reference", "mi355x"):
+            raise ValueError("split_policy must be 'reference' or 'mi355x'")
+        self.num_heads = num_heads
+        self.num_kv_heads = num_kv_heads
+        self.head_size = head_size
+        self.scale = float(scale)
+        self.cfg = cfg or OscarConfig.from_env()
+        self.split_policy = split_policy
+        self.rk = self.rv = None
+        self.history = self.window = None
+        self.cache_identity = None
+
+    def initialize_layer(self, rk, rv):
+        """Install the layer's calibrated K/V rotations (bf16 [256, 256] on the device)."""
+        for r in (rk, rv):
+            if tuple(r.shape) != (256, 256):
+                raise ValueError("rotations must be 256x256")
+        self.rk = rk.to(torch.bfloat16).contiguous()
+        self.rv = rv.to(torch.bfloat16).contiguous()
+
+    def splits_for(self, meta):
+        if self.split_policy == "reference":
+            return choose_splits(meta.num_reqs, self.num_kv_heads, meta.max_query_len)
+        tasks = -(-meta.num_actual_tokens // self.cfg.queries_per_tile) if meta.max_query_len > 1 \
+            else meta.num_reqs
+        return choose_splits_mi355x(tasks, self.num_kv_heads, meta.max_query_len,
+                                    getattr(meta, "max_seq_len", None))
+
+    def forward(self, layer, query, key, value, kv_cache, attn_metadata, output=None):
+        """Reference: backend.py:190-292 (minus the Ascend prefill call)."""
+        if output is None:
+            raise ValueError("an attention output buffer is required")
+        if attn_metadata is None:
+            return output.zero_()
+        if self.rk is None or self.rv is None:
+            raise RuntimeError("OSCAR rotations were not initialized for this layer")
+        if key is None or value is None:
+            raise ValueError("OSCAR requires the current K/V to maintain exact BF16 windows")
+        if query.device.type != "cuda":
+            raise RuntimeError("OSCAR kernels run on a ROCm GPU")
+        meta = attn_metadata
+        n = query.shape[0]
+        query = query.view(n, self.num_heads, self.head_size)
+        key = key.view(key.shape[0], self.num_kv_heads, self.head_size)
+        value = value.view(value.shape[0], self.num_kv_heads, self.head_size)
+        if key.shape[0] != n or value.shape[0] != n:
+            raise ValueError("Q/K/V must have matching current-token dimensions")
+        identity = (kv_cache[0].data_ptr(), kv_cache[1].data_ptr(), meta.layout)
+        if self.cache_identity != identity:
+            self.history, self.window = meta.layout.tensor_views(kv_cache)
+            self.cache_identity = identity
+        if not output.is_contiguous():
+            raise ValueError("Attention output must be contiguous")
+        if n == 0:
+            return output
+
+        krot = kernels.rotate(key, self.rk)
+        vrot = kernels.rotate(value, self.rv)
+        kernels.store_int2(krot, vrot, self.history, meta.slot_mapping, meta.counts, meta.layout)
+        qrot = kernels.rotate(query, self.rk)
+        splits = self.splits_for(meta)
+        hp, hl = kernels.attention_partials(qrot, key, value, self.history, self.window, meta,
+                                            meta.layout, self.scale, splits, raw=False)
+        hrot, hlogsum = kernels.merge_splits(hp, hl, meta.counts)
+        hout = kernels.rotate(hrot, self.rv.T)
+        rp, rl = kernels.attention_partials(query, key, value, self.history, self.window, meta,
+                                            meta.layout, self.scale, 1, raw=True)
+        kernels.merge_paths(hout, hlogsum, rp, rl, meta.counts, output.view(n, -1),
+                            getattr(meta, "merged_lse", None))
+        # Must follow BOTH attention branches: long current chunks wrap the ring.
+        kernels.store_windows(key, value, self.window, meta, meta.layout)
+        return output

@@ -189,11 +189,25 @@ __device__ __forceinline__ void update_max(State<RT>& st, const float (&s2)[RT][
 // ---------------------------------------------------------------- epilogue
 
 // Merge the 4 wavefront states through LDS and write normalized partials + LSE.
+// LDS bytes finish() needs for RT row tiles.
+template <int RT>
+constexpr int finish_lds_bytes() {
+  return 4 * RT * 16 * 16 * 16 + (3 * 4 + 3) * RT * 16 * 4;
+}
+
 template <int RT, bool kHist>
-__device__ void finish(const AttnArgs& a, const Task& t, int head, int split, State<RT>& st) {
-  __shared__ float s_m[4][RT * 16], s_p[4][RT * 16], s_z[4][RT * 16];
-  __shared__ float s_max[RT * 16], s_den[RT * 16], s_lse[RT * 16];
-  __shared__ f32x4 s_red[4][RT * 16][16];
+__device__ void finish(const AttnArgs& a, const Task& t, int head, int split, State<RT>& st,
+                       uint8_t* lds) {
+  typedef f32x4 RedRow[16];
+  typedef RedRow RedWave[RT * 16];
+  RedWave* s_red = reinterpret_cast<RedWave*>(lds);
+  typedef float StatWave[RT * 16];
+  StatWave* s_m = reinterpret_cast<StatWave*>(lds + 4 * RT * 16 * 16 * 16);
+  StatWave* s_p = s_m + 4;
+  StatWave* s_z = s_p + 4;
+  float* s_max = reinterpret_cast<float*>(s_z + 4);
+  float* s_den = s_max + RT * 16;
+  float* s_lse = s_den + RT * 16;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int n = lane & 15, g = lane >> 4;
 #pragma unroll
@@ -275,37 +289,47 @@ __device__ void finish(const AttnArgs& a, const Task& t, int head, int split, St
 
 // ---------------------------------------------------------------- history branch
 
-struct HistBlock {
-  u32x4 kc[2];   // K codes of tokens n and 16 + n, bytes 16g..16g+15
-  uint32_t vc[8];   // V code dword n of tokens tau(g, e)
-  uint32_t ksz[8];  // K scale | zero << 16 of tokens tau(g, e)
-  uint32_t vsz[8];  // V scale | zero << 16
-};
+// Per-wavefront LDS pipeline: kStages buffers of one 32-token block each (32 x 160-byte
+// records, compact). One query row tile (decode): 3 stages, 2 workgroups per CU. Two row
+// tiles (MTP verification, more registers, 1 workgroup per CU): 5 stages. Blocks arrive by direct-to-LDS DMA (global_load_lds_dwordx4), five
+// 16-byte loads per lane per block, so staging costs no VGPRs. kStages - 1 blocks are in
+// flight while the wavefront computes the oldest one.
+constexpr int kBlockBytes = kBlock * kSlot;      // 5120
+constexpr int kDmaPerBlock = kBlockBytes / 1024;  // 16 B x 64 lanes per instruction
 
-struct HistLane {
-  uint32_t k[2];
-  uint32_t tok[8];
-  uint32_t vcode;
-};
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
-__device__ __forceinline__ void hist_load(const uint8_t* base, const HistLane& o, HistBlock& b) {
-  b.kc[0] = *reinterpret_cast<const u32x4*>(base + o.k[0]);
-  b.kc[1] = *reinterpret_cast<const u32x4*>(base + o.k[1]);
-#pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    b.ksz[e] = *reinterpret_cast<const uint32_t*>(base + o.tok[e] + 64);
-    b.vc[e] = *reinterpret_cast<const uint32_t*>(base + o.tok[e] + o.vcode);
-    b.vsz[e] = *reinterpret_cast<const uint32_t*>(base + o.tok[e] + kVector + 64);
-  }
+// One 16-byte-per-lane direct-to-LDS load: lane l writes LDS bytes [lds + 16 l, +16).
+// Issued through asm so the compiler does not serialize every later LDS read behind all
+// outstanding DMA (it cannot tell pipeline stages apart); ordering is by the explicit
+// vmcnt waits below. M0 holds the LDS base; one wait state separates its write from the DMA.
+__device__ __forceinline__ void dma16(const void* src, uint32_t lds_addr) {
+  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %1, off" : : "{m0}"(lds_addr), "v"(src)
+               : "memory");
 }
+
+// LDS DMA is issued by asm (see dma16), so waits are explicit.
+#define OSCAR_WAIT_VM(n) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(n) : "memory")
+#define OSCAR_WAIT_LDS() asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory")
+
+// Block-table entries of a workgroup's split range are staged in LDS once, so the KV loop
+// never issues a vector-memory load whose wait would also drain the in-flight LDS DMA.
+constexpr int kTableCache = 2048;  // kernel blocks (262144 tokens at 128 per block)
 
 // Byte address of a 32-token aligned block of this request/head, or nullptr if the block
 // table entry or the block's bytes are out of range.
+typedef __attribute__((address_space(3))) const int32_t* lds_i32_ptr_t;
+
 __device__ __forceinline__ const uint8_t* hist_block_base(const AttnArgs& a, const Task& t,
-                                                          int head, int t0) {
+                                                          int head, int t0, lds_i32_ptr_t s_tab,
+                                                          int kb_first) {
   const int kb = t0 >> a.L.bk_shift;
   if (kb >= a.table_columns) return nullptr;
-  const int blk = a.table[static_cast<int64_t>(t.req) * a.table_stride + kb];
+  const int local = kb - kb_first;
+  // Unconditional LDS read; the global read below only runs for splits longer than the cache.
+  int blk = uniform(s_tab[min(local, kTableCache - 1)]);
+  if (local >= kTableCache)
+    blk = uniform(a.table[static_cast<int64_t>(t.req) * a.table_stride + kb]);
   if (blk < 0) return nullptr;
   const uint32_t page = fastdiv(static_cast<uint32_t>(blk), a.L.bpp_div);
   const uint32_t inpage = static_cast<uint32_t>(blk) - page * a.L.bpp;
@@ -317,8 +341,8 @@ __device__ __forceinline__ const uint8_t* hist_block_base(const AttnArgs& a, con
 }
 
 template <int RT>
-__device__ __forceinline__ void hist_compute(const AttnArgs& a, const HistBlock& b, bool full,
-                                             int t0, int p_lo, int p_hi, int g,
+__device__ __forceinline__ void hist_compute(const AttnArgs& a, const uint8_t* blk, bool full,
+                                             int t0, int p_lo, int p_hi, int n, int g,
                                              const u32x4 (&qb)[RT][8], const float (&corr)[RT],
                                              const float (&qsum)[RT], State<RT>& st) {
   f32x4 sc[RT][2];
@@ -328,10 +352,11 @@ __device__ __forceinline__ void hist_compute(const AttnArgs& a, const HistBlock&
     for (int tt = 0; tt < 2; ++tt) sc[rt][tt] = f32x4{-corr[rt], -corr[rt], -corr[rt], -corr[rt]};
 #pragma unroll
   for (int tt = 0; tt < 2; ++tt) {
+    const u32x4 kc = *reinterpret_cast<const u32x4*>(blk + (16 * tt + n) * kSlot + 16 * g);
 #pragma unroll
     for (int w = 0; w < 4; ++w) {
       u32x4 s0, s1;
-      codes_to_steps(b.kc[tt][w], s0, s1);
+      codes_to_steps(kc[w], s0, s1);
 #pragma unroll
       for (int rt = 0; rt < RT; ++rt) {
         sc[rt][tt] = mfma16x16x32(s0, qb[rt][2 * w], sc[rt][tt]);
@@ -340,15 +365,20 @@ __device__ __forceinline__ void hist_compute(const AttnArgs& a, const HistBlock&
     }
   }
   float sk[8], zk[8], sv[8], zv[8];
+  uint32_t vc[8];
   bool ok[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
+    const uint8_t* rec = blk + tau(g, e) * kSlot;
+    const uint32_t ksz = *reinterpret_cast<const uint32_t*>(rec + 64);
+    const uint32_t vsz = *reinterpret_cast<const uint32_t*>(rec + kVector + 64);
+    vc[e] = *reinterpret_cast<const uint32_t*>(rec + kVector + 4 * n);
     const int pos = t0 + tau(g, e);
     ok[e] = full || (pos >= p_lo && pos < p_hi);
-    sk[e] = half_lo_to_float(b.ksz[e]);
-    zk[e] = half_hi_to_float(b.ksz[e]);
-    sv[e] = ok[e] ? half_lo_to_float(b.vsz[e]) : 0.f;
-    zv[e] = ok[e] ? half_hi_to_float(b.vsz[e]) : 0.f;
+    sk[e] = half_lo_to_float(ksz);
+    zk[e] = half_hi_to_float(ksz);
+    sv[e] = ok[e] ? half_lo_to_float(vsz) : 0.f;
+    zv[e] = ok[e] ? half_hi_to_float(vsz) : 0.f;
   }
   float s2[RT][8];
 #pragma unroll
@@ -376,8 +406,8 @@ __device__ __forceinline__ void hist_compute(const AttnArgs& a, const HistBlock&
   u32x4 zlo, zhi;
 #pragma unroll
   for (int f = 0; f < 4; ++f) {
-    zlo[f] = __builtin_amdgcn_perm(b.vc[2 * f + 1], b.vc[2 * f], 0x05040100u);
-    zhi[f] = __builtin_amdgcn_perm(b.vc[2 * f + 1], b.vc[2 * f], 0x07060302u);
+    zlo[f] = __builtin_amdgcn_perm(vc[2 * f + 1], vc[2 * f], 0x05040100u);
+    zhi[f] = __builtin_amdgcn_perm(vc[2 * f + 1], vc[2 * f], 0x07060302u);
   }
 #pragma unroll
   for (int tile = 0; tile < 16; ++tile) {
@@ -438,13 +468,25 @@ __device__ __forceinline__ void hist_query(const AttnArgs& a, const Task& t, int
 }
 
 template <int RT>
-__global__ __launch_bounds__(kThreads) void history_kernel(const AttnArgs a) {
+__global__ __launch_bounds__(kThreads, 3 - RT) void history_kernel(const AttnArgs a) {
+  constexpr int kStages = RT == 1 ? 3 : 5;
+  static_assert(4 * kStages * kBlockBytes >= finish_lds_bytes<RT>(), "epilogue LDS alias");
+  __shared__ __attribute__((aligned(16))) uint8_t smem[4 * kStages * kBlockBytes];
+  __shared__ int32_t s_tab[kTableCache];
   Task t;
   if (!read_task(a, t)) return;
   const int head = blockIdx.y, split = blockIdx.z;
   int begin, end;
   split_range(t.recent_begin - t.sink_len, a.block_n, a.splits, split, begin, end);
   const int p_lo = max(t.sink_len + begin, 0), p_hi = t.sink_len + end;
+  const int kb_first = p_lo >> a.L.bk_shift;
+  if (p_lo < p_hi) {
+    const int nkb = min(((p_hi - 1) >> a.L.bk_shift) - kb_first + 1, kTableCache);
+    const int32_t* row = a.table + static_cast<int64_t>(t.req) * a.table_stride;
+    for (int j = threadIdx.x; j < nkb; j += kThreads)
+      s_tab[j] = kb_first + j < a.table_columns ? row[kb_first + j] : -1;
+  }
+  __syncthreads();
   const int lane = threadIdx.x & 63;
   const int wave = uniform(threadIdx.x >> 6);
   const int n = lane & 15, g = lane >> 4;
@@ -458,32 +500,47 @@ __global__ __launch_bounds__(kThreads) void history_kernel(const AttnArgs a) {
   if (p_lo < p_hi) {
     const int first = p_lo >> 5;
     const int nblk = ((p_hi - 1) >> 5) - first + 1;
-    const uint32_t tok = static_cast<uint32_t>(a.L.kv_heads) * kSlot;
-    HistLane o;
-    o.k[0] = n * tok + 16 * g;
-    o.k[1] = (16 + n) * tok + 16 * g;
+    // DMA piece i of this lane: 16 bytes of record c / 10, bytes 16 * (c % 10), c = 64 i + lane.
+    uint32_t goff[kDmaPerBlock];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) o.tok[e] = tau(g, e) * tok;
-    o.vcode = kVector + 4 * n;
-
-    HistBlock cur, nxt;
-    int ib = wave;
-    const uint8_t* bc = ib < nblk ? hist_block_base(a, t, head, (first + ib) << 5) : nullptr;
-    if (bc) hist_load(bc, o, cur);
-    for (; ib < nblk; ib += 4) {
-      const int ibn = ib + 4;
-      const uint8_t* bn = ibn < nblk ? hist_block_base(a, t, head, (first + ibn) << 5) : nullptr;
-      if (bn) hist_load(bn, o, nxt);
-      if (bc) {
+    for (int i = 0; i < kDmaPerBlock; ++i) {
+      const int c = i * 64 + lane;
+      goff[i] = static_cast<uint32_t>((c / 10) * a.L.kv_heads * kSlot + (c % 10) * 16);
+    }
+    uint8_t* wbuf = smem + wave * (kStages * kBlockBytes);
+    int valid_mask = 0;
+    // Always five loads per block (a safe in-bounds dummy block when out of range) so the
+    // number of loads younger than any block is a constant: 5 * (kStages - 1).
+    auto issue = [&](int ib, int stage) {
+      const uint8_t* base =
+          ib < nblk ? hist_block_base(a, t, head, (first + ib) << 5, (lds_i32_ptr_t)s_tab, kb_first)
+                    : nullptr;
+      valid_mask = base ? (valid_mask | (1 << stage)) : (valid_mask & ~(1 << stage));
+      if (!base) base = a.history;
+      OSCAR_WAIT_LDS();
+      const uint32_t lds = static_cast<uint32_t>(
+          reinterpret_cast<uintptr_t>((lds_ptr_t)(wbuf + stage * kBlockBytes)));
+#pragma unroll
+      for (int i = 0; i < kDmaPerBlock; ++i) dma16(base + goff[i], uniform(lds + i * 1024));
+    };
+#pragma unroll
+    for (int k = 0; k < kStages - 1; ++k) issue(wave + 4 * k, k);
+    int stage = 0;
+    for (int ib = wave; ib < nblk; ib += 4) {
+      issue(ib + 4 * (kStages - 1), stage == 0 ? kStages - 1 : stage - 1);
+      OSCAR_WAIT_VM(kDmaPerBlock * (kStages - 1));
+      if (valid_mask & (1 << stage)) {
         const int t0 = (first + ib) << 5;
         const bool full = t0 >= p_lo && t0 + kBlock <= p_hi;
-        hist_compute<RT>(a, cur, full, t0, p_lo, p_hi, g, qb, corr, qsum, st);
+        hist_compute<RT>(a, wbuf + stage * kBlockBytes, full, t0, p_lo, p_hi, n, g, qb, corr,
+                         qsum, st);
       }
-      cur = nxt;
-      bc = bn;
+      stage = stage == kStages - 1 ? 0 : stage + 1;
     }
+    OSCAR_WAIT_VM(0);
   }
-  finish<RT, true>(a, t, head, split, st);
+  __syncthreads();  // the epilogue reuses the pipeline's LDS
+  finish<RT, true>(a, t, head, split, st, smem);
 }
 
 // ---------------------------------------------------------------- raw (BF16) branch
@@ -519,6 +576,7 @@ __device__ __forceinline__ const uint16_t* raw_token(const AttnArgs& a, const Ta
 
 template <int RT>
 __global__ __launch_bounds__(kThreads) void raw_kernel(const AttnArgs a) {
+  __shared__ __attribute__((aligned(16))) uint8_t smem[finish_lds_bytes<RT>()];
   Task t;
   if (!read_task(a, t)) return;
   const int head = blockIdx.y, split = blockIdx.z;
@@ -618,7 +676,7 @@ __global__ __launch_bounds__(kThreads) void raw_kernel(const AttnArgs a) {
       for (int rt = 0; rt < RT; ++rt) st.o[rt][tile] = mfma16x16x32(ap[rt], bv, st.o[rt][tile]);
     }
   }
-  finish<RT, false>(a, t, head, split, st);
+  finish<RT, false>(a, t, head, split, st, smem);
 }
 
 }  // namespace
@@ -660,6 +718,7 @@ extern "C" int oscar_attention_partials(
   } else {
     if (!history) return OSCAR_E_NULL;
     if (!aligned16(history)) return OSCAR_E_ALIGN;
+    if (history_bytes < 32 * h * 160) return OSCAR_E_SHAPE;  // smaller than one 32-token block
   }
   a.query = static_cast<const uint16_t*>(query);
   a.qs0 = q_s0;

@@ -45,9 +45,10 @@ def test_rotation_strides_match_oracle():
     got = bits(out)
     torch.testing.assert_close(torch.from_numpy(O.bf16_to_f32(got)),
                                torch.from_numpy(O.bf16_to_f32(want)), atol=0.03125, rtol=0.015)
-    # fp32 accumulation in a different order flips at most the last bf16 bit, rarely.
-    diff = np.abs(got.astype(np.int32) - want.astype(np.int32))
-    assert diff.max() <= 1 and (diff > 0).mean() < 0.02
+    # fp32 accumulation in a different order moves a result by at most one bf16 step.
+    g32, w32 = O.bf16_to_f32(got), O.bf16_to_f32(want)
+    assert np.all(np.abs(g32 - w32) <= 2.0**-7 * np.abs(w32) + 1e-4)
+    assert (g32 != w32).mean() < 0.02
 
 
 @pytest.mark.parametrize("rows", [1, 7, 64, 65, 4096])
@@ -55,10 +56,11 @@ def test_rotation_sizes_contiguous(rows):
     g = torch.Generator().manual_seed(rows)
     x = torch.randn(rows, 1, 256, generator=g).bfloat16().to(DEV)
     r = _qr_bf16(3)
-    got = bits(kernels.rotate(x, r))
-    want = O.rotate(bits(x), bits(r))
-    diff = np.abs(got.astype(np.int32) - want.astype(np.int32))
-    assert diff.max() <= 1 and (diff > 0).mean() < 0.02
+    got = O.bf16_to_f32(bits(kernels.rotate(x, r)))
+    want = O.bf16_to_f32(O.rotate(bits(x), bits(r)))
+    # A different fp32 summation order may move a result across one bf16 rounding boundary.
+    assert np.all(np.abs(got - want) <= 2.0**-7 * np.abs(want) + 1e-4)
+    assert (got != want).mean() < 0.02
 
 
 # ------------------------------------------------------------------ store_int2 / unpack

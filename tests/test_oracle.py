@@ -482,3 +482,19 @@ def test_merge_paths_limits():
     np.testing.assert_allclose(out[0, 0], 0.5, rtol=1e-2)
     np.testing.assert_allclose(out[0, 1], (3 * 2 - 1) / 4, rtol=1e-2)
     np.testing.assert_allclose(lse[0], [math.log(2), math.log(4)], rtol=1e-6)
+
+
+def test_cached_decode_reference_equals_hybrid_reference():
+    """The cache read-back restatement equals the dense hybrid reference on one request."""
+    geo = O.Geometry(768, sink_tokens=4, recent_tokens=16, speculative_tokens=3)
+    lengths, prefixes = [300], [299]
+    history, window, table, ks, vs, rk, rv = _paged_state(lengths, prefixes, geo, seed=9)
+    q = O.f32_to_bf16(np.random.default_rng(1).standard_normal((1, 6, 256)).astype(np.float32))
+    got, lse = O.cached_decode_reference(history, window, table[0], 300, q, ks[0][299:],
+                                         vs[0][299:], rk, rv, geo)
+    want, want_lse = O.hybrid_reference(q, ks[0], vs[0], 299, rk, rv,
+                                        {"sink_tokens": 4, "recent_tokens": 16})
+    np.testing.assert_allclose(got, want, atol=2e-3)
+    np.testing.assert_allclose(lse, want_lse, atol=2e-4)
+    rows = O.dequant_rows(history, [geo.slot_offset(geo.logical_slot(table[0], 50))])
+    assert np.array_equal(rows[0], O.load_vec(history, geo.slot_offset(geo.logical_slot(table[0], 50))))
