@@ -54,7 +54,26 @@ def parse_args(argv=None):
     p.add_argument("--cpu-sample", type=int, default=2, help="requests timed on the CPU oracle")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-graph", action="store_true", help="eager launches instead of HIP graphs")
+    p.add_argument("--mode", default="step", choices=("step", "history", "copy"),
+                   help="step: full benchmark; history: only the history-attention launches "
+                        "(for rocprofv3 counters); copy: a plain device copy of --copy-mib MiB "
+                        "(counter calibration)")
+    p.add_argument("--copy-mib", type=int, default=1024)
     return p.parse_args(argv)
+
+
+def copy_calibration(args, device):
+    """A plain copy of known size, to scale FETCH_SIZE / WRITE_SIZE counters."""
+    import torch
+
+    n = args.copy_mib << 20
+    src = torch.randint(0, 255, (n,), dtype=torch.uint8, device=device)
+    dst = torch.empty_like(src)
+    for _ in range(args.steps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"mode": "copy", "bytes_per_copy": n, "copies": args.steps}))
+    return 0
 
 
 # ------------------------------------------------------------------ workload
@@ -315,6 +334,8 @@ def main(argv=None):
         return 1
     device = torch.device("cuda:0")
     torch.cuda.set_device(device)
+    if args.mode == "copy":
+        return copy_calibration(args, device)
     cfg = CONFIGS[args.config]
     print(f"[bench] building {args.config} workload ({args.layers} layers)", file=sys.stderr, flush=True)
     w = build_workload(args, cfg, device)
@@ -332,6 +353,20 @@ def main(argv=None):
 
     def step(i):
         impls[i].forward(None, w.q, w.k, w.v, layers[i], w.meta, outputs[i])
+
+    if args.mode == "history":
+        qrot = kernels.rotate(w.q, w.rk)
+        views = [w.layout.tensor_views(c) for c in layers]
+        for i in range(args.warmup + args.steps):
+            h, win = views[i % len(layers)]
+            kernels.attention_partials(qrot, w.k, w.v, h, win, w.meta, w.layout, 1 / 16, splits,
+                                       False)
+        torch.cuda.synchronize()
+        alg = algorithmic_bytes(w)
+        print(json.dumps({"mode": "history", "launches": args.warmup + args.steps,
+                          "splits": splits, "history_tokens": alg.history_tokens,
+                          "int2_bytes": alg.int2, "physical_record_bytes": 160 * alg.history_tokens}))
+        return 0
 
     for i in range(len(layers)):  # eager warm-up (also builds the tensor views)
         step(i)

@@ -59,6 +59,7 @@ struct AttnArgs {
   Layout L;
   int32_t g, hq, qt, splits, block_n;
   float scale_log2;
+  uint32_t mask[3];  // 0x00030003 << 2s, s = 0..2: code-field masks (see and_or)
 };
 
 struct Task {
@@ -117,18 +118,40 @@ __device__ __forceinline__ float field_scale_inv(int jp) {
   return s == 0 ? 1.0f : (s == 1 ? 0.25f : 0.0625f);
 }
 
+// (a & mask) | magic in ONE v_and_or_b32. gfx9 VOP3 reads at most one scalar or literal
+// operand, so the masks arrive as kernel arguments (SGPRs, see AttnArgs::mask) and magic is
+// a VGPR the compiler cannot fold (opaque_magic). Plain C, not asm: VALU results feeding
+// MFMA operands must stay visible to the compiler's hazard tracking.
+__device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t mask, uint32_t magic) {
+  return (a & mask) | magic;
+}
+
+__device__ __forceinline__ uint32_t opaque_magic() {
+  return static_cast<uint32_t>(
+      __builtin_amdgcn_mov_dpp(static_cast<int>(kMagic), 0xe4, 0xf, 0xf, false));
+}
+
 // One 16-code K dword -> the A operands of two consecutive k-steps (8 bf16 each).
 // D-dword j' holds (128 + 4^s c_{j'}, 128 + 4^s c_{8+j'}), s = j' % 3.
-__device__ __forceinline__ void codes_to_steps(uint32_t w, u32x4& s0, u32x4& s1) {
+__device__ __forceinline__ void codes_to_steps(uint32_t w, const uint32_t (&mk)[3],
+                                               uint32_t magic, u32x4& s0, u32x4& s1) {
   const uint32_t w6 = w >> 6, w12 = w >> 12;
-  s0[0] = (w & 0x00030003u) | kMagic;
-  s0[1] = (w & 0x000c000cu) | kMagic;
-  s0[2] = (w & 0x00300030u) | kMagic;
-  s0[3] = (w6 & 0x00030003u) | kMagic;
-  s1[0] = (w6 & 0x000c000cu) | kMagic;
-  s1[1] = (w6 & 0x00300030u) | kMagic;
-  s1[2] = (w12 & 0x00030003u) | kMagic;
-  s1[3] = (w12 & 0x000c000cu) | kMagic;
+  s0[0] = and_or(w, mk[0], magic);
+  s0[1] = and_or(w, mk[1], magic);
+  s0[2] = and_or(w, mk[2], magic);
+  s0[3] = and_or(w6, mk[0], magic);
+  s1[0] = and_or(w6, mk[1], magic);
+  s1[1] = and_or(w6, mk[2], magic);
+  s1[2] = and_or(w12, mk[0], magic);
+  s1[3] = and_or(w12, mk[1], magic);
+}
+
+__device__ __forceinline__ float h16(_Float16 h) { return static_cast<float>(h); }
+__device__ __forceinline__ _Float16 lo16(uint32_t x) {
+  return __builtin_bit_cast(_Float16, static_cast<uint16_t>(x & 0xffffu));
+}
+__device__ __forceinline__ _Float16 hi16(uint32_t x) {
+  return __builtin_bit_cast(_Float16, static_cast<uint16_t>(x >> 16));
 }
 
 // ---------------------------------------------------------------- softmax state
@@ -312,37 +335,34 @@ __device__ __forceinline__ void dma16(const void* src, uint32_t lds_addr) {
 #define OSCAR_WAIT_VM(n) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(n) : "memory")
 #define OSCAR_WAIT_LDS() asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory")
 
-// Block-table entries of a workgroup's split range are staged in LDS once, so the KV loop
-// never issues a vector-memory load whose wait would also drain the in-flight LDS DMA.
+// The byte offsets of the kernel blocks a workgroup reads (in 32-byte units, or kNoBlock)
+// are resolved once, into LDS, by the whole workgroup. The KV loop then reads one LDS word
+// per block: no vector-memory load whose wait would also drain the in-flight LDS DMA, and
+// little scalar arithmetic.
 constexpr int kTableCache = 2048;  // kernel blocks (262144 tokens at 128 per block)
+constexpr uint32_t kNoBlock = 0xffffffffu;
 
-// Byte address of a 32-token aligned block of this request/head, or nullptr if the block
-// table entry or the block's bytes are out of range.
-typedef __attribute__((address_space(3))) const int32_t* lds_i32_ptr_t;
+typedef __attribute__((address_space(3))) const uint32_t* lds_u32_ptr_t;
 
-__device__ __forceinline__ const uint8_t* hist_block_base(const AttnArgs& a, const Task& t,
-                                                          int head, int t0, lds_i32_ptr_t s_tab,
-                                                          int kb_first) {
-  const int kb = t0 >> a.L.bk_shift;
-  if (kb >= a.table_columns) return nullptr;
-  const int local = kb - kb_first;
-  // Unconditional LDS read; the global read below only runs for splits longer than the cache.
-  int blk = uniform(s_tab[min(local, kTableCache - 1)]);
-  if (local >= kTableCache)
-    blk = uniform(a.table[static_cast<int64_t>(t.req) * a.table_stride + kb]);
-  if (blk < 0) return nullptr;
+// Offset (32-byte units) of kernel block kb of this request/head, or kNoBlock.
+__device__ __forceinline__ uint32_t kernel_block_offset(const AttnArgs& a, const Task& t, int head,
+                                                        int kb) {
+  if (kb < 0 || kb >= a.table_columns) return kNoBlock;
+  const int blk = a.table[static_cast<int64_t>(t.req) * a.table_stride + kb];
+  if (blk < 0) return kNoBlock;
   const uint32_t page = fastdiv(static_cast<uint32_t>(blk), a.L.bpp_div);
   const uint32_t inpage = static_cast<uint32_t>(blk) - page * a.L.bpp;
-  const int64_t tok0 = static_cast<int64_t>(inpage) * a.L.bk + (t0 & (a.L.bk - 1));
   const int64_t off = static_cast<int64_t>(page) * a.L.page_bytes +
-                      (tok0 * a.L.kv_heads + head) * kSlot;
-  if (off + static_cast<int64_t>(kBlock) * a.L.kv_heads * kSlot > a.history_bytes) return nullptr;
-  return a.history + off;
+                      (static_cast<int64_t>(inpage) * a.L.bk * a.L.kv_heads + head) * kSlot;
+  // The whole kernel block must lie inside the history buffer.
+  if (off + static_cast<int64_t>(a.L.bk) * a.L.kv_heads * kSlot > a.history_bytes) return kNoBlock;
+  return static_cast<uint32_t>(off >> 5);
 }
 
 template <int RT>
-__device__ __forceinline__ void hist_compute(const AttnArgs& a, const uint8_t* blk, bool full,
-                                             int t0, int p_lo, int p_hi, int n, int g,
+__device__ __forceinline__ void hist_compute(const AttnArgs& a, const uint8_t* blk, int t0,
+                                             int p_lo, int p_hi, int n, int g,
+                                             const uint32_t (&mk)[3], uint32_t magic,
                                              const u32x4 (&qb)[RT][8], const float (&corr)[RT],
                                              const float (&qsum)[RT], State<RT>& st) {
   f32x4 sc[RT][2];
@@ -356,7 +376,7 @@ __device__ __forceinline__ void hist_compute(const AttnArgs& a, const uint8_t* b
 #pragma unroll
     for (int w = 0; w < 4; ++w) {
       u32x4 s0, s1;
-      codes_to_steps(kc[w], s0, s1);
+      codes_to_steps(kc[w], mk, magic, s0, s1);
 #pragma unroll
       for (int rt = 0; rt < RT; ++rt) {
         sc[rt][tt] = mfma16x16x32(s0, qb[rt][2 * w], sc[rt][tt]);
@@ -364,31 +384,32 @@ __device__ __forceinline__ void hist_compute(const AttnArgs& a, const uint8_t* b
       }
     }
   }
-  float sk[8], zk[8], sv[8], zv[8];
-  uint32_t vc[8];
+  // Every block overlaps [p_lo, p_hi), so the running max is finite after update_max and
+  // a -inf score gives p = 0 exactly; only V's scale/zero need masking (against NaN bits).
+  uint32_t ksz[8], vsz[8], vc[8];
   bool ok[8];
+  const uint32_t span = static_cast<uint32_t>(p_hi - p_lo);
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
     const uint8_t* rec = blk + tau(g, e) * kSlot;
-    const uint32_t ksz = *reinterpret_cast<const uint32_t*>(rec + 64);
-    const uint32_t vsz = *reinterpret_cast<const uint32_t*>(rec + kVector + 64);
+    ksz[e] = *reinterpret_cast<const uint32_t*>(rec + 64);
+    vsz[e] = *reinterpret_cast<const uint32_t*>(rec + kVector + 64);
     vc[e] = *reinterpret_cast<const uint32_t*>(rec + kVector + 4 * n);
-    const int pos = t0 + tau(g, e);
-    ok[e] = full || (pos >= p_lo && pos < p_hi);
-    sk[e] = half_lo_to_float(ksz);
-    zk[e] = half_hi_to_float(ksz);
-    sv[e] = ok[e] ? half_lo_to_float(vsz) : 0.f;
-    zv[e] = ok[e] ? half_hi_to_float(vsz) : 0.f;
+    ok[e] = static_cast<uint32_t>(t0 + tau(g, e) - p_lo) < span;
+    vsz[e] = ok[e] ? vsz[e] : 0u;
   }
+  // Scores in log2 units: (s_k (q.c) + z_k sum(q)) * scale * log2(e).
   float s2[RT][8];
 #pragma unroll
-  for (int rt = 0; rt < RT; ++rt)
+  for (int rt = 0; rt < RT; ++rt) {
+    const float qs = qsum[rt] * a.scale_log2;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      const float qc = sc[rt][e >> 2][e & 3];
-      const float v = fmaf(sk[e], qc, zk[e] * qsum[rt]) * a.scale_log2;
+      const float qc = sc[rt][e >> 2][e & 3] * a.scale_log2;
+      const float v = fmaf(h16(lo16(ksz[e])), qc, h16(hi16(ksz[e])) * qs);
       s2[rt][e] = ok[e] ? v : -INFINITY;
     }
+  }
   update_max<RT, 17>(st, s2, g);
   u32x4 aw[RT];
 #pragma unroll
@@ -396,12 +417,14 @@ __device__ __forceinline__ void hist_compute(const AttnArgs& a, const uint8_t* b
     float p[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      p[e] = ok[e] ? exp2f(s2[rt][e] - st.m[rt]) : 0.f;
+      p[e] = __builtin_amdgcn_exp2f(s2[rt][e] - st.m[rt]);
       st.psum[rt] += p[e];
-      st.zsum[rt] = fmaf(p[e], zv[e], st.zsum[rt]);
+      st.zsum[rt] = fmaf(p[e], h16(hi16(vsz[e])), st.zsum[rt]);
     }
 #pragma unroll
-    for (int f = 0; f < 4; ++f) aw[rt][f] = pack_bf16x2(p[2 * f] * sv[2 * f], p[2 * f + 1] * sv[2 * f + 1]);
+    for (int f = 0; f < 4; ++f)
+      aw[rt][f] = pack_bf16x2(p[2 * f] * h16(lo16(vsz[2 * f])),
+                              p[2 * f + 1] * h16(lo16(vsz[2 * f + 1])));
   }
   u32x4 zlo, zhi;
 #pragma unroll
@@ -413,14 +436,14 @@ __device__ __forceinline__ void hist_compute(const AttnArgs& a, const uint8_t* b
   for (int tile = 0; tile < 16; ++tile) {
     const int jp = tile & 7;
     const int sh = 6 * (jp / 3);
-    const uint32_t mask = 0x00030003u << (2 * (jp % 3));
+    const uint32_t mask = mk[jp % 3];
     u32x4 bv;
 #pragma unroll
-    for (int f = 0; f < 4; ++f) bv[f] = (((tile < 8 ? zlo[f] : zhi[f]) >> sh) & mask) | kMagic;
+    for (int f = 0; f < 4; ++f) bv[f] = and_or((tile < 8 ? zlo[f] : zhi[f]) >> sh, mask, magic);
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) st.o[rt][tile] = mfma16x16x32(aw[rt], bv, st.o[rt][tile]);
   }
-  const u32x4 b128 = u32x4{kMagic, kMagic, kMagic, kMagic};
+  const u32x4 b128 = u32x4{magic, magic, magic, magic};
 #pragma unroll
   for (int rt = 0; rt < RT; ++rt) st.o[rt][16] = mfma16x16x32(aw[rt], b128, st.o[rt][16]);
 }
@@ -472,7 +495,7 @@ __global__ __launch_bounds__(kThreads, 3 - RT) void history_kernel(const AttnArg
   constexpr int kStages = RT == 1 ? 3 : 5;
   static_assert(4 * kStages * kBlockBytes >= finish_lds_bytes<RT>(), "epilogue LDS alias");
   __shared__ __attribute__((aligned(16))) uint8_t smem[4 * kStages * kBlockBytes];
-  __shared__ int32_t s_tab[kTableCache];
+  __shared__ uint32_t s_off[kTableCache];
   Task t;
   if (!read_task(a, t)) return;
   const int head = blockIdx.y, split = blockIdx.z;
@@ -482,9 +505,8 @@ __global__ __launch_bounds__(kThreads, 3 - RT) void history_kernel(const AttnArg
   const int kb_first = p_lo >> a.L.bk_shift;
   if (p_lo < p_hi) {
     const int nkb = min(((p_hi - 1) >> a.L.bk_shift) - kb_first + 1, kTableCache);
-    const int32_t* row = a.table + static_cast<int64_t>(t.req) * a.table_stride;
     for (int j = threadIdx.x; j < nkb; j += kThreads)
-      s_tab[j] = kb_first + j < a.table_columns ? row[kb_first + j] : -1;
+      s_off[j] = kernel_block_offset(a, t, head, kb_first + j);
   }
   __syncthreads();
   const int lane = threadIdx.x & 63;
@@ -496,32 +518,45 @@ __global__ __launch_bounds__(kThreads, 3 - RT) void history_kernel(const AttnArg
   hist_query<RT>(a, t, head, n, g, qb, corr, qsum);
   State<RT> st;
   state_init(st);
+  const uint32_t magic = opaque_magic();
+  const uint32_t mk[3] = {a.mask[0], a.mask[1], a.mask[2]};
 
   if (p_lo < p_hi) {
     const int first = p_lo >> 5;
     const int nblk = ((p_hi - 1) >> 5) - first + 1;
+    const uint32_t tok_bytes = static_cast<uint32_t>(a.L.kv_heads) * kSlot;
     // DMA piece i of this lane: 16 bytes of record c / 10, bytes 16 * (c % 10), c = 64 i + lane.
     uint32_t goff[kDmaPerBlock];
 #pragma unroll
     for (int i = 0; i < kDmaPerBlock; ++i) {
       const int c = i * 64 + lane;
-      goff[i] = static_cast<uint32_t>((c / 10) * a.L.kv_heads * kSlot + (c % 10) * 16);
+      goff[i] = static_cast<uint32_t>((c / 10) * tok_bytes + (c % 10) * 16);
     }
     uint8_t* wbuf = smem + wave * (kStages * kBlockBytes);
+    const uint32_t wbuf_lds = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_ptr_t)wbuf));
+    const uint32_t in_kb_mask = static_cast<uint32_t>(a.L.bk - 1);
     int valid_mask = 0;
     // Always five loads per block (a safe in-bounds dummy block when out of range) so the
     // number of loads younger than any block is a constant: 5 * (kStages - 1).
     auto issue = [&](int ib, int stage) {
-      const uint8_t* base =
-          ib < nblk ? hist_block_base(a, t, head, (first + ib) << 5, (lds_i32_ptr_t)s_tab, kb_first)
-                    : nullptr;
-      valid_mask = base ? (valid_mask | (1 << stage)) : (valid_mask & ~(1 << stage));
-      if (!base) base = a.history;
+      const uint8_t* base = a.history;
+      bool ok = false;
+      if (ib < nblk) {
+        const int t0 = (first + ib) << 5;
+        const int local = (t0 >> a.L.bk_shift) - kb_first;
+        uint32_t off32 = uniform(((lds_u32_ptr_t)s_off)[min(local, kTableCache - 1)]);
+        if (local >= kTableCache) off32 = kernel_block_offset(a, t, head, t0 >> a.L.bk_shift);
+        if (off32 != kNoBlock) {
+          ok = true;
+          base = a.history + (static_cast<uint64_t>(off32) << 5) +
+                 (static_cast<uint32_t>(t0) & in_kb_mask) * tok_bytes;
+        }
+      }
+      valid_mask = ok ? (valid_mask | (1 << stage)) : (valid_mask & ~(1 << stage));
       OSCAR_WAIT_LDS();
-      const uint32_t lds = static_cast<uint32_t>(
-          reinterpret_cast<uintptr_t>((lds_ptr_t)(wbuf + stage * kBlockBytes)));
+      const uint32_t lds = wbuf_lds + stage * kBlockBytes;
 #pragma unroll
-      for (int i = 0; i < kDmaPerBlock; ++i) dma16(base + goff[i], uniform(lds + i * 1024));
+      for (int i = 0; i < kDmaPerBlock; ++i) dma16(base + goff[i], lds + i * 1024);
     };
 #pragma unroll
     for (int k = 0; k < kStages - 1; ++k) issue(wave + 4 * k, k);
@@ -530,10 +565,8 @@ __global__ __launch_bounds__(kThreads, 3 - RT) void history_kernel(const AttnArg
       issue(ib + 4 * (kStages - 1), stage == 0 ? kStages - 1 : stage - 1);
       OSCAR_WAIT_VM(kDmaPerBlock * (kStages - 1));
       if (valid_mask & (1 << stage)) {
-        const int t0 = (first + ib) << 5;
-        const bool full = t0 >= p_lo && t0 + kBlock <= p_hi;
-        hist_compute<RT>(a, wbuf + stage * kBlockBytes, full, t0, p_lo, p_hi, n, g, qb, corr,
-                         qsum, st);
+        hist_compute<RT>(a, wbuf + stage * kBlockBytes, (first + ib) << 5, p_lo, p_hi, n, g,
+                         mk, magic, qb, corr, qsum, st);
       }
       stage = stage == kStages - 1 ? 0 : stage + 1;
     }
@@ -750,6 +783,9 @@ extern "C" int oscar_attention_partials(
   a.splits = splits;
   a.block_n = block_n;
   a.scale_log2 = scale * kLog2e;
+  a.mask[0] = 0x00030003u;
+  a.mask[1] = 0x000c000cu;
+  a.mask[2] = 0x00300030u;
   const dim3 grid(static_cast<unsigned>(programs), static_cast<unsigned>(h),
                   static_cast<unsigned>(splits));
   hipStream_t s = as_stream(stream);

@@ -27,17 +27,15 @@ __device__ __forceinline__ float bf16_to_float(uint32_t bits16) {
   return __uint_as_float(bits16 << 16);
 }
 
-// float -> bf16 bits, round to nearest even, NaN kept quiet (matches torch's .bfloat16()).
-__device__ __forceinline__ uint32_t float_to_bf16(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return ((u >> 16) & 0x8000u) | 0x7fc0u;
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return u >> 16;
-}
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 
+// float -> bf16 bits with the gfx950 hardware conversion (v_cvt_pk_bf16_f32): round to
+// nearest even, NaN stays NaN -- the rounding of torch's .bfloat16().
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
-  return float_to_bf16(lo) | (float_to_bf16(hi) << 16);
+  const bf16x2_t v = {static_cast<__bf16>(lo), static_cast<__bf16>(hi)};
+  return __builtin_bit_cast(uint32_t, v);
 }
+__device__ __forceinline__ uint32_t float_to_bf16(float f) { return pack_bf16x2(f, 0.f) & 0xffffu; }
 
 // IEEE fp16 <-> fp32 (hardware conversion, round to nearest even, subnormals kept).
 __device__ __forceinline__ float f16_bits_to_float(uint32_t bits16) {
