@@ -176,34 +176,37 @@ __device__ __forceinline__ void state_init(State<RT>& st) {
   }
 }
 
-// Row max of the block, lazy rescale; returns nothing, updates st.m and accumulators.
+// Lazy running max. Each lane first checks its own 8 scores against m + 2^8 (no cross-lane
+// traffic); only if some lane of the wavefront sees a larger score is the row max reduced
+// across the 4 lane groups and the accumulators rescaled. Between updates p <= 2^8.
 template <int RT, int kTiles>
 __device__ __forceinline__ void update_max(State<RT>& st, const float (&s2)[RT][8], int g) {
-  float bm[RT];
+  float lm[RT];
   bool need = false;
 #pragma unroll
   for (int rt = 0; rt < RT; ++rt) {
     float v = s2[rt][0];
 #pragma unroll
     for (int e = 1; e < 8; ++e) v = fmaxf(v, s2[rt][e]);
-    v = fmaxf(v, __shfl_xor(v, 16, kWave));
-    v = fmaxf(v, __shfl_xor(v, 32, kWave));
-    bm[rt] = v;
+    lm[rt] = v;
     need |= v > st.m[rt] + kRescale;
   }
   if (__any(need)) {
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) {
-      const float mn = fmaxf(st.m[rt], bm[rt]);
+      float v = lm[rt];
+      v = fmaxf(v, __shfl_xor(v, 16, kWave));
+      v = fmaxf(v, __shfl_xor(v, 32, kWave));
+      const float mn = fmaxf(st.m[rt], v);
       const float alpha = mn == -INFINITY ? 1.0f : exp2f(st.m[rt] - mn);
       st.m[rt] = mn;
       st.psum[rt] *= alpha;
       st.zsum[rt] *= alpha;
 #pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const float av = __shfl(alpha, 4 * g + v, kWave);
+      for (int v4 = 0; v4 < 4; ++v4) {
+        const float av = __shfl(alpha, 4 * g + v4, kWave);
 #pragma unroll
-        for (int t = 0; t < kTiles; ++t) st.o[rt][t][v] *= av;
+        for (int t = 0; t < kTiles; ++t) st.o[rt][t][v4] *= av;
       }
     }
   }
@@ -365,38 +368,52 @@ __device__ __forceinline__ void hist_compute(const AttnArgs& a, const uint8_t* b
                                              const uint32_t (&mk)[3], uint32_t magic,
                                              const u32x4 (&qb)[RT][8], const float (&corr)[RT],
                                              const float (&qsum)[RT], State<RT>& st) {
+  // S^T tiles (tokens 0-15, 16-31): the two MFMA chains alternate so that every dependent
+  // accumulation has an independent MFMA between it and its predecessor.
+  const u32x4 kc0 = *reinterpret_cast<const u32x4*>(blk + n * kSlot + 16 * g);
+  const u32x4 kc1 = *reinterpret_cast<const u32x4*>(blk + (16 + n) * kSlot + 16 * g);
   f32x4 sc[RT][2];
 #pragma unroll
   for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
     for (int tt = 0; tt < 2; ++tt) sc[rt][tt] = f32x4{-corr[rt], -corr[rt], -corr[rt], -corr[rt]};
 #pragma unroll
-  for (int tt = 0; tt < 2; ++tt) {
-    const u32x4 kc = *reinterpret_cast<const u32x4*>(blk + (16 * tt + n) * kSlot + 16 * g);
+  for (int w = 0; w < 4; ++w) {
+    u32x4 a0, a1, b0, b1;
+    codes_to_steps(kc0[w], mk, magic, a0, a1);
+    codes_to_steps(kc1[w], mk, magic, b0, b1);
 #pragma unroll
-    for (int w = 0; w < 4; ++w) {
-      u32x4 s0, s1;
-      codes_to_steps(kc[w], mk, magic, s0, s1);
-#pragma unroll
-      for (int rt = 0; rt < RT; ++rt) {
-        sc[rt][tt] = mfma16x16x32(s0, qb[rt][2 * w], sc[rt][tt]);
-        sc[rt][tt] = mfma16x16x32(s1, qb[rt][2 * w + 1], sc[rt][tt]);
-      }
+    for (int rt = 0; rt < RT; ++rt) {
+      sc[rt][0] = mfma16x16x32(a0, qb[rt][2 * w], sc[rt][0]);
+      sc[rt][1] = mfma16x16x32(b0, qb[rt][2 * w], sc[rt][1]);
+      sc[rt][0] = mfma16x16x32(a1, qb[rt][2 * w + 1], sc[rt][0]);
+      sc[rt][1] = mfma16x16x32(b1, qb[rt][2 * w + 1], sc[rt][1]);
     }
   }
-  // Every block overlaps [p_lo, p_hi), so the running max is finite after update_max and
-  // a -inf score gives p = 0 exactly; only V's scale/zero need masking (against NaN bits).
+  // Records of this lane's 8 tokens tau(g, 0..7): one base, constant offsets.
+  const uint8_t* rec = blk + 4 * g * kSlot;
   uint32_t ksz[8], vsz[8], vc[8];
-  bool ok[8];
-  const uint32_t span = static_cast<uint32_t>(p_hi - p_lo);
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
-    const uint8_t* rec = blk + tau(g, e) * kSlot;
-    ksz[e] = *reinterpret_cast<const uint32_t*>(rec + 64);
-    vsz[e] = *reinterpret_cast<const uint32_t*>(rec + kVector + 64);
-    vc[e] = *reinterpret_cast<const uint32_t*>(rec + kVector + 4 * n);
-    ok[e] = static_cast<uint32_t>(t0 + tau(g, e) - p_lo) < span;
-    vsz[e] = ok[e] ? vsz[e] : 0u;
+    const int off = (e < 4 ? e : 12 + e) * kSlot;
+    ksz[e] = *reinterpret_cast<const uint32_t*>(rec + off + 64);
+    vsz[e] = *reinterpret_cast<const uint32_t*>(rec + off + kVector + 64);
+    vc[e] = *reinterpret_cast<const uint32_t*>(rec + off + kVector + 4 * n);
+  }
+  // Only the first/last block of a split is partial. There, tokens outside [p_lo, p_hi)
+  // get score -inf (p = 0 exactly: every block overlaps the split, so the running max is
+  // finite) and zeroed V scale/zero (their bytes may hold NaN patterns).
+  const bool full = t0 >= p_lo && t0 + kBlock <= p_hi;
+  uint32_t okmask = 0xffu;
+  if (!full) {
+    okmask = 0u;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const bool ok = static_cast<uint32_t>(t0 + tau(g, e) - p_lo) <
+                      static_cast<uint32_t>(p_hi - p_lo);
+      okmask |= ok ? (1u << e) : 0u;
+      vsz[e] = ok ? vsz[e] : 0u;
+    }
   }
   // Scores in log2 units: (s_k (q.c) + z_k sum(q)) * scale * log2(e).
   float s2[RT][8];
@@ -406,9 +423,14 @@ __device__ __forceinline__ void hist_compute(const AttnArgs& a, const uint8_t* b
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       const float qc = sc[rt][e >> 2][e & 3] * a.scale_log2;
-      const float v = fmaf(h16(lo16(ksz[e])), qc, h16(hi16(ksz[e])) * qs);
-      s2[rt][e] = ok[e] ? v : -INFINITY;
+      s2[rt][e] = fmaf(h16(lo16(ksz[e])), qc, h16(hi16(ksz[e])) * qs);
     }
+  }
+  if (!full) {
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) s2[rt][e] = (okmask >> e) & 1u ? s2[rt][e] : -INFINITY;
   }
   update_max<RT, 17>(st, s2, g);
   u32x4 aw[RT];
@@ -515,12 +537,12 @@ __global__ __launch_bounds__(kThreads, 3 - RT) void history_kernel(const AttnArg
 
   u32x4 qb[RT][8];
   float corr[RT], qsum[RT];
-  hist_query<RT>(a, t, head, n, g, qb, corr, qsum);
   State<RT> st;
   state_init(st);
   const uint32_t magic = opaque_magic();
   const uint32_t mk[3] = {a.mask[0], a.mask[1], a.mask[2]};
 
+  if (p_lo >= p_hi) hist_query<RT>(a, t, head, n, g, qb, corr, qsum);
   if (p_lo < p_hi) {
     const int first = p_lo >> 5;
     const int nblk = ((p_hi - 1) >> 5) - first + 1;
@@ -560,6 +582,10 @@ __global__ __launch_bounds__(kThreads, 3 - RT) void history_kernel(const AttnArg
     };
 #pragma unroll
     for (int k = 0; k < kStages - 1; ++k) issue(wave + 4 * k, k);
+    // The query loads overlap the first blocks' DMA latency. The compiler does not see
+    // the asm DMA, so its own wait for these loads cannot drain them (vmcnt counts in
+    // order; it waits for the query loads, which are the youngest).
+    hist_query<RT>(a, t, head, n, g, qb, corr, qsum);
     int stage = 0;
     for (int ib = wave; ib < nblk; ib += 4) {
       issue(ib + 4 * (kStages - 1), stage == 0 ? kStages - 1 : stage - 1);
