@@ -109,7 +109,8 @@ int oscar_prepare_tasks(const int32_t* qstarts, const int32_t* counts, int32_t* 
 /*
  * attention_partials -- replaces kernels.py:439-482 `attention_partials(query, key,
  * value, history, window, meta, layout, scale, splits, raw)`.
- * Grid (programs, H, splits): program i serves task i if i < task_count[0].
+ * Grid (programs, H, splits): program i serves task i if i < task_count[0]; `tasks` must
+ * hold `programs` rows (prepare_tasks' task_capacity >= programs), all of which are read.
  * raw == 0: INT2 history positions [min(S, prefix), max(sink_len, prefix - R)) read from
  *           `history` through `block_tables` (query must be the ROTATED query);
  * raw != 0: BF16 sink/ring window positions plus the causal current tokens (key/value).

@@ -34,7 +34,7 @@ class OscarAttentionImpl:
         self.scale = float(scale)
         self.cfg = cfg or OscarConfig.from_env()
         self.split_policy = split_policy
-        self.rk = self.rv = None
+        self.rk = self.rv = self.rk_cols = self.rv_cols = None
         self.history = self.window = None
         self.cache_identity = None
 
@@ -45,6 +45,10 @@ class OscarAttentionImpl:
                 raise ValueError("rotations must be 256x256")
         self.rk = rk.to(torch.bfloat16).contiguous()
         self.rv = rv.to(torch.bfloat16).contiguous()
+        # x @ R reads R column-wise; a transposed view of R^T stored row-major keeps those
+        # reads contiguous (the inverse rotation's R^T view of rv already is).
+        self.rk_cols = self.rk.T.contiguous().T
+        self.rv_cols = self.rv.T.contiguous().T
 
     def splits_for(self, meta):
         if self.split_policy == "reference":
@@ -82,10 +86,10 @@ class OscarAttentionImpl:
         if n == 0:
             return output
 
-        krot = kernels.rotate(key, self.rk)
-        vrot = kernels.rotate(value, self.rv)
+        krot = kernels.rotate(key, self.rk_cols)
+        vrot = kernels.rotate(value, self.rv_cols)
         kernels.store_int2(krot, vrot, self.history, meta.slot_mapping, meta.counts, meta.layout)
-        qrot = kernels.rotate(query, self.rk)
+        qrot = kernels.rotate(query, self.rk_cols)
         splits = self.splits_for(meta)
         hp, hl = kernels.attention_partials(qrot, key, value, self.history, self.window, meta,
                                             meta.layout, self.scale, splits, raw=False)

@@ -1,0 +1,97 @@
+// Task, split and query-row bookkeeping shared by the two attention branches (INT2 history
+// in history.hip, BF16 sink/ring/current window in attention.hip).
+//
+// Reference: oscar_ascend/kernels.py:290-482 (`_attention_kernel`, `attention_partials`).
+// One workgroup per (task, kv head, split); a task is (request, first query row) from the
+// compact task table; partial outputs are per-split normalized with a natural-log LSE.
+#pragma once
+
+#include "common.h"
+
+namespace oscar {
+
+constexpr float kLn2 = 0.69314718055994531f;
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr int kSlot = 160, kVector = 68;
+
+struct AttnArgs {
+  const uint16_t* query;
+  int64_t qs0, qs1;
+  const uint16_t* key;
+  int64_t ks0, ks1;
+  const uint16_t* value;
+  int64_t vs0, vs1;
+  const uint8_t* history;
+  int64_t history_bytes;
+  const uint16_t* window;
+  int64_t window_elems;
+  const int32_t* qstarts;
+  const int32_t* seq_lens;
+  const int32_t* table;
+  int64_t table_stride, table_columns;
+  const int32_t* counts;
+  const int32_t* tasks;
+  const int32_t* task_count;
+  float* partials;
+  float* lse;
+  int64_t n;
+  Layout L;
+  int32_t g, hq, qt, splits, block_n;
+  FastDiv g_div;  // division by g (query heads per kv head)
+  float scale_log2;
+};
+
+struct Task {
+  int req, qoff, qstart, qlen, prefix, sink_len, recent_begin;
+};
+
+// kernels.py:316-333: the task row, the request's query span and its history bounds.
+// The task row is loaded together with the task count (rows below `programs` are always
+// allocated), so the dependent loads form two levels instead of three.
+__device__ __forceinline__ bool read_task(const AttnArgs& a, Task& t) {
+  const int task = blockIdx.x;
+  const int count = a.task_count[0];
+  const int req = a.tasks[2 * task];
+  const int qoff = a.tasks[2 * task + 1];
+  if (task >= count) return false;
+  t.req = req;
+  t.qoff = qoff;
+  t.qstart = a.qstarts[t.req];
+  const int qend = min(a.qstarts[t.req + 1], a.counts[1]);
+  t.qlen = qend - t.qstart;
+  t.prefix = a.seq_lens[t.req] - t.qlen;
+  t.sink_len = min(a.L.sink, t.prefix);
+  t.recent_begin = max(t.sink_len, t.prefix - a.L.recent);
+  return true;
+}
+
+// kernels.py:368-370: every split covers ceil(ceil(len / BN) / splits) tiles of BN tokens.
+__device__ __forceinline__ void split_range(int length, int block_n, int splits, int split,
+                                            int& begin, int& end) {
+  length = max(length, 0);
+  const int per = cdiv(cdiv(length, block_n), splits);
+  begin = split * per * block_n;
+  end = min((split + 1) * per * block_n, length);
+}
+
+struct RowInfo {
+  bool valid;
+  int qi, qhead;
+  int64_t token;
+};
+
+// Query row `row` of a task: query index qi = qoff + row / G, head = head * G + row % G.
+__device__ __forceinline__ RowInfo row_info(const AttnArgs& a, const Task& t, int head, int row) {
+  RowInfo r;
+  const int qrow = static_cast<int>(fastdiv(static_cast<uint32_t>(row), a.g_div));
+  r.qi = t.qoff + qrow;
+  r.token = static_cast<int64_t>(t.qstart) + r.qi;
+  r.valid = row < a.qt * a.g && r.qi < t.qlen && r.token >= 0 && r.token < a.n;
+  r.qhead = head * a.g + (row - qrow * a.g);
+  return r;
+}
+
+// INT2 history branch (history.hip); rows = query rows per task (<= 32).
+hipError_t launch_history(const AttnArgs& a, dim3 grid, int rows, hipStream_t stream);
+
+}  // namespace oscar

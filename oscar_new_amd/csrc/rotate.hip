@@ -1,17 +1,17 @@
 // rotate: out[t, h, :] = bf16(x[t, h, :] @ R) on bf16 MFMA (v_mfma_f32_16x16x32_bf16).
 //
 // Reference: oscar_ascend/kernels.py:14-66 (`_rotate_kernel`, `rotate`).
-// Workgroup tile: 64 rows x 64 output columns; each wavefront owns 16 rows and the four
-// 16-column MFMA tiles of the slice. The 256x64 slice of R is staged transposed in LDS
-// (k contiguous) so both MFMA operands are 16-byte vector reads.
+// The products here are small (a decode step rotates 32-200 rows), so the kernel is
+// latency-bound: it maximizes parallelism instead of reuse. One wavefront computes one
+// 16-row x 16-column output tile; both MFMA operands are read straight from global memory
+// (every row of x and every column of R is re-read by the 16 tiles that need it, from L2),
+// all 16 loads of a lane in flight at once. R is read column-wise: when its columns are
+// contiguous (a transposed view of a row-major matrix, e.g. R^T for the inverse rotation
+// or a cached transpose) each lane reads 16 bytes at a time, otherwise element by element.
 #include "common.h"
 
 namespace oscar {
 namespace {
-
-constexpr int kRowsPerBlock = 64;
-constexpr int kColsPerBlock = 64;
-constexpr int kLdsPitch = kHeadDim + 8;  // bf16 elements per staged column (padding vs banks)
 
 struct RotateArgs {
   const uint16_t* x;
@@ -20,75 +20,68 @@ struct RotateArgs {
   const uint16_t* r;
   int64_t rs0, rs1;
   uint16_t* out;
+  FastDiv h_div;
 };
 
-template <bool kVecX>
-__global__ __launch_bounds__(kThreads) void rotate_kernel(const RotateArgs a) {
-  __shared__ __attribute__((aligned(16))) uint16_t rt[kColsPerBlock * kLdsPitch];
-  const int c0 = blockIdx.y * kColsPerBlock;
-  const int64_t r0 = static_cast<int64_t>(blockIdx.x) * kRowsPerBlock;
+constexpr int kWavesPerBlock = 4;  // four column tiles of one 16-row block
 
-  // Stage R[:, c0:c0+64] as rt[j][k]; read along whichever axis of R is contiguous.
-  if (a.rs0 == 1) {
-    for (int e = threadIdx.x; e < kColsPerBlock * kHeadDim; e += kThreads) {
-      const int j = e >> 8, k = e & 255;
-      rt[j * kLdsPitch + k] = a.r[k * a.rs0 + (c0 + j) * a.rs1];
-    }
-  } else {
-    for (int e = threadIdx.x; e < kColsPerBlock * kHeadDim; e += kThreads) {
-      const int k = e >> 6, j = e & 63;
-      rt[j * kLdsPitch + k] = a.r[k * a.rs0 + (c0 + j) * a.rs1];
-    }
-  }
-  __syncthreads();
-
+// kVecX: x rows contiguous and 16-byte aligned; kColR: R columns contiguous (rs0 == 1).
+template <bool kVecX, bool kColR>
+__global__ __launch_bounds__(kWavesPerBlock * kWave) void rotate_kernel(const RotateArgs a) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int col = lane & 15, grp = lane >> 4;
-  const int64_t row = r0 + wave * 16 + col;
+  const int n = lane & 15, g = lane >> 4;
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * 16 + n;  // A row of this lane
+  const int col = (blockIdx.y * kWavesPerBlock + wave) * 16 + n;  // B column of this lane
   const bool row_ok = row < a.rows;
-  const int64_t token = row_ok ? row / a.h : 0;
-  const int64_t head = row_ok ? row - token * a.h : 0;
-  const uint16_t* xp = a.x + token * a.xs0 + head * a.xs1;
+  const uint32_t token = row_ok ? fastdiv(static_cast<uint32_t>(row), a.h_div) : 0u;
+  const int64_t head = row_ok ? row - static_cast<int64_t>(token) * a.h : 0;
+  const uint16_t* xp = a.x + static_cast<int64_t>(token) * a.xs0 + head * a.xs1;
 
-  f32x4 acc[4];
-#pragma unroll
-  for (int t = 0; t < 4; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
-
+  // k-step m: A lane (n, g) = x[row][32m + 8g .. +7]; B lane (n, g) = R[32m + 8g .. +7][col].
+  u32x4 av[8], bv[8];
 #pragma unroll
   for (int m = 0; m < 8; ++m) {
-    const int k0 = m * 32 + grp * 8;
-    u32x4 av = u32x4{0u, 0u, 0u, 0u};
+    const int k0 = 32 * m + 8 * g;
+    av[m] = u32x4{0u, 0u, 0u, 0u};
     if (row_ok) {
       if (kVecX) {
-        av = *reinterpret_cast<const u32x4*>(xp + k0);
+        av[m] = *reinterpret_cast<const u32x4*>(xp + k0);
       } else {
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const uint32_t lo = xp[(k0 + 2 * e) * a.xs2];
-          const uint32_t hi = xp[(k0 + 2 * e + 1) * a.xs2];
-          av[e] = lo | (hi << 16);
-        }
+        for (int e = 0; e < 4; ++e)
+          av[m][e] = static_cast<uint32_t>(xp[(k0 + 2 * e) * a.xs2]) |
+                     (static_cast<uint32_t>(xp[(k0 + 2 * e + 1) * a.xs2]) << 16);
       }
     }
+    const uint16_t* rp = a.r + static_cast<int64_t>(col) * a.rs1 + static_cast<int64_t>(k0) * a.rs0;
+    if (kColR) {
+      bv[m] = *reinterpret_cast<const u32x4*>(rp);
+    } else {
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      const u32x4 bv = *reinterpret_cast<const u32x4*>(&rt[(t * 16 + col) * kLdsPitch + k0]);
-      acc[t] = mfma16x16x32(av, bv, acc[t]);
+      for (int e = 0; e < 4; ++e)
+        bv[m][e] = static_cast<uint32_t>(rp[(2 * e) * a.rs0]) |
+                   (static_cast<uint32_t>(rp[(2 * e + 1) * a.rs0]) << 16);
     }
   }
+  f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int m = 0; m < 8; ++m) acc = mfma16x16x32(av[m], bv[m], acc);
 
-  // C layout: lane holds rows 4*grp + v of the wavefront's 16, column `col` of each tile.
+  // C layout: lane (n, g) holds rows 4g + v of the tile, column n.
+  const int ocol = (blockIdx.y * kWavesPerBlock + wave) * 16 + n;
 #pragma unroll
-  for (int t = 0; t < 4; ++t) {
-#pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      const int64_t orow = r0 + wave * 16 + grp * 4 + v;
-      if (orow < a.rows) {
-        a.out[orow * kHeadDim + c0 + t * 16 + col] =
-            static_cast<uint16_t>(float_to_bf16(acc[t][v]));
-      }
-    }
+  for (int v = 0; v < 4; ++v) {
+    const int64_t orow = static_cast<int64_t>(blockIdx.x) * 16 + 4 * g + v;
+    if (orow < a.rows) a.out[orow * kHeadDim + ocol] = static_cast<uint16_t>(float_to_bf16(acc[v]));
   }
+}
+
+template <bool kVecX>
+void launch(const RotateArgs& a, bool col_r, dim3 grid, hipStream_t s) {
+  if (col_r)
+    hipLaunchKernelGGL((rotate_kernel<kVecX, true>), grid, dim3(kWavesPerBlock * kWave), 0, s, a);
+  else
+    hipLaunchKernelGGL((rotate_kernel<kVecX, false>), grid, dim3(kWavesPerBlock * kWave), 0, s, a);
 }
 
 }  // namespace
@@ -102,15 +95,19 @@ extern "C" int oscar_rotate(const void* x, int64_t n, int64_t h, int64_t d, int6
   if (d != kHeadDim) return OSCAR_E_UNSUPPORTED;
   if (n == 0) return OSCAR_OK;
   if (!x || !rotation || !out) return OSCAR_E_NULL;
+  if (n * h > 0x7fffffffll) return OSCAR_E_SHAPE;
   RotateArgs a{static_cast<const uint16_t*>(x), n * h, h, x_s0, x_s1, x_s2,
-               static_cast<const uint16_t*>(rotation), r_s0, r_s1, static_cast<uint16_t*>(out)};
+               static_cast<const uint16_t*>(rotation), r_s0, r_s1, static_cast<uint16_t*>(out),
+               make_fastdiv(static_cast<uint32_t>(h))};
   const bool vec = x_s2 == 1 && (x_s0 % 8 == 0) && (x_s1 % 8 == 0) &&
                    (reinterpret_cast<uintptr_t>(x) % 16 == 0);
-  dim3 grid(static_cast<unsigned>((a.rows + kRowsPerBlock - 1) / kRowsPerBlock),
-            kHeadDim / kColsPerBlock);
+  const bool col_r = r_s0 == 1 && (r_s1 % 8 == 0) &&
+                     (reinterpret_cast<uintptr_t>(rotation) % 16 == 0);
+  const dim3 grid(static_cast<unsigned>((a.rows + 15) / 16), kHeadDim / (16 * kWavesPerBlock));
+  hipStream_t s = as_stream(stream);
   if (vec)
-    hipLaunchKernelGGL(rotate_kernel<true>, grid, dim3(kThreads), 0, as_stream(stream), a);
+    launch<true>(a, col_r, grid, s);
   else
-    hipLaunchKernelGGL(rotate_kernel<false>, grid, dim3(kThreads), 0, as_stream(stream), a);
+    launch<false>(a, col_r, grid, s);
   return static_cast<int>(hipGetLastError());
 }
