@@ -178,6 +178,48 @@ int oscar_store_windows(const void* key, int64_t k_s0, int64_t k_s1, int64_t k_s
 int oscar_unpack(const void* history, int64_t history_bytes, const int64_t* slots, int64_t n,
                  const oscar_layout* layout, void* key_out, void* value_out, void* stream);
 
+/*
+ * pre_attention -- the first of the two fused launches around the history kernel; it has
+ * no single counterpart in the reference, it replaces backend.py:171-173 + 195 + 211-222
+ * (oscar_ascend/backend.py): `rotate(key, Rk)`, `rotate(value, Rv)`, `store_int2(...)`,
+ * `rotate(query, Rk)` and `attention_partials(..., splits=1, raw=True)`.
+ * Writes raw_partials fp32 [n, hq, 1, 256] / raw_lse [n, hq, 1] (exactly as
+ * oscar_attention_partials with raw != 0 and one split), qrot bf16 [n, hq, 256] (exactly as
+ * oscar_rotate of query by Rk) and the INT2 slots of the current tokens (exactly as
+ * oscar_store_int2 of the rotated K/V). rk_t / rv_t: R_k^T and R_v^T, contiguous bf16
+ * [256][256] (rk_t[c][k] = R_k[k][c]). query/key/value rows must be contiguous and 16-byte
+ * aligned (row strides in elements, multiples of 8).
+ */
+int oscar_pre_attention(const void* query, int64_t q_s0, int64_t q_s1, const void* key,
+                        int64_t k_s0, int64_t k_s1, const void* value, int64_t v_s0, int64_t v_s1,
+                        const void* window, int64_t window_elems, const int32_t* qstarts,
+                        const int32_t* seq_lens, const int32_t* block_tables,
+                        int64_t table_stride, int64_t table_columns, const int32_t* counts,
+                        const int32_t* tasks, const int32_t* task_count, int64_t n, int64_t hq,
+                        int64_t programs, int32_t block_n, int32_t query_tile,
+                        int32_t max_query_len, float scale, const void* rk_t, const void* rv_t,
+                        void* history, int64_t history_bytes, const int64_t* slots,
+                        const oscar_clip* clip, const oscar_layout* layout, float* raw_partials,
+                        float* raw_lse, void* qrot, void* stream);
+
+/*
+ * post_attention -- the second fused launch; it replaces backend.py:209-210 + 223-226
+ * (oscar_ascend/backend.py): `merge_splits(hp, hl, counts)`, `rotate(hrot, Rv.T)`,
+ * `merge_paths(...)` and `store_windows(...)`, in that order of dependence, with the same
+ * bits as those entry points. rv: R_v row-major bf16 [256][256]. output: bf16 [n, hq*256];
+ * merged_lse (optional): fp32 [n, hq]. The window store runs after the merge has consumed
+ * both branches, so it must follow the history launch of the same step on the stream.
+ */
+int oscar_post_attention(const float* history_partials, const float* history_lse,
+                         int32_t splits, const float* raw_partials, const float* raw_lse,
+                         const int32_t* counts, const void* rv, int64_t n, int64_t hq,
+                         void* output, float* merged_lse, const void* key, int64_t k_s0,
+                         int64_t k_s1, const void* value, int64_t v_s0, int64_t v_s1,
+                         void* window, int64_t window_elems, const int32_t* qstarts,
+                         const int32_t* seq_lens, const int32_t* block_tables,
+                         int64_t table_stride, int64_t max_reqs, const oscar_layout* layout,
+                         void* stream);
+
 #ifdef __cplusplus
 }
 #endif

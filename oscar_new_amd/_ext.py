@@ -71,6 +71,23 @@ SIGNATURES = {
     "oscar_store_windows": [_P, _I64, _I64, _I64, _P, _I64, _I64, _I64, _I64, _P, _I64, _P, _P,
                             _P, _I64, _P, _I64, POINTER(OscarLayout), _P],
     "oscar_unpack": [_P, _I64, _P, _I64, POINTER(OscarLayout), _P, _P, _P],
+    "oscar_pre_attention": [
+        _P, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64,  # query, key, value (+ row strides)
+        _P, _I64,  # window
+        _P, _P, _P, _I64, _I64,  # qstarts, seq_lens, block_tables, stride, columns
+        _P, _P, _P,  # counts, tasks, task_count
+        _I64, _I64, _I64, _I32, _I32, _I32, _F,  # n hq programs bn qt mql scale
+        _P, _P,  # rk_t, rv_t
+        _P, _I64, _P, POINTER(OscarClip),  # history, bytes, slots, clip
+        POINTER(OscarLayout), _P, _P, _P, _P,  # layout, raw partials, raw lse, qrot, stream
+    ],
+    "oscar_post_attention": [
+        _P, _P, _I32, _P, _P, _P, _P,  # hp, hl, splits, rp, rl, counts, rv
+        _I64, _I64, _P, _P,  # n, hq, output, merged_lse
+        _P, _I64, _I64, _P, _I64, _I64,  # key, value (+ row strides)
+        _P, _I64, _P, _P, _P, _I64, _I64,  # window, elems, qstarts, seq_lens, table, stride, max_reqs
+        POINTER(OscarLayout), _P,
+    ],
 }
 
 _lib = None

@@ -17,11 +17,11 @@ from .config import OscarConfig, choose_splits, choose_splits_mi355x
 
 
 class OscarAttentionImpl:
-    """Reference: backend.py:132-227. ``split_policy`` "reference" keeps config.py:84-89,
+    """Reference: backend.py:67-227. ``split_policy`` "reference" keeps config.py:84-89,
     "mi355x" fills the 256 CUs (config.choose_splits_mi355x)."""
 
     def __init__(self, num_heads, head_size, scale, num_kv_heads, cfg=None,
-                 split_policy="reference"):
+                 split_policy="reference", fused=True):
         if head_size != 256:
             raise ValueError("OSCAR requires FULL decoder attention with D256")
         if num_kv_heads <= 0 or num_heads % num_kv_heads:
@@ -34,7 +34,8 @@ class OscarAttentionImpl:
         self.scale = float(scale)
         self.cfg = cfg or OscarConfig.from_env()
         self.split_policy = split_policy
-        self.rk = self.rv = self.rk_cols = self.rv_cols = None
+        self.fused = fused
+        self.rk = self.rv = self.rk_cols = self.rv_cols = self.rk_t = self.rv_t = None
         self.history = self.window = None
         self.cache_identity = None
 
@@ -47,8 +48,10 @@ class OscarAttentionImpl:
         self.rv = rv.to(torch.bfloat16).contiguous()
         # x @ R reads R column-wise; a transposed view of R^T stored row-major keeps those
         # reads contiguous (the inverse rotation's R^T view of rv already is).
-        self.rk_cols = self.rk.T.contiguous().T
-        self.rv_cols = self.rv.T.contiguous().T
+        self.rk_t = self.rk.T.contiguous()
+        self.rv_t = self.rv.T.contiguous()
+        self.rk_cols = self.rk_t.T
+        self.rv_cols = self.rv_t.T
 
     def splits_for(self, meta):
         if self.split_policy == "reference":
@@ -59,7 +62,12 @@ class OscarAttentionImpl:
                                     getattr(meta, "max_seq_len", None))
 
     def forward(self, layer, query, key, value, kv_cache, attn_metadata, output=None):
-        """Reference: backend.py:190-292 (minus the Ascend prefill call)."""
+        """Reference: backend.py:125-227 (minus the Ascend prefill call).
+
+        ``fused`` (default) runs the step as three launches (``pre_attention``, the history
+        kernel, ``post_attention``) that produce the same bits as the reference order of
+        single launches below.
+        """
         if output is None:
             raise ValueError("an attention output buffer is required")
         if attn_metadata is None:
@@ -86,11 +94,22 @@ class OscarAttentionImpl:
         if n == 0:
             return output
 
+        splits = self.splits_for(meta)
+        if self.fused:
+            # Three launches: BF16 branch + rotations + INT2 store, history, merges + window.
+            qrot, rp, rl = kernels.pre_attention(query, key, value, self.history, self.window,
+                                                 meta, meta.layout, self.scale, self.rk_t,
+                                                 self.rv_t)
+            hp, hl = kernels.attention_partials(qrot, key, value, self.history, self.window, meta,
+                                                meta.layout, self.scale, splits, raw=False)
+            kernels.post_attention(hp, hl, rp, rl, self.rv, key, value, self.window, meta,
+                                   meta.layout, output.view(n, -1), getattr(meta, "merged_lse", None))
+            return output
+
         krot = kernels.rotate(key, self.rk_cols)
         vrot = kernels.rotate(value, self.rv_cols)
         kernels.store_int2(krot, vrot, self.history, meta.slot_mapping, meta.counts, meta.layout)
         qrot = kernels.rotate(query, self.rk_cols)
-        splits = self.splits_for(meta)
         hp, hl = kernels.attention_partials(qrot, key, value, self.history, self.window, meta,
                                             meta.layout, self.scale, splits, raw=False)
         hrot, hlogsum = kernels.merge_splits(hp, hl, meta.counts)

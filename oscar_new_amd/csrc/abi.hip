@@ -33,6 +33,7 @@ int make_layout(const oscar_layout* in, Layout* out) {
   out->recent = in->recent_tokens;
   out->ring = in->ring_tokens;
   out->bpp_div = make_fastdiv(static_cast<uint32_t>(out->bpp));
+  out->ring_div = make_fastdiv(static_cast<uint32_t>(out->ring));
   return OSCAR_OK;
 }
 

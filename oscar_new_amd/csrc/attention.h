@@ -48,8 +48,7 @@ struct Task {
 // kernels.py:316-333: the task row, the request's query span and its history bounds.
 // The task row is loaded together with the task count (rows below `programs` are always
 // allocated), so the dependent loads form two levels instead of three.
-__device__ __forceinline__ bool read_task(const AttnArgs& a, Task& t) {
-  const int task = blockIdx.x;
+__device__ __forceinline__ bool read_task(const AttnArgs& a, Task& t, int task) {
   const int count = a.task_count[0];
   const int req = a.tasks[2 * task];
   const int qoff = a.tasks[2 * task + 1];

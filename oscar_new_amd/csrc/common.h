@@ -115,6 +115,7 @@ struct Layout {
   int32_t head_dim, kv_heads, bp, bk, bk_shift, bpp;
   int32_t slot_bytes, vector_bytes, sink, recent, ring;
   FastDiv bpp_div;
+  FastDiv ring_div;
 };
 
 // Returns OSCAR_OK or an argument error code.

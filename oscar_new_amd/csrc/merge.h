@@ -1,0 +1,92 @@
+// Row arithmetic of the two LSE merges, shared by the merge_splits / merge_paths entry points
+// and the fused post-attention kernel so that both paths produce the same bits.
+//
+// Reference: oscar_ascend/kernels.py:485-527 (`_merge_splits_kernel`, `_merge_paths_kernel`).
+// One wavefront per (token, query head) row; lane l owns dims 4l..4l+3.
+#pragma once
+
+#include "common.h"
+
+namespace oscar {
+
+constexpr float kDenFloor = 1.0e-30f;
+
+struct SplitMerge {
+  float acc[4];  // sum_s w_s P_s for this lane's dims
+  float den;     // sum_s w_s
+  float mx;      // max_s lse_s (-inf: no live split)
+};
+
+// kernels.py:489-503: w_s = e^{lse_s - M}, splits with lse -inf contribute nothing. `part`
+// is the row's [splits][256] partials, `ls` its [splits] LSEs. Rows of padded tokens
+// (valid false) merge to nothing. Split rows are requested eight at a time, before any of
+// them is needed, and accumulated in split order.
+__device__ __forceinline__ SplitMerge merge_splits_row(const float* part, const float* ls,
+                                                       int splits, bool valid, int lane) {
+  SplitMerge r;
+  r.mx = -INFINITY;
+  if (valid)
+    for (int s = lane; s < splits; s += kWave) r.mx = fmaxf(r.mx, ls[s]);
+  r.mx = wave_max(r.mx);
+  const float safe = r.mx == -INFINITY ? 0.f : r.mx;
+  r.den = 0.f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) r.acc[i] = 0.f;
+  if (!valid) return r;
+  const float* p = part + lane * 4;
+  for (int s0 = 0; s0 < splits; s0 += 8) {
+    float l[8];
+    float4 v[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const bool in = s0 + k < splits;
+      l[k] = in ? ls[s0 + k] : -INFINITY;
+      v[k] = in ? *reinterpret_cast<const float4*>(p + static_cast<int64_t>(s0 + k) * kHeadDim)
+                : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      if (l[k] == -INFINITY) continue;  // zero weight: that split's row is never used
+      const float w = expf(l[k] - safe);
+      r.den += w;
+      r.acc[0] = fmaf(w, v[k].x, r.acc[0]);
+      r.acc[1] = fmaf(w, v[k].y, r.acc[1]);
+      r.acc[2] = fmaf(w, v[k].z, r.acc[2]);
+      r.acc[3] = fmaf(w, v[k].w, r.acc[3]);
+    }
+  }
+  return r;
+}
+
+// The merged row as bf16 (two packed words) and its natural-log LSE.
+__device__ __forceinline__ uint2 merge_splits_out(const SplitMerge& r) {
+  const float dn = fmaxf(r.den, kDenFloor);
+  return make_uint2(pack_bf16x2(r.acc[0] / dn, r.acc[1] / dn),
+                    pack_bf16x2(r.acc[2] / dn, r.acc[3] / dn));
+}
+__device__ __forceinline__ float merge_splits_lse(const SplitMerge& r) {
+  return r.den > 0.f ? r.mx + logf(fmaxf(r.den, kDenFloor)) : -INFINITY;
+}
+
+// kernels.py:514-527: (e^{la-M} a + e^{lb-M} b) / (e^{la-M} + e^{lb-M}), M = max(la, lb)
+// (0 when both are -inf). Padded rows pass la = lb = -inf and zero a, b.
+struct PathWeights {
+  float wa, wb, den, mx;
+};
+__device__ __forceinline__ PathWeights path_weights(float la, float lb) {
+  PathWeights w;
+  w.mx = fmaxf(la, lb);
+  w.mx = w.mx == -INFINITY ? 0.f : w.mx;
+  w.wa = expf(la - w.mx);
+  w.wb = expf(lb - w.mx);
+  w.den = fmaxf(w.wa + w.wb, kDenFloor);
+  return w;
+}
+__device__ __forceinline__ float path_merge(const PathWeights& w, float a, float b) {
+  return fmaf(w.wa, a, w.wb * b) / w.den;
+}
+__device__ __forceinline__ float path_lse(const PathWeights& w) {
+  return (w.wa + w.wb) > 0.f ? w.mx + logf(w.wa + w.wb) : -INFINITY;
+}
+
+}  // namespace oscar

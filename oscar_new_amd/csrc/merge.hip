@@ -3,12 +3,10 @@
 // Reference: oscar_ascend/kernels.py:485-541. One wavefront per (token, query head) row;
 // lane l owns dims 4l..4l+3. Every row is written, padded rows (token >= counts[1]) too,
 // because the inverse rotation that follows reads them.
-#include "common.h"
+#include "merge.h"
 
 namespace oscar {
 namespace {
-
-constexpr float kDenFloor = 1.0e-30f;
 
 struct MergeSplitsArgs {
   const float* partials;
@@ -25,33 +23,10 @@ __global__ __launch_bounds__(kThreads) void merge_splits_kernel(const MergeSplit
   const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
   if (row >= a.rows) return;
   const bool valid = row / a.hq < a.counts[1];
-  const float* ls = a.lse + row * a.splits;
-  float mx = -INFINITY;
-  if (valid)
-    for (int s = lane; s < a.splits; s += kWave) mx = fmaxf(mx, ls[s]);
-  mx = wave_max(mx);
-  const float safe = mx == -INFINITY ? 0.f : mx;
-  float den = 0.f;
-  float acc[4] = {0.f, 0.f, 0.f, 0.f};
-  if (valid) {
-    const float* p = a.partials + row * a.splits * kHeadDim + lane * 4;
-    for (int s = 0; s < a.splits; ++s) {
-      const float l = ls[s];
-      if (l == -INFINITY) continue;  // zero weight: never touch that split's row
-      const float w = expf(l - safe);
-      den += w;
-      const float4 v = *reinterpret_cast<const float4*>(p + s * kHeadDim);
-      acc[0] += w * v.x;
-      acc[1] += w * v.y;
-      acc[2] += w * v.z;
-      acc[3] += w * v.w;
-    }
-  }
-  const float dn = fmaxf(den, kDenFloor);
-  uint16_t* o = a.out + row * kHeadDim + lane * 4;
-  *reinterpret_cast<uint2*>(o) =
-      make_uint2(pack_bf16x2(acc[0] / dn, acc[1] / dn), pack_bf16x2(acc[2] / dn, acc[3] / dn));
-  if (lane == 0) a.logsum[row] = den > 0.f ? mx + logf(fmaxf(den, kDenFloor)) : -INFINITY;
+  const SplitMerge r = merge_splits_row(a.partials + row * a.splits * kHeadDim,
+                                        a.lse + row * a.splits, a.splits, valid, lane);
+  *reinterpret_cast<uint2*>(a.out + row * kHeadDim + lane * 4) = merge_splits_out(r);
+  if (lane == 0) a.logsum[row] = merge_splits_lse(r);
 }
 
 struct MergePathsArgs {
@@ -71,11 +46,7 @@ __global__ __launch_bounds__(kThreads) void merge_paths_kernel(const MergePathsA
   const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
   if (row >= m.rows) return;
   const bool valid = row / m.hq < m.counts[1];
-  const float la = valid ? m.la[row] : -INFINITY;
-  const float lb = valid ? m.lb[row] : -INFINITY;
-  float mx = fmaxf(la, lb);
-  mx = mx == -INFINITY ? 0.f : mx;
-  const float wa = expf(la - mx), wb = expf(lb - mx);
+  const PathWeights w = path_weights(valid ? m.la[row] : -INFINITY, valid ? m.lb[row] : -INFINITY);
   float av[4] = {0.f, 0.f, 0.f, 0.f}, bv[4] = {0.f, 0.f, 0.f, 0.f};
   if (valid) {
     const uint2 ar = *reinterpret_cast<const uint2*>(m.a + row * kHeadDim + lane * 4);
@@ -89,13 +60,12 @@ __global__ __launch_bounds__(kThreads) void merge_paths_kernel(const MergePathsA
     bv[2] = br.z;
     bv[3] = br.w;
   }
-  const float den = fmaxf(wa + wb, kDenFloor);
   float r[4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) r[i] = (wa * av[i] + wb * bv[i]) / den;
+  for (int i = 0; i < 4; ++i) r[i] = path_merge(w, av[i], bv[i]);
   *reinterpret_cast<uint2*>(m.out + row * kHeadDim + lane * 4) =
       make_uint2(pack_bf16x2(r[0], r[1]), pack_bf16x2(r[2], r[3]));
-  if (m.lse && lane == 0) m.lse[row] = (wa + wb) > 0.f ? mx + logf(wa + wb) : -INFINITY;
+  if (m.lse && lane == 0) m.lse[row] = path_lse(w);
 }
 
 }  // namespace

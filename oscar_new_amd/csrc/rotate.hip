@@ -8,7 +8,7 @@
 // all 16 loads of a lane in flight at once. R is read column-wise: when its columns are
 // contiguous (a transposed view of a row-major matrix, e.g. R^T for the inverse rotation
 // or a cached transpose) each lane reads 16 bytes at a time, otherwise element by element.
-#include "common.h"
+#include "rotate.h"
 
 namespace oscar {
 namespace {
@@ -37,35 +37,10 @@ __global__ __launch_bounds__(kWavesPerBlock * kWave) void rotate_kernel(const Ro
   const int64_t head = row_ok ? row - static_cast<int64_t>(token) * a.h : 0;
   const uint16_t* xp = a.x + static_cast<int64_t>(token) * a.xs0 + head * a.xs1;
 
-  // k-step m: A lane (n, g) = x[row][32m + 8g .. +7]; B lane (n, g) = R[32m + 8g .. +7][col].
-  u32x4 av[8], bv[8];
-#pragma unroll
-  for (int m = 0; m < 8; ++m) {
-    const int k0 = 32 * m + 8 * g;
-    av[m] = u32x4{0u, 0u, 0u, 0u};
-    if (row_ok) {
-      if (kVecX) {
-        av[m] = *reinterpret_cast<const u32x4*>(xp + k0);
-      } else {
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-          av[m][e] = static_cast<uint32_t>(xp[(k0 + 2 * e) * a.xs2]) |
-                     (static_cast<uint32_t>(xp[(k0 + 2 * e + 1) * a.xs2]) << 16);
-      }
-    }
-    const uint16_t* rp = a.r + static_cast<int64_t>(col) * a.rs1 + static_cast<int64_t>(k0) * a.rs0;
-    if (kColR) {
-      bv[m] = *reinterpret_cast<const u32x4*>(rp);
-    } else {
-#pragma unroll
-      for (int e = 0; e < 4; ++e)
-        bv[m][e] = static_cast<uint32_t>(rp[(2 * e) * a.rs0]) |
-                   (static_cast<uint32_t>(rp[(2 * e + 1) * a.rs0]) << 16);
-    }
-  }
-  f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-  for (int m = 0; m < 8; ++m) acc = mfma16x16x32(av[m], bv[m], acc);
+  RotateOperands op;
+  rotate_load_a<kVecX>(op, row_ok ? xp : nullptr, a.xs2, g);
+  rotate_load_b<kColR>(op, a.r + static_cast<int64_t>(col) * a.rs1, a.rs0, g);
+  const f32x4 acc = rotate_mfma(op);
 
   // C layout: lane (n, g) holds rows 4g + v of the tile, column n.
   const int ocol = (blockIdx.y * kWavesPerBlock + wave) * 16 + n;

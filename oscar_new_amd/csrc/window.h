@@ -1,0 +1,74 @@
+// Window store of one request: the current BF16 K/V into its sink/ring window, shared by the
+// store_windows entry point and the fused post-attention kernel.
+//
+// Reference: oscar_ascend/kernels.py:544-620 (`_window_store_kernel`, `store_windows`).
+// Window index i < S holds position i. Ring index i >= S holds the LATEST position
+// pos < seq with pos = i - S (mod C); only current tokens (prefix <= pos < seq) are
+// written, so each ring slot has exactly one writer per step. Wavefront w of the workgroup
+// copies window indices w, w+4, ... (1 KiB each).
+#pragma once
+
+#include "common.h"
+
+namespace oscar {
+
+
+struct WindowArgs {
+  const uint16_t* k;
+  int64_t ks0, ks1, ks2;
+  const uint16_t* v;
+  int64_t vs0, vs1, vs2;
+  int64_t n;
+  uint16_t* window;
+  int64_t window_elems;
+  const int32_t* qstarts;
+  const int32_t* seq_lens;
+  const int32_t* table;
+  int64_t table_stride;
+  const int32_t* counts;
+  Layout L;
+};
+
+// One (request, kv head) of kernels.py:569-595, by the four wavefronts of a workgroup.
+__device__ __forceinline__ void store_window_request(const WindowArgs& a, int req, int head) {
+  if (req >= a.counts[0]) return;
+  const int qstart = a.qstarts[req];
+  const int qend = min(a.qstarts[req + 1], a.counts[1]);
+  if (qend <= qstart) return;
+  const int seq = a.seq_lens[req];
+  const int prefix = seq - (qend - qstart);
+  const int first = a.table[static_cast<int64_t>(req) * a.table_stride];
+  if (first < 0) return;
+  const int64_t owner = fastdiv(static_cast<uint32_t>(first), a.L.bpp_div);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int h = a.L.kv_heads, sink = a.L.sink, ring = a.L.ring;
+  const int64_t page_elems = a.L.page_bytes / 2;
+  for (int index = wave; index < sink + ring; index += kThreads / kWave) {
+    int pos;
+    if (index < sink) {
+      pos = index;
+    } else {
+      const int back = seq - 1 - (index - sink);  // distance of the newest candidate
+      if (back < 0) continue;
+      pos = seq - 1 - back % ring;
+      if (pos < sink) continue;
+    }
+    if (pos < prefix || pos >= seq) continue;
+    const int64_t current = static_cast<int64_t>(qstart) + pos - prefix;
+    if (current < 0 || current >= a.n) continue;
+    const int64_t dst = owner * page_elems + (static_cast<int64_t>(index) * 2 * h + head) * kHeadDim;
+    if (dst + static_cast<int64_t>(h) * kHeadDim + kHeadDim > a.window_elems) continue;
+    const uint16_t* ks = a.k + current * a.ks0 + head * a.ks1;
+    const uint16_t* vs = a.v + current * a.vs0 + head * a.vs1;
+    uint16_t* kd = a.window + dst;
+    uint16_t* vd = a.window + dst + static_cast<int64_t>(h) * kHeadDim;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int d = lane * 4 + i;
+      kd[d] = ks[d * a.ks2];
+      vd[d] = vs[d * a.vs2];
+    }
+  }
+}
+
+}  // namespace oscar

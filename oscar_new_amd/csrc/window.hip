@@ -5,67 +5,13 @@
 // pos < seq with pos = i - S (mod C); only current tokens (prefix <= pos < seq) are
 // written, so each ring slot has exactly one writer per step. One workgroup per
 // (request, kv head); wavefront w copies window indices w, w+4, ... (1 KiB each).
-#include "common.h"
+#include "window.h"
 
 namespace oscar {
 namespace {
 
-struct WindowArgs {
-  const uint16_t* k;
-  int64_t ks0, ks1, ks2;
-  const uint16_t* v;
-  int64_t vs0, vs1, vs2;
-  int64_t n;
-  uint16_t* window;
-  int64_t window_elems;
-  const int32_t* qstarts;
-  const int32_t* seq_lens;
-  const int32_t* table;
-  int64_t table_stride;
-  const int32_t* counts;
-  Layout L;
-};
-
 __global__ __launch_bounds__(kThreads) void store_windows_kernel(const WindowArgs a) {
-  const int req = blockIdx.x, head = blockIdx.y;
-  if (req >= a.counts[0]) return;
-  const int qstart = a.qstarts[req];
-  const int qend = min(a.qstarts[req + 1], a.counts[1]);
-  if (qend <= qstart) return;
-  const int seq = a.seq_lens[req];
-  const int prefix = seq - (qend - qstart);
-  const int first = a.table[static_cast<int64_t>(req) * a.table_stride];
-  if (first < 0) return;
-  const int64_t owner = fastdiv(static_cast<uint32_t>(first), a.L.bpp_div);
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int h = a.L.kv_heads, sink = a.L.sink, ring = a.L.ring;
-  const int64_t page_elems = a.L.page_bytes / 2;
-  for (int index = wave; index < sink + ring; index += kThreads / kWave) {
-    int pos;
-    if (index < sink) {
-      pos = index;
-    } else {
-      const int back = seq - 1 - (index - sink);  // distance of the newest candidate
-      if (back < 0) continue;
-      pos = seq - 1 - back % ring;
-      if (pos < sink) continue;
-    }
-    if (pos < prefix || pos >= seq) continue;
-    const int64_t current = static_cast<int64_t>(qstart) + pos - prefix;
-    if (current < 0 || current >= a.n) continue;
-    const int64_t dst = owner * page_elems + (static_cast<int64_t>(index) * 2 * h + head) * kHeadDim;
-    if (dst + static_cast<int64_t>(h) * kHeadDim + kHeadDim > a.window_elems) continue;
-    const uint16_t* ks = a.k + current * a.ks0 + head * a.ks1;
-    const uint16_t* vs = a.v + current * a.vs0 + head * a.vs1;
-    uint16_t* kd = a.window + dst;
-    uint16_t* vd = a.window + dst + static_cast<int64_t>(h) * kHeadDim;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int d = lane * 4 + i;
-      kd[d] = ks[d * a.ks2];
-      vd[d] = vs[d * a.vs2];
-    }
-  }
+  store_window_request(a, blockIdx.x, blockIdx.y);
 }
 
 }  // namespace

@@ -24,6 +24,8 @@ __all__ = [
     "merge_paths",
     "store_windows",
     "dequant_inverse_rotate",
+    "pre_attention",
+    "post_attention",
     "layout_struct",
     "clip_struct",
 ]
@@ -295,3 +297,99 @@ def dequant_inverse_rotate(history, slots, rk, rv, layout):
             "dequant_inverse_rotate",
         )
     return rotate(k, rk.T), rotate(v, rv.T)
+
+
+# --------------------------------------------------------------------------- fused launches
+#
+# Not reference entry points: the backend's layer step uses these two launches around the
+# history kernel instead of the nine single launches above (same bits, fewer launches).
+
+
+def _row_strides(t, name):
+    t = _bf16(t)
+    s0, s1, s2 = t.stride()
+    if s2 != 1 or s0 % 8 or s1 % 8 or t.data_ptr() % 16:
+        raise ValueError(f"{name} rows must be contiguous and 16-byte aligned")
+    return t, s0, s1
+
+
+def pre_attention(query, key, value, history, window, meta, layout, scale, rk_t, rv_t):
+    """BF16-branch partials, q rotation and the K/V INT2 store of one step, in one launch.
+
+    Replaces ``rotate(key, Rk)``, ``rotate(value, Rv)``, ``store_int2``, ``rotate(query, Rk)``
+    and ``attention_partials(..., 1, raw=True)`` of the reference layer step
+    (backend.py:171-173, 195, 211-222). ``rk_t``/``rv_t`` are R^T as contiguous bf16 [256, 256].
+    Returns ``(qrot bf16 [n, hq, 256], raw_partials fp32 [n, hq, 1, 256], raw_lse [n, hq, 1])``.
+    """
+    _device_check(query, key, value, history, window, rk_t, rv_t)
+    n, hq, d = query.shape
+    cfg = layout.config
+    qrot = torch.empty((n, hq, d), dtype=torch.bfloat16, device=query.device)
+    partials = torch.empty((n, hq, 1, d), dtype=torch.float32, device=query.device)
+    lse = torch.empty((n, hq, 1), dtype=torch.float32, device=query.device)
+    if n == 0:
+        return qrot, partials, lse
+    programs = attention_programs(n, meta.max_num_reqs, cfg.queries_per_tile)
+    if meta.tasks.shape[0] < programs:
+        raise ValueError(f"task table holds {meta.tasks.shape[0]} rows; the grid needs {programs}")
+    for r in (rk_t, rv_t):
+        if r.dtype != torch.bfloat16 or not r.is_contiguous() or tuple(r.shape) != (d, d):
+            raise ValueError("rk_t / rv_t must be contiguous bf16 [256, 256] (R transposed)")
+    query, q0, q1 = _row_strides(query, "query")
+    key, k0, k1 = _row_strides(key, "key")
+    value, v0, v1 = _row_strides(value, "value")
+    if meta.slot_mapping.dtype != torch.int64:
+        raise ValueError("slot mapping must be int64")
+    table = _int32(meta.block_tables, "block_tables")
+    max_query_len = getattr(meta, "max_query_len", None)
+    max_query_len = int(max_query_len) if isinstance(max_query_len, int) else 0
+    _ext.check(
+        _ext.library().oscar_pre_attention(
+            _ptr(query), q0, q1, _ptr(key), k0, k1, _ptr(value), v0, v1,
+            _ptr(window), window.numel(),
+            _ptr(_int32(meta.query_start_loc, "query_start_loc")),
+            _ptr(_int32(meta.seq_lens, "seq_lens")), _ptr(table), table.stride(0), table.shape[1],
+            _ptr(_int32(meta.counts, "counts")), _ptr(_int32(meta.tasks, "tasks")),
+            _ptr(_int32(meta.task_count, "task_count")),
+            n, hq, programs, cfg.block_n, cfg.queries_per_tile, max_query_len, float(scale),
+            _ptr(rk_t), _ptr(rv_t), _ptr(history), history.numel() * history.element_size(),
+            _ptr(meta.slot_mapping), clip_struct(cfg), layout_struct(layout), _ptr(partials),
+            _ptr(lse), _ptr(qrot), _stream(query),
+        ),
+        "pre_attention",
+    )
+    return qrot, partials, lse
+
+
+def post_attention(history_partials, history_lse, raw_partials, raw_lse, rv, key, value, window,
+                   meta, layout, output, merged_lse=None):
+    """Split merge, inverse V rotation, path merge and window store of one step, in one launch.
+
+    Replaces ``merge_splits``, ``rotate(hrot, Rv.T)``, ``merge_paths`` and ``store_windows``
+    (backend.py:209-210, 223-226). ``rv`` is R_v as contiguous bf16 [256, 256]; ``output`` is
+    the contiguous bf16 [n, hq * 256] attention output.
+    """
+    _device_check(history_partials, history_lse, raw_partials, raw_lse, rv, key, value, window,
+                  output, merged_lse)
+    n, hq, splits, d = history_partials.shape
+    if not output.is_contiguous():
+        raise ValueError("Attention output must be contiguous")
+    if n == 0:
+        return
+    if rv.dtype != torch.bfloat16 or not rv.is_contiguous():
+        raise ValueError("rv must be contiguous bf16 [256, 256]")
+    key, k0, k1 = _row_strides(key, "key")
+    value, v0, v1 = _row_strides(value, "value")
+    table = _int32(meta.block_tables, "block_tables")
+    _ext.check(
+        _ext.library().oscar_post_attention(
+            _ptr(history_partials.contiguous()), _ptr(history_lse.contiguous()), splits,
+            _ptr(raw_partials.contiguous()), _ptr(raw_lse.contiguous()),
+            _ptr(_int32(meta.counts, "counts")), _ptr(rv), n, hq, _ptr(output), _ptr(merged_lse),
+            _ptr(key), k0, k1, _ptr(value), v0, v1, _ptr(window), window.numel(),
+            _ptr(_int32(meta.query_start_loc, "query_start_loc")),
+            _ptr(_int32(meta.seq_lens, "seq_lens")), _ptr(table), table.stride(0),
+            meta.max_num_reqs, layout_struct(layout), _stream(history_partials),
+        ),
+        "post_attention",
+    )

@@ -1,0 +1,180 @@
+"""The fused layer step (pre_attention, history kernel, post_attention) against the reference
+order of single launches (oscar_ascend/backend.py:171-226) and against the dense oracle.
+
+The fused launches run the same device code as the single entry points, so the comparison
+with the single-launch path is bit for bit: attention output, merged LSE, every byte of the
+K stripe (INT2 slots + untouched padding) and of the V stripe (BF16 windows).
+"""
+
+from types import SimpleNamespace
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from oscar_new_amd import kernels
+from oscar_new_amd.backend import OscarAttentionImpl
+from oscar_new_amd.config import OscarConfig
+from tests._state import bits, make_state, prepare_prefix
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _qr(seed):
+    g = torch.Generator().manual_seed(seed)
+    return torch.linalg.qr(torch.randn(256, 256, generator=g))[0].bfloat16().to(DEV)
+
+
+def _case(lengths, prefixes, seed, cfg=None):
+    torch.manual_seed(seed)
+    layout, raw, hist, window, meta, tables = make_state(lengths, prefixes, cfg)
+    rk, rv = _qr(seed), _qr(seed + 1)
+    ks = [torch.randn(n, 1, 256).bfloat16() for n in lengths]
+    vs = [torch.randn(n, 1, 256).bfloat16() for n in lengths]
+    qs = [torch.randn(n - p, 6, 256).bfloat16() for n, p in zip(lengths, prefixes)]
+    prepare_prefix(ks, vs, rk, rv, hist, window, meta, tables, layout, prefixes)
+    q = torch.cat(qs).to(DEV)
+    k = torch.cat([x[p:] for x, p in zip(ks, prefixes)]).to(DEV)
+    v = torch.cat([x[p:] for x, p in zip(vs, prefixes)]).to(DEV)
+    meta.layout = layout
+    meta.num_actual_tokens = q.shape[0]
+    kernels.prepare_tasks(meta.query_start_loc, meta.counts, meta.tasks, meta.task_count,
+                          meta.max_num_reqs, layout.config.queries_per_tile)
+    return SimpleNamespace(layout=layout, raw=raw, meta=meta, rk=rk, rv=rv, ks=ks, vs=vs, qs=qs,
+                           q=q, k=k, v=v, prefixes=prefixes)
+
+
+def _views(raw, layout, pages=20):
+    """Native (K, V) cache views of a make_state byte buffer (conv | K | V)."""
+    stripe = pages * layout.stripe_page_bytes
+    conv = raw.numel() - 2 * stripe
+    k = raw[conv : conv + stripe].view(torch.bfloat16).view(-1, 128, 1, 256)
+    v = raw[conv + stripe :].view(torch.bfloat16).view(-1, 128, 1, 256)
+    return k, v
+
+
+CASES = [
+    ([4], [0], 32),  # empty history, all-masked splits
+    ([69, 263], [65, 260], 16),  # ragged MTP, no history
+    ([1804, 2601], [1800, 2600], 8),  # non-monotonic pages, GQA + MTP
+    ([1700], [800], 1),  # continuation chunk wraps the ring
+    ([3000, 1500, 777], [2999, 1499, 776], 16),  # decode
+]
+
+
+@pytest.mark.parametrize("lengths,prefixes,splits", CASES)
+def test_fused_step_is_bitwise_the_single_launch_step(lengths, prefixes, splits):
+    c = _case(lengths, prefixes, seed=7)
+    n = c.q.shape[0]
+    outs, lses, images = [], [], []
+    for fused in (False, True):
+        raw = c.raw.clone()
+        k_cache, v_cache = _views(raw, c.layout)
+        impl = OscarAttentionImpl(6, 256, 1 / 16, 1, c.layout.config, fused=fused)
+        impl.initialize_layer(c.rk, c.rv)
+        impl.splits_for = lambda meta, s=splits: s
+        c.meta.merged_lse = torch.full((n, 6), 7.0, device=DEV)
+        out = torch.full((n, 6 * 256), 3.0, device=DEV, dtype=torch.bfloat16)
+        impl.forward(None, c.q, c.k, c.v, (k_cache, v_cache), c.meta, out)
+        torch.cuda.synchronize()
+        outs.append(out.view(torch.int16).cpu())
+        lses.append(c.meta.merged_lse.cpu())
+        images.append(raw.cpu())
+    assert torch.equal(outs[0], outs[1])
+    assert torch.equal(lses[0], lses[1])
+    assert torch.equal(images[0], images[1])
+
+
+@pytest.mark.parametrize("lengths,prefixes,splits", CASES[1:4])
+def test_fused_step_against_dense_reference(lengths, prefixes, splits):
+    # Reference tests/test_npu_kernels.py:166-194 through the fused launches.
+    c = _case(lengths, prefixes, seed=11)
+    n = c.q.shape[0]
+    k_cache, v_cache = _views(c.raw, c.layout)
+    impl = OscarAttentionImpl(6, 256, 1 / 16, 1, c.layout.config, fused=True)
+    impl.initialize_layer(c.rk, c.rv)
+    impl.splits_for = lambda meta, s=splits: s
+    c.meta.merged_lse = torch.empty((n, 6), device=DEV)
+    out = torch.empty((n, 6 * 256), device=DEV, dtype=torch.bfloat16)
+    impl.forward(None, c.q, c.k, c.v, (k_cache, v_cache), c.meta, out)
+    want, want_lse = [], []
+    for qi, ki, vi, p in zip(c.qs, c.ks, c.vs, c.prefixes):
+        o, l = O.hybrid_reference(bits(qi), bits(ki), bits(vi), p, bits(c.rk), bits(c.rv),
+                                  c.layout.config)
+        want.append(o)
+        want_lse.append(l)
+    want = torch.from_numpy(np.concatenate(want)).reshape(n, -1)
+    got = out.float().cpu()
+    torch.testing.assert_close(got, want, atol=0.035, rtol=0.04)
+    assert (got - want).abs().mean().item() <= 2e-3
+    torch.testing.assert_close(c.meta.merged_lse.cpu(), torch.from_numpy(np.concatenate(want_lse)),
+                               atol=2e-2, rtol=0)
+
+
+def test_pre_attention_matches_single_entry_points():
+    c = _case([1804, 2601], [1800, 2600], seed=3)
+    meta, layout = c.meta, c.layout
+    hist_a, win_a = layout.tensor_views(_views(c.raw.clone(), layout))
+    hist_b, win_b = layout.tensor_views(_views(c.raw.clone(), layout))
+    rk_t, rv_t = c.rk.T.contiguous(), c.rv.T.contiguous()
+    qrot, rp, rl = kernels.pre_attention(c.q, c.k, c.v, hist_a, win_a, meta, layout, 1 / 16,
+                                         rk_t, rv_t)
+    kernels.store_int2(kernels.rotate(c.k, rk_t.T), kernels.rotate(c.v, rv_t.T), hist_b,
+                       meta.slot_mapping, meta.counts, layout)
+    q_ref = kernels.rotate(c.q, rk_t.T)
+    rp_ref, rl_ref = kernels.attention_partials(c.q, c.k, c.v, hist_b, win_b, meta, layout,
+                                                1 / 16, 1, True)
+    torch.cuda.synchronize()
+    assert torch.equal(qrot.view(torch.int16), q_ref.view(torch.int16))
+    assert torch.equal(rp, rp_ref)
+    assert torch.equal(rl, rl_ref)
+    assert torch.equal(hist_a, hist_b)
+
+
+def test_post_attention_matches_single_entry_points():
+    c = _case([69, 263, 1804], [65, 260, 1800], seed=5)
+    meta, layout = c.meta, c.layout
+    n = c.q.shape[0]
+    splits = 8
+    qrot = kernels.rotate(c.q, c.rk.T.contiguous().T)
+    hist, win = layout.tensor_views(_views(c.raw, layout))
+    hp, hl = kernels.attention_partials(qrot, c.k, c.v, hist, win, meta, layout, 1 / 16, splits,
+                                        False)
+    rp, rl = kernels.attention_partials(c.q, c.k, c.v, hist, win, meta, layout, 1 / 16, 1, True)
+    win_a, win_b = win.clone(), win.clone()
+    out_a = torch.empty(n, 6 * 256, device=DEV, dtype=torch.bfloat16)
+    lse_a = torch.empty(n, 6, device=DEV)
+    kernels.post_attention(hp, hl, rp, rl, c.rv.contiguous(), c.k, c.v, win_a, meta, layout, out_a,
+                           lse_a)
+    hr, hls = kernels.merge_splits(hp, hl, meta.counts)
+    out_b = torch.empty_like(out_a)
+    lse_b = torch.empty_like(lse_a)
+    kernels.merge_paths(kernels.rotate(hr, c.rv.T), hls, rp, rl, meta.counts, out_b, lse_b)
+    kernels.store_windows(c.k, c.v, win_b, meta, layout)
+    torch.cuda.synchronize()
+    assert torch.equal(out_a.view(torch.int16), out_b.view(torch.int16))
+    assert torch.equal(lse_a, lse_b)
+    assert torch.equal(win_a.view(torch.int16), win_b.view(torch.int16))
+
+
+def test_fused_step_masks_padded_tokens_and_dummy_runs():
+    # counts = [0, 0] (a dummy / capture run) must leave every cache byte untouched and write
+    # zero output rows with -inf LSE, as the single-launch path does.
+    c = _case([900, 517], [896, 516], seed=9, cfg=OscarConfig(sink_tokens=4, recent_tokens=64))
+    n = c.q.shape[0]
+    c.meta.counts.zero_()
+    kernels.prepare_tasks(c.meta.query_start_loc, c.meta.counts, c.meta.tasks, c.meta.task_count,
+                          c.meta.max_num_reqs, 4)
+    before = c.raw.clone()
+    k_cache, v_cache = _views(c.raw, c.layout)
+    impl = OscarAttentionImpl(6, 256, 1 / 16, 1, c.layout.config, fused=True)
+    impl.initialize_layer(c.rk, c.rv)
+    c.meta.merged_lse = torch.empty((n, 6), device=DEV)
+    out = torch.full((n, 6 * 256), 3.0, device=DEV, dtype=torch.bfloat16)
+    impl.forward(None, c.q, c.k, c.v, (k_cache, v_cache), c.meta, out)
+    torch.cuda.synchronize()
+    assert torch.equal(c.raw, before)
+    assert torch.count_nonzero(out).item() == 0
+    assert torch.isneginf(c.meta.merged_lse).all()
