@@ -4,9 +4,9 @@
 One step = one FULL-attention layer forward of a decode batch (BASELINE config 3 by
 default): rotate K/V/q, INT2 store of the current token, split-KV history attention,
 split merge, inverse V rotation, BF16 sink/recent/current attention, LSE path merge,
-window store. Each layer step is captured once as a HIP graph and replayed; steps cycle
-over ``--layers`` independent KV caches (each > 1 GB) so the 256 MB Infinity Cache cannot
-serve a step from the previous step's reads.
+window store. The steps of ``--layers`` consecutive layers, each with its own KV cache
+(> 1 GB each, so the 256 MB Infinity Cache cannot serve a step from the previous step's
+reads), are captured back to back in one HIP graph, as a model's decode graph holds them.
 
 Printed JSON (one line): ``value`` is the whole step's algorithmic HBM GB/s; also the
 per-layer-step microseconds, the dominant (history) kernel's roofline from HIP events, the
@@ -371,35 +371,43 @@ def main(argv=None):
     for i in range(len(layers)):  # eager warm-up (also builds the tensor views)
         step(i)
     torch.cuda.synchronize()
+    # The layer steps of consecutive layers are captured back to back in one HIP graph, as a
+    # model's decode graph holds them; a step is one layer's forward. `full` replays all
+    # layers once, `tail` covers a remainder so that exactly --steps steps are timed.
+    nl = len(layers)
     graphs = None
     if not args.no_graph:
-        graphs = []
         stream = torch.cuda.Stream()
         stream.wait_stream(torch.cuda.current_stream())
+        graphs = {}
         pool = None
-        for i in range(len(layers)):
+        for count in sorted({nl, args.steps % nl, args.warmup % nl} - {0}):
             g = torch.cuda.CUDAGraph()
             with torch.cuda.graph(g, stream=stream, pool=pool):
-                step(i)
+                for i in range(count):
+                    step(i)
             pool = g.pool()
-            graphs.append(g)
+            graphs[count] = g
         torch.cuda.synchronize()
 
-    def run(i):
-        if graphs is not None:
-            graphs[i % len(layers)].replay()
-        else:
-            step(i % len(layers))
+    def run_steps(count):
+        """`count` layer steps, cycling layers 0, 1, ..., nl - 1, 0, ..."""
+        if graphs is None:
+            for i in range(count):
+                step(i % nl)
+            return
+        for _ in range(count // nl):
+            graphs[nl].replay()
+        if count % nl:
+            graphs[count % nl].replay()
 
     print(f"[bench] warmup {args.warmup}, timed {args.steps}", file=sys.stderr, flush=True)
-    for i in range(args.warmup):
-        run(i)
+    run_steps(args.warmup)
     torch.cuda.synchronize()
     ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
     ev0.record()
-    for i in range(args.steps):
-        run(i)
+    run_steps(args.steps)
     ev1.record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
@@ -476,7 +484,7 @@ def main(argv=None):
     }
     if not args.no_cpu_baseline:
         print("[bench] CPU oracle baseline", file=sys.stderr, flush=True)
-        graphs[0].replay() if graphs is not None else step(0)
+        step(0)
         torch.cuda.synchronize()
         cpu, parity = cpu_baseline(SimpleNamespace(**{**vars(w), "k_cache": layers[0][0],
                                                       "v_cache": layers[0][1]}),

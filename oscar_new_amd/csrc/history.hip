@@ -51,7 +51,7 @@ constexpr int kDma = kChunk * kPieces / 64;      // 9 loads of 16 bytes per lane
 constexpr int kRingBytes = 4 * 2 * kStageBytes;  // two stages per wavefront
 constexpr int kTableCache = 256;                 // kernel blocks whose offsets live in LDS
 constexpr float kTheta = 8.0f;                   // lazy-max slack, log2 units
-constexpr int kQTerms = 3;
+constexpr int kQTerms = 2;
 constexpr uint32_t kNoBlock = 0xffffffffu;
 
 static_assert(kDma * 64 == kChunk * kPieces, "a chunk image is whole DMA instructions");
@@ -568,11 +568,11 @@ __global__ __launch_bounds__(kThreads, 3 - RT) void history_kernel(const AttnArg
       for (int q4 = 0; q4 < 4; ++q4) {
         const float4 x0 = so[16 * q4], x1 = so[16 * 256 / 4 + 16 * q4];
         const float4 x2 = so[2 * 16 * 256 / 4 + 16 * q4], x3 = so[3 * 16 * 256 / 4 + 16 * q4];
-        *reinterpret_cast<float4*>(out + 64 * q4) =
-            make_float4((2.0f * ((x0.x + x1.x) + (x2.x + x3.x)) + zs) * inv,
-                        (2.0f * ((x0.y + x1.y) + (x2.y + x3.y)) + zs) * inv,
-                        (2.0f * ((x0.z + x1.z) + (x2.z + x3.z)) + zs) * inv,
-                        (2.0f * ((x0.w + x1.w) + (x2.w + x3.w)) + zs) * inv);
+        const float4 r = make_float4((2.0f * ((x0.x + x1.x) + (x2.x + x3.x)) + zs) * inv,
+                                     (2.0f * ((x0.y + x1.y) + (x2.y + x3.y)) + zs) * inv,
+                                     (2.0f * ((x0.z + x1.z) + (x2.z + x3.z)) + zs) * inv,
+                                     (2.0f * ((x0.w + x1.w) + (x2.w + x3.w)) + zs) * inv);
+        *reinterpret_cast<float4*>(out + 64 * q4) = r;
       }
       if ((threadIdx.x & 15) == 0)
         a.lse[(ri.token * a.hq + ri.qhead) * a.splits + split] =

@@ -19,41 +19,58 @@ struct SplitMerge {
 
 // kernels.py:489-503: w_s = e^{lse_s - M}, splits with lse -inf contribute nothing. `part`
 // is the row's [splits][256] partials, `ls` its [splits] LSEs. Rows of padded tokens
-// (valid false) merge to nothing. Split rows are requested eight at a time, before any of
-// them is needed, and accumulated in split order.
+// (valid false, uniform over the wavefront) merge to nothing. Up to 16 splits take one
+// round of loads (LSEs and partial rows together); the partials are accumulated in split
+// order either way.
+__device__ __forceinline__ void merge_group(SplitMerge& r, const float (&l)[16],
+                                            const float4 (&v)[16], float safe) {
+#pragma unroll
+  for (int k = 0; k < 16; ++k) {
+    if (l[k] == -INFINITY) continue;  // zero weight: that split's row is never used
+    const float w = expf(l[k] - safe);
+    r.den += w;
+    r.acc[0] = fmaf(w, v[k].x, r.acc[0]);
+    r.acc[1] = fmaf(w, v[k].y, r.acc[1]);
+    r.acc[2] = fmaf(w, v[k].z, r.acc[2]);
+    r.acc[3] = fmaf(w, v[k].w, r.acc[3]);
+  }
+}
+
+__device__ __forceinline__ void load_group(const float* p, const float* ls, int s0, int splits,
+                                           float (&l)[16], float4 (&v)[16]) {
+#pragma unroll
+  for (int k = 0; k < 16; ++k) {
+    const bool in = s0 + k < splits;
+    l[k] = in ? ls[s0 + k] : -INFINITY;
+    v[k] = in ? *reinterpret_cast<const float4*>(p + static_cast<int64_t>(s0 + k) * kHeadDim)
+              : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+}
+
 __device__ __forceinline__ SplitMerge merge_splits_row(const float* part, const float* ls,
                                                        int splits, bool valid, int lane) {
   SplitMerge r;
   r.mx = -INFINITY;
-  if (valid)
-    for (int s = lane; s < splits; s += kWave) r.mx = fmaxf(r.mx, ls[s]);
-  r.mx = wave_max(r.mx);
-  const float safe = r.mx == -INFINITY ? 0.f : r.mx;
   r.den = 0.f;
 #pragma unroll
   for (int i = 0; i < 4; ++i) r.acc[i] = 0.f;
   if (!valid) return r;
   const float* p = part + lane * 4;
-  for (int s0 = 0; s0 < splits; s0 += 8) {
-    float l[8];
-    float4 v[8];
+  float l[16];
+  float4 v[16];
+  if (splits <= 16) {
+    load_group(p, ls, 0, splits, l, v);
 #pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      const bool in = s0 + k < splits;
-      l[k] = in ? ls[s0 + k] : -INFINITY;
-      v[k] = in ? *reinterpret_cast<const float4*>(p + static_cast<int64_t>(s0 + k) * kHeadDim)
-                : make_float4(0.f, 0.f, 0.f, 0.f);
-    }
-#pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      if (l[k] == -INFINITY) continue;  // zero weight: that split's row is never used
-      const float w = expf(l[k] - safe);
-      r.den += w;
-      r.acc[0] = fmaf(w, v[k].x, r.acc[0]);
-      r.acc[1] = fmaf(w, v[k].y, r.acc[1]);
-      r.acc[2] = fmaf(w, v[k].z, r.acc[2]);
-      r.acc[3] = fmaf(w, v[k].w, r.acc[3]);
-    }
+    for (int k = 0; k < 16; ++k) r.mx = fmaxf(r.mx, l[k]);
+    merge_group(r, l, v, r.mx == -INFINITY ? 0.f : r.mx);
+    return r;
+  }
+  for (int s = lane; s < splits; s += kWave) r.mx = fmaxf(r.mx, ls[s]);
+  r.mx = wave_max(r.mx);
+  const float safe = r.mx == -INFINITY ? 0.f : r.mx;
+  for (int s0 = 0; s0 < splits; s0 += 16) {
+    load_group(p, ls, s0, splits, l, v);
+    merge_group(r, l, v, safe);
   }
   return r;
 }

@@ -79,21 +79,21 @@ __device__ __forceinline__ void update_max(State<RT>& st, const float (&s2)[RT][
 
 // ---------------------------------------------------------------- epilogue
 
-// Merge the 4 wavefront states through LDS and write normalized partials + LSE.
-// LDS bytes finish() needs for RT row tiles.
+// Merge the 4 wavefront states through LDS and write normalized partials + LSE: per row tile,
+// every wavefront publishes its scaled accumulators at once, then each thread sums one
+// (row, 16 dims) over the four wavefronts in wavefront order.
 template <int RT>
 constexpr int finish_lds_bytes() {
-  return 4 * RT * 16 * 16 * 16 + (2 * 4 + 3) * RT * 16 * 4;
+  return 4 * 16 * kHeadDim * 4 + (2 * 4 + 3) * RT * 16 * 4;
 }
 
 template <int RT>
 __device__ void finish(const AttnArgs& a, const Task& t, int head, int split, State<RT>& st,
                        uint8_t* lds) {
-  typedef f32x4 RedRow[16];
-  typedef RedRow RedWave[RT * 16];
-  RedWave* s_red = reinterpret_cast<RedWave*>(lds);
+  typedef float OutWave[16][kHeadDim];
+  OutWave* s_o = reinterpret_cast<OutWave*>(lds);
   typedef float StatWave[RT * 16];
-  StatWave* s_m = reinterpret_cast<StatWave*>(lds + 4 * RT * 16 * 16 * 16);
+  StatWave* s_m = reinterpret_cast<StatWave*>(lds + 4 * 16 * kHeadDim * 4);
   StatWave* s_p = s_m + 4;
   float* s_max = reinterpret_cast<float*>(s_p + 4);
   float* s_den = s_max + RT * 16;
@@ -126,39 +126,37 @@ __device__ void finish(const AttnArgs& a, const Task& t, int head, int split, St
   __syncthreads();
 #pragma unroll
   for (int rt = 0; rt < RT; ++rt) {
+    if (rt > 0) __syncthreads();  // the previous tile's sums have been read
+    // Lane (g, n) holds dims 16n + tile of rows 4g + v.
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
       const int row = 16 * rt + 4 * g + v;
       const float mw = s_m[wave][row];
       const float f = mw == -INFINITY ? 0.f : exp2f(mw - s_max[row]);
 #pragma unroll
-      for (int tt = 0; tt < 16; ++tt) st.o[rt][tt][v] *= f;
+      for (int c = 0; c < 4; ++c)
+        *reinterpret_cast<f32x4*>(&s_o[wave][4 * g + v][16 * n + 4 * c]) =
+            f32x4{st.o[rt][4 * c][v] * f, st.o[rt][4 * c + 1][v] * f, st.o[rt][4 * c + 2][v] * f,
+                  st.o[rt][4 * c + 3][v] * f};
     }
-  }
-  // Lane (g, n) holds dims 16n + tile; chunk c gathers tiles 4c..4c+3 of every wavefront.
-#pragma unroll
-  for (int c = 0; c < 4; ++c) {
-#pragma unroll
-    for (int rt = 0; rt < RT; ++rt)
-#pragma unroll
-      for (int v = 0; v < 4; ++v)
-        s_red[wave][16 * rt + 4 * g + v][n] =
-            f32x4{st.o[rt][4 * c][v], st.o[rt][4 * c + 1][v], st.o[rt][4 * c + 2][v],
-                  st.o[rt][4 * c + 3][v]};
     __syncthreads();
-    for (int idx = threadIdx.x; idx < RT * 16 * 16; idx += kThreads) {
-      const int row = idx >> 4, nn = idx & 15;
-      const RowInfo ri = row_info(a, t, head, row);
-      if (ri.valid) {
-        const f32x4 sum = s_red[0][row][nn] + s_red[1][row][nn] + s_red[2][row][nn] +
-                          s_red[3][row][nn];
-        const float den = fmaxf(s_den[row], 1.0e-30f);
-        const int64_t orow = (ri.token * a.hq + ri.qhead) * a.splits + split;
-        *reinterpret_cast<float4*>(a.partials + orow * kHeadDim + 16 * nn + 4 * c) =
+    const int row16 = threadIdx.x >> 4, dq = threadIdx.x & 15;
+    const int row = 16 * rt + row16;
+    const RowInfo ri = row_info(a, t, head, row);
+    if (ri.valid) {
+      const float den = fmaxf(s_den[row], 1.0e-30f);
+      const int64_t orow = (ri.token * a.hq + ri.qhead) * a.splits + split;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const int d = 16 * dq + 4 * c;
+        const f32x4 sum = *reinterpret_cast<const f32x4*>(&s_o[0][row16][d]) +
+                          *reinterpret_cast<const f32x4*>(&s_o[1][row16][d]) +
+                          *reinterpret_cast<const f32x4*>(&s_o[2][row16][d]) +
+                          *reinterpret_cast<const f32x4*>(&s_o[3][row16][d]);
+        *reinterpret_cast<float4*>(a.partials + orow * kHeadDim + d) =
             make_float4(sum[0] / den, sum[1] / den, sum[2] / den, sum[3] / den);
       }
     }
-    __syncthreads();
   }
   if (threadIdx.x < RT * 16) {
     const RowInfo ri = row_info(a, t, head, threadIdx.x);
@@ -205,15 +203,16 @@ __device__ __forceinline__ void raw_block(const AttnArgs& a, int task, int head,
                                           uint8_t* smem) {
   Task t;
   if (!read_task(a, t, task)) return;
+  // The owner page (block-table column 0) is requested together with the request's
+  // metadata rows: both depend only on the task row.
+  const int first = a.table_columns > 0 ? a.table[static_cast<int64_t>(t.req) * a.table_stride]
+                                        : -1;
   RawTask r;
   r.high = t.sink_len + t.prefix - t.recent_begin;
   r.win = -1;
-  if (a.table_columns > 0) {
-    const int first = a.table[static_cast<int64_t>(t.req) * a.table_stride];
-    if (first >= 0) {
-      const int64_t owner = fastdiv(static_cast<uint32_t>(first), a.L.bpp_div);
-      r.win = owner * (a.L.page_bytes / 2) + static_cast<int64_t>(head) * kHeadDim;
-    }
+  if (first >= 0) {
+    const int64_t owner = fastdiv(static_cast<uint32_t>(first), a.L.bpp_div);
+    r.win = owner * (a.L.page_bytes / 2) + static_cast<int64_t>(head) * kHeadDim;
   }
   int begin, end;
   split_range(r.high + t.qlen, a.block_n, a.splits, split, begin, end);

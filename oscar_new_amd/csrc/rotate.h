@@ -58,11 +58,14 @@ __device__ __forceinline__ void rotate_load_b(RotateOperands& op, const uint16_t
 }
 
 // The tile: lane (n, g) receives rows 4g + v (v = 0..3) of column n, fp32.
-__device__ __forceinline__ f32x4 rotate_mfma(const RotateOperands& op) {
+__device__ __forceinline__ f32x4 rotate_mfma(const u32x4 (&a)[8], const u32x4 (&b)[8]) {
   f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int m = 0; m < 8; ++m) acc = mfma16x16x32(op.a[m], op.b[m], acc);
+  for (int m = 0; m < 8; ++m) acc = mfma16x16x32(a[m], b[m], acc);
   return acc;
+}
+__device__ __forceinline__ f32x4 rotate_mfma(const RotateOperands& op) {
+  return rotate_mfma(op.a, op.b);
 }
 
 }  // namespace oscar

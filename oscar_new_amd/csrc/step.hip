@@ -17,11 +17,9 @@
 //     prefix), so the INT2 store of the step may run beside it;
 //   * the window store follows both branches (it is in the post-attention launch), as
 //     backend.py:225-226 requires.
-#include "merge.h"
+#include "post.h"
 #include "quant.h"
 #include "raw.h"
-#include "rotate.h"
-#include "window.h"
 
 namespace oscar {
 namespace {
@@ -56,13 +54,21 @@ __device__ __forceinline__ void rotate_rows16(const uint16_t* x, int64_t xs0, in
     const uint32_t token = fastdiv(static_cast<uint32_t>(row), h_div);
     xp = x + static_cast<int64_t>(token) * xs0 + (row - static_cast<int64_t>(token) * h) * xs1;
   }
+  // Every operand (the A rows and the four column tiles of R) is requested before the first
+  // MFMA: one round of memory latency.
   RotateOperands op;
+  u32x4 rb[4][8];
   rotate_load_a<true>(op, xp, 1, g);
 #pragma unroll
   for (int ct = 0; ct < 4; ++ct) {
+    rotate_load_b<true>(op, rt + static_cast<int64_t>(64 * wave + 16 * ct + n) * kHeadDim, 1, g);
+#pragma unroll
+    for (int m = 0; m < 8; ++m) rb[ct][m] = op.b[m];
+  }
+#pragma unroll
+  for (int ct = 0; ct < 4; ++ct) {
     const int col = 64 * wave + 16 * ct + n;
-    rotate_load_b<true>(op, rt + static_cast<int64_t>(col) * kHeadDim, 1, g);
-    const f32x4 acc = rotate_mfma(op);
+    const f32x4 acc = rotate_mfma(op.a, rb[ct]);
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
       const int r = 4 * g + v;
@@ -128,62 +134,12 @@ __global__ __launch_bounds__(kThreads) void pre_attention_kernel(const PreArgs p
   rotate_rows16(a.query, a.qs0, a.qs1, p.hq_div, a.hq, p.q_rows, tile, p.rk_t, nullptr, p.qrot);
 }
 
-struct PostArgs {
-  const float* hp;  // history partials [rows][splits][256]
-  const float* hl;  // history LSE [rows][splits]
-  int32_t splits;
-  const float* rp;  // BF16-branch partials [rows][256]
-  const float* rl;  // BF16-branch LSE [rows]
-  const int32_t* counts;
-  const uint16_t* rv;  // R_v, row-major: column c of R_v^T is row c of R_v
-  int64_t rows;        // n * hq
-  int32_t hq;
-  uint16_t* out;       // [rows][256]
-  float* merged_lse;   // [rows] or null
-  WindowArgs win;
-  int64_t win_requests;  // min(n, max_reqs)
-};
-
-// Four (token, query head) rows per workgroup, one wavefront per row for the split merge.
+// Four (token, query head) rows per workgroup, one wavefront per row for the split merge;
+// then the window store of requests blockIdx.x, + gridDim.x, ... (after both branches).
 __global__ __launch_bounds__(kThreads) void post_attention_kernel(const PostArgs p) {
   __shared__ __attribute__((aligned(16))) uint16_t s_h[4][kHeadDim];  // merged history rows
   __shared__ float s_l[4];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int n = lane & 15, g = lane >> 4;
-  const int64_t row0 = static_cast<int64_t>(blockIdx.x) * 4;
-  {
-    const int64_t row = row0 + wave;
-    const bool in = row < p.rows;
-    const bool valid = in && row / p.hq < p.counts[1];
-    const SplitMerge r = merge_splits_row(p.hp + (in ? row : 0) * p.splits * kHeadDim,
-                                          p.hl + (in ? row : 0) * p.splits, p.splits, valid, lane);
-    *reinterpret_cast<uint2*>(&s_h[wave][lane * 4]) = merge_splits_out(r);
-    if (lane == 0) s_l[wave] = merge_splits_lse(r);
-  }
-  __syncthreads();
-  // Inverse rotation of the four merged rows (rows 4..15 of the MFMA tile are zero), then the
-  // path merge of each element with the BF16 branch.
-  RotateOperands op;
-  rotate_load_a<true>(op, n < 4 ? &s_h[n][0] : nullptr, 1, g);
-#pragma unroll
-  for (int ct = 0; ct < 4; ++ct) {
-    const int col = 64 * wave + 16 * ct + n;
-    rotate_load_b<true>(op, p.rv + static_cast<int64_t>(col) * kHeadDim, 1, g);
-    const f32x4 acc = rotate_mfma(op);
-    if (g != 0) continue;  // lanes of group 0 hold tile rows 0..3
-#pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      const int64_t row = row0 + v;
-      if (row >= p.rows) continue;
-      const bool valid = row / p.hq < p.counts[1];
-      const PathWeights w = path_weights(valid ? s_l[v] : -INFINITY, valid ? p.rl[row] : -INFINITY);
-      const float av = valid ? bf16_to_float(float_to_bf16(acc[v])) : 0.f;
-      const float bv = valid ? p.rp[row * kHeadDim + col] : 0.f;
-      p.out[row * kHeadDim + col] = static_cast<uint16_t>(float_to_bf16(path_merge(w, av, bv)));
-      if (p.merged_lse && wave == 0 && ct == 0 && n == 0) p.merged_lse[row] = path_lse(w);
-    }
-  }
-  // Window store, after both branches of the step: requests blockIdx.x, + gridDim.x, ...
+  post_rows<4>(p, static_cast<int64_t>(blockIdx.x) * 4, p.rows, s_h, s_l);
   for (int64_t req = blockIdx.x; req < p.win_requests; req += gridDim.x)
     for (int head = 0; head < p.win.L.kv_heads; ++head)
       store_window_request(p.win, static_cast<int>(req), head);

@@ -4,8 +4,7 @@
 // Reference: oscar_ascend/kernels.py:544-620 (`_window_store_kernel`, `store_windows`).
 // Window index i < S holds position i. Ring index i >= S holds the LATEST position
 // pos < seq with pos = i - S (mod C); only current tokens (prefix <= pos < seq) are
-// written, so each ring slot has exactly one writer per step. Wavefront w of the workgroup
-// copies window indices w, w+4, ... (1 KiB each).
+// written, so each ring slot has exactly one writer per step.
 #pragma once
 
 #include "common.h"
@@ -30,30 +29,33 @@ struct WindowArgs {
 };
 
 // One (request, kv head) of kernels.py:569-595, by the four wavefronts of a workgroup.
+// Stated per index, the reference rule is: index i < S receives position i, ring index i
+// receives the latest position pos < seq with pos = i - S (mod C), and only current tokens
+// (prefix <= pos < seq) are written, never a ring write of a position below S. Stated per
+// current token, that is the same set of writes: token pos writes index pos if pos < S, else
+// index S + pos % C if no later token of the request has the same residue (pos + C >= seq).
+// Each index therefore has at most one writer; wavefront w handles tokens prefix + w, + 4, ...
 __device__ __forceinline__ void store_window_request(const WindowArgs& a, int req, int head) {
   if (req >= a.counts[0]) return;
   const int qstart = a.qstarts[req];
   const int qend = min(a.qstarts[req + 1], a.counts[1]);
-  if (qend <= qstart) return;
   const int seq = a.seq_lens[req];
-  const int prefix = seq - (qend - qstart);
   const int first = a.table[static_cast<int64_t>(req) * a.table_stride];
-  if (first < 0) return;
+  if (qend <= qstart || first < 0) return;
+  const int prefix = seq - (qend - qstart);
   const int64_t owner = fastdiv(static_cast<uint32_t>(first), a.L.bpp_div);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int h = a.L.kv_heads, sink = a.L.sink, ring = a.L.ring;
   const int64_t page_elems = a.L.page_bytes / 2;
-  for (int index = wave; index < sink + ring; index += kThreads / kWave) {
-    int pos;
-    if (index < sink) {
-      pos = index;
+  for (int pos = max(prefix, 0) + wave; pos < seq; pos += kThreads / kWave) {
+    int index;
+    if (pos < sink) {
+      index = pos;
     } else {
-      const int back = seq - 1 - (index - sink);  // distance of the newest candidate
-      if (back < 0) continue;
-      pos = seq - 1 - back % ring;
-      if (pos < sink) continue;
+      if (pos + ring < seq) continue;  // a later current token owns this ring index
+      const uint32_t lap = fastdiv(static_cast<uint32_t>(pos), a.L.ring_div);
+      index = sink + pos - static_cast<int>(lap) * ring;
     }
-    if (pos < prefix || pos >= seq) continue;
     const int64_t current = static_cast<int64_t>(qstart) + pos - prefix;
     if (current < 0 || current >= a.n) continue;
     const int64_t dst = owner * page_elems + (static_cast<int64_t>(index) * 2 * h + head) * kHeadDim;

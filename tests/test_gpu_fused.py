@@ -64,27 +64,64 @@ CASES = [
 ]
 
 
+def _forward(c, form, splits, raw=None):
+    """One layer step in `form` ("single" or "fused" launches) on a copy of the cache."""
+    n = c.q.shape[0]
+    raw = c.raw.clone() if raw is None else raw
+    k_cache, v_cache = _views(raw, c.layout)
+    impl = OscarAttentionImpl(6, 256, 1 / 16, 1, c.layout.config, fused=form != "single")
+    impl.initialize_layer(c.rk, c.rv)
+    impl.splits_for = lambda meta, s=splits: s
+    c.meta.merged_lse = torch.full((n, 6), 7.0, device=DEV)
+    out = torch.full((n, 6 * 256), 3.0, device=DEV, dtype=torch.bfloat16)
+    impl.forward(None, c.q, c.k, c.v, (k_cache, v_cache), c.meta, out)
+    torch.cuda.synchronize()
+    return out.view(torch.int16).cpu(), c.meta.merged_lse.cpu(), raw.cpu()
+
+
 @pytest.mark.parametrize("lengths,prefixes,splits", CASES)
 def test_fused_step_is_bitwise_the_single_launch_step(lengths, prefixes, splits):
     c = _case(lengths, prefixes, seed=7)
+    want = _forward(c, "single", splits)
+    got = _forward(c, "fused", splits)
+    for a, b in zip(want, got):
+        assert torch.equal(a, b)
+
+
+def test_fused_step_replays_in_a_graph():
+    # Reference tests/test_npu_kernels.py:197-245 through the fused step: a captured step
+    # replayed with new queries on a reset cache matches the eager single-launch step every
+    # time.
+    c = _case([900, 517], [896, 516], seed=21, cfg=OscarConfig(sink_tokens=4, recent_tokens=64))
     n = c.q.shape[0]
-    outs, lses, images = [], [], []
-    for fused in (False, True):
-        raw = c.raw.clone()
-        k_cache, v_cache = _views(raw, c.layout)
-        impl = OscarAttentionImpl(6, 256, 1 / 16, 1, c.layout.config, fused=fused)
-        impl.initialize_layer(c.rk, c.rv)
-        impl.splits_for = lambda meta, s=splits: s
-        c.meta.merged_lse = torch.full((n, 6), 7.0, device=DEV)
-        out = torch.full((n, 6 * 256), 3.0, device=DEV, dtype=torch.bfloat16)
-        impl.forward(None, c.q, c.k, c.v, (k_cache, v_cache), c.meta, out)
+    raw_graph, raw_eager = c.raw.clone(), c.raw.clone()
+    kg, vg = _views(raw_graph, c.layout)
+    impl = OscarAttentionImpl(6, 256, 1 / 16, 1, c.layout.config, fused=True)
+    impl.initialize_layer(c.rk, c.rv)
+    impl.splits_for = lambda meta: 8
+    lse = c.meta.merged_lse = torch.empty((n, 6), device=DEV)
+    out = torch.empty((n, 6 * 256), device=DEV, dtype=torch.bfloat16)
+    impl.forward(None, c.q, c.k, c.v, (kg, vg), c.meta, out)  # warm-up (views, library)
+    torch.cuda.synchronize()
+    raw_graph.copy_(c.raw)
+    graph = torch.cuda.CUDAGraph()
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.graph(graph, stream=stream):
+        impl.forward(None, c.q, c.k, c.v, (kg, vg), c.meta, out)
+    torch.cuda.synchronize()
+    for replay in range(3):
+        c.q.normal_()
+        raw_graph.copy_(c.raw)
+        raw_eager.copy_(c.raw)
+        graph.replay()
         torch.cuda.synchronize()
-        outs.append(out.view(torch.int16).cpu())
-        lses.append(c.meta.merged_lse.cpu())
-        images.append(raw.cpu())
-    assert torch.equal(outs[0], outs[1])
-    assert torch.equal(lses[0], lses[1])
-    assert torch.equal(images[0], images[1])
+        got = (out.view(torch.int16).cpu(), lse.cpu(), raw_graph.cpu())
+        c.meta.merged_lse = lse
+        want = _forward(c, "single", 8, raw=raw_eager)
+        for a, b in zip(want, got):
+            assert torch.equal(a, b), replay
+        _ = (c.q * 2).sum().item()  # eager work between replays
 
 
 @pytest.mark.parametrize("lengths,prefixes,splits", CASES[1:4])
