@@ -108,6 +108,50 @@ __device__ __forceinline__ float wave_tree_sum(float v) {
   return v;
 }
 
+// DPP forms of the wavefront reductions: 16-lane rows reduce through data-parallel
+// primitives (quad_perm xor 1, xor 2, row half-mirror, row mirror), then the four row results
+// combine as uniform values. The sum keeps the pairwise tree of wave_tree_sum bit for bit:
+// every level adds two equal-sized blocks, and a mirror partner holds the same block value as
+// the xor partner once the blocks below are reduced.
+constexpr int kDppQuadXor1 = 0xB1;       // quad_perm [1, 0, 3, 2]
+constexpr int kDppQuadXor2 = 0x4E;       // quad_perm [2, 3, 0, 1]
+constexpr int kDppRowHalfMirror = 0x141;  // lane i <-> 7 - i within 8 lanes
+constexpr int kDppRowMirror = 0x140;      // lane i <-> 15 - i within 16 lanes
+
+template <int kCtrl>
+__device__ __forceinline__ float dpp(float v) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), kCtrl, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float lane_value(float v, int lane) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
+}
+
+__device__ __forceinline__ float wave_max_dpp(float v) {
+  v = fmaxf(v, dpp<kDppQuadXor1>(v));
+  v = fmaxf(v, dpp<kDppQuadXor2>(v));
+  v = fmaxf(v, dpp<kDppRowHalfMirror>(v));
+  v = fmaxf(v, dpp<kDppRowMirror>(v));
+  return fmaxf(fmaxf(lane_value(v, 0), lane_value(v, 16)),
+               fmaxf(lane_value(v, 32), lane_value(v, 48)));
+}
+__device__ __forceinline__ float wave_min_dpp(float v) {
+  v = fminf(v, dpp<kDppQuadXor1>(v));
+  v = fminf(v, dpp<kDppQuadXor2>(v));
+  v = fminf(v, dpp<kDppRowHalfMirror>(v));
+  v = fminf(v, dpp<kDppRowMirror>(v));
+  return fminf(fminf(lane_value(v, 0), lane_value(v, 16)),
+               fminf(lane_value(v, 32), lane_value(v, 48)));
+}
+__device__ __forceinline__ float wave_tree_sum_dpp(float v) {
+#pragma clang fp contract(off)
+  v = v + dpp<kDppQuadXor1>(v);
+  v = v + dpp<kDppQuadXor2>(v);
+  v = v + dpp<kDppRowHalfMirror>(v);
+  v = v + dpp<kDppRowMirror>(v);
+  return (lane_value(v, 0) + lane_value(v, 16)) + (lane_value(v, 32) + lane_value(v, 48));
+}
+
 // ---------------------------------------------------------------- layout (device copy)
 
 struct Layout {

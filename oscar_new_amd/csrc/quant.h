@@ -66,7 +66,7 @@ __device__ __forceinline__ float percentile_threshold(const float x[4], float ra
 #pragma unroll
     for (int i = 0; i < 4; ++i)
       if (key[i] > t) m = fminf(m, __uint_as_float(key[i]));
-    b = wave_min(m);
+    b = wave_min_dpp(m);
   }
   return __fmaf_rn(weight, b - a, a);
 }
@@ -79,22 +79,37 @@ struct Quantized {
   int code[4];
 };
 
-__device__ __forceinline__ Quantized quantize_clipped(const float xc[4]) {
+// Codes, scale and zero of clipped values whose minimum and maximum over the vector are mn and
+// mx (tests/oracle.py:15-17): code = clamp(trunc(fl(fl(x - zero) / scale) + 0.5), 0, 3). The
+// quotient is taken through the correctly rounded reciprocal of the (uniform) scale: within
+// [0.5, 3.5] it differs from the correctly rounded quotient by less than 1.2e-6, so a value of
+// y = q + 0.5 further than 2^-16 from 1, 2 and 3 truncates to the same code. If any lane has a
+// value that close, the wavefront redoes its quotients with IEEE division.
+__device__ __forceinline__ Quantized quantize_clipped(const float xc[4], float mn, float mx) {
 #pragma clang fp contract(off)
   Quantized q;
-  const float mn = wave_min(fminf(fminf(xc[0], xc[1]), fminf(xc[2], xc[3])));
-  const float mx = wave_max(fmaxf(fmaxf(xc[0], xc[1]), fmaxf(xc[2], xc[3])));
   float spread = (mx - mn) / 3.0f;
   spread = spread < 6.103515625e-05f ? 6.103515625e-05f : spread;
   q.zero = float_to_f16_bits(mn);
   q.scale = float_to_f16_bits(spread);
   q.zf = f16_bits_to_float(q.zero);
   q.sf = f16_bits_to_float(q.scale);
+  const float r = 1.0f / q.sf;
+  float y[4];
+  bool near = false;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    y[i] = (xc[i] - q.zf) * r + 0.5f;
+    near |= y[i] > 0.5f && y[i] < 3.5f && fabsf(y[i] - rintf(y[i])) < 1.52587890625e-05f;
+  }
+  if (__any(near)) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) y[i] = (xc[i] - q.zf) / q.sf + 0.5f;
+  }
   q.byte = 0;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const float v = (xc[i] - q.zf) / q.sf + 0.5f;
-    int c = static_cast<int>(v);  // truncation toward zero, as torch .to(int32)
+    int c = static_cast<int>(y[i]);  // truncation toward zero, as torch .to(int32)
     c = c < 0 ? 0 : (c > 3 ? 3 : c);
     q.code[i] = c;
     q.byte |= static_cast<uint32_t>(c) << (2 * i);
@@ -107,26 +122,29 @@ __device__ __forceinline__ void clamp4(const float x[4], float thr, float out[4]
 #pragma unroll
   for (int i = 0; i < 4; ++i) out[i] = fminf(fmaxf(x[i], -thr), thr);
 }
+__device__ __forceinline__ float clamp1(float x, float thr) { return fminf(fmaxf(x, -thr), thr); }
 
-// Quantize one vector and write codes + scale + zero (68 bytes) at `dst`.
+// Quantize one vector and write codes + scale + zero (68 bytes) at `dst`. Clipping is
+// monotone, so the extremes of the clipped vector are the clipped extremes of the vector: one
+// pair of wavefront reductions serves every candidate threshold.
 __device__ __forceinline__ void quantize_store(const float x[4], int mode, float ratio, float factor,
-                               uint8_t* dst) {
+                                               uint8_t* dst) {
 #pragma clang fp contract(off)
-  float xc[4];
   const int lane = threadIdx.x & 63;
+  const float mn = wave_min_dpp(fminf(fminf(x[0], x[1]), fminf(x[2], x[3])));
+  const float mx = wave_max_dpp(fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3])));
+  const float maxabs = fmaxf(fabsf(mn), fabsf(mx));
+  float thr = INFINITY;  // no clipping
   if (mode == OSCAR_CLIP_FACTOR) {
-    const float maxabs =
-        wave_max(fmaxf(fmaxf(fabsf(x[0]), fabsf(x[1])), fmaxf(fabsf(x[2]), fabsf(x[3]))));
-    clamp4(x, maxabs * factor, xc);
+    thr = maxabs * factor;
   } else if (mode == OSCAR_CLIP_SEARCH) {
-    const float maxabs =
-        wave_max(fmaxf(fmaxf(fabsf(x[0]), fabsf(x[1])), fmaxf(fabsf(x[2]), fabsf(x[3]))));
     float best_err = 0.f;
     int best = 0;
     for (int i = 0; i < 8; ++i) {
+      const float t = maxabs * search_factor(i);
       float xi[4];
-      clamp4(x, maxabs * search_factor(i), xi);
-      const Quantized q = quantize_clipped(xi);
+      clamp4(x, t, xi);
+      const Quantized q = quantize_clipped(xi, clamp1(mn, t), clamp1(mx, t));
       float sq[4];
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
@@ -134,29 +152,28 @@ __device__ __forceinline__ void quantize_store(const float x[4], int mode, float
         const float err = x[e] - dec;
         sq[e] = err * err;
       }
-      const float err = wave_tree_sum((sq[0] + sq[1]) + (sq[2] + sq[3]));
+      const float err = wave_tree_sum_dpp((sq[0] + sq[1]) + (sq[2] + sq[3]));
       if (i == 0 || err < best_err) {
         best_err = err;
         best = i;
       }
     }
-    clamp4(x, maxabs * search_factor(best), xc);
+    thr = maxabs * search_factor(best);
   } else if (ratio != 0.0f) {
-    clamp4(x, percentile_threshold(x, ratio), xc);
-  } else {
+    thr = percentile_threshold(x, ratio);
+  }
+  float xc[4];
+  if (thr == INFINITY) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) xc[i] = x[i];
+  } else {
+    clamp4(x, thr, xc);
   }
-  const Quantized q = quantize_clipped(xc);
-  // Gather the four bytes of packed dword (lane & 15) and store 16 dwords + scale/zero.
-  const int src = (lane & 15) * 4;
-  const uint32_t b0 = __shfl(q.byte, src, kWave), b1 = __shfl(q.byte, src + 1, kWave);
-  const uint32_t b2 = __shfl(q.byte, src + 2, kWave), b3 = __shfl(q.byte, src + 3, kWave);
-  if (lane < 16) {
-    reinterpret_cast<uint32_t*>(dst)[lane] = b0 | (b1 << 8) | (b2 << 16) | (b3 << 24);
-  } else if (lane == 16) {
-    reinterpret_cast<uint32_t*>(dst)[16] = q.scale | (q.zero << 16);
-  }
+  const Quantized q = thr == INFINITY ? quantize_clipped(xc, mn, mx)
+                                      : quantize_clipped(xc, clamp1(mn, thr), clamp1(mx, thr));
+  // Lane l owns packed byte l; lane 0 also writes scale | zero (bytes 64..67, 4-aligned).
+  dst[lane] = static_cast<uint8_t>(q.byte);
+  if (lane == 0) *reinterpret_cast<uint32_t*>(dst + 64) = q.scale | (q.zero << 16);
 }
 
 }  // namespace oscar
