@@ -117,11 +117,39 @@ constexpr int kDppQuadXor1 = 0xB1;       // quad_perm [1, 0, 3, 2]
 constexpr int kDppQuadXor2 = 0x4E;       // quad_perm [2, 3, 0, 1]
 constexpr int kDppRowHalfMirror = 0x141;  // lane i <-> 7 - i within 8 lanes
 constexpr int kDppRowMirror = 0x140;      // lane i <-> 15 - i within 16 lanes
+constexpr int kDppRowRor8 = 0x128;        // lane i <- lane (i + 8) % 16 within 16 lanes
 
 template <int kCtrl>
 __device__ __forceinline__ float dpp(float v) {
   return __builtin_bit_cast(
       float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), kCtrl, 0xF, 0xF, false));
+}
+template <int kCtrl>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
+  return static_cast<uint32_t>(
+      __builtin_amdgcn_update_dpp(0, static_cast<int>(v), kCtrl, 0xF, 0xF, false));
+}
+// Lane pairs (l, l ^ 16) and (l, l ^ 32) through v_permlane16_swap / v_permlane32_swap: both
+// lanes of a pair receive the same combination (lower-numbered lane's value first).
+__device__ __forceinline__ float max_xor16(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                  false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float max_xor32(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                  false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float sum_xor16(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                  false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float sum_xor32(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                  false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 __device__ __forceinline__ float lane_value(float v, int lane) {
   return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));

@@ -171,7 +171,8 @@ __host__ __device__ constexpr int p_token(int g, int e) { return 16 * (e >> 2) +
 // 16 (G>>1) + i = bytes 16 (G>>1) + i of A group 2 (G&1), and nibbles 16..31 the same bytes of
 // A group 2 (G&1) + 1: lane n of B group G supplies the LDS row of token p_token(2 (G&1), n)
 // to the first transposed read and p_token(2 (G&1) + 1, n) to the second. One E8M0 scale per
-// query row covers all four scale blocks.
+// query row covers all four scale blocks: the scale of k block kb is read from lane group kb,
+// while an FP8 lane group G holds its bytes 0..15 in block G / 2 and 16..31 in block 2 + G / 2.
 template <int RT>
 __global__ __launch_bounds__(kThreads, 3 - RT) void history_kernel(const AttnArgs a) {
   __shared__ __attribute__((aligned(16))) uint8_t s_ring[kRingBytes];
@@ -428,9 +429,7 @@ __global__ __launch_bounds__(kThreads, 3 - RT) void history_kernel(const AttnArg
     if (__any(need)) {
 #pragma unroll
       for (int rt = 0; rt < RT; ++rt) {
-        float v = lm[rt];
-        v = fmaxf(v, __shfl_xor(v, 16, kWave));
-        v = fmaxf(v, __shfl_xor(v, 32, kWave));
+        const float v = max_xor32(max_xor16(lm[rt]));
         const float mn = fmaxf(m[rt], v);
         const float alpha = mn == -INFINITY ? 1.0f : exp2f(m[rt] - mn);
         m[rt] = mn;
@@ -460,8 +459,7 @@ __global__ __launch_bounds__(kThreads, 3 - RT) void history_kernel(const AttnArg
         av[e] = p * h16lo(vsz[e]);
         amax = fmaxf(amax, av[e]);
       }
-      amax = fmaxf(amax, __shfl_xor(amax, 16, kWave));
-      amax = fmaxf(amax, __shfl_xor(amax, 32, kWave));
+      amax = max_xor32(max_xor16(amax));
       // mult = 2^(133 - eb) puts the row max in [64, 128); the MFMA scales back by
       // 2^(eb - 133) = E8M0 byte eb - 6.
       const uint32_t eb = max(__float_as_uint(amax) >> 23, 7u);
@@ -515,10 +513,8 @@ __global__ __launch_bounds__(kThreads, 3 - RT) void history_kernel(const AttnArg
   // ---- epilogue: merge the four wavefront states, then write normalized partials + LSE.
 #pragma unroll
   for (int rt = 0; rt < RT; ++rt) {
-    psum[rt] += __shfl_xor(psum[rt], 16, kWave);
-    psum[rt] += __shfl_xor(psum[rt], 32, kWave);
-    zsum[rt] += __shfl_xor(zsum[rt], 16, kWave);
-    zsum[rt] += __shfl_xor(zsum[rt], 32, kWave);
+    psum[rt] = sum_xor32(sum_xor16(psum[rt]));
+    zsum[rt] = sum_xor32(sum_xor16(zsum[rt]));
     if (g == 0) {
       s_red[0][wave][16 * rt + n] = m[rt];
       s_red[1][wave][16 * rt + n] = psum[rt];
@@ -581,10 +577,398 @@ __global__ __launch_bounds__(kThreads, 3 - RT) void history_kernel(const AttnArg
   }
 }
 
+// ---------------------------------------------------------------- paired-token kernel
+
+// Up to 8 query rows (decode with G <= 8): each QK MFMA covers two 16-token sets on the two
+// 64-wide halves of k (block-diagonal operands), so 12 of the 16 score columns are live
+// instead of 6 and every lane carries 8 scores of a chunk instead of 16.
+//   * Pair tile pt (0, 1) of a chunk: A row i holds token X = 32 pt + i in k < 64 and token
+//     Y = 32 pt + 16 + i in k >= 64, 64 head dims per MFMA (block b = dims 64 b .. +63); the
+//     query is column j < 8 (row j, k < 64 live) and column j + 8 (row j, k >= 64 live).
+//   * Score lane (j, g) holds tokens 32 pt + 16 (j >= 8) + 4 g + v of query row j % 8; lanes
+//     j and j ^ 8 share a row, its running max and the row's E8M0 scale of the P operand.
+//   * P * V is the 16-row MFMA of the general kernel: P row j (< 8) takes its own 8 tokens
+//     and those of lane j + 8 (one row_ror:8 DPP move per dword).
+// Operand index maps (f8f6f4 layouts):
+//   FP4 A lane (i, G) nibble v: k = 64 (G&1) + 16 (G>>1) + 32 (v/16) + v%16; with raw code
+//   dwords 4b + 2 (G>>1) + {0, 1} emitted [even, odd, even, odd] its head dim is
+//   64 b + 32 (G>>1) + 16 (v/16) + s(v%16), s(t) = 2 (t%8) + t/8.
+//   FP8 B lane (j, G) byte e: k = 32 G + e, live when (j < 8) == (G < 2); head dim
+//   64 b + 32 (e/16) + 16 (G&1) + s(e%16). Dword d of it holds dims
+//   64 b + 32 (d/4) + 16 (G&1) + 8 (d%2) + ((d/2)%2) + {0, 2, 4, 6}.
+//   PV: A lane (j, G) byte e (< 16 hi, +16 lo) is token T(G, e) = 32 ((e/4)%2) + 16 (e/8) +
+//   4 G + e%4; B lane group G reads token rows T(2 (G&1), i) and T(2 (G&1) + 1, i).
+__host__ __device__ constexpr int pair_token(int ga, int e) {
+  return 32 * ((e >> 2) & 1) + 16 * (e >> 3) + 4 * ga + (e & 3);
+}
+
+__global__ __launch_bounds__(kThreads, 2) void history_pair_kernel(const AttnArgs a) {
+  __shared__ __attribute__((aligned(16))) uint8_t s_ring[kRingBytes];
+  __shared__ uint32_t s_off[kTableCache];
+  __shared__ float s_red[3][4][8];  // per wavefront: row max, sum p, sum p z_v
+  static_assert(8 * 512 + 4 * 2 * 8 * 16 * 4 <= 2 * kStageBytes,
+                "query rows and operand images fit wavefront 3's stages");
+  static_assert(4 * 8 * 256 * 4 <= kRingBytes, "the epilogue merge fits the ring");
+
+  Task t;
+  if (!read_task(a, t, blockIdx.x)) return;
+  const int head = blockIdx.y, split = blockIdx.z;
+  int begin, end;
+  split_range(t.recent_begin - t.sink_len, a.block_n, a.splits, split, begin, end);
+  const int p_lo = max(t.sink_len + begin, 0), p_hi = t.sink_len + end;
+  const int lane = threadIdx.x & 63;
+  const int wave = uniform(threadIdx.x >> 6);
+  const int n = lane & 15, g = lane >> 4;
+  const int first = p_lo >> 6;
+  const int nchunk = p_lo < p_hi ? ((p_hi - 1) >> 6) - first + 1 : 0;
+  const int nmine = nchunk > wave ? (nchunk - wave + 3) >> 2 : 0;  // chunks wave + 4 j
+  const int kb_first = p_lo >> a.L.bk_shift;
+
+  // ---- DMA plan (as in the general kernel).
+  const uint32_t tok_bytes = static_cast<uint32_t>(a.L.kv_heads) * kSlot;
+  uint32_t voff[kDma];
+#pragma unroll
+  for (int i = 0; i < kDma; ++i) {
+    const int c = 64 * i + lane;
+    voff[i] = static_cast<uint32_t>(c / kPieces) * tok_bytes + 16 * (c % kPieces);
+  }
+  const uint32_t my_ring = lds_addr(s_ring) + wave * 2 * kStageBytes;
+  const uint32_t in_kb_mask = static_cast<uint32_t>(a.L.bk - 1);
+  uint32_t valid_bits = 0;
+  auto issue = [&](int j, int s) {
+    const int t0 = (first + wave + 4 * j) << 6;
+    const int local = (t0 >> a.L.bk_shift) - kb_first;
+    uint32_t off32 = s_off[min(local, kTableCache - 1)];
+    if (local >= kTableCache) off32 = kernel_block_offset(a, t, head, t0 >> a.L.bk_shift);
+    off32 = uniform(off32);
+    const uint8_t* base = a.history;
+    const bool ok = off32 != kNoBlock;
+    if (ok)
+      base = a.history + (static_cast<uint64_t>(off32) << 5) +
+             (static_cast<uint32_t>(t0) & in_kb_mask) * tok_bytes;
+    valid_bits = ok ? (valid_bits | (1u << s)) : (valid_bits & ~(1u << s));
+    const uint32_t lds = my_ring + s * kStageBytes + kSkew;
+#pragma unroll
+    for (int i = 0; i < kDma; ++i) dma_x4(base, voff[i], lds + 1024 * i);
+  };
+
+  // ---- query rows -> LDS (wavefront 3's stages): piece p of row r at r * 32 + (p ^ r).
+  uint8_t* q_lds = s_ring + 6 * kStageBytes;
+  uint32_t* q_img = reinterpret_cast<uint32_t*>(q_lds + 8 * 512);  // [b][term][r][h][d]
+  {
+    const int slot = wave * 64 + lane;
+    const int row = slot >> 5, piece = (slot & 31) ^ row;
+    const RowInfo ri = row_info(a, t, head, row);
+    const uint16_t* src =
+        ri.valid ? a.query + ri.token * a.qs0 + ri.qhead * a.qs1 + 8 * piece : a.query;
+    dma_dwordx4(src, lds_addr(q_lds) + 1024 * wave);
+  }
+  if (nchunk > 0) {
+    const int nkb = min(((p_hi - 1) >> a.L.bk_shift) - kb_first + 1, kTableCache);
+    for (int j = threadIdx.x; j < nkb; j += kThreads)
+      s_off[j] = kernel_block_offset(a, t, head, kb_first + j);
+  }
+  OSCAR_WAIT_VM(0);
+  __syncthreads();
+  if (wave < 3) {
+    if (nmine > 0) issue(0, 0);
+    if (nmine > 1) issue(1, 1);
+  }
+
+  // ---- row statistics (every wavefront, redundantly): lane l reduces row l / 8 over dims
+  // 32 (l % 8) .. +31; the row's power-of-two multiplier puts its max |q| in [128, 256).
+  float qmult_l, qsum_l;
+  {
+    const int row = lane >> 3;
+    const bool live = row_info(a, t, head, row).valid;
+    float mx = 0.f, qs = 0.f;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int piece = 4 * (lane & 7) + k;
+      const u32x4 w = *reinterpret_cast<const u32x4*>(q_lds + row * 512 + 16 * (piece ^ row));
+#pragma unroll
+      for (int x = 0; x < 4; ++x) {
+        const float lo = live ? bf16_to_float(w[x] & 0xffffu) : 0.f;
+        const float hi = live ? bf16_to_float(w[x] >> 16) : 0.f;
+        mx = fmaxf(mx, fmaxf(fabsf(lo), fabsf(hi)));
+        qs += lo + hi;
+      }
+    }
+    mx = fmaxf(mx, dpp<kDppQuadXor1>(mx));
+    mx = fmaxf(mx, dpp<kDppQuadXor2>(mx));
+    mx = fmaxf(mx, dpp<kDppRowHalfMirror>(mx));
+    qs += dpp<kDppQuadXor1>(qs);
+    qs += dpp<kDppQuadXor2>(qs);
+    qs += dpp<kDppRowHalfMirror>(qs);
+    const uint32_t eb = max((__float_as_uint(mx) >> 23) & 0xffu, 7u);
+    qmult_l = __uint_as_float((261u - eb) << 23);
+    qsum_l = qs;
+  }
+  // This lane's score row j % 8: FP4 holds c / 2, the score in log2 units is r fq.
+  const int my_row = n & 7;
+  const float qmult = __shfl(qmult_l, 8 * my_row, kWave);
+  const float fq = 2.0f * a.scale_log2 / qmult;
+  const float qs2 = 0.5f * __shfl(qsum_l, 8 * my_row, kWave) * qmult;
+
+  // ---- operand images: wavefront w converts head-dim block b = w. Item (r, h, d) = dword d
+  // of the live B operand of row r, k half h: FP8 terms of 4 dims, term 1 the residual.
+#pragma unroll
+  for (int it = 0; it < 2; ++it) {
+    const int item = 64 * it + lane;
+    const int r = item >> 4, h = (item >> 3) & 1, d = item & 7;
+    const float mult = __shfl(qmult_l, 8 * r, kWave);
+    const bool live = row_info(a, t, head, r).valid;  // padding rows stage the wrong bytes
+    const int piece = 8 * wave + 4 * (d >> 2) + 2 * h + (d & 1);
+    const u32x4 w = *reinterpret_cast<const u32x4*>(q_lds + r * 512 + 16 * (piece ^ r));
+    const bool odd = (d >> 1) & 1;
+    float v[4];
+#pragma unroll
+    for (int x = 0; x < 4; ++x)
+      v[x] = live ? bf16_to_float(odd ? (w[x] >> 16) : (w[x] & 0xffffu)) * mult : 0.f;
+    const uint32_t t0 = fp8x4_take(v);
+    const uint32_t t1 = fp8x4(v[0], v[1], v[2], v[3]);
+    q_img[((wave * 2 + 0) * 8 + r) * 16 + h * 8 + d] = t0;
+    q_img[((wave * 2 + 1) * 8 + r) * 16 + h * 8 + d] = t1;
+  }
+  barrier_lds();
+  i32x8 qb[4][kQTerms];
+  {
+    const bool live = (n < 8) == (g < 2);
+    const int h = g & 1;
+#pragma unroll
+    for (int b = 0; b < 4; ++b)
+#pragma unroll
+      for (int term = 0; term < kQTerms; ++term) {
+        const u32x4* src =
+            reinterpret_cast<const u32x4*>(q_img + ((b * 2 + term) * 8 + my_row) * 16 + h * 8);
+        const u32x4 lo = src[0], hi = src[1];
+        qb[b][term] = live ? i32x8{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3],
+                                   (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]}
+                           : i32x8{0, 0, 0, 0, 0, 0, 0, 0};
+      }
+  }
+  barrier_lds();  // everyone is done with wavefront 3's stages
+  if (wave == 3) {
+    if (nmine > 0) issue(0, 0);
+    if (nmine > 1) issue(1, 1);
+  }
+
+  // ---- per-lane LDS offsets inside a stage (record r starts at kSkew + 144 r)
+  const int side = n >> 3;  // 0: X tokens, 1: Y tokens of each pair tile
+  // QK A operand: token i + 16 (G&1) of the pair tile, code dwords 4b + 2 (G>>1), +1.
+  const int k_off = kSkew + kRec * (n + 16 * (g & 1)) + 8 * (g >> 1);
+  // Scale|zero of this lane's score tokens 32 pt + 16 side + 4 g + v.
+  const int sz_off = kSkew + kRec * (16 * side + 4 * g) + 64;
+  // Transposed V reads: token rows T(2 (g&1), n) and T(2 (g&1) + 1, n) = T(2 (g&1), n) + 4.
+  const int v_off = kSkew + kRec * pair_token(2 * (g & 1), n) + kVector;
+
+  float m = -INFINITY, psum = 0.f, zsum = 0.f;
+  f32x4 o[16];  // o[2c + par]: rows 4g + v, dim 32c + 2n + par (units of c/2)
+#pragma unroll
+  for (int c = 0; c < 16; ++c) o[c] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  auto process = [&](int j, auto stage_tag) {
+    constexpr int S = decltype(stage_tag)::value;
+    const uint8_t* st = s_ring + wave * 2 * kStageBytes + S * kStageBytes;
+    // Scores: two pair tiles, four head-dim blocks, kQTerms query terms.
+    f32x4 acc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      i32x8 kf[2];
+#pragma unroll
+      for (int pt = 0; pt < 2; ++pt) {
+        const uint32_t* kp =
+            reinterpret_cast<const uint32_t*>(st + k_off + 32 * kRec * pt + 16 * b);
+        const uint32_t w0 = kp[0], w1 = kp[1];
+        kf[pt] = i32x8{even_codes(w0), odd_codes(w0), even_codes(w1), odd_codes(w1), 0, 0, 0, 0};
+      }
+#pragma unroll
+      for (int term = 0; term < kQTerms; ++term)
+#pragma unroll
+        for (int pt = 0; pt < 2; ++pt) acc[pt] = mfma_qk(kf[pt], qb[b][term], acc[pt]);
+    }
+    uint32_t ksz[8], vsz[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int off = sz_off + kRec * (32 * (e >> 2) + (e & 3));
+      ksz[e] = *reinterpret_cast<const uint32_t*>(st + off);
+      vsz[e] = *reinterpret_cast<const uint32_t*>(st + off + kVector);
+    }
+    float r2[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+      r2[e] = fmaf(h16lo(ksz[e]), acc[e >> 2][e & 3], h16hi(ksz[e]) * qs2);
+    const int t0 = (first + wave + 4 * j) << 6;
+    const bool ok_block = (valid_bits >> S) & 1u;
+    if (!(ok_block && t0 >= p_lo && t0 + kChunk <= p_hi)) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int tok = 32 * (e >> 2) + 16 * side + 4 * g + (e & 3);
+        const bool ok = ok_block && static_cast<uint32_t>(t0 + tok - p_lo) <
+                                        static_cast<uint32_t>(p_hi - p_lo);
+        vsz[e] = ok ? vsz[e] : 0u;
+        r2[e] = ok ? r2[e] : -INFINITY;
+      }
+    }
+    // Lazy running max, shared by the lanes of a row: j, j ^ 8 and all four lane groups.
+    float lm = r2[0];
+#pragma unroll
+    for (int e = 1; e < 8; ++e) lm = fmaxf(lm, r2[e]);
+    lm *= fq;
+    if (__any(lm > m + kTheta)) {
+      float v = fmaxf(lm, dpp<kDppRowRor8>(lm));
+      v = max_xor32(max_xor16(v));
+      const float mn = fmaxf(m, v);
+      const float alpha = mn == -INFINITY ? 1.0f : exp2f(m - mn);
+      m = mn;
+      psum *= alpha;
+      zsum *= alpha;
+#pragma unroll
+      for (int v4 = 0; v4 < 4; ++v4) {
+        const float av = __shfl(alpha, 4 * g + v4, kWave);  // accumulator row 4g + v4
+#pragma unroll
+        for (int c = 0; c < 16; ++c) o[c][v4] *= av;
+      }
+    }
+    // P operand: p s_v as FP8 hi + lo with one E8M0 scale per query row (the scale of k
+    // block kb comes from lane group kb, while FP8 lane group G holds its hi bytes in block
+    // G / 2 and its lo bytes in block 2 + G / 2, so a per-lane scale would mix rows' data).
+    const float nm = m == -INFINITY ? 0.f : -m;
+    float av[8];
+    float amax = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float p = __builtin_amdgcn_exp2f(fmaf(r2[e], fq, nm));
+      psum += p;
+      zsum = fmaf(p, h16hi(vsz[e]), zsum);
+      av[e] = p * h16lo(vsz[e]);
+      amax = fmaxf(amax, av[e]);
+    }
+    amax = max_xor32(max_xor16(fmaxf(amax, dpp<kDppRowRor8>(amax))));
+    const uint32_t eb = max(__float_as_uint(amax) >> 23, 7u);
+    const float mult = __uint_as_float((260u - eb) << 23);
+    const int sa = static_cast<int>(eb) - 6;
+    uint32_t hi[2], lo[2];
+#pragma unroll
+    for (int pt = 0; pt < 2; ++pt) {
+      float x[4] = {av[4 * pt] * mult, av[4 * pt + 1] * mult, av[4 * pt + 2] * mult,
+                    av[4 * pt + 3] * mult};
+      hi[pt] = fp8x4_take(x);
+      lo[pt] = fp8x4(x[0], x[1], x[2], x[3]);
+    }
+    const i32x8 pa = i32x8{(int)hi[0], (int)hi[1], (int)dpp_u32<kDppRowRor8>(hi[0]),
+                           (int)dpp_u32<kDppRowRor8>(hi[1]), (int)lo[0], (int)lo[1],
+                           (int)dpp_u32<kDppRowRor8>(lo[0]), (int)dpp_u32<kDppRowRor8>(lo[1])};
+    // O += P V over the chunk's 64 tokens, 32 dims (16 dim pairs) per transposed read pair.
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      const i32x2 r0 = __builtin_amdgcn_ds_read_tr4_b64_v2i32((lds_i32x2_ptr_t)(st + v_off + 8 * c));
+      const i32x2 r1 =
+          __builtin_amdgcn_ds_read_tr4_b64_v2i32((lds_i32x2_ptr_t)(st + v_off + 4 * kRec + 8 * c));
+      const i32x8 be = i32x8{even_codes(r0[0]), even_codes(r0[1]), even_codes(r1[0]),
+                             even_codes(r1[1]), 0, 0, 0, 0};
+      const i32x8 bo = i32x8{odd_codes(r0[0]), odd_codes(r0[1]), odd_codes(r1[0]),
+                             odd_codes(r1[1]), 0, 0, 0, 0};
+      o[2 * c] = mfma_pv(pa, be, o[2 * c], sa);
+      o[2 * c + 1] = mfma_pv(pa, bo, o[2 * c + 1], sa);
+    }
+  };
+
+  // ---- token loop, two chunks (one per ring stage) per iteration: wait for chunk j,
+  // consume it, refill its stage with chunk j + 2.
+  int j = 0;
+  for (; j + 1 < nmine; j += 2) {
+    OSCAR_WAIT_VM(kDma);
+    process(j, std::integral_constant<int, 0>());
+    if (j + 2 < nmine) {
+      OSCAR_WAIT_LGKM();
+      issue(j + 2, 0);
+      OSCAR_WAIT_VM(kDma);
+    } else {
+      OSCAR_WAIT_VM(0);
+    }
+    process(j + 1, std::integral_constant<int, 1>());
+    if (j + 3 < nmine) {
+      OSCAR_WAIT_LGKM();
+      issue(j + 3, 1);
+    }
+  }
+  if (j < nmine) {
+    OSCAR_WAIT_VM(0);
+    process(j, std::integral_constant<int, 0>());
+  }
+
+  // ---- epilogue: row totals over the lanes of a row, then the four wavefront states.
+  // Lane indices are recomputed here (mbcnt) so that none stays live across the token loop.
+  const int el = static_cast<int>(__builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u)));
+  const int etid = wave * 64 + el, en = el & 15, eg = el >> 4;
+  psum += dpp<kDppRowRor8>(psum);
+  zsum += dpp<kDppRowRor8>(zsum);
+  psum = sum_xor32(sum_xor16(psum));
+  zsum = sum_xor32(sum_xor16(zsum));
+  if (el < 8) {
+    s_red[0][wave][el] = m;
+    s_red[1][wave][el] = psum;
+    s_red[2][wave][el] = zsum;
+  }
+  __syncthreads();  // every chunk consumed; the ring is free for the merge
+  float* s_o = reinterpret_cast<float*>(s_ring);  // [wave][row 0..7][256]
+  if (eg < 2) {
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int row = 4 * eg + v;
+      const float mx = fmaxf(fmaxf(s_red[0][0][row], s_red[0][1][row]),
+                             fmaxf(s_red[0][2][row], s_red[0][3][row]));
+      const float mw = s_red[0][wave][row];
+      const float f = mw == -INFINITY ? 0.f : exp2f(mw - mx);
+      float* dst = s_o + (wave * 8 + row) * 256 + 2 * en;
+#pragma unroll
+      for (int c = 0; c < 8; ++c)
+        *reinterpret_cast<float2*>(dst + 32 * c) =
+            make_float2(o[2 * c][v] * f, o[2 * c + 1][v] * f);
+    }
+  }
+  __syncthreads();
+  // Thread -> (row, dims 4 (tid % 32) + 128 q): 32 threads write 512 contiguous bytes.
+  const int row = etid >> 5, d0 = 4 * (etid & 31);
+  const RowInfo ri = row_info(a, t, head, row);
+  if (ri.valid) {
+    float mx = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) mx = fmaxf(mx, s_red[0][w][row]);
+    float den = 0.f, zs = 0.f;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const float mw = s_red[0][w][row];
+      const float f = mw == -INFINITY ? 0.f : exp2f(mw - mx);
+      den = fmaf(f, s_red[1][w][row], den);
+      zs = fmaf(f, s_red[2][w][row], zs);
+    }
+    const float inv = 1.0f / fmaxf(den, 1.0e-30f);
+    float* out = a.partials + ((ri.token * a.hq + ri.qhead) * a.splits + split) * kHeadDim + d0;
+    const float4* so = reinterpret_cast<const float4*>(s_o + row * 256 + d0);
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const float4 x0 = so[32 * q], x1 = so[8 * 256 / 4 + 32 * q];
+      const float4 x2 = so[2 * 8 * 256 / 4 + 32 * q], x3 = so[3 * 8 * 256 / 4 + 32 * q];
+      const float4 r = make_float4((2.0f * ((x0.x + x1.x) + (x2.x + x3.x)) + zs) * inv,
+                                   (2.0f * ((x0.y + x1.y) + (x2.y + x3.y)) + zs) * inv,
+                                   (2.0f * ((x0.z + x1.z) + (x2.z + x3.z)) + zs) * inv,
+                                   (2.0f * ((x0.w + x1.w) + (x2.w + x3.w)) + zs) * inv);
+      *reinterpret_cast<float4*>(out + 128 * q) = r;
+    }
+    if ((etid & 31) == 0)
+      a.lse[(ri.token * a.hq + ri.qhead) * a.splits + split] =
+          den > 0.f ? (mx + log2f(den)) * kLn2 : -INFINITY;
+  }
+}
+
 }  // namespace
 
 hipError_t launch_history(const AttnArgs& a, dim3 grid, int rows, hipStream_t stream) {
-  if (rows <= 16)
+  if (rows <= 8)
+    hipLaunchKernelGGL(history_pair_kernel, grid, dim3(kThreads), 0, stream, a);
+  else if (rows <= 16)
     hipLaunchKernelGGL(history_kernel<1>, grid, dim3(kThreads), 0, stream, a);
   else
     hipLaunchKernelGGL(history_kernel<2>, grid, dim3(kThreads), 0, stream, a);
