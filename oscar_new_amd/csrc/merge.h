@@ -18,10 +18,10 @@ struct SplitMerge {
 };
 
 // kernels.py:489-503: w_s = e^{lse_s - M}, splits with lse -inf contribute nothing. `part`
-// is the row's [splits][256] partials, `ls` its [splits] LSEs. Rows of padded tokens
-// (valid false, uniform over the wavefront) merge to nothing. Up to 16 splits take one
-// round of loads (LSEs and partial rows together); the partials are accumulated in split
-// order either way.
+// is the row's [splits][256] partials (this lane's dims), `ls` its [splits] LSEs. Padded rows
+// (valid false, uniform over the wavefront) merge to nothing; their loads are issued anyway,
+// since they stay inside the row's buffers, so that no load waits for the token count.
+// The partials are accumulated in split order.
 __device__ __forceinline__ void merge_group(SplitMerge& r, const float (&l)[16],
                                             const float4 (&v)[16], float safe) {
 #pragma unroll
@@ -36,42 +36,89 @@ __device__ __forceinline__ void merge_group(SplitMerge& r, const float (&l)[16],
   }
 }
 
-__device__ __forceinline__ void load_group(const float* p, const float* ls, int s0, int splits,
-                                           float (&l)[16], float4 (&v)[16]) {
+// Splits [s0, min(s0 + 16, end)) of a row: LSEs and this lane's partial values (-inf / zero
+// past `end`, or for every split of a padded row).
+__device__ __forceinline__ void load_group(const float* p, const float* ls, int s0, int end,
+                                           bool valid, float (&l)[16], float4 (&v)[16]) {
 #pragma unroll
   for (int k = 0; k < 16; ++k) {
-    const bool in = s0 + k < splits;
+    const bool in = s0 + k < end;
     l[k] = in ? ls[s0 + k] : -INFINITY;
     v[k] = in ? *reinterpret_cast<const float4*>(p + static_cast<int64_t>(s0 + k) * kHeadDim)
               : make_float4(0.f, 0.f, 0.f, 0.f);
+    l[k] = valid ? l[k] : -INFINITY;
   }
 }
 
-__device__ __forceinline__ SplitMerge merge_splits_row(const float* part, const float* ls,
-                                                       int splits, bool valid, int lane) {
+__device__ __forceinline__ SplitMerge empty_merge() {
   SplitMerge r;
   r.mx = -INFINITY;
   r.den = 0.f;
 #pragma unroll
   for (int i = 0; i < 4; ++i) r.acc[i] = 0.f;
-  if (!valid) return r;
+  return r;
+}
+
+// Up to 16 splits: one wavefront, one round of loads.
+__device__ __forceinline__ SplitMerge merge_splits_row(const float* part, const float* ls,
+                                                       int splits, bool valid, int lane) {
+  SplitMerge r = empty_merge();
+  float l[16];
+  float4 v[16];
+  load_group(part + lane * 4, ls, 0, splits, valid, l, v);
+#pragma unroll
+  for (int k = 0; k < 16; ++k) r.mx = fmaxf(r.mx, l[k]);
+  merge_group(r, l, v, r.mx == -INFINITY ? 0.f : r.mx);
+  return r;
+}
+
+// Splits above this count are merged by the four wavefronts of a workgroup.
+constexpr int kWaveMergeSplits = 16;
+
+struct GroupMergeLds {
+  float acc[4][kHeadDim];
+  float den[4];
+};
+
+// More than 16 splits: wavefront w accumulates splits [w q, (w + 1) q), q = ceil(splits / 4),
+// 16 per round with the next round's loads in flight, against the row max over every split;
+// the four partial sums are then added in wavefront order through LDS. Every wavefront of the
+// workgroup calls this for the same row and receives the same result.
+__device__ __forceinline__ SplitMerge merge_splits_row_group(const float* part, const float* ls,
+                                                             int splits, bool valid,
+                                                             GroupMergeLds* lds) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  SplitMerge r = empty_merge();
+  for (int s = lane; s < splits; s += kWave) r.mx = fmaxf(r.mx, ls[s]);
+  r.mx = valid ? wave_max_dpp(r.mx) : -INFINITY;
+  const float safe = r.mx == -INFINITY ? 0.f : r.mx;
+  const int q = (splits + 3) >> 2;
+  const int s_begin = min(wave * q, splits), s_end = min(s_begin + q, splits);
   const float* p = part + lane * 4;
   float l[16];
   float4 v[16];
-  if (splits <= 16) {
-    load_group(p, ls, 0, splits, l, v);
-#pragma unroll
-    for (int k = 0; k < 16; ++k) r.mx = fmaxf(r.mx, l[k]);
-    merge_group(r, l, v, r.mx == -INFINITY ? 0.f : r.mx);
-    return r;
-  }
-  for (int s = lane; s < splits; s += kWave) r.mx = fmaxf(r.mx, ls[s]);
-  r.mx = wave_max(r.mx);
-  const float safe = r.mx == -INFINITY ? 0.f : r.mx;
-  for (int s0 = 0; s0 < splits; s0 += 16) {
-    load_group(p, ls, s0, splits, l, v);
+  load_group(p, ls, s_begin, s_end, valid, l, v);
+  for (int s0 = s_begin; s0 < s_end; s0 += 16) {
+    float ln[16];
+    float4 vn[16];
+    load_group(p, ls, s0 + 16, s_end, valid, ln, vn);  // empty past the wavefront's range
     merge_group(r, l, v, safe);
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      l[k] = ln[k];
+      v[k] = vn[k];
+    }
   }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) lds->acc[wave][lane * 4 + i] = r.acc[i];
+  if (lane == 0) lds->den[wave] = r.den;
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    r.acc[i] = ((lds->acc[0][lane * 4 + i] + lds->acc[1][lane * 4 + i]) +
+                lds->acc[2][lane * 4 + i]) + lds->acc[3][lane * 4 + i];
+  r.den = ((lds->den[0] + lds->den[1]) + lds->den[2]) + lds->den[3];
+  __syncthreads();  // the area may be reused by the caller
   return r;
 }
 

@@ -1,7 +1,7 @@
 // merge_splits / merge_paths: LSE-weighted combination of attention partials.
 //
-// Reference: oscar_ascend/kernels.py:485-541. One wavefront per (token, query head) row;
-// lane l owns dims 4l..4l+3. Every row is written, padded rows (token >= counts[1]) too,
+// Reference: oscar_ascend/kernels.py:485-541. One wavefront per (token, query head) row (one
+// workgroup per row above 16 splits); lane l owns dims 4l..4l+3. Every row is written, padded rows (token >= counts[1]) too,
 // because the inverse rotation that follows reads them.
 #include "merge.h"
 
@@ -18,6 +18,7 @@ struct MergeSplitsArgs {
   float* logsum;
 };
 
+// Up to 16 splits: one wavefront per row, four rows per workgroup.
 __global__ __launch_bounds__(kThreads) void merge_splits_kernel(const MergeSplitsArgs a) {
   const int lane = threadIdx.x & 63;
   const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
@@ -25,6 +26,19 @@ __global__ __launch_bounds__(kThreads) void merge_splits_kernel(const MergeSplit
   const bool valid = row / a.hq < a.counts[1];
   const SplitMerge r = merge_splits_row(a.partials + row * a.splits * kHeadDim,
                                         a.lse + row * a.splits, a.splits, valid, lane);
+  *reinterpret_cast<uint2*>(a.out + row * kHeadDim + lane * 4) = merge_splits_out(r);
+  if (lane == 0) a.logsum[row] = merge_splits_lse(r);
+}
+
+// More splits: one workgroup per row.
+__global__ __launch_bounds__(kThreads) void merge_splits_group_kernel(const MergeSplitsArgs a) {
+  __shared__ GroupMergeLds lds;
+  const int lane = threadIdx.x & 63;
+  const int64_t row = blockIdx.x;
+  const bool valid = row / a.hq < a.counts[1];
+  const SplitMerge r = merge_splits_row_group(a.partials + row * a.splits * kHeadDim,
+                                              a.lse + row * a.splits, a.splits, valid, &lds);
+  if (threadIdx.x >= kWave) return;
   *reinterpret_cast<uint2*>(a.out + row * kHeadDim + lane * 4) = merge_splits_out(r);
   if (lane == 0) a.logsum[row] = merge_splits_lse(r);
 }
@@ -83,8 +97,12 @@ extern "C" int oscar_merge_splits(const float* partials, const float* lse, const
     return OSCAR_E_ALIGN;
   MergeSplitsArgs a{partials, lse, counts, n * hq, static_cast<int32_t>(hq), splits,
                     static_cast<uint16_t*>(out), logsum};
-  hipLaunchKernelGGL(merge_splits_kernel, dim3(static_cast<unsigned>((a.rows + 3) / 4)),
-                     dim3(kThreads), 0, as_stream(stream), a);
+  if (splits <= kWaveMergeSplits)
+    hipLaunchKernelGGL(merge_splits_kernel, dim3(static_cast<unsigned>((a.rows + 3) / 4)),
+                       dim3(kThreads), 0, as_stream(stream), a);
+  else
+    hipLaunchKernelGGL(merge_splits_group_kernel, dim3(static_cast<unsigned>(a.rows)),
+                       dim3(kThreads), 0, as_stream(stream), a);
   return static_cast<int>(hipGetLastError());
 }
 

@@ -26,17 +26,20 @@ struct PostArgs {
   float* merged_lse;   // [rows] or null
   WindowArgs win;
   int64_t win_requests;  // min(n, max_reqs)
+  int32_t merge_wgs;     // workgroups of the merge role; the rest store windows
 };
 
 // Rows [row0, min(row0 + R, row_end, p.rows)) by the four wavefronts of a workgroup:
-// wavefront w merges rows w, w + 4, ... into LDS (s_h: R x 256 bf16, s_l: R floats), then
-// every wavefront rotates the R rows back for 64 output columns and merges them with the BF16
-// branch. Every read that does not depend on the merge (R_v, the BF16-branch values and LSEs)
-// is requested before it.
+// wavefront w merges rows w, w + 4, ... into LDS (s_h: R x 256 bf16, s_l: R floats), or, with
+// R = 1 (more than 16 splits), all four merge the one row together; then every wavefront
+// rotates the R rows back for 64 output columns and merges them with the BF16 branch. Every
+// read that does not depend on the merge (R_v, the BF16-branch values and LSEs) is requested
+// before it, and none waits for the token count.
 template <int R>
 __device__ __forceinline__ void post_rows(const PostArgs& p, int64_t row0, int64_t row_end,
-                                          uint16_t (*s_h)[kHeadDim], float* s_l) {
-  static_assert(R == 4 || R == 16, "row groups of 4 or 16");
+                                          uint16_t (*s_h)[kHeadDim], float* s_l,
+                                          GroupMergeLds* group_lds) {
+  static_assert(R == 1 || R == 4 || R == 16, "row groups of 1, 4 or 16");
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int n = lane & 15, g = lane >> 4;
   const int active = p.counts[1];
@@ -57,20 +60,37 @@ __device__ __forceinline__ void post_rows(const PostArgs& p, int64_t row0, int64
   for (int v = 0; v < 4; ++v) {
     const int r = 4 * g + v;
     const int64_t row = row0 + r;
-    valid[v] = r < R && row < row_end && row / p.hq < active;
-    lb[v] = valid[v] ? p.rl[row] : -INFINITY;
+    const bool in = r < R && row < row_end;
+    const int64_t lrow = in ? row : 0;
+    valid[v] = in && row / p.hq < active;
+    const float l = p.rl[lrow];
+    lb[v] = valid[v] ? l : -INFINITY;
 #pragma unroll
-    for (int ct = 0; ct < 4; ++ct)
-      bv[v][ct] = valid[v] ? p.rp[row * kHeadDim + 64 * wave + 16 * ct + n] : 0.f;
+    for (int ct = 0; ct < 4; ++ct) {
+      const float x = p.rp[lrow * kHeadDim + 64 * wave + 16 * ct + n];
+      bv[v][ct] = valid[v] ? x : 0.f;
+    }
   }
-  for (int r = wave; r < R; r += kThreads / kWave) {
-    const int64_t row = row0 + r;
-    const bool in = row < row_end;
-    const SplitMerge m = merge_splits_row(p.hp + (in ? row : 0) * p.splits * kHeadDim,
-                                          p.hl + (in ? row : 0) * p.splits, p.splits,
-                                          in && row / p.hq < active, lane);
-    *reinterpret_cast<uint2*>(&s_h[r][lane * 4]) = merge_splits_out(m);
-    if (lane == 0) s_l[r] = merge_splits_lse(m);
+  if (R == 1) {
+    const bool in = row0 < row_end;
+    const int64_t lrow = in ? row0 : 0;
+    const SplitMerge m = merge_splits_row_group(p.hp + lrow * p.splits * kHeadDim,
+                                                p.hl + lrow * p.splits, p.splits,
+                                                in && row0 / p.hq < active, group_lds);
+    if (wave == 0) {
+      *reinterpret_cast<uint2*>(&s_h[0][lane * 4]) = merge_splits_out(m);
+      if (lane == 0) s_l[0] = merge_splits_lse(m);
+    }
+  } else {
+    for (int r = wave; r < R; r += kThreads / kWave) {
+      const int64_t row = row0 + r;
+      const bool in = row < row_end;
+      const SplitMerge m = merge_splits_row(p.hp + (in ? row : 0) * p.splits * kHeadDim,
+                                            p.hl + (in ? row : 0) * p.splits, p.splits,
+                                            in && row / p.hq < active, lane);
+      *reinterpret_cast<uint2*>(&s_h[r][lane * 4]) = merge_splits_out(m);
+      if (lane == 0) s_l[r] = merge_splits_lse(m);
+    }
   }
   __syncthreads();
   // Inverse rotation of the R merged rows (rows R..15 of the MFMA tile are zero), then the

@@ -98,35 +98,35 @@ __global__ __launch_bounds__(kThreads) void pre_attention_kernel(const PreArgs p
   }
   const FastDiv h_div = p.h_div;
   if (bid < p.raw_wgs + p.kv_wgs) {
-    // K or V tile: rotate 16 rows, then clip/quantize/pack each into its slot.
+    // K or V rows: four workgroups share a 16-row rotation tile (each computes it) and each
+    // clips/quantizes/packs four of its rows, one per wavefront, into their slots. The
+    // row's token count and slot are requested before the rotation.
     const int r = bid - p.raw_wgs;
-    const int64_t tile = r >> 1;
     const int is_v = r & 1;
+    const int64_t quad = r >> 1, tile = quad >> 2;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int rr = 4 * static_cast<int>(quad & 3) + wave;
+    const int64_t row = tile * 16 + rr;
+    const bool in = row < p.kv_rows;
+    const uint32_t token = fastdiv(static_cast<uint32_t>(in ? row : 0), h_div);
+    const int head = static_cast<int>((in ? row : 0) - static_cast<int64_t>(token) * a.L.kv_heads);
+    const bool live = in && static_cast<int64_t>(token) < a.counts[1];
+    const int64_t slot = live ? p.slots[token] : -1;  // in flight beside the rotation loads
     uint16_t* tile_lds = reinterpret_cast<uint16_t*>(smem);
     rotate_rows16(is_v ? a.value : a.key, is_v ? a.vs0 : a.ks0, is_v ? a.vs1 : a.ks1, h_div,
                   a.L.kv_heads, p.kv_rows, tile, is_v ? p.rv_t : p.rk_t, tile_lds, nullptr);
     __syncthreads();
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    for (int rr = wave; rr < 16; rr += kThreads / kWave) {
-      const int64_t row = tile * 16 + rr;
-      if (row >= p.kv_rows) break;
-      // Same skips as store_int2 (kernels.py:168-169 and the buffer bound).
-      const uint32_t token = fastdiv(static_cast<uint32_t>(row), h_div);
-      const int head = static_cast<int>(row - static_cast<int64_t>(token) * a.L.kv_heads);
-      if (static_cast<int64_t>(token) >= a.counts[1]) continue;
-      const int64_t slot = p.slots[token];
-      if (slot < 0) continue;
-      const int64_t page = slot / a.L.bp;
-      const int64_t within = slot - page * a.L.bp;
-      const int64_t base =
-          page * a.L.page_bytes + (within * a.L.kv_heads + head) * a.L.slot_bytes;
-      if (base + 2 * a.L.vector_bytes > p.history_bytes) continue;
-      const uint2 raw = *reinterpret_cast<const uint2*>(tile_lds + rr * kHeadDim + lane * 4);
-      const float x[4] = {bf16_to_float(raw.x & 0xffffu), bf16_to_float(raw.x >> 16),
-                          bf16_to_float(raw.y & 0xffffu), bf16_to_float(raw.y >> 16)};
-      quantize_store(x, p.mode, is_v ? p.v_ratio : p.k_ratio, is_v ? p.v_factor : p.k_factor,
-                     p.history + base + is_v * a.L.vector_bytes);
-    }
+    // Same skips as store_int2 (kernels.py:168-169 and the buffer bound).
+    if (!live || slot < 0) return;
+    const int64_t page = slot / a.L.bp;
+    const int64_t within = slot - page * a.L.bp;
+    const int64_t base = page * a.L.page_bytes + (within * a.L.kv_heads + head) * a.L.slot_bytes;
+    if (base + 2 * a.L.vector_bytes > p.history_bytes) return;
+    const uint2 raw = *reinterpret_cast<const uint2*>(tile_lds + rr * kHeadDim + lane * 4);
+    const float x[4] = {bf16_to_float(raw.x & 0xffffu), bf16_to_float(raw.x >> 16),
+                        bf16_to_float(raw.y & 0xffffu), bf16_to_float(raw.y >> 16)};
+    quantize_store(x, p.mode, is_v ? p.v_ratio : p.k_ratio, is_v ? p.v_factor : p.k_factor,
+                   p.history + base + is_v * a.L.vector_bytes);
     return;
   }
   // q tile: rotated rows straight to qrot.
@@ -134,15 +134,21 @@ __global__ __launch_bounds__(kThreads) void pre_attention_kernel(const PreArgs p
   rotate_rows16(a.query, a.qs0, a.qs1, p.hq_div, a.hq, p.q_rows, tile, p.rk_t, nullptr, p.qrot);
 }
 
-// Four (token, query head) rows per workgroup, one wavefront per row for the split merge;
-// then the window store of requests blockIdx.x, + gridDim.x, ... (after both branches).
+// Workgroups [0, merge_wgs): R (token, query head) rows each (R = 4: one wavefront per row for
+// the split merge; R = 1 above 16 splits: the four wavefronts merge the row together). The
+// remaining workgroups store the window of one request each; both branches have read the
+// window before this launch, and the merges do not touch it.
+template <int R>
 __global__ __launch_bounds__(kThreads) void post_attention_kernel(const PostArgs p) {
-  __shared__ __attribute__((aligned(16))) uint16_t s_h[4][kHeadDim];  // merged history rows
-  __shared__ float s_l[4];
-  post_rows<4>(p, static_cast<int64_t>(blockIdx.x) * 4, p.rows, s_h, s_l);
-  for (int64_t req = blockIdx.x; req < p.win_requests; req += gridDim.x)
-    for (int head = 0; head < p.win.L.kv_heads; ++head)
-      store_window_request(p.win, static_cast<int>(req), head);
+  __shared__ __attribute__((aligned(16))) uint16_t s_h[R][kHeadDim];  // merged history rows
+  __shared__ float s_l[R];
+  __shared__ GroupMergeLds group_lds;
+  if (static_cast<int>(blockIdx.x) < p.merge_wgs) {
+    post_rows<R>(p, static_cast<int64_t>(blockIdx.x) * R, p.rows, s_h, s_l, &group_lds);
+    return;
+  }
+  const int req = static_cast<int>(blockIdx.x) - p.merge_wgs;
+  for (int head = 0; head < p.win.L.kv_heads; ++head) store_window_request(p.win, req, head);
 }
 
 }  // namespace
@@ -231,7 +237,7 @@ extern "C" int oscar_pre_attention(
   p.h_div = make_fastdiv(static_cast<uint32_t>(h));
   p.hq_div = make_fastdiv(static_cast<uint32_t>(hq));
   p.raw_wgs = static_cast<int32_t>(programs * h);
-  p.kv_wgs = static_cast<int32_t>(2 * ((p.kv_rows + 15) / 16));
+  p.kv_wgs = static_cast<int32_t>(2 * 4 * ((p.kv_rows + 15) / 16));
   const int64_t q_wgs = (p.q_rows + 15) / 16;
   const dim3 grid(static_cast<unsigned>(p.raw_wgs + p.kv_wgs + q_wgs));
   hipStream_t s = as_stream(stream);
@@ -292,7 +298,14 @@ extern "C" int oscar_post_attention(
   w.table_stride = table_stride;
   w.counts = counts;
   p.win_requests = n < max_reqs ? n : max_reqs;
-  const dim3 grid(static_cast<unsigned>((p.rows + 3) / 4));
-  hipLaunchKernelGGL(post_attention_kernel, grid, dim3(kThreads), 0, as_stream(stream), p);
+  const bool group = splits > kWaveMergeSplits;
+  const int64_t merge_wgs = group ? p.rows : (p.rows + 3) / 4;
+  if (merge_wgs + p.win_requests > 0x7fffffffll) return OSCAR_E_SHAPE;
+  p.merge_wgs = static_cast<int32_t>(merge_wgs);
+  const dim3 grid(static_cast<unsigned>(merge_wgs + p.win_requests));
+  if (group)
+    hipLaunchKernelGGL(post_attention_kernel<1>, grid, dim3(kThreads), 0, as_stream(stream), p);
+  else
+    hipLaunchKernelGGL(post_attention_kernel<4>, grid, dim3(kThreads), 0, as_stream(stream), p);
   return static_cast<int>(hipGetLastError());
 }

@@ -123,12 +123,15 @@ def test_inactive_programs_write_nothing_and_empty_history_is_zero(raw, active):
         assert partials[..., 1, :].eq(0).all()
 
 
-def test_merges_match_oracle_with_empty_splits_and_padded_rows():
+@pytest.mark.parametrize("splits", [5, 16, 40, 130])
+def test_merges_match_oracle_with_empty_splits_and_padded_rows(splits):
+    # Above 16 splits a row is merged by a whole workgroup (four wavefront ranges of splits).
     g = torch.Generator().manual_seed(5)
-    n, hq, splits = 7, 6, 5
+    n, hq = 7, 6
     partials = torch.randn(n, hq, splits, 256, generator=g)
     lse = torch.randn(n, hq, splits, generator=g) * 3
     lse[0, :, 2] = -float("inf")
+    lse[2, :, splits // 2:] = -float("inf")  # the upper wavefront ranges see only empty splits
     lse[1] = -float("inf")
     partials[1] = float("nan")  # never read: every split of this row has zero weight
     counts = torch.tensor([3, 5], dtype=torch.int32)
