@@ -196,6 +196,42 @@ __device__ __forceinline__ const uint16_t* raw_token(const AttnArgs& a, const Ta
   return a.window + off;
 }
 
+// K rows of the block's two 16-token score tiles (A operands) and V rows of this lane's eight
+// tokens (B operands of P*V), with the positions that mask them.
+struct RawBlock {
+  u32x4 kd[2][8];
+  u32x4 vd[8][2];
+  int pos[8];
+  bool live[8];
+};
+
+__device__ __forceinline__ void raw_load_block(const AttnArgs& a, const Task& t, const RawTask& r,
+                                               int head, int t0, int end, int g, int n,
+                                               RawBlock& b) {
+  const uint16_t* kp[2];
+  int kpos;
+#pragma unroll
+  for (int tt = 0; tt < 2; ++tt) kp[tt] = raw_token(a, t, r, head, t0 + 16 * tt + n, end, 0, kpos);
+  const uint16_t* vp[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    vp[e] = raw_token(a, t, r, head, t0 + tau(g, e), end, 1, b.pos[e]);
+    b.live[e] = vp[e] != nullptr;
+  }
+#pragma unroll
+  for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+    for (int m = 0; m < 8; ++m)
+      b.kd[tt][m] = kp[tt] ? *reinterpret_cast<const u32x4*>(kp[tt] + 64 * g + 8 * m)
+                           : u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    b.vd[e][0] = vp[e] ? *reinterpret_cast<const u32x4*>(vp[e] + 16 * n) : u32x4{0u, 0u, 0u, 0u};
+    b.vd[e][1] = vp[e] ? *reinterpret_cast<const u32x4*>(vp[e] + 16 * n + 8)
+                       : u32x4{0u, 0u, 0u, 0u};
+  }
+}
+
 // One workgroup of the BF16 branch: (task, kv head, split).
 // `smem`: finish_lds_bytes<RT>() bytes of 16-byte aligned LDS.
 template <int RT>
@@ -238,31 +274,18 @@ __device__ __forceinline__ void raw_block(const AttnArgs& a, int task, int head,
   State<RT> st;
   state_init(st);
 
-  for (int t0 = begin + kBlock * wave; t0 < end; t0 += 4 * kBlock) {
-    // Every K and V row of the block is requested before the first MFMA, so the block costs
-    // one memory round trip.
-    const uint16_t* kp[2];
-    int kpos;
-#pragma unroll
-    for (int tt = 0; tt < 2; ++tt) kp[tt] = raw_token(a, t, r, head, t0 + 16 * tt + n, end, 0, kpos);
-    const uint16_t* vp[8];
-    int pos[8];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) vp[e] = raw_token(a, t, r, head, t0 + tau(g, e), end, 1, pos[e]);
-    u32x4 kd[2][8];
-#pragma unroll
-    for (int tt = 0; tt < 2; ++tt)
-#pragma unroll
-      for (int m = 0; m < 8; ++m)
-        kd[tt][m] = kp[tt] ? *reinterpret_cast<const u32x4*>(kp[tt] + 64 * g + 8 * m)
-                           : u32x4{0u, 0u, 0u, 0u};
-    u32x4 vd[8][2];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      vd[e][0] = vp[e] ? *reinterpret_cast<const u32x4*>(vp[e] + 16 * n) : u32x4{0u, 0u, 0u, 0u};
-      vd[e][1] = vp[e] ? *reinterpret_cast<const u32x4*>(vp[e] + 16 * n + 8)
-                       : u32x4{0u, 0u, 0u, 0u};
-    }
+  // A wavefront's blocks are t0 = begin + 32 w, + 128, ...; the K/V rows of the next block
+  // are requested before the current block is computed, so a wavefront with two blocks (a
+  // decode step's 133 BF16 tokens over four wavefronts) still waits one memory round trip.
+  // (Two row tiles (RT = 2) leave no registers for the second block: loaded in turn.)
+  constexpr bool kPrefetch = RT == 1;
+  RawBlock cur, nxt;
+  int t0 = begin + kBlock * wave;
+  if (kPrefetch && t0 < end) raw_load_block(a, t, r, head, t0, end, g, n, cur);
+  for (; t0 < end; t0 += 4 * kBlock) {
+    const bool more = kPrefetch && t0 + 4 * kBlock < end;
+    if (more) raw_load_block(a, t, r, head, t0 + 4 * kBlock, end, g, n, nxt);
+    if (!kPrefetch) raw_load_block(a, t, r, head, t0, end, g, n, cur);
     f32x4 sc[RT][2];
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt)
@@ -273,13 +296,14 @@ __device__ __forceinline__ void raw_block(const AttnArgs& a, int task, int head,
 #pragma unroll
       for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
-        for (int rt = 0; rt < RT; ++rt) sc[rt][tt] = mfma16x16x32(kd[tt][m], qb[rt][m], sc[rt][tt]);
+        for (int rt = 0; rt < RT; ++rt)
+          sc[rt][tt] = mfma16x16x32(cur.kd[tt][m], qb[rt][m], sc[rt][tt]);
     float s2[RT][8];
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        const bool ok = vp[e] != nullptr && pos[e] <= t.prefix + qi_row[rt];
+        const bool ok = cur.live[e] && cur.pos[e] <= t.prefix + qi_row[rt];
         s2[rt][e] = ok ? sc[rt][e >> 2][e & 3] * a.scale_log2 : -INFINITY;
       }
     update_max<RT, 16>(st, s2, g);
@@ -301,11 +325,12 @@ __device__ __forceinline__ void raw_block(const AttnArgs& a, int task, int head,
       u32x4 bv;
 #pragma unroll
       for (int f = 0; f < 4; ++f)
-        bv[f] = __builtin_amdgcn_perm(vd[2 * f + 1][tile >> 3][(tile & 7) >> 1],
-                                      vd[2 * f][tile >> 3][(tile & 7) >> 1], sel);
+        bv[f] = __builtin_amdgcn_perm(cur.vd[2 * f + 1][tile >> 3][(tile & 7) >> 1],
+                                      cur.vd[2 * f][tile >> 3][(tile & 7) >> 1], sel);
 #pragma unroll
       for (int rt = 0; rt < RT; ++rt) st.o[rt][tile] = mfma16x16x32(ap[rt], bv, st.o[rt][tile]);
     }
+    if (more) cur = nxt;
   }
   finish<RT>(a, t, head, split, st, smem);
 }
