@@ -207,8 +207,9 @@ int oscar_pre_attention(const void* query, int64_t q_s0, int64_t q_s1, const voi
  * (oscar_ascend/backend.py): `merge_splits(hp, hl, counts)`, `rotate(hrot, Rv.T)`,
  * `merge_paths(...)` and `store_windows(...)`, in that order of dependence, with the same
  * bits as those entry points. rv: R_v row-major bf16 [256][256]. output: bf16 [n, hq*256];
- * merged_lse (optional): fp32 [n, hq]. The window store runs after the merge has consumed
- * both branches, so it must follow the history launch of the same step on the stream.
+ * merged_lse (optional): fp32 [n, hq]. The window store runs in workgroups of its own beside
+ * the merges; both attention branches read the window in the earlier launches of the step,
+ * so this launch must follow the history launch of the same step on the stream.
  */
 int oscar_post_attention(const float* history_partials, const float* history_lse,
                          int32_t splits, const float* raw_partials, const float* raw_lse,
