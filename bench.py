@@ -161,7 +161,7 @@ def build_workload(args, cfg, device):
         slot_mapping=torch.tensor(slot_list, dtype=torch.int64, device=device),
         counts=torch.tensor([b, ntok], dtype=torch.int32, device=device),
         num_reqs=b, num_actual_tokens=ntok, max_query_len=qlen, max_num_reqs=b,
-        max_seq_len=max(seqs), layout=layout,
+        max_seq_len=max(seqs), total_seq_len=sum(seqs), layout=layout,
         tasks=torch.zeros((task_capacity(ntok, b, ocfg.queries_per_tile), 2), dtype=torch.int32,
                           device=device),
         task_count=torch.zeros(1, dtype=torch.int32, device=device),
@@ -189,6 +189,19 @@ def algorithmic_bytes(w):
     q_out = 2 * ntok * 6 * 256 * 2
     return SimpleNamespace(history_tokens=hist, int2=136 * hist, bf16=1024 * bf16,
                            q_out=q_out, table=4 * cols, total=136 * hist + 1024 * bf16 + q_out + 4 * cols)
+
+
+def split_partial_bytes(w, splits, split_tokens):
+    """Bytes the history launch writes: a 1024-byte partial row + 4-byte LSE per live split
+    of each query row; only the LSE for the split slots a request does not use."""
+    cfg = w.cfg
+    total = 0
+    for s, prefix in zip(w.seqs, w.prefixes):
+        sink = min(cfg.sink_tokens, prefix)
+        hist = max(sink, prefix - cfg.recent_tokens) - sink
+        used = splits if not split_tokens else min(splits, max(1, -(-hist // split_tokens)))
+        total += w.qlen * 6 * (used * (256 * 4 + 4) + (splits - used) * 4)
+    return total
 
 
 # ------------------------------------------------------------------ measurements
@@ -349,7 +362,7 @@ def main(argv=None):
         impls.append(impl)
     ntok = w.q.shape[0]
     outputs = [torch.empty(ntok, 6 * 256, dtype=torch.bfloat16, device=device) for _ in layers]
-    splits = impls[0].splits_for(w.meta)
+    splits, split_tokens = impls[0].partition_for(w.meta)
 
     def step(i):
         impls[i].forward(None, w.q, w.k, w.v, layers[i], w.meta, outputs[i])
@@ -360,11 +373,12 @@ def main(argv=None):
         for i in range(args.warmup + args.steps):
             h, win = views[i % len(layers)]
             kernels.attention_partials(qrot, w.k, w.v, h, win, w.meta, w.layout, 1 / 16, splits,
-                                       False)
+                                       False, split_tokens=split_tokens)
         torch.cuda.synchronize()
         alg = algorithmic_bytes(w)
         print(json.dumps({"mode": "history", "launches": args.warmup + args.steps,
-                          "splits": splits, "history_tokens": alg.history_tokens,
+                          "splits": splits, "split_tokens": split_tokens,
+                          "history_tokens": alg.history_tokens,
                           "int2_bytes": alg.int2, "physical_record_bytes": 160 * alg.history_tokens}))
         return 0
 
@@ -419,7 +433,7 @@ def main(argv=None):
     hist_views = [w.layout.tensor_views(c) for c in layers]
     for i in range(len(layers)):
         kernels.attention_partials(qrot, w.k, w.v, hist_views[i][0], hist_views[i][1], w.meta,
-                                   w.layout, 1 / 16, splits, False)
+                                   w.layout, 1 / 16, splits, False, split_tokens=split_tokens)
     torch.cuda.synchronize()
     evs = []
     for i in range(args.steps):
@@ -427,13 +441,13 @@ def main(argv=None):
         h, win = hist_views[i % len(layers)]
         a.record()
         kernels.attention_partials(qrot, w.k, w.v, h, win, w.meta, w.layout, 1 / 16, splits,
-                                   False)
+                                   False, split_tokens=split_tokens)
         b.record()
         evs.append((a, b))
     torch.cuda.synchronize()
     hist_us = statistics.mean(a.elapsed_time(b) for a, b in evs) * 1e3
     alg = algorithmic_bytes(w)
-    partial_bytes = ntok * 6 * splits * (256 * 4 + 4)
+    partial_bytes = split_partial_bytes(w, splits, split_tokens)
     hist_alg = alg.int2 + ntok * 6 * 256 * 2 + alg.table + partial_bytes
     print(f"[bench] step {us_step:.1f} us, history kernel {hist_us:.1f} us", file=sys.stderr,
           flush=True)
@@ -459,7 +473,7 @@ def main(argv=None):
             "query_tokens_per_request": w.qlen,
             "q_heads": 6, "kv_heads": 1, "head_dim": 256,
             "page_tokens": 768, "kernel_block_tokens": 128,
-            "splits": splits, "layers_cycled": len(layers),
+            "splits": splits, "split_tokens": split_tokens, "layers_cycled": len(layers),
             "hip_graph": graphs is not None, "seed": args.seed,
         },
         "us_per_layer_step": us_step,

@@ -117,6 +117,11 @@ int oscar_prepare_tasks(const int32_t* qstarts, const int32_t* counts, int32_t* 
  * partials: fp32 [n, hq, splits, 256]; lse: fp32 [n, hq, splits] (natural log).
  * Live rows of an empty split get 0 / -inf; rows of inactive programs are not written.
  * Split boundaries follow kernels.py:368-370 with block_n tokens per tile.
+ * split_tokens (history branch only; 0 = the reference rule above): a request with L history
+ * tokens uses min(splits, max(1, ceil(L / split_tokens))) splits, its ranges following the
+ * same rule with that count; the split slots above it get lse -inf and no partial row (no
+ * reference counterpart: for ragged batches, whose long requests would otherwise hold the
+ * whole launch). raw != 0 requires split_tokens == 0.
  * max_query_len: host upper bound on query tokens per request (0 = unknown). Only
  * min(query_tile, max_query_len) * (hq / H) rows per task are computed, so a decode step
  * (max_query_len 1) does not pay for the query_tile padding; it must not undercount.
@@ -131,8 +136,8 @@ int oscar_attention_partials(const void* query, int64_t q_s0, int64_t q_s1, int6
                              const int32_t* tasks, const int32_t* task_count, int64_t n,
                              int64_t hq, int64_t programs, int32_t splits, int32_t block_n,
                              int32_t query_tile, int32_t max_query_len, float scale, int32_t raw,
-                             const oscar_layout* layout, float* partials, float* lse,
-                             void* stream);
+                             int32_t split_tokens, const oscar_layout* layout, float* partials,
+                             float* lse, void* stream);
 
 /*
  * merge_splits -- replaces kernels.py:506-511 `merge_splits(partials, lse, counts)`.

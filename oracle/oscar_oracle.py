@@ -457,13 +457,17 @@ def _row_softmax(scores: np.ndarray, values: np.ndarray):
 
 def attention_partials(q_bits, k_bits, v_bits, history, window, qstarts, seq_lens, table,
                        counts, tasks, task_count, geometry: Geometry, scale, splits, raw,
-                       block_n=32, query_tile=4, programs=None):
+                       block_n=32, query_tile=4, programs=None, split_tokens=0):
     """Split-exact partials and LSE of one attention branch (kernels.py:290-482).
 
     History (raw=False): INT2 positions [min(S, prefix), max(sink_len, prefix - R)) through the
     block table, dequantized to bf16 (``load_vec``) and dotted with the (rotated) query.
     Raw (raw=True): BF16 sink + recent window positions plus the causal current tokens.
     Rows not written by a live task stay NaN. Split ranges follow kernels.py:368-370.
+    ``split_tokens`` > 0 (history only; this build's token-bounded rule, no reference
+    counterpart): a request of ``length`` history tokens uses
+    ``min(splits, max(1, ceil(length / split_tokens)))`` splits with the same range rule; the
+    split slots above that get LSE -inf and keep NaN partials (never written).
     """
     n, hq, d = q_bits.shape
     h = geometry.kv_heads
@@ -496,7 +500,10 @@ def attention_partials(q_bits, k_bits, v_bits, history, window, qstarts, seq_len
         else:
             lo = sink_len
             length = recent_begin - lo
-        tps = -(-(-(-length // block_n)) // splits)
+        nsplit = splits
+        if split_tokens and not raw:
+            nsplit = min(splits, max(1, -(-max(length, 0) // split_tokens)))
+        tps = -(-(-(-length // block_n)) // nsplit)
         for head in range(h):
             # Gather this task's keys/values once, in position order.
             keys, values, positions = [], [], []
@@ -539,6 +546,9 @@ def attention_partials(q_bits, k_bits, v_bits, history, window, qstarts, seq_len
                 qhead = head * g + row % g
                 token = qstart + qi
                 for split in range(splits):
+                    if split >= nsplit:
+                        lse[token, qhead, split] = -np.inf
+                        continue
                     begin = split * tps * block_n
                     end = min((split + 1) * tps * block_n, length)
                     sel = slice(begin, max(begin, end))

@@ -13,7 +13,7 @@ from __future__ import annotations
 import torch
 
 from . import kernels
-from .config import OscarConfig, choose_splits, choose_splits_mi355x
+from .config import OscarConfig, choose_history_partition, choose_splits
 
 
 class OscarAttentionImpl:
@@ -54,12 +54,19 @@ class OscarAttentionImpl:
         self.rv_cols = self.rv_t.T
 
     def splits_for(self, meta):
+        return self.partition_for(meta)[0]
+
+    def partition_for(self, meta):
+        """``(splits, split_tokens)`` of the history branch. "reference": config.py:84-89
+        with the reference split rule; "mi355x": ``choose_history_partition`` (reads the
+        host-side ``meta.max_seq_len`` and, when present, ``meta.total_seq_len``)."""
         if self.split_policy == "reference":
-            return choose_splits(meta.num_reqs, self.num_kv_heads, meta.max_query_len)
+            return choose_splits(meta.num_reqs, self.num_kv_heads, meta.max_query_len), 0
         tasks = -(-meta.num_actual_tokens // self.cfg.queries_per_tile) if meta.max_query_len > 1 \
             else meta.num_reqs
-        return choose_splits_mi355x(tasks, self.num_kv_heads, meta.max_query_len,
-                                    getattr(meta, "max_seq_len", None))
+        return choose_history_partition(tasks, self.num_kv_heads, meta.max_query_len,
+                                        getattr(meta, "max_seq_len", None),
+                                        getattr(meta, "total_seq_len", None))
 
     def forward(self, layer, query, key, value, kv_cache, attn_metadata, output=None):
         """Reference: backend.py:125-227 (minus the Ascend prefill call).
@@ -94,14 +101,15 @@ class OscarAttentionImpl:
         if n == 0:
             return output
 
-        splits = self.splits_for(meta)
+        splits, split_tokens = self.partition_for(meta)
         if self.fused:
             # Three launches: BF16 branch + rotations + INT2 store, history, merges + window.
             qrot, rp, rl = kernels.pre_attention(query, key, value, self.history, self.window,
                                                  meta, meta.layout, self.scale, self.rk_t,
                                                  self.rv_t)
             hp, hl = kernels.attention_partials(qrot, key, value, self.history, self.window, meta,
-                                                meta.layout, self.scale, splits, raw=False)
+                                                meta.layout, self.scale, splits, raw=False,
+                                                split_tokens=split_tokens)
             kernels.post_attention(hp, hl, rp, rl, self.rv, key, value, self.window, meta,
                                    meta.layout, output.view(n, -1), getattr(meta, "merged_lse", None))
             return output
@@ -111,7 +119,8 @@ class OscarAttentionImpl:
         kernels.store_int2(krot, vrot, self.history, meta.slot_mapping, meta.counts, meta.layout)
         qrot = kernels.rotate(query, self.rk_cols)
         hp, hl = kernels.attention_partials(qrot, key, value, self.history, self.window, meta,
-                                            meta.layout, self.scale, splits, raw=False)
+                                            meta.layout, self.scale, splits, raw=False,
+                                            split_tokens=split_tokens)
         hrot, hlogsum = kernels.merge_splits(hp, hl, meta.counts)
         hout = kernels.rotate(hrot, self.rv.T)
         rp, rl = kernels.attention_partials(query, key, value, self.history, self.window, meta,

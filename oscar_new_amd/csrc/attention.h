@@ -37,6 +37,7 @@ struct AttnArgs {
   int64_t n;
   Layout L;
   int32_t g, hq, qt, splits, block_n;
+  int32_t split_tokens;  // history branch: 0 = kernels.py:368-370 rule, else token-bounded
   FastDiv g_div;  // division by g (query heads per kv head)
   float scale_log2;
 };
@@ -73,6 +74,16 @@ __device__ __forceinline__ void split_range(int length, int block_n, int splits,
   end = min((split + 1) * per * block_n, length);
 }
 
+// Splits a request's history uses. The reference rule (split_tokens 0) gives every request
+// all `splits`; the token-bounded rule gives a request of `length` history tokens
+// min(splits, max(1, ceil(length / split_tokens))) of them, so that a ragged batch splits
+// its long requests finely and its short ones not at all. The ranges inside that count
+// follow split_range either way.
+__device__ __forceinline__ int history_splits(const AttnArgs& a, int length) {
+  if (a.split_tokens <= 0) return a.splits;
+  return min(a.splits, max(1, cdiv(max(length, 0), a.split_tokens)));
+}
+
 struct RowInfo {
   bool valid;
   int qi, qhead;
@@ -88,6 +99,16 @@ __device__ __forceinline__ RowInfo row_info(const AttnArgs& a, const Task& t, in
   r.valid = row < a.qt * a.g && r.qi < t.qlen && r.token >= 0 && r.token < a.n;
   r.qhead = head * a.g + (row - qrow * a.g);
   return r;
+}
+
+// A split slot beyond the request's history_splits: only its LSE is written (-inf), which
+// the split merges skip without reading the partial row.
+__device__ __forceinline__ void write_unused_split(const AttnArgs& a, const Task& t, int head,
+                                                   int split) {
+  for (int row = threadIdx.x; row < a.qt * a.g; row += kThreads) {
+    const RowInfo ri = row_info(a, t, head, row);
+    if (ri.valid) a.lse[(ri.token * a.hq + ri.qhead) * a.splits + split] = -INFINITY;
+  }
 }
 
 // INT2 history branch (history.hip); rows = query rows per task (<= 32).

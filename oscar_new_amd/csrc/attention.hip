@@ -31,15 +31,18 @@ extern "C" int oscar_attention_partials(
     int64_t table_stride, int64_t table_columns, const int32_t* counts, const int32_t* tasks,
     const int32_t* task_count, int64_t n, int64_t hq, int64_t programs, int32_t splits,
     int32_t block_n, int32_t query_tile, int32_t max_query_len, float scale, int32_t raw,
-    const oscar_layout* layout, float* partials, float* lse, void* stream) {
+    int32_t split_tokens, const oscar_layout* layout, float* partials, float* lse,
+    void* stream) {
   using namespace oscar;
   AttnArgs a{};
   const int st = make_layout(layout, &a.L);
   if (st != OSCAR_OK) return st;
   const int64_t h = a.L.kv_heads;
   if (n < 0 || hq <= 0 || hq % h || programs < 1 || splits < 1 || splits > 65535 ||
-      block_n < 1 || query_tile < 1 || table_columns < 0 || programs > (1ll << 31) - 1)
+      block_n < 1 || query_tile < 1 || table_columns < 0 || programs > (1ll << 31) - 1 ||
+      split_tokens < 0)
     return OSCAR_E_SHAPE;
+  if (raw && split_tokens) return OSCAR_E_UNSUPPORTED;  // the BF16 branch keeps one rule
   const int64_t g = hq / h;
   const int64_t qrows = (max_query_len > 0 && max_query_len < query_tile ? max_query_len
                                                                          : query_tile) * g;
@@ -95,6 +98,7 @@ extern "C" int oscar_attention_partials(
   a.qt = query_tile;
   a.splits = splits;
   a.block_n = block_n;
+  a.split_tokens = split_tokens;
   a.scale_log2 = scale * kLog2e;
   const dim3 grid(static_cast<unsigned>(programs), static_cast<unsigned>(h),
                   static_cast<unsigned>(splits));

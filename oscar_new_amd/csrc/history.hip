@@ -185,8 +185,14 @@ __global__ __launch_bounds__(kThreads, 3 - RT) void history_kernel(const AttnArg
   Task t;
   if (!read_task(a, t, blockIdx.x)) return;
   const int head = blockIdx.y, split = blockIdx.z;
+  const int length = t.recent_begin - t.sink_len;
+  const int nsplit = history_splits(a, length);
+  if (split >= nsplit) {
+    write_unused_split(a, t, head, split);
+    return;
+  }
   int begin, end;
-  split_range(t.recent_begin - t.sink_len, a.block_n, a.splits, split, begin, end);
+  split_range(length, a.block_n, nsplit, split, begin, end);
   const int p_lo = max(t.sink_len + begin, 0), p_hi = t.sink_len + end;
   const int lane = threadIdx.x & 63;
   const int wave = uniform(threadIdx.x >> 6);
@@ -613,8 +619,14 @@ __global__ __launch_bounds__(kThreads, 2) void history_pair_kernel(const AttnArg
   Task t;
   if (!read_task(a, t, blockIdx.x)) return;
   const int head = blockIdx.y, split = blockIdx.z;
+  const int length = t.recent_begin - t.sink_len;
+  const int nsplit = history_splits(a, length);
+  if (split >= nsplit) {
+    write_unused_split(a, t, head, split);
+    return;
+  }
   int begin, end;
-  split_range(t.recent_begin - t.sink_len, a.block_n, a.splits, split, begin, end);
+  split_range(length, a.block_n, nsplit, split, begin, end);
   const int p_lo = max(t.sink_len + begin, 0), p_hi = t.sink_len + end;
   const int lane = threadIdx.x & 63;
   const int wave = uniform(threadIdx.x >> 6);

@@ -72,36 +72,43 @@ __device__ __forceinline__ SplitMerge merge_splits_row(const float* part, const 
   return r;
 }
 
-// Splits above this count are merged by the four wavefronts of a workgroup.
+// Above 16 splits a row's split slots may be partly unwritten (token-bounded splits give a
+// request fewer splits than the launch; kernels write LSE -inf and no partial row there).
+// A first pass over the row's LSEs (one per lane, 64 at a time) gives the row max and `end`,
+// one past the last finite LSE: every slot below `end` holds a partial row, so the second
+// round reads only those.
 constexpr int kWaveMergeSplits = 16;
 
-struct GroupMergeLds {
-  float acc[4][kHeadDim];
-  float den[4];
+struct LseScan {
+  float mx;
+  int end;
 };
+__device__ __forceinline__ LseScan scan_lse(const float* ls, int splits, bool valid) {
+  const int lane = threadIdx.x & 63;
+  float mx = -INFINITY, last = -1.f;
+  for (int s = lane; s < splits; s += kWave) {
+    const float l = ls[s];
+    mx = fmaxf(mx, l);
+    last = l != -INFINITY ? static_cast<float>(s) : last;  // exact below 2^24
+  }
+  LseScan r;
+  r.mx = valid ? wave_max_dpp(mx) : -INFINITY;
+  r.end = valid ? static_cast<int>(wave_max_dpp(last)) + 1 : 0;
+  return r;
+}
 
-// More than 16 splits: wavefront w accumulates splits [w q, (w + 1) q), q = ceil(splits / 4),
-// 16 per round with the next round's loads in flight, against the row max over every split;
-// the four partial sums are then added in wavefront order through LDS. Every wavefront of the
-// workgroup calls this for the same row and receives the same result.
-__device__ __forceinline__ SplitMerge merge_splits_row_group(const float* part, const float* ls,
-                                                             int splits, bool valid,
-                                                             GroupMergeLds* lds) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  SplitMerge r = empty_merge();
-  for (int s = lane; s < splits; s += kWave) r.mx = fmaxf(r.mx, ls[s]);
-  r.mx = valid ? wave_max_dpp(r.mx) : -INFINITY;
+// Splits [s_begin, s_end) of a row by one wavefront into r (r.mx set), 16 per round with
+// the next round's loads in flight, in split order.
+__device__ __forceinline__ void merge_range(SplitMerge& r, const float* p, const float* ls,
+                                            int s_begin, int s_end) {
   const float safe = r.mx == -INFINITY ? 0.f : r.mx;
-  const int q = (splits + 3) >> 2;
-  const int s_begin = min(wave * q, splits), s_end = min(s_begin + q, splits);
-  const float* p = part + lane * 4;
   float l[16];
   float4 v[16];
-  load_group(p, ls, s_begin, s_end, valid, l, v);
+  load_group(p, ls, s_begin, s_end, true, l, v);
   for (int s0 = s_begin; s0 < s_end; s0 += 16) {
     float ln[16];
     float4 vn[16];
-    load_group(p, ls, s0 + 16, s_end, valid, ln, vn);  // empty past the wavefront's range
+    load_group(p, ls, s0 + 16, s_end, true, ln, vn);  // empty past the range
     merge_group(r, l, v, safe);
 #pragma unroll
     for (int k = 0; k < 16; ++k) {
@@ -109,6 +116,37 @@ __device__ __forceinline__ SplitMerge merge_splits_row_group(const float* part, 
       v[k] = vn[k];
     }
   }
+}
+
+// More than 16 splits, one wavefront per row (batches with many rows).
+__device__ __forceinline__ SplitMerge merge_splits_row_scan(const float* part, const float* ls,
+                                                            int splits, bool valid, int lane) {
+  SplitMerge r = empty_merge();
+  const LseScan sc = scan_lse(ls, splits, valid);
+  r.mx = sc.mx;
+  merge_range(r, part + lane * 4, ls, 0, sc.end);
+  return r;
+}
+
+struct GroupMergeLds {
+  float acc[4][kHeadDim];
+  float den[4];
+};
+
+// More than 16 splits, one workgroup per row (batches with few rows): wavefront w merges
+// splits [w q, (w + 1) q) below `end`, q = ceil(splits / 4), and the four partial sums are
+// added in wavefront order through LDS. Every wavefront of the workgroup calls this for the
+// same row and receives the same result.
+__device__ __forceinline__ SplitMerge merge_splits_row_group(const float* part, const float* ls,
+                                                             int splits, bool valid,
+                                                             GroupMergeLds* lds) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  SplitMerge r = empty_merge();
+  const LseScan sc = scan_lse(ls, splits, valid);
+  r.mx = sc.mx;
+  const int q = (splits + 3) >> 2;
+  const int s_begin = min(wave * q, sc.end), s_end = min(s_begin + q, sc.end);
+  merge_range(r, part + lane * 4, ls, s_begin, s_end);
 #pragma unroll
   for (int i = 0; i < 4; ++i) lds->acc[wave][lane * 4 + i] = r.acc[i];
   if (lane == 0) lds->den[wave] = r.den;
@@ -120,6 +158,16 @@ __device__ __forceinline__ SplitMerge merge_splits_row_group(const float* part, 
   r.den = ((lds->den[0] + lds->den[1]) + lds->den[2]) + lds->den[3];
   __syncthreads();  // the area may be reused by the caller
   return r;
+}
+
+// How a launch merges its rows: one round per wavefront-row (<= 16 splits), a scanned
+// wavefront-row (more splits, at least 256 rows: four rows share a workgroup), or a
+// scanned workgroup-row (more splits, fewer rows). The split merge entry point and the
+// post-attention launch use the same rule, so both produce the same bits.
+enum MergeMode { kMergeOneRound = 0, kMergeScanWave = 1, kMergeScanGroup = 2 };
+__host__ __device__ inline int merge_mode(int64_t rows, int splits) {
+  if (splits <= kWaveMergeSplits) return kMergeOneRound;
+  return rows >= 256 ? kMergeScanWave : kMergeScanGroup;
 }
 
 // The merged row as bf16 (two packed words) and its natural-log LSE.

@@ -1,7 +1,8 @@
 // merge_splits / merge_paths: LSE-weighted combination of attention partials.
 //
 // Reference: oscar_ascend/kernels.py:485-541. One wavefront per (token, query head) row (one
-// workgroup per row above 16 splits); lane l owns dims 4l..4l+3. Every row is written, padded rows (token >= counts[1]) too,
+// workgroup per row above 16 splits when rows are few, merge.h merge_mode); lane l owns dims
+// 4l..4l+3. Every row is written, padded rows (token >= counts[1]) too,
 // because the inverse rotation that follows reads them.
 #include "merge.h"
 
@@ -18,19 +19,23 @@ struct MergeSplitsArgs {
   float* logsum;
 };
 
-// Up to 16 splits: one wavefront per row, four rows per workgroup.
+// One wavefront per row, four rows per workgroup (kMergeOneRound, kMergeScanWave).
+template <int kMode>
 __global__ __launch_bounds__(kThreads) void merge_splits_kernel(const MergeSplitsArgs a) {
   const int lane = threadIdx.x & 63;
   const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
   if (row >= a.rows) return;
   const bool valid = row / a.hq < a.counts[1];
-  const SplitMerge r = merge_splits_row(a.partials + row * a.splits * kHeadDim,
-                                        a.lse + row * a.splits, a.splits, valid, lane);
+  const float* part = a.partials + row * a.splits * kHeadDim;
+  const float* ls = a.lse + row * a.splits;
+  const SplitMerge r = kMode == kMergeOneRound
+                           ? merge_splits_row(part, ls, a.splits, valid, lane)
+                           : merge_splits_row_scan(part, ls, a.splits, valid, lane);
   *reinterpret_cast<uint2*>(a.out + row * kHeadDim + lane * 4) = merge_splits_out(r);
   if (lane == 0) a.logsum[row] = merge_splits_lse(r);
 }
 
-// More splits: one workgroup per row.
+// One workgroup per row (kMergeScanGroup).
 __global__ __launch_bounds__(kThreads) void merge_splits_group_kernel(const MergeSplitsArgs a) {
   __shared__ GroupMergeLds lds;
   const int lane = threadIdx.x & 63;
@@ -97,12 +102,20 @@ extern "C" int oscar_merge_splits(const float* partials, const float* lse, const
     return OSCAR_E_ALIGN;
   MergeSplitsArgs a{partials, lse, counts, n * hq, static_cast<int32_t>(hq), splits,
                     static_cast<uint16_t*>(out), logsum};
-  if (splits <= kWaveMergeSplits)
-    hipLaunchKernelGGL(merge_splits_kernel, dim3(static_cast<unsigned>((a.rows + 3) / 4)),
-                       dim3(kThreads), 0, as_stream(stream), a);
-  else
-    hipLaunchKernelGGL(merge_splits_group_kernel, dim3(static_cast<unsigned>(a.rows)),
-                       dim3(kThreads), 0, as_stream(stream), a);
+  const dim3 four_rows(static_cast<unsigned>((a.rows + 3) / 4));
+  switch (merge_mode(a.rows, splits)) {
+    case kMergeOneRound:
+      hipLaunchKernelGGL(merge_splits_kernel<kMergeOneRound>, four_rows, dim3(kThreads), 0,
+                         as_stream(stream), a);
+      break;
+    case kMergeScanWave:
+      hipLaunchKernelGGL(merge_splits_kernel<kMergeScanWave>, four_rows, dim3(kThreads), 0,
+                         as_stream(stream), a);
+      break;
+    default:
+      hipLaunchKernelGGL(merge_splits_group_kernel, dim3(static_cast<unsigned>(a.rows)),
+                         dim3(kThreads), 0, as_stream(stream), a);
+  }
   return static_cast<int>(hipGetLastError());
 }
 

@@ -31,11 +31,11 @@ struct PostArgs {
 
 // Rows [row0, min(row0 + R, row_end, p.rows)) by the four wavefronts of a workgroup:
 // wavefront w merges rows w, w + 4, ... into LDS (s_h: R x 256 bf16, s_l: R floats), or, with
-// R = 1 (more than 16 splits), all four merge the one row together; then every wavefront
-// rotates the R rows back for 64 output columns and merges them with the BF16 branch. Every
-// read that does not depend on the merge (R_v, the BF16-branch values and LSEs) is requested
+// R = 1 (kMergeScanGroup), all four merge the one row together; then every wavefront rotates
+// the R rows back for 64 output columns and merges them with the BF16 branch. Every read
+// that does not depend on the merge (R_v, the BF16-branch values and LSEs) is requested
 // before it, and none waits for the token count.
-template <int R>
+template <int R, int kMode>
 __device__ __forceinline__ void post_rows(const PostArgs& p, int64_t row0, int64_t row_end,
                                           uint16_t (*s_h)[kHeadDim], float* s_l,
                                           GroupMergeLds* group_lds) {
@@ -85,9 +85,12 @@ __device__ __forceinline__ void post_rows(const PostArgs& p, int64_t row0, int64
     for (int r = wave; r < R; r += kThreads / kWave) {
       const int64_t row = row0 + r;
       const bool in = row < row_end;
-      const SplitMerge m = merge_splits_row(p.hp + (in ? row : 0) * p.splits * kHeadDim,
-                                            p.hl + (in ? row : 0) * p.splits, p.splits,
-                                            in && row / p.hq < active, lane);
+      const float* part = p.hp + (in ? row : 0) * p.splits * kHeadDim;
+      const float* ls = p.hl + (in ? row : 0) * p.splits;
+      const bool live = in && row / p.hq < active;
+      const SplitMerge m = kMode == kMergeOneRound
+                               ? merge_splits_row(part, ls, p.splits, live, lane)
+                               : merge_splits_row_scan(part, ls, p.splits, live, lane);
       *reinterpret_cast<uint2*>(&s_h[r][lane * 4]) = merge_splits_out(m);
       if (lane == 0) s_l[r] = merge_splits_lse(m);
     }

@@ -138,13 +138,13 @@ __global__ __launch_bounds__(kThreads) void pre_attention_kernel(const PreArgs p
 // the split merge; R = 1 above 16 splits: the four wavefronts merge the row together). The
 // remaining workgroups store the window of one request each; both branches have read the
 // window before this launch, and the merges do not touch it.
-template <int R>
+template <int R, int kMode>
 __global__ __launch_bounds__(kThreads) void post_attention_kernel(const PostArgs p) {
   __shared__ __attribute__((aligned(16))) uint16_t s_h[R][kHeadDim];  // merged history rows
   __shared__ float s_l[R];
   __shared__ GroupMergeLds group_lds;
   if (static_cast<int>(blockIdx.x) < p.merge_wgs) {
-    post_rows<R>(p, static_cast<int64_t>(blockIdx.x) * R, p.rows, s_h, s_l, &group_lds);
+    post_rows<R, kMode>(p, static_cast<int64_t>(blockIdx.x) * R, p.rows, s_h, s_l, &group_lds);
     return;
   }
   const int req = static_cast<int>(blockIdx.x) - p.merge_wgs;
@@ -298,14 +298,17 @@ extern "C" int oscar_post_attention(
   w.table_stride = table_stride;
   w.counts = counts;
   p.win_requests = n < max_reqs ? n : max_reqs;
-  const bool group = splits > kWaveMergeSplits;
-  const int64_t merge_wgs = group ? p.rows : (p.rows + 3) / 4;
+  const int mode = merge_mode(p.rows, splits);
+  const int64_t merge_wgs = mode == kMergeScanGroup ? p.rows : (p.rows + 3) / 4;
   if (merge_wgs + p.win_requests > 0x7fffffffll) return OSCAR_E_SHAPE;
   p.merge_wgs = static_cast<int32_t>(merge_wgs);
   const dim3 grid(static_cast<unsigned>(merge_wgs + p.win_requests));
-  if (group)
-    hipLaunchKernelGGL(post_attention_kernel<1>, grid, dim3(kThreads), 0, as_stream(stream), p);
+  hipStream_t s = as_stream(stream);
+  if (mode == kMergeOneRound)
+    hipLaunchKernelGGL((post_attention_kernel<4, kMergeOneRound>), grid, dim3(kThreads), 0, s, p);
+  else if (mode == kMergeScanWave)
+    hipLaunchKernelGGL((post_attention_kernel<4, kMergeScanWave>), grid, dim3(kThreads), 0, s, p);
   else
-    hipLaunchKernelGGL(post_attention_kernel<4>, grid, dim3(kThreads), 0, as_stream(stream), p);
+    hipLaunchKernelGGL((post_attention_kernel<1, kMergeScanGroup>), grid, dim3(kThreads), 0, s, p);
   return static_cast<int>(hipGetLastError());
 }

@@ -169,14 +169,22 @@ def prepare_tasks(qstarts, counts, tasks, task_count, max_reqs, query_tile, num_
     )
 
 
-def attention_partials(query, key, value, history, window, meta, layout, scale, splits, raw):
+def attention_partials(query, key, value, history, window, meta, layout, scale, splits, raw,
+                       split_tokens=0):
     """Per-split partial attention and LSE of one branch (reference kernels.py:439-482).
 
     raw=False: INT2 history (``query`` must be the rotated query). raw=True: BF16 sink /
     recent window plus causal current tokens (unrotated query/key/value).
     Returns ``(partials float32 [n, hq, splits, 256], lse float32 [n, hq, splits])``.
     ``meta.max_query_len``, when present, lets decode steps skip query-tile padding rows.
+    ``split_tokens`` (history branch; no reference counterpart, 0 keeps kernels.py:368-370):
+    a request with L history tokens uses min(splits, ceil(L / split_tokens)) splits and its
+    remaining split slots get LSE -inf with no partial row, which the split merges skip.
     """
+    if raw and split_tokens:
+        raise ValueError("split_tokens applies to the history branch only")
+    if split_tokens < 0:
+        raise ValueError("split_tokens must be >= 0")
     _device_check(query, key, value, history, window)
     n, hq, d = query.shape
     cfg = layout.config
@@ -209,8 +217,8 @@ def attention_partials(query, key, value, history, window, meta, layout, scale, 
             _ptr(_int32(meta.counts, "counts")), _ptr(_int32(meta.tasks, "tasks")),
             _ptr(_int32(meta.task_count, "task_count")),
             n, hq, programs, splits, cfg.block_n, cfg.queries_per_tile, max_query_len,
-            float(scale), 1 if raw else 0, layout_struct(layout), _ptr(partials), _ptr(lse),
-            _stream(query),
+            float(scale), 1 if raw else 0, int(split_tokens), layout_struct(layout),
+            _ptr(partials), _ptr(lse), _stream(query),
         ),
         "attention_partials",
     )

@@ -9,6 +9,7 @@ from oscar_new_amd.config import (
     OscarConfig,
     attention_programs,
     choose_splits,
+    choose_history_partition,
     choose_splits_mi355x,
     percentile_selection,
     task_capacity,
@@ -119,6 +120,18 @@ def test_mi355x_split_policy_fills_the_chip():
     assert choose_splits_mi355x(64, 1, 4, 131072) == 8
     assert choose_splits_mi355x(4, 1, 1, 2048) == 2  # never below 1024 tokens per split
     assert choose_splits_mi355x(1, 1, 17) == 1
+
+
+def test_history_partition_mi355x():
+    # Uniform batches: the same splits as choose_splits_mi355x, split_tokens = the even share.
+    assert choose_history_partition(32, 1, 1, 32768, 32 * 32768) == (16, 2048)
+    assert choose_history_partition(4, 1, 1, 262144, 4 * 262144) == (128, 2048)
+    # Ragged batch: the longest request takes ceil(131072 / 2368) splits of the even share.
+    assert choose_history_partition(64, 1, 4, 131072, 1212000) == (56, 2368)
+    # Small batches keep at least 1024 tokens per split; unknown bounds fall back.
+    assert choose_history_partition(1, 1, 1, 4096, 4096) == (4, 1024)
+    assert choose_history_partition(4, 1, 1, None) == (choose_splits_mi355x(4, 1, 1), 0)
+    assert choose_history_partition(2, 1, 17, 8192, 9000) == (1, 0)
 
 
 def test_bad_config_rejected():

@@ -44,7 +44,7 @@ def _setup(lengths, prefixes, seed=42, cfg=None, max_reqs=8):
     return layout, raw, hist, window, meta, tables, rk, rv, ks, vs, qs, q, k, v
 
 
-def _oracle_partials(q, k, v, hist, window, meta, layout, splits, raw):
+def _oracle_partials(q, k, v, hist, window, meta, layout, splits, raw, split_tokens=0):
     counts = meta.counts.cpu().numpy()
     tasks = [tuple(t) for t in meta.tasks.cpu().tolist()]
     count = int(meta.task_count.item())
@@ -54,6 +54,7 @@ def _oracle_partials(q, k, v, hist, window, meta, layout, splits, raw):
         oracle_geometry(layout), 1 / 16, splits, raw, layout.config.block_n,
         layout.config.queries_per_tile,
         programs=attention_programs(q.shape[0], meta.max_num_reqs, layout.config.queries_per_tile),
+        split_tokens=split_tokens,
     )
 
 
@@ -79,6 +80,38 @@ def test_history_and_raw_partials_match_oracle(lengths, prefixes, splits):
         np.testing.assert_allclose(got_p[live], po[live], atol=1e-2, rtol=1e-2)
 
 
+@pytest.mark.parametrize("splits,split_tokens", [(16, 512), (40, 256)])
+def test_token_bounded_splits_match_oracle_and_merge_to_one_split(splits, split_tokens):
+    # Token-bounded rule: request r uses min(splits, ceil(L_r / split_tokens)) splits; the
+    # other slots get LSE -inf and no partial row. 40 splits take the workgroup merge, whose
+    # partial loads are gated on the LSE: the unused slots are filled with NaN to prove it.
+    lengths, prefixes = [300, 5000, 700], [299, 4999, 699]
+    layout, _, hist, window, meta, _, rk, rv, *_, q, k, v = _setup(lengths, prefixes)
+    kernels.prepare_tasks(meta.query_start_loc, meta.counts, meta.tasks, meta.task_count,
+                          meta.max_num_reqs, layout.config.queries_per_tile)
+    kernels.store_int2(kernels.rotate(k, rk), kernels.rotate(v, rv), hist, meta.slot_mapping,
+                       meta.counts, layout)
+    qr = kernels.rotate(q, rk)
+    p, l = kernels.attention_partials(qr, k, v, hist, window, meta, layout, 1 / 16, splits,
+                                      False, split_tokens=split_tokens)
+    po, lo = _oracle_partials(qr, k, v, hist, window, meta, layout, splits, False, split_tokens)
+    got_p, got_l = p.cpu().numpy(), l.cpu().numpy()
+    written = ~np.isnan(lo)
+    assert (np.isneginf(lo) & written).any()  # some slots are unused
+    np.testing.assert_array_equal(np.isneginf(got_l[written]), np.isneginf(lo[written]))
+    fin = written & np.isfinite(lo)
+    np.testing.assert_allclose(got_l[fin], lo[fin], atol=1e-2, rtol=0)
+    rows = ~np.isnan(po[..., 0])
+    np.testing.assert_allclose(got_p[rows], po[rows], atol=1e-2, rtol=1e-2)
+
+    p[torch.from_numpy(~rows).to(DEV)] = float("nan")
+    out, ls = kernels.merge_splits(p, l, meta.counts)
+    p1, l1 = kernels.attention_partials(qr, k, v, hist, window, meta, layout, 1 / 16, 1, False)
+    out1, ls1 = kernels.merge_splits(p1, l1, meta.counts)
+    torch.testing.assert_close(out.float(), out1.float(), atol=1e-2, rtol=1e-2)
+    torch.testing.assert_close(ls, ls1, atol=1e-4, rtol=0)
+
+
 def _abi_partials(query, meta, layout, splits, raw, hist, window, k, v, partials, lse):
     """Direct C-ABI call with caller-provided (sentinel-filled) outputs."""
     cfg = layout.config
@@ -90,7 +123,7 @@ def _abi_partials(query, meta, layout, splits, raw, hist, window, k, v, partials
         meta.block_tables.stride(0), meta.block_tables.shape[1], meta.counts.data_ptr(),
         meta.tasks.data_ptr(), meta.task_count.data_ptr(), n, hq,
         attention_programs(n, meta.max_num_reqs, cfg.queries_per_tile), splits, cfg.block_n,
-        cfg.queries_per_tile, 0, 1 / 16, int(raw), kernels.layout_struct(layout),
+        cfg.queries_per_tile, 0, 1 / 16, int(raw), 0, kernels.layout_struct(layout),
         partials.data_ptr(), lse.data_ptr(), torch.cuda.current_stream().cuda_stream)
     _ext.check(status, "attention_partials")
 
@@ -123,21 +156,24 @@ def test_inactive_programs_write_nothing_and_empty_history_is_zero(raw, active):
         assert partials[..., 1, :].eq(0).all()
 
 
-@pytest.mark.parametrize("splits", [5, 16, 40, 130])
-def test_merges_match_oracle_with_empty_splits_and_padded_rows(splits):
-    # Above 16 splits a row is merged by a whole workgroup (four wavefront ranges of splits).
+@pytest.mark.parametrize("n,splits", [(7, 5), (7, 16), (7, 40), (7, 130), (48, 40)])
+def test_merges_match_oracle_with_empty_splits_and_padded_rows(n, splits):
+    # Above 16 splits the LSEs are scanned first and only slots below the last finite one are
+    # read: by a whole workgroup per row (few rows) or one wavefront per row (>= 256 rows).
     g = torch.Generator().manual_seed(5)
-    n, hq = 7, 6
+    hq = 6
     partials = torch.randn(n, hq, splits, 256, generator=g)
     lse = torch.randn(n, hq, splits, generator=g) * 3
     lse[0, :, 2] = -float("inf")
-    lse[2, :, splits // 2:] = -float("inf")  # the upper wavefront ranges see only empty splits
+    lse[2, :, splits // 2:] = -float("inf")  # unwritten slots: never read
+    partials[2, :, splits // 2:] = float("nan")
     lse[1] = -float("inf")
     partials[1] = float("nan")  # never read: every split of this row has zero weight
     counts = torch.tensor([3, 5], dtype=torch.int32)
     out, logsum = kernels.merge_splits(partials.to(DEV), lse.to(DEV), counts.to(DEV))
     p_clean = partials.clone()
     p_clean[1] = 0
+    p_clean[2, :, splits // 2:] = 0
     want_out, want_l = O.merge_splits(p_clean.numpy(), lse.numpy(), counts.numpy())
     np.testing.assert_allclose(O.bf16_to_f32(bits(out)), O.bf16_to_f32(want_out), atol=1e-2,
                                rtol=1e-2)

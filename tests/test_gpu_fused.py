@@ -88,6 +88,46 @@ def test_fused_step_is_bitwise_the_single_launch_step(lengths, prefixes, splits)
         assert torch.equal(a, b)
 
 
+@pytest.mark.parametrize("lengths,prefixes,partition", [
+    ([6000, 1500, 300], [5999, 1499, 299], (6, 1024)),
+    ([6000, 1500, 300], [5999, 1499, 299], (40, 256)),  # workgroup-per-row merge
+    ([1700, 900], [800, 896], (40, 256)),  # 5424 rows: wavefront-per-row scanned merge
+])
+def test_token_bounded_fused_step_against_dense_reference(lengths, prefixes, partition):
+    # The MI355X split partition of a ragged batch through the fused launches (unwritten
+    # split slots above 16 splits) against the dense oracle, and bit for bit against the
+    # single-launch order with the same partition.
+    c = _case(lengths, prefixes, seed=13)
+    n = c.q.shape[0]
+    outs = []
+    for fused in (True, False):
+        raw = c.raw.clone()
+        k_cache, v_cache = _views(raw, c.layout)
+        impl = OscarAttentionImpl(6, 256, 1 / 16, 1, c.layout.config, split_policy="mi355x",
+                                  fused=fused)
+        impl.initialize_layer(c.rk, c.rv)
+        impl.partition_for = lambda meta, pt=partition: pt
+        c.meta.merged_lse = torch.empty((n, 6), device=DEV)
+        out = torch.empty((n, 6 * 256), device=DEV, dtype=torch.bfloat16)
+        impl.forward(None, c.q, c.k, c.v, (k_cache, v_cache), c.meta, out)
+        torch.cuda.synchronize()
+        outs.append((out.view(torch.int16).cpu(), c.meta.merged_lse.cpu(), raw.cpu(), out))
+    for a, b in zip(outs[0][:3], outs[1][:3]):
+        assert torch.equal(a, b)
+    want, want_lse = [], []
+    for qi, ki, vi, p in zip(c.qs, c.ks, c.vs, c.prefixes):
+        o, l = O.hybrid_reference(bits(qi), bits(ki), bits(vi), p, bits(c.rk), bits(c.rv),
+                                  c.layout.config)
+        want.append(o)
+        want_lse.append(l)
+    want = torch.from_numpy(np.concatenate(want)).reshape(n, -1)
+    got = outs[0][3].float().cpu()
+    torch.testing.assert_close(got, want, atol=0.035, rtol=0.04)
+    assert (got - want).abs().mean().item() <= 2e-3
+    torch.testing.assert_close(outs[0][1], torch.from_numpy(np.concatenate(want_lse)), atol=2e-2,
+                               rtol=0)
+
+
 def test_fused_step_replays_in_a_graph():
     # Reference tests/test_npu_kernels.py:197-245 through the fused step: a captured step
     # replayed with new queries on a reset cache matches the eager single-launch step every

@@ -367,8 +367,8 @@ def _paged_state(lengths, prefixes, geo, seed=0):
     return history, window, table, ks, vs, rk, rv
 
 
-@pytest.mark.parametrize("splits", [1, 3, 8])
-def test_history_partials_merge_to_split_invariant_result(splits):
+@pytest.mark.parametrize("splits,split_tokens", [(1, 0), (3, 0), (8, 0), (8, 64), (40, 32)])
+def test_history_partials_merge_to_split_invariant_result(splits, split_tokens):
     geo = O.Geometry(768, sink_tokens=4, recent_tokens=16, speculative_tokens=3)
     lengths, prefixes = [300, 130], [299, 128]
     history, window, table, ks, vs, rk, rv = _paged_state(lengths, prefixes, geo)
@@ -384,7 +384,19 @@ def test_history_partials_merge_to_split_invariant_result(splits):
     ref_p, ref_l = O.attention_partials(qrot, kc, vc, history, window, qstarts, lengths, table,
                                         counts, tasks, count, geo, 1 / 16, 1, False)
     p, l = O.attention_partials(qrot, kc, vc, history, window, qstarts, lengths, table, counts,
-                                tasks, count, geo, 1 / 16, splits, False)
+                                tasks, count, geo, 1 / 16, splits, False,
+                                split_tokens=split_tokens)
+    if split_tokens:
+        # Token-bounded rule: request r (history length L_r) leaves splits - min(splits,
+        # ceil(L_r / split_tokens)) slots unwritten (NaN partials, LSE -inf).
+        for r, (seq, qlen) in enumerate(zip(lengths, qlens)):
+            prefix = seq - qlen
+            sink = min(4, prefix)
+            hist_len = max(sink, prefix - 16) - sink
+            used = min(splits, max(1, -(-hist_len // split_tokens)))
+            rows = slice(int(qstarts[r]), int(qstarts[r + 1]))
+            assert np.isnan(p[rows, :, used:]).all() and np.isneginf(l[rows, :, used:]).all()
+            assert not np.isnan(p[rows, :, :used]).any()
     out1, lse1 = O.merge_splits(ref_p, ref_l, counts)
     outk, lsek = O.merge_splits(p, l, counts)
     np.testing.assert_allclose(O.bf16_to_f32(outk), O.bf16_to_f32(out1), atol=1e-2)
