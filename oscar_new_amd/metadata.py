@@ -37,6 +37,7 @@ class OscarMetadata:
     task_count: torch.Tensor | None = None
     max_seq_len: int | None = None
     merged_lse: torch.Tensor | None = None
+    total_seq_len: int | None = None  # host-side sum of seq_lens (MI355X split partition)
 
 
 class OscarMetadataBuilder:
@@ -45,7 +46,8 @@ class OscarMetadataBuilder:
     ``common`` passed to ``build`` is duck-typed like vLLM's CommonAttentionMetadata:
     ``num_reqs``, ``num_actual_tokens``, ``max_query_len``, ``query_start_loc``,
     ``seq_lens``, ``block_table_tensor``, ``slot_mapping`` (device tensors) and optionally
-    ``max_seq_len`` (host int) and ``causal``.
+    ``max_seq_len`` (host int), ``seq_lens_cpu`` (host tensor, for the batch's total history)
+    and ``causal``.
     """
 
     def __init__(self, layout: CacheLayout, max_num_seqs: int, max_num_batched_tokens: int,
@@ -94,8 +96,10 @@ class OscarMetadataBuilder:
                               self.max_reqs, self.query_tile, num_reqs=1 if dummy else nr,
                               source_table=common.block_table_tensor, table=self.table,
                               copy_columns=copy_columns)
+        seq_cpu = getattr(common, "seq_lens_cpu", None)
         return OscarMetadata(
             self.qstarts, self.seqs, self.table, self.slots, self.counts, nr, nt,
             common.max_query_len, self.max_reqs, self.layout, is_dummy=dummy, tasks=self.tasks,
             task_count=self.task_count, max_seq_len=getattr(common, "max_seq_len", None),
+            total_seq_len=None if dummy or seq_cpu is None else int(seq_cpu[:nr].sum()),
         )

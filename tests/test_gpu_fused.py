@@ -71,7 +71,7 @@ def _forward(c, form, splits, raw=None):
     k_cache, v_cache = _views(raw, c.layout)
     impl = OscarAttentionImpl(6, 256, 1 / 16, 1, c.layout.config, fused=form != "single")
     impl.initialize_layer(c.rk, c.rv)
-    impl.splits_for = lambda meta, s=splits: s
+    impl.partition_for = lambda meta, s=splits: (s, 0)
     c.meta.merged_lse = torch.full((n, 6), 7.0, device=DEV)
     out = torch.full((n, 6 * 256), 3.0, device=DEV, dtype=torch.bfloat16)
     impl.forward(None, c.q, c.k, c.v, (k_cache, v_cache), c.meta, out)
@@ -138,7 +138,7 @@ def test_fused_step_replays_in_a_graph():
     kg, vg = _views(raw_graph, c.layout)
     impl = OscarAttentionImpl(6, 256, 1 / 16, 1, c.layout.config, fused=True)
     impl.initialize_layer(c.rk, c.rv)
-    impl.splits_for = lambda meta: 8
+    impl.partition_for = lambda meta: (8, 0)
     lse = c.meta.merged_lse = torch.empty((n, 6), device=DEV)
     out = torch.empty((n, 6 * 256), device=DEV, dtype=torch.bfloat16)
     impl.forward(None, c.q, c.k, c.v, (kg, vg), c.meta, out)  # warm-up (views, library)
@@ -172,7 +172,7 @@ def test_fused_step_against_dense_reference(lengths, prefixes, splits):
     k_cache, v_cache = _views(c.raw, c.layout)
     impl = OscarAttentionImpl(6, 256, 1 / 16, 1, c.layout.config, fused=True)
     impl.initialize_layer(c.rk, c.rv)
-    impl.splits_for = lambda meta, s=splits: s
+    impl.partition_for = lambda meta, s=splits: (s, 0)
     c.meta.merged_lse = torch.empty((n, 6), device=DEV)
     out = torch.empty((n, 6 * 256), device=DEV, dtype=torch.bfloat16)
     impl.forward(None, c.q, c.k, c.v, (k_cache, v_cache), c.meta, out)
