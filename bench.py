@@ -320,10 +320,17 @@ def cpu_baseline(w, args, outputs):
     return cpu, parity
 
 
-def read_traffic():
-    """HBM bytes per history-kernel launch from the committed rocprof PMC summary, if any."""
-    path = ROOT / "profiles" / "history_kernel_c3_traffic.txt"
-    if not path.exists():
+TRAFFIC_PROFILES = {  # c3 PMC summaries (FETCH_SIZE / WRITE_SIZE runs) per kernel
+    "history_pair_kernel": "history_kernel_c3_traffic.txt",
+    "history_pair_finish_kernel": "history_finish_kernel_c3_traffic.txt",
+}
+
+
+def read_traffic(kernel, config):
+    """HBM bytes per launch of `kernel` from the committed rocprof PMC summary, if any."""
+    name = TRAFFIC_PROFILES.get(kernel)
+    path = ROOT / "profiles" / name if name and config == "c3" else None
+    if path is None or not path.exists():
         return None
     for line in path.read_text().splitlines():
         if line.startswith("traffic_bytes_per_launch:"):
@@ -428,20 +435,32 @@ def main(argv=None):
     gpu_ms = ev0.elapsed_time(ev1)
     us_step = wall / args.steps * 1e6
 
-    # Dominant kernel alone: history attention, HIP events around each launch.
-    qrot = kernels.rotate(w.q, w.rk)
+    # Dominant kernel alone, HIP events around each launch: the history launch of the step
+    # (history + split merge + path merge + window store when history_post covers the step,
+    # else the history branch alone).
     hist_views = [w.layout.tensor_views(c) for c in layers]
+    one_launch = kernels.history_post_supported(w.meta, w.layout, 6, splits)
+    qrot, rp, rl = kernels.pre_attention(w.q, w.k, w.v, hist_views[0][0], hist_views[0][1],
+                                         w.meta, w.layout, 1 / 16, impls[0].rk_t, impls[0].rv_t)
+    out = torch.empty(ntok, 6 * 256, dtype=torch.bfloat16, device=device)
+
+    def history_launch(i):
+        h, win = hist_views[i % len(layers)]
+        if one_launch:
+            kernels.history_post(qrot, h, w.meta, w.layout, 1 / 16, splits, rp, rl,
+                                 impls[0].rv, w.k, w.v, win, out, split_tokens=split_tokens)
+        else:
+            kernels.attention_partials(qrot, w.k, w.v, h, win, w.meta, w.layout, 1 / 16, splits,
+                                       False, split_tokens=split_tokens)
+
     for i in range(len(layers)):
-        kernels.attention_partials(qrot, w.k, w.v, hist_views[i][0], hist_views[i][1], w.meta,
-                                   w.layout, 1 / 16, splits, False, split_tokens=split_tokens)
+        history_launch(i)
     torch.cuda.synchronize()
     evs = []
     for i in range(args.steps):
         a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        h, win = hist_views[i % len(layers)]
         a.record()
-        kernels.attention_partials(qrot, w.k, w.v, h, win, w.meta, w.layout, 1 / 16, splits,
-                                   False, split_tokens=split_tokens)
+        history_launch(i)
         b.record()
         evs.append((a, b))
     torch.cuda.synchronize()
@@ -449,6 +468,13 @@ def main(argv=None):
     alg = algorithmic_bytes(w)
     partial_bytes = split_partial_bytes(w, splits, split_tokens)
     hist_alg = alg.int2 + ntok * 6 * 256 * 2 + alg.table + partial_bytes
+    if one_launch:
+        # + the partial rows and LSEs read back by the merges, the BF16-branch rows, the output
+        # and merged LSE, R_v once, and the window store's current K/V (read and written).
+        rows = ntok * 6
+        hist_alg += partial_bytes + rows * (1024 + 4) + rows * (512 + 4) + 256 * 256 * 2
+        hist_alg += 2 * 2 * ntok * 512
+    hist_kernel = "history_pair_finish_kernel" if one_launch else "history_pair_kernel"
     print(f"[bench] step {us_step:.1f} us, history kernel {hist_us:.1f} us", file=sys.stderr,
           flush=True)
 
@@ -480,6 +506,7 @@ def main(argv=None):
         "gpu_us_per_layer_step": gpu_ms / args.steps * 1e3,
         "algorithmic_bytes_per_step": alg.total,
         "history_kernel": {
+            "kernel": hist_kernel,
             "us": hist_us,
             "history_tokens": alg.history_tokens,
             "algorithmic_bytes": hist_alg,
@@ -493,7 +520,7 @@ def main(argv=None):
             "peak": PEAK_HBM_GBPS,
             "unit": "GB/s",
             "frac": hist_alg / (hist_us * 1e-6) / 1e9 / PEAK_HBM_GBPS,
-            "traffic": read_traffic(),
+            "traffic": read_traffic(hist_kernel, args.config),
         },
     }
     if not args.no_cpu_baseline:

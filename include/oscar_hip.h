@@ -226,6 +226,33 @@ int oscar_post_attention(const float* history_partials, const float* history_lse
                          int64_t table_stride, int64_t max_reqs, const oscar_layout* layout,
                          void* stream);
 
+/*
+ * history_post -- the history branch and post_attention in ONE launch (no reference
+ * counterpart: it replaces oscar_attention_partials(raw = 0) followed by
+ * oscar_post_attention, with the same output and merged_lse bits). The arguments are those of
+ * the two calls (query = the rotated query; partials / lse: fp32 [n, hq, splits, 256] /
+ * [n, hq, splits] scratch rows of the launch). The workgroup that completes a (task, kv head)
+ * merges that task's rows; counters: int32 [counter_slots >= programs * kv_heads], all zero
+ * before the first call, left zero by every call. Calls that overlap on one device must not
+ * share counters. Supports query rows per task (min(query_tile, max_query_len) * hq / kv_heads)
+ * <= 8 and splits <= 16 (OSCAR_E_UNSUPPORTED otherwise: use the two calls). Split slots a
+ * token-bounded request does not use are left unwritten. Must follow oscar_pre_attention of
+ * the same step on the stream (it reads raw_partials / raw_lse and stores the windows).
+ */
+int oscar_history_post(const void* query, int64_t q_s0, int64_t q_s1, int64_t q_s2,
+                       const void* history, int64_t history_bytes, const int32_t* qstarts,
+                       const int32_t* seq_lens, const int32_t* block_tables,
+                       int64_t table_stride, int64_t table_columns, const int32_t* counts,
+                       const int32_t* tasks, const int32_t* task_count, int64_t n, int64_t hq,
+                       int64_t programs, int32_t splits, int32_t block_n, int32_t query_tile,
+                       int32_t max_query_len, float scale, int32_t split_tokens,
+                       const oscar_layout* layout, float* partials, float* lse,
+                       int32_t* counters, int64_t counter_slots, const float* raw_partials,
+                       const float* raw_lse, const void* rv, void* output, float* merged_lse,
+                       const void* key, int64_t k_s0, int64_t k_s1, const void* value,
+                       int64_t v_s0, int64_t v_s1, void* window, int64_t window_elems,
+                       int64_t max_reqs, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

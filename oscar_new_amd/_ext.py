@@ -89,6 +89,18 @@ SIGNATURES = {
         _P, _I64, _P, _P, _P, _I64, _I64,  # window, elems, qstarts, seq_lens, table, stride, max_reqs
         POINTER(OscarLayout), _P,
     ],
+    "oscar_history_post": [
+        _P, _I64, _I64, _I64,  # query (rotated)
+        _P, _I64,  # history, bytes
+        _P, _P, _P, _I64, _I64,  # qstarts, seq_lens, block_tables, stride, columns
+        _P, _P, _P,  # counts, tasks, task_count
+        _I64, _I64, _I64, _I32, _I32, _I32, _I32, _F, _I32,  # n hq programs splits bn qt mql scale st
+        POINTER(OscarLayout), _P, _P,  # layout, partials, lse
+        _P, _I64,  # counters, slots
+        _P, _P, _P, _P, _P,  # raw partials, raw lse, rv, output, merged_lse
+        _P, _I64, _I64, _P, _I64, _I64,  # key, value (+ row strides)
+        _P, _I64, _I64, _P,  # window, elems, max_reqs, stream
+    ],
 }
 
 _lib = None

@@ -103,10 +103,16 @@ class OscarAttentionImpl:
 
         splits, split_tokens = self.partition_for(meta)
         if self.fused:
-            # Three launches: BF16 branch + rotations + INT2 store, history, merges + window.
+            # BF16 branch + rotations + INT2 store; then history + merges + window in one launch
+            # (decode-sized tasks, <= 16 splits) or in two.
             qrot, rp, rl = kernels.pre_attention(query, key, value, self.history, self.window,
                                                  meta, meta.layout, self.scale, self.rk_t,
                                                  self.rv_t)
+            if kernels.history_post_supported(meta, meta.layout, self.num_heads, splits, n):
+                kernels.history_post(qrot, self.history, meta, meta.layout, self.scale, splits, rp,
+                                     rl, self.rv, key, value, self.window, output.view(n, -1),
+                                     getattr(meta, "merged_lse", None), split_tokens=split_tokens)
+                return output
             hp, hl = kernels.attention_partials(qrot, key, value, self.history, self.window, meta,
                                                 meta.layout, self.scale, splits, raw=False,
                                                 split_tokens=split_tokens)

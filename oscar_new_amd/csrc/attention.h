@@ -114,4 +114,18 @@ __device__ __forceinline__ void write_unused_split(const AttnArgs& a, const Task
 // INT2 history branch (history.hip); rows = query rows per task (<= 32).
 hipError_t launch_history(const AttnArgs& a, dim3 grid, int rows, hipStream_t stream);
 
+// The checks and fields of one attention_partials launch (attention.hip): OSCAR_OK with *out
+// filled and *qrows = query rows per task, or the entry point's error code. Nothing is
+// launched when n == 0 (OSCAR_OK before the pointer checks).
+int make_attn_args(const void* query, int64_t q_s0, int64_t q_s1, int64_t q_s2, const void* key,
+                   int64_t k_s0, int64_t k_s1, int64_t k_s2, const void* value, int64_t v_s0,
+                   int64_t v_s1, int64_t v_s2, const void* history, int64_t history_bytes,
+                   const void* window, int64_t window_elems, const int32_t* qstarts,
+                   const int32_t* seq_lens, const int32_t* block_tables, int64_t table_stride,
+                   int64_t table_columns, const int32_t* counts, const int32_t* tasks,
+                   const int32_t* task_count, int64_t n, int64_t hq, int64_t programs,
+                   int32_t splits, int32_t block_n, int32_t query_tile, int32_t max_query_len,
+                   float scale, int32_t raw, int32_t split_tokens, const oscar_layout* layout,
+                   float* partials, float* lse, AttnArgs* out, int64_t* qrows);
+
 }  // namespace oscar

@@ -23,18 +23,20 @@ __global__ __launch_bounds__(kThreads) void raw_kernel(const AttnArgs a) {
 }  // namespace
 }  // namespace oscar
 
-extern "C" int oscar_attention_partials(
-    const void* query, int64_t q_s0, int64_t q_s1, int64_t q_s2, const void* key, int64_t k_s0,
-    int64_t k_s1, int64_t k_s2, const void* value, int64_t v_s0, int64_t v_s1, int64_t v_s2,
-    const void* history, int64_t history_bytes, const void* window, int64_t window_elems,
-    const int32_t* qstarts, const int32_t* seq_lens, const int32_t* block_tables,
-    int64_t table_stride, int64_t table_columns, const int32_t* counts, const int32_t* tasks,
-    const int32_t* task_count, int64_t n, int64_t hq, int64_t programs, int32_t splits,
-    int32_t block_n, int32_t query_tile, int32_t max_query_len, float scale, int32_t raw,
-    int32_t split_tokens, const oscar_layout* layout, float* partials, float* lse,
-    void* stream) {
-  using namespace oscar;
-  AttnArgs a{};
+namespace oscar {
+
+int make_attn_args(const void* query, int64_t q_s0, int64_t q_s1, int64_t q_s2, const void* key,
+                   int64_t k_s0, int64_t k_s1, int64_t k_s2, const void* value, int64_t v_s0,
+                   int64_t v_s1, int64_t v_s2, const void* history, int64_t history_bytes,
+                   const void* window, int64_t window_elems, const int32_t* qstarts,
+                   const int32_t* seq_lens, const int32_t* block_tables, int64_t table_stride,
+                   int64_t table_columns, const int32_t* counts, const int32_t* tasks,
+                   const int32_t* task_count, int64_t n, int64_t hq, int64_t programs,
+                   int32_t splits, int32_t block_n, int32_t query_tile, int32_t max_query_len,
+                   float scale, int32_t raw, int32_t split_tokens, const oscar_layout* layout,
+                   float* partials, float* lse, AttnArgs* out, int64_t* qrows_out) {
+  AttnArgs& a = *out;
+  a = AttnArgs{};
   const int st = make_layout(layout, &a.L);
   if (st != OSCAR_OK) return st;
   const int64_t h = a.L.kv_heads;
@@ -47,6 +49,7 @@ extern "C" int oscar_attention_partials(
   const int64_t qrows = (max_query_len > 0 && max_query_len < query_tile ? max_query_len
                                                                          : query_tile) * g;
   if (qrows > 32) return OSCAR_E_UNSUPPORTED;
+  *qrows_out = qrows;
   if (n == 0) return OSCAR_OK;
   if (!query || !qstarts || !seq_lens || !block_tables || !counts || !tasks || !task_count ||
       !partials || !lse)
@@ -100,7 +103,32 @@ extern "C" int oscar_attention_partials(
   a.block_n = block_n;
   a.split_tokens = split_tokens;
   a.scale_log2 = scale * kLog2e;
-  const dim3 grid(static_cast<unsigned>(programs), static_cast<unsigned>(h),
+  return OSCAR_OK;
+}
+
+}  // namespace oscar
+
+extern "C" int oscar_attention_partials(
+    const void* query, int64_t q_s0, int64_t q_s1, int64_t q_s2, const void* key, int64_t k_s0,
+    int64_t k_s1, int64_t k_s2, const void* value, int64_t v_s0, int64_t v_s1, int64_t v_s2,
+    const void* history, int64_t history_bytes, const void* window, int64_t window_elems,
+    const int32_t* qstarts, const int32_t* seq_lens, const int32_t* block_tables,
+    int64_t table_stride, int64_t table_columns, const int32_t* counts, const int32_t* tasks,
+    const int32_t* task_count, int64_t n, int64_t hq, int64_t programs, int32_t splits,
+    int32_t block_n, int32_t query_tile, int32_t max_query_len, float scale, int32_t raw,
+    int32_t split_tokens, const oscar_layout* layout, float* partials, float* lse,
+    void* stream) {
+  using namespace oscar;
+  AttnArgs a;
+  int64_t qrows = 0;
+  const int st = make_attn_args(query, q_s0, q_s1, q_s2, key, k_s0, k_s1, k_s2, value, v_s0, v_s1,
+                                v_s2, history, history_bytes, window, window_elems, qstarts,
+                                seq_lens, block_tables, table_stride, table_columns, counts, tasks,
+                                task_count, n, hq, programs, splits, block_n, query_tile,
+                                max_query_len, scale, raw, split_tokens, layout, partials, lse, &a,
+                                &qrows);
+  if (st != OSCAR_OK || n == 0) return st;
+  const dim3 grid(static_cast<unsigned>(programs), static_cast<unsigned>(a.L.kv_heads),
                   static_cast<unsigned>(splits));
   hipStream_t s = as_stream(stream);
   if (!raw) return static_cast<int>(launch_history(a, grid, static_cast<int>(qrows), s));

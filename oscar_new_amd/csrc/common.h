@@ -195,4 +195,38 @@ int make_layout(const oscar_layout* in, Layout* out);
 
 hipStream_t as_stream(void* s);
 
+// Device-coherent accesses for rows that one workgroup writes and another reads in the same
+// launch: an agent-scope relaxed atomic store writes through to the device's point of
+// coherence (the L2 of each XCD is not coherent with the others'), and the matching load reads
+// from there. Pairing them with a wait for the stores and a counter atomic avoids whole-L2
+// write-back / invalidate fences.
+__device__ __forceinline__ void store_coherent(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void store_coherent(float* p, float4 v) {
+  store_coherent(p, v.x);
+  store_coherent(p + 1, v.y);
+  store_coherent(p + 2, v.z);
+  store_coherent(p + 3, v.w);
+}
+// Loads of such rows through a raw buffer resource over a whole buffer (wave-uniform base,
+// `bytes` < 2^32 long; reads past the end return zero; per-lane byte offsets) with the same
+// device-coherent cache policy (sc1) as the stores above, 4 or 16 bytes at a time.
+constexpr int32_t kBufferWord3 = 0x00020000;  // raw buffer, dword data (gfx9)
+constexpr int kCoherentPolicy = 16;           // sc1
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t coherent_rsrc(const float* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base), 0, static_cast<int>(bytes),
+                                           kBufferWord3);
+}
+__device__ __forceinline__ float load_coherent(__amdgpu_buffer_rsrc_t r, uint32_t offset) {
+  return __uint_as_float(
+      __builtin_amdgcn_raw_buffer_load_b32(r, static_cast<int>(offset), 0, kCoherentPolicy));
+}
+__device__ __forceinline__ float4 load_coherent4(__amdgpu_buffer_rsrc_t r, uint32_t offset) {
+  const u32x4 v =
+      __builtin_amdgcn_raw_buffer_load_b128(r, static_cast<int>(offset), 0, kCoherentPolicy);
+  return make_float4(__uint_as_float(v[0]), __uint_as_float(v[1]), __uint_as_float(v[2]),
+                     __uint_as_float(v[3]));
+}
+
 }  // namespace oscar

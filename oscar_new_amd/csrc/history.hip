@@ -32,6 +32,8 @@
 #include <type_traits>
 
 #include "attention.h"
+#include "dma.h"
+#include "finish.h"
 
 namespace oscar {
 namespace {
@@ -39,7 +41,6 @@ namespace {
 typedef int32_t i32x8 __attribute__((ext_vector_type(8)));
 typedef int32_t i32x2 __attribute__((ext_vector_type(2)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
-typedef __attribute__((address_space(3))) void* lds_ptr_t;
 typedef __attribute__((address_space(3))) i32x2* lds_i32x2_ptr_t;
 
 constexpr int kChunk = 64;                       // tokens per wavefront iteration
@@ -56,41 +57,6 @@ constexpr uint32_t kNoBlock = 0xffffffffu;
 
 static_assert(kDma * 64 == kChunk * kPieces, "a chunk image is whole DMA instructions");
 static_assert(kStageBytes % 16 == 0, "stages stay 16-byte aligned");
-
-// ---------------------------------------------------------------- asm plumbing
-
-// Direct-to-LDS loads are issued by asm so that the compiler does not serialize LDS reads
-// behind outstanding DMA (it cannot tell the two ring stages apart); ordering comes from
-// the explicit vmcnt waits below. M0 holds the LDS base (any dword address); one wait state
-// separates its write from the DMA. Lane l writes LDS bytes [M0 + 16 l, +16).
-// A wave-uniform pointer, kept in SGPRs for the saddr form of the DMA.
-__device__ __forceinline__ const uint8_t* uniform_ptr(const uint8_t* p) {
-  const uint64_t v = reinterpret_cast<uint64_t>(p);
-  const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v));
-  const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v >> 32));
-  return reinterpret_cast<const uint8_t*>((static_cast<uint64_t>(hi) << 32) | lo);
-}
-__device__ __forceinline__ void dma_x4(const uint8_t* base, uint32_t voff, uint32_t lds) {
-  base = uniform_ptr(base);
-  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %1, %2" : : "{m0}"(lds), "v"(voff), "s"(base)
-               : "memory");
-}
-__device__ __forceinline__ void dma_dwordx4(const void* src, uint32_t lds) {
-  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %1, off" : : "{m0}"(lds), "v"(src)
-               : "memory");
-}
-#define OSCAR_WAIT_VM(n) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(n) : "memory")
-#define OSCAR_WAIT_LGKM() asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory")
-
-// Workgroup barrier that waits for this wavefront's LDS traffic but not for its DMA
-// (__syncthreads would also drain every outstanding load).
-__device__ __forceinline__ void barrier_lds() {
-  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-}
-
-__device__ __forceinline__ uint32_t lds_addr(const void* p) {
-  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_ptr_t)p));
-}
 
 // ---------------------------------------------------------------- number formats
 
@@ -608,13 +574,24 @@ __host__ __device__ constexpr int pair_token(int ga, int e) {
   return 32 * ((e >> 2) & 1) + 16 * (e >> 3) + 4 * ga + (e & 3);
 }
 
-__global__ __launch_bounds__(kThreads, 2) void history_pair_kernel(const AttnArgs a) {
+// kFinish: the two-launch step's history launch (finish.h): the grid has one more z slice
+// (window stores, padded rows), unused split slots are left unwritten (the merge reads only
+// the task's splits), and the workgroup that completes a (task, head) finishes its rows.
+template <bool kFinish>
+__device__ __forceinline__ void history_pair_body(const AttnArgs& a, const FinishArgs* fin) {
+  if constexpr (kFinish) {
+    if (static_cast<int>(blockIdx.z) == a.splits) {
+      finish_extra(*fin, blockIdx.y);
+      return;
+    }
+  }
   __shared__ __attribute__((aligned(16))) uint8_t s_ring[kRingBytes];
   __shared__ uint32_t s_off[kTableCache];
   __shared__ float s_red[3][4][8];  // per wavefront: row max, sum p, sum p z_v
   static_assert(8 * 512 + 4 * 2 * 8 * 16 * 4 <= 2 * kStageBytes,
                 "query rows and operand images fit wavefront 3's stages");
   static_assert(4 * 8 * 256 * 4 <= kRingBytes, "the epilogue merge fits the ring");
+  static_assert(kFinishLdsBytes <= kRingBytes, "the finisher fits the ring");
 
   Task t;
   if (!read_task(a, t, blockIdx.x)) return;
@@ -622,7 +599,7 @@ __global__ __launch_bounds__(kThreads, 2) void history_pair_kernel(const AttnArg
   const int length = t.recent_begin - t.sink_len;
   const int nsplit = history_splits(a, length);
   if (split >= nsplit) {
-    write_unused_split(a, t, head, split);
+    if constexpr (!kFinish) write_unused_split(a, t, head, split);
     return;
   }
   int begin, end;
@@ -967,12 +944,38 @@ __global__ __launch_bounds__(kThreads, 2) void history_pair_kernel(const AttnArg
                                    (2.0f * ((x0.y + x1.y) + (x2.y + x3.y)) + zs) * inv,
                                    (2.0f * ((x0.z + x1.z) + (x2.z + x3.z)) + zs) * inv,
                                    (2.0f * ((x0.w + x1.w) + (x2.w + x3.w)) + zs) * inv);
-      *reinterpret_cast<float4*>(out + 128 * q) = r;
+      if constexpr (kFinish)
+        store_coherent(out + 128 * q, r);
+      else
+        *reinterpret_cast<float4*>(out + 128 * q) = r;
     }
-    if ((etid & 31) == 0)
-      a.lse[(ri.token * a.hq + ri.qhead) * a.splits + split] =
-          den > 0.f ? (mx + log2f(den)) * kLn2 : -INFINITY;
+    if ((etid & 31) == 0) {
+      float* dst = a.lse + (ri.token * a.hq + ri.qhead) * a.splits + split;
+      const float l = den > 0.f ? (mx + log2f(den)) * kLn2 : -INFINITY;
+      if constexpr (kFinish)
+        store_coherent(dst, l);
+      else
+        *dst = l;
+    }
   }
+  if constexpr (kFinish) {
+    __shared__ int s_flag;
+    int32_t* counter = fin->counters + static_cast<int64_t>(blockIdx.x) * a.L.kv_heads + head;
+    if (finish_arrive(counter, nsplit, &s_flag)) finish_task8(*fin, a, t, head, nsplit, s_ring);
+  }
+}
+
+__global__ __launch_bounds__(kThreads, 2) void history_pair_kernel(const AttnArgs a) {
+  history_pair_body<false>(a, nullptr);
+}
+
+struct HistoryFinishArgs {
+  AttnArgs a;
+  FinishArgs f;
+};
+
+__global__ __launch_bounds__(kThreads, 2) void history_pair_finish_kernel(const HistoryFinishArgs h) {
+  history_pair_body<true>(h.a, &h.f);
 }
 
 }  // namespace
@@ -984,6 +987,14 @@ hipError_t launch_history(const AttnArgs& a, dim3 grid, int rows, hipStream_t st
     hipLaunchKernelGGL(history_kernel<1>, grid, dim3(kThreads), 0, stream, a);
   else
     hipLaunchKernelGGL(history_kernel<2>, grid, dim3(kThreads), 0, stream, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_history_finish(const AttnArgs& a, const FinishArgs& f, hipStream_t stream) {
+  const HistoryFinishArgs h{a, f};
+  const dim3 grid(static_cast<unsigned>(f.programs), static_cast<unsigned>(a.L.kv_heads),
+                  static_cast<unsigned>(a.splits + 1));
+  hipLaunchKernelGGL(history_pair_finish_kernel, grid, dim3(kThreads), 0, stream, h);
   return hipGetLastError();
 }
 

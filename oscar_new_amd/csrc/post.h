@@ -29,53 +29,101 @@ struct PostArgs {
   int32_t merge_wgs;     // workgroups of the merge role; the rest store windows
 };
 
-// Rows [row0, min(row0 + R, row_end, p.rows)) by the four wavefronts of a workgroup:
-// wavefront w merges rows w, w + 4, ... into LDS (s_h: R x 256 bf16, s_l: R floats), or, with
-// R = 1 (kMergeScanGroup), all four merge the one row together; then every wavefront rotates
-// the R rows back for 64 output columns and merges them with the BF16 branch. Every read
-// that does not depend on the merge (R_v, the BF16-branch values and LSEs) is requested
-// before it, and none waits for the token count.
-template <int R, int kMode>
-__device__ __forceinline__ void post_rows(const PostArgs& p, int64_t row0, int64_t row_end,
-                                          uint16_t (*s_h)[kHeadDim], float* s_l,
-                                          GroupMergeLds* group_lds) {
-  static_assert(R == 1 || R == 4 || R == 16, "row groups of 1, 4 or 16");
+// BF16-branch operands of this lane's tile rows 4g + v (rows below R) for the path merge.
+struct PathRows {
+  int64_t row[4];  // row index, or -1
+  bool valid[4];   // a row below the token count
+  float bv[4][4];  // BF16-branch values of columns 64 wave + 16 ct + n
+  float lb[4];     // BF16-branch LSEs
+};
+
+template <int R, class RowOf>
+__device__ __forceinline__ void load_path_rows(const PostArgs& p, RowOf row_of, int active,
+                                               PathRows& pr) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int n = lane & 15, g = lane >> 4;
-  const int active = p.counts[1];
-  row_end = min(row_end, p.rows);
-  // R_v operands of this wavefront's four column tiles, requested first.
-  RotateOperands op;
-  u32x4 rb[4][8];
-#pragma unroll
-  for (int ct = 0; ct < 4; ++ct) {
-    rotate_load_b<true>(op, p.rv + static_cast<int64_t>(64 * wave + 16 * ct + n) * kHeadDim, 1, g);
-#pragma unroll
-    for (int m = 0; m < 8; ++m) rb[ct][m] = op.b[m];
-  }
-  // BF16-branch values merged by this lane: tile rows 4g + v (rows below R).
-  float bv[4][4], lb[4];
-  bool valid[4];
 #pragma unroll
   for (int v = 0; v < 4; ++v) {
     const int r = 4 * g + v;
-    const int64_t row = row0 + r;
-    const bool in = r < R && row < row_end;
-    const int64_t lrow = in ? row : 0;
-    valid[v] = in && row / p.hq < active;
+    pr.row[v] = r < R ? row_of(r) : -1;
+    const bool in = pr.row[v] >= 0;
+    const int64_t lrow = in ? pr.row[v] : 0;
+    pr.valid[v] = in && pr.row[v] / p.hq < active;
     const float l = p.rl[lrow];
-    lb[v] = valid[v] ? l : -INFINITY;
+    pr.lb[v] = pr.valid[v] ? l : -INFINITY;
 #pragma unroll
     for (int ct = 0; ct < 4; ++ct) {
       const float x = p.rp[lrow * kHeadDim + 64 * wave + 16 * ct + n];
-      bv[v][ct] = valid[v] ? x : 0.f;
+      pr.bv[v][ct] = pr.valid[v] ? x : 0.f;
     }
   }
+}
+
+// Inverse rotation of the R merged rows in s_h (rows R..15 of the MFMA tile are zero) by this
+// wavefront's four R_v column tiles (get_b(ct, b) supplies tile ct's B operand), then the path
+// merge of each element with the BF16 branch; put(r, row, col, bits) stores output element
+// (tile row r, row index `row`, column col), and the merged LSE is stored here.
+template <int R, class GetB, class Put>
+__device__ __forceinline__ void rotate_merge(const PostArgs& p, const PathRows& pr, GetB get_b,
+                                             uint16_t (*s_h)[kHeadDim], const float* s_l,
+                                             Put put) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int n = lane & 15, g = lane >> 4;
+  RotateOperands op;
+  rotate_load_a<true>(op, n < R ? &s_h[n][0] : nullptr, 1, g);
+#pragma unroll
+  for (int ct = 0; ct < 4; ++ct) {
+    const int col = 64 * wave + 16 * ct + n;
+    u32x4 b[8];
+    get_b(ct, b);
+    const f32x4 acc = rotate_mfma(op.a, b);
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int r = 4 * g + v;
+      const int64_t row = pr.row[v];
+      if (r >= R || row < 0) continue;
+      const PathWeights w = path_weights(pr.valid[v] ? s_l[r] : -INFINITY, pr.lb[v]);
+      const float av = pr.valid[v] ? bf16_to_float(float_to_bf16(acc[v])) : 0.f;
+      put(r, row, col, static_cast<uint16_t>(float_to_bf16(path_merge(w, av, pr.bv[v][ct]))));
+      if (p.merged_lse && wave == 0 && ct == 0 && n == 0) p.merged_lse[row] = path_lse(w);
+    }
+  }
+}
+
+// Rows row_of(0 .. R-1) (a row index in [0, p.rows), or -1 for none) by the four wavefronts
+// of a workgroup: wavefront w merges rows w, w + 4, ... into LDS (s_h: R x 256 bf16, s_l: R
+// floats), or, with R = 1 (kMergeScanGroup), all four merge the one row together; then every
+// wavefront rotates the R rows back for 64 output columns and merges them with the BF16
+// branch. Splits at or past `live_splits` are not read (the row stride stays p.splits).
+// The reads that do not depend on the merge (the BF16-branch values and LSEs, and the R_v
+// operands of the first kEarly column tiles) are requested before it, the other R_v tiles
+// after it (fewer registers live across the merge); none waits for the token count.
+template <int R, int kMode, int kEarly = 4, class RowOf>
+__device__ __forceinline__ void post_rows_map(const PostArgs& p, RowOf row_of, int live_splits,
+                                              uint16_t (*s_h)[kHeadDim], float* s_l,
+                                              GroupMergeLds* group_lds) {
+  static_assert(R == 1 || R == 4 || R == 8 || R == 16, "row groups of 1, 4, 8 or 16");
+  static_assert(kEarly >= 0 && kEarly <= 4, "four column tiles per wavefront");
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int n = lane & 15, g = lane >> 4;
+  const int active = p.counts[1];
+  RotateOperands op;
+  u32x4 rb[4][8];
+  auto load_rv = [&](int ct) {
+    rotate_load_b<true>(op, p.rv + static_cast<int64_t>(64 * wave + 16 * ct + n) * kHeadDim, 1, g);
+#pragma unroll
+    for (int m = 0; m < 8; ++m) rb[ct][m] = op.b[m];
+  };
+#pragma unroll
+  for (int ct = 0; ct < kEarly; ++ct) load_rv(ct);
+  PathRows pr;
+  load_path_rows<R>(p, row_of, active, pr);
   if (R == 1) {
-    const bool in = row0 < row_end;
+    const int64_t row0 = row_of(0);
+    const bool in = row0 >= 0;
     const int64_t lrow = in ? row0 : 0;
     const SplitMerge m = merge_splits_row_group(p.hp + lrow * p.splits * kHeadDim,
-                                                p.hl + lrow * p.splits, p.splits,
+                                                p.hl + lrow * p.splits, live_splits,
                                                 in && row0 / p.hq < active, group_lds);
     if (wave == 0) {
       *reinterpret_cast<uint2*>(&s_h[0][lane * 4]) = merge_splits_out(m);
@@ -83,38 +131,40 @@ __device__ __forceinline__ void post_rows(const PostArgs& p, int64_t row0, int64
     }
   } else {
     for (int r = wave; r < R; r += kThreads / kWave) {
-      const int64_t row = row0 + r;
-      const bool in = row < row_end;
+      const int64_t row = row_of(r);
+      const bool in = row >= 0;
       const float* part = p.hp + (in ? row : 0) * p.splits * kHeadDim;
       const float* ls = p.hl + (in ? row : 0) * p.splits;
       const bool live = in && row / p.hq < active;
       const SplitMerge m = kMode == kMergeOneRound
-                               ? merge_splits_row(part, ls, p.splits, live, lane)
-                               : merge_splits_row_scan(part, ls, p.splits, live, lane);
+                               ? merge_splits_row(part, ls, live_splits, live, lane)
+                               : merge_splits_row_scan(part, ls, live_splits, live, lane);
       *reinterpret_cast<uint2*>(&s_h[r][lane * 4]) = merge_splits_out(m);
       if (lane == 0) s_l[r] = merge_splits_lse(m);
     }
   }
+#pragma unroll
+  for (int ct = kEarly; ct < 4; ++ct) load_rv(ct);
   __syncthreads();
-  // Inverse rotation of the R merged rows (rows R..15 of the MFMA tile are zero), then the
-  // path merge of each element with the BF16 branch.
-  rotate_load_a<true>(op, n < R ? &s_h[n][0] : nullptr, 1, g);
+  rotate_merge<R>(
+      p, pr,
+      [&](int ct, u32x4(&b)[8]) {
 #pragma unroll
-  for (int ct = 0; ct < 4; ++ct) {
-    const int col = 64 * wave + 16 * ct + n;
-    const f32x4 acc = rotate_mfma(op.a, rb[ct]);
-#pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      const int r = 4 * g + v;
-      const int64_t row = row0 + r;
-      if (r >= R || row >= row_end) continue;
-      const PathWeights w = path_weights(valid[v] ? s_l[r] : -INFINITY, lb[v]);
-      const float av = valid[v] ? bf16_to_float(float_to_bf16(acc[v])) : 0.f;
-      p.out[row * kHeadDim + col] =
-          static_cast<uint16_t>(float_to_bf16(path_merge(w, av, bv[v][ct])));
-      if (p.merged_lse && wave == 0 && ct == 0 && n == 0) p.merged_lse[row] = path_lse(w);
-    }
-  }
+        for (int m = 0; m < 8; ++m) b[m] = rb[ct][m];
+      },
+      s_h, s_l,
+      [&](int, int64_t row, int col, uint16_t bits) { p.out[row * kHeadDim + col] = bits; });
+}
+
+// Rows [row0, min(row0 + R, row_end, p.rows)) (the post-attention launch).
+template <int R, int kMode>
+__device__ __forceinline__ void post_rows(const PostArgs& p, int64_t row0, int64_t row_end,
+                                          uint16_t (*s_h)[kHeadDim], float* s_l,
+                                          GroupMergeLds* group_lds) {
+  const int64_t end = min(row_end, p.rows);
+  post_rows_map<R, kMode>(
+      p, [=](int r) { return row0 + r < end ? row0 + r : static_cast<int64_t>(-1); }, p.splits,
+      s_h, s_l, group_lds);
 }
 
 }  // namespace oscar

@@ -17,6 +17,7 @@
 //     prefix), so the INT2 store of the step may run beside it;
 //   * the window store follows both branches (it is in the post-attention launch), as
 //     backend.py:225-226 requires.
+#include "finish.h"
 #include "post.h"
 #include "quant.h"
 #include "raw.h"
@@ -248,16 +249,19 @@ extern "C" int oscar_pre_attention(
   return static_cast<int>(hipGetLastError());
 }
 
-extern "C" int oscar_post_attention(
-    const float* history_partials, const float* history_lse, int32_t splits,
-    const float* raw_partials, const float* raw_lse, const int32_t* counts, const void* rv,
-    int64_t n, int64_t hq, void* output, float* merged_lse, const void* key, int64_t k_s0,
-    int64_t k_s1, const void* value, int64_t v_s0, int64_t v_s1, void* window,
-    int64_t window_elems, const int32_t* qstarts, const int32_t* seq_lens,
-    const int32_t* block_tables, int64_t table_stride, int64_t max_reqs,
-    const oscar_layout* layout, void* stream) {
-  using namespace oscar;
-  PostArgs p{};
+namespace oscar {
+namespace {
+
+// The checks and fields of one post-attention launch (everything but the merge grid).
+int make_post_args(const float* history_partials, const float* history_lse, int32_t splits,
+                   const float* raw_partials, const float* raw_lse, const int32_t* counts,
+                   const void* rv, int64_t n, int64_t hq, void* output, float* merged_lse,
+                   const void* key, int64_t k_s0, int64_t k_s1, const void* value, int64_t v_s0,
+                   int64_t v_s1, void* window, int64_t window_elems, const int32_t* qstarts,
+                   const int32_t* seq_lens, const int32_t* block_tables, int64_t table_stride,
+                   int64_t max_reqs, const oscar_layout* layout, PostArgs* out) {
+  PostArgs& p = *out;
+  p = PostArgs{};
   const int st = make_layout(layout, &p.win.L);
   if (st != OSCAR_OK) return st;
   if (n < 0 || hq <= 0 || hq % p.win.L.kv_heads || splits < 1 || max_reqs < 0 ||
@@ -298,6 +302,27 @@ extern "C" int oscar_post_attention(
   w.table_stride = table_stride;
   w.counts = counts;
   p.win_requests = n < max_reqs ? n : max_reqs;
+  return OSCAR_OK;
+}
+
+}  // namespace
+}  // namespace oscar
+
+extern "C" int oscar_post_attention(
+    const float* history_partials, const float* history_lse, int32_t splits,
+    const float* raw_partials, const float* raw_lse, const int32_t* counts, const void* rv,
+    int64_t n, int64_t hq, void* output, float* merged_lse, const void* key, int64_t k_s0,
+    int64_t k_s1, const void* value, int64_t v_s0, int64_t v_s1, void* window,
+    int64_t window_elems, const int32_t* qstarts, const int32_t* seq_lens,
+    const int32_t* block_tables, int64_t table_stride, int64_t max_reqs,
+    const oscar_layout* layout, void* stream) {
+  using namespace oscar;
+  PostArgs p;
+  const int st = make_post_args(history_partials, history_lse, splits, raw_partials, raw_lse,
+                                counts, rv, n, hq, output, merged_lse, key, k_s0, k_s1, value,
+                                v_s0, v_s1, window, window_elems, qstarts, seq_lens, block_tables,
+                                table_stride, max_reqs, layout, &p);
+  if (st != OSCAR_OK || n == 0) return st;
   const int mode = merge_mode(p.rows, splits);
   const int64_t merge_wgs = mode == kMergeScanGroup ? p.rows : (p.rows + 3) / 4;
   if (merge_wgs + p.win_requests > 0x7fffffffll) return OSCAR_E_SHAPE;
@@ -311,4 +336,41 @@ extern "C" int oscar_post_attention(
   else
     hipLaunchKernelGGL((post_attention_kernel<1, kMergeScanGroup>), grid, dim3(kThreads), 0, s, p);
   return static_cast<int>(hipGetLastError());
+}
+
+extern "C" int oscar_history_post(
+    const void* query, int64_t q_s0, int64_t q_s1, int64_t q_s2, const void* history,
+    int64_t history_bytes, const int32_t* qstarts, const int32_t* seq_lens,
+    const int32_t* block_tables, int64_t table_stride, int64_t table_columns,
+    const int32_t* counts, const int32_t* tasks, const int32_t* task_count, int64_t n, int64_t hq,
+    int64_t programs, int32_t splits, int32_t block_n, int32_t query_tile, int32_t max_query_len,
+    float scale, int32_t split_tokens, const oscar_layout* layout, float* partials, float* lse,
+    int32_t* counters, int64_t counter_slots, const float* raw_partials, const float* raw_lse,
+    const void* rv, void* output, float* merged_lse, const void* key, int64_t k_s0, int64_t k_s1,
+    const void* value, int64_t v_s0, int64_t v_s1, void* window, int64_t window_elems,
+    int64_t max_reqs, void* stream) {
+  using namespace oscar;
+  AttnArgs a;
+  int64_t qrows = 0;
+  int st = make_attn_args(query, q_s0, q_s1, q_s2, nullptr, 0, 0, 1, nullptr, 0, 0, 1, history,
+                          history_bytes, nullptr, 0, qstarts, seq_lens, block_tables, table_stride,
+                          table_columns, counts, tasks, task_count, n, hq, programs, splits,
+                          block_n, query_tile, max_query_len, scale, 0, split_tokens, layout,
+                          partials, lse, &a, &qrows);
+  if (st != OSCAR_OK) return st;
+  // One-round split merge by the completing workgroup, paired-token history kernel.
+  if (qrows > 8 || splits > kWaveMergeSplits || splits + 1 > 65535) return OSCAR_E_UNSUPPORTED;
+  FinishArgs f{};
+  st = make_post_args(partials, lse, splits, raw_partials, raw_lse, counts, rv, n, hq, output,
+                      merged_lse, key, k_s0, k_s1, value, v_s0, v_s1, window, window_elems,
+                      qstarts, seq_lens, block_tables, table_stride, max_reqs, layout, &f.p);
+  if (st != OSCAR_OK || n == 0) return st;
+  if (!counters) return OSCAR_E_NULL;
+  if (reinterpret_cast<uintptr_t>(counters) % 4) return OSCAR_E_ALIGN;
+  if (counter_slots < programs * a.L.kv_heads) return OSCAR_E_SHAPE;
+  // The completing workgroup reads the split rows through 32-bit buffer offsets.
+  if (n * hq * splits * kHeadDim * 4 >= (1ll << 32)) return OSCAR_E_UNSUPPORTED;
+  f.counters = counters;
+  f.programs = static_cast<int32_t>(programs);
+  return static_cast<int>(launch_history_finish(a, f, as_stream(stream)));
 }

@@ -369,6 +369,86 @@ def pre_attention(query, key, value, history, window, meta, layout, scale, rk_t,
     return qrot, partials, lse
 
 
+_COUNTERS = {}
+
+
+def _finish_counters(device, slots):
+    """Zeroed int32 completion counters of one device, grown on demand (allocate them before a
+    graph capture: a first call outside the capture does). Every history_post launch leaves
+    them zero; launches that overlap on one device (two streams at once) would race on them."""
+    buf = _COUNTERS.get(device)
+    if buf is None or buf.numel() < slots:
+        buf = torch.zeros(max(slots, 4096), dtype=torch.int32, device=device)
+        _COUNTERS[device] = buf
+    return buf
+
+
+def history_post_supported(meta, layout, hq, splits, tokens=None):
+    """Whether ``history_post`` covers this launch: <= 8 query rows per task, <= 16 splits,
+    split rows below 4 GiB (``tokens``: the launch's query rows n, when known)."""
+    cfg = layout.config
+    mql = getattr(meta, "max_query_len", None)
+    qt = cfg.queries_per_tile
+    rows = (mql if isinstance(mql, int) and 0 < mql < qt else qt) * (hq // layout.kv_heads)
+    small = tokens is None or tokens * hq * splits * cfg.head_dim * 4 < 1 << 32
+    return rows <= 8 and 1 <= splits <= 16 and small
+
+
+def history_post(query, history, meta, layout, scale, splits, raw_partials, raw_lse, rv, key,
+                 value, window, output, merged_lse=None, split_tokens=0):
+    """History branch + post-attention of one step in ONE launch (no reference counterpart).
+
+    Same output / merged LSE bits as ``attention_partials(raw=False)`` followed by
+    ``post_attention`` (backend.py:205-226 order); the split workgroup that completes a
+    (task, kv head) merges that task's rows. ``query`` is the rotated query [n, hq, 256].
+    Requires ``history_post_supported``.
+    """
+    _device_check(query, history, raw_partials, raw_lse, rv, key, value, window, output,
+                  merged_lse)
+    n, hq, d = query.shape
+    if not output.is_contiguous():
+        raise ValueError("Attention output must be contiguous")
+    if n == 0:
+        return
+    if not history_post_supported(meta, layout, hq, splits, n):
+        raise ValueError("history_post covers <= 8 query rows per task, <= 16 splits and "
+                         "split rows below 4 GiB")
+    if rv.dtype != torch.bfloat16 or not rv.is_contiguous():
+        raise ValueError("rv must be contiguous bf16 [256, 256]")
+    cfg = layout.config
+    programs = attention_programs(n, meta.max_num_reqs, cfg.queries_per_tile)
+    if meta.tasks.shape[0] < programs:
+        raise ValueError(f"task table holds {meta.tasks.shape[0]} rows; the grid needs {programs}")
+    query = _rows_contiguous(query)
+    key, k0, k1 = _row_strides(key, "key")
+    value, v0, v1 = _row_strides(value, "value")
+    partials = torch.empty((n, hq, splits, d), dtype=torch.float32, device=query.device)
+    lse = torch.empty((n, hq, splits), dtype=torch.float32, device=query.device)
+    stream = _stream(query)
+    counters = _finish_counters(query.device, programs * layout.kv_heads)
+    table = _int32(meta.block_tables, "block_tables")
+    max_query_len = getattr(meta, "max_query_len", None)
+    max_query_len = int(max_query_len) if isinstance(max_query_len, int) else 0
+    _ext.check(
+        _ext.library().oscar_history_post(
+            _ptr(query), *query.stride(),
+            _ptr(history), history.numel() * history.element_size(),
+            _ptr(_int32(meta.query_start_loc, "query_start_loc")),
+            _ptr(_int32(meta.seq_lens, "seq_lens")),
+            _ptr(table), table.stride(0), table.shape[1],
+            _ptr(_int32(meta.counts, "counts")), _ptr(_int32(meta.tasks, "tasks")),
+            _ptr(_int32(meta.task_count, "task_count")),
+            n, hq, programs, splits, cfg.block_n, cfg.queries_per_tile, max_query_len,
+            float(scale), int(split_tokens), layout_struct(layout), _ptr(partials), _ptr(lse),
+            _ptr(counters), counters.numel(),
+            _ptr(raw_partials.contiguous()), _ptr(raw_lse.contiguous()), _ptr(rv), _ptr(output),
+            _ptr(merged_lse), _ptr(key), k0, k1, _ptr(value), v0, v1, _ptr(window),
+            window.numel(), meta.max_num_reqs, stream,
+        ),
+        "history_post",
+    )
+
+
 def post_attention(history_partials, history_lse, raw_partials, raw_lse, rv, key, value, window,
                    meta, layout, output, merged_lse=None):
     """Split merge, inverse V rotation, path merge and window store of one step, in one launch.

@@ -44,6 +44,25 @@ def test_host_side_argument_errors():
         _ext.check(-2, "probe")
 
 
+def test_history_post_host_side_errors():
+    # Fake, aligned, never dereferenced addresses: every call below returns before a launch.
+    lib = _ext.library()
+    good = _ext.OscarLayout(256, 1, 768, 128, 160, 68, 4, 128, 132, 0, 393216)
+    a = 1 << 20
+
+    def call(mql=1, splits=8, counters=a, slots=64, programs=8):
+        return lib.oscar_history_post(
+            a, 1536, 256, 1, a, 1 << 24, a, a, a, 64, 64, a, a, a, 8, 6, programs, splits, 32, 4,
+            mql, 1 / 16, 0, good, a, a, counters, slots, a, a, a, a, None, a, 256, 256, a, 256,
+            256, a, 1 << 20, 8, None)
+
+    assert call(mql=4) == -5  # 24 query rows per task: the two-launch form covers it
+    assert call(splits=17) == -5  # above the one-round split merge
+    assert call(counters=None) == -1
+    assert call(counters=a + 2) == -4
+    assert call(slots=7) == -2  # fewer counters than programs x kv heads
+
+
 def test_status_strings():
     lib = _ext.library()
     assert lib.oscar_status_string(0) == b"ok"
