@@ -54,6 +54,8 @@ def parse_args(argv=None):
     p.add_argument("--cpu-sample", type=int, default=2, help="requests timed on the CPU oracle")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-graph", action="store_true", help="eager launches instead of HIP graphs")
+    p.add_argument("--one-launch-post", action="store_true",
+                   help="history branch and post-attention in one launch (kernels.history_post)")
     p.add_argument("--mode", default="step", choices=("step", "history", "copy"),
                    help="step: full benchmark; history: only the history-attention launches "
                         "(for rocprofv3 counters); copy: a plain device copy of --copy-mib MiB "
@@ -364,7 +366,8 @@ def main(argv=None):
         layers.append((w.k_cache.clone(), w.v_cache.clone()))
     impls = []
     for _ in layers:
-        impl = OscarAttentionImpl(6, 256, 1 / 16, 1, w.cfg, split_policy=cfg["splits"])
+        impl = OscarAttentionImpl(6, 256, 1 / 16, 1, w.cfg, split_policy=cfg["splits"],
+                                  one_launch_post=args.one_launch_post)
         impl.initialize_layer(w.rk, w.rv)
         impls.append(impl)
     ntok = w.q.shape[0]
@@ -439,7 +442,8 @@ def main(argv=None):
     # (history + split merge + path merge + window store when history_post covers the step,
     # else the history branch alone).
     hist_views = [w.layout.tensor_views(c) for c in layers]
-    one_launch = kernels.history_post_supported(w.meta, w.layout, 6, splits)
+    one_launch = impls[0].one_launch_post and kernels.history_post_supported(
+        w.meta, w.layout, 6, splits, ntok)
     qrot, rp, rl = kernels.pre_attention(w.q, w.k, w.v, hist_views[0][0], hist_views[0][1],
                                          w.meta, w.layout, 1 / 16, impls[0].rk_t, impls[0].rv_t)
     out = torch.empty(ntok, 6 * 256, dtype=torch.bfloat16, device=device)
@@ -501,6 +505,7 @@ def main(argv=None):
             "page_tokens": 768, "kernel_block_tokens": 128,
             "splits": splits, "split_tokens": split_tokens, "layers_cycled": len(layers),
             "hip_graph": graphs is not None, "seed": args.seed,
+            "one_launch_post": bool(args.one_launch_post),
         },
         "us_per_layer_step": us_step,
         "gpu_us_per_layer_step": gpu_ms / args.steps * 1e3,

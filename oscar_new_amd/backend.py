@@ -18,10 +18,12 @@ from .config import OscarConfig, choose_history_partition, choose_splits
 
 class OscarAttentionImpl:
     """Reference: backend.py:67-227. ``split_policy`` "reference" keeps config.py:84-89,
-    "mi355x" fills the 256 CUs (config.choose_splits_mi355x)."""
+    "mi355x" fills the 256 CUs (config.choose_splits_mi355x). ``one_launch_post`` runs the
+    history branch and post-attention as one launch (``kernels.history_post``) where it applies;
+    the result is the same bits either way."""
 
     def __init__(self, num_heads, head_size, scale, num_kv_heads, cfg=None,
-                 split_policy="reference", fused=True):
+                 split_policy="reference", fused=True, one_launch_post=False):
         if head_size != 256:
             raise ValueError("OSCAR requires FULL decoder attention with D256")
         if num_kv_heads <= 0 or num_heads % num_kv_heads:
@@ -35,6 +37,7 @@ class OscarAttentionImpl:
         self.cfg = cfg or OscarConfig.from_env()
         self.split_policy = split_policy
         self.fused = fused
+        self.one_launch_post = one_launch_post
         self.rk = self.rv = self.rk_cols = self.rv_cols = self.rk_t = self.rv_t = None
         self.history = self.window = None
         self.cache_identity = None
@@ -103,12 +106,13 @@ class OscarAttentionImpl:
 
         splits, split_tokens = self.partition_for(meta)
         if self.fused:
-            # BF16 branch + rotations + INT2 store; then history + merges + window in one launch
-            # (decode-sized tasks, <= 16 splits) or in two.
+            # BF16 branch + rotations + INT2 store; then history, merges + window in two
+            # launches, or (one_launch_post, decode-sized tasks, <= 16 splits) in one.
             qrot, rp, rl = kernels.pre_attention(query, key, value, self.history, self.window,
                                                  meta, meta.layout, self.scale, self.rk_t,
                                                  self.rv_t)
-            if kernels.history_post_supported(meta, meta.layout, self.num_heads, splits, n):
+            if self.one_launch_post and kernels.history_post_supported(
+                    meta, meta.layout, self.num_heads, splits, n):
                 kernels.history_post(qrot, self.history, meta, meta.layout, self.scale, splits, rp,
                                      rl, self.rv, key, value, self.window, output.view(n, -1),
                                      getattr(meta, "merged_lse", None), split_tokens=split_tokens)

@@ -65,11 +65,13 @@ CASES = [
 
 
 def _forward(c, form, splits, raw=None):
-    """One layer step in `form` ("single" or "fused" launches) on a copy of the cache."""
+    """One layer step in `form` ("single", "fused" or "fused1": history + post in one launch
+    where it applies) on a copy of the cache."""
     n = c.q.shape[0]
     raw = c.raw.clone() if raw is None else raw
     k_cache, v_cache = _views(raw, c.layout)
-    impl = OscarAttentionImpl(6, 256, 1 / 16, 1, c.layout.config, fused=form != "single")
+    impl = OscarAttentionImpl(6, 256, 1 / 16, 1, c.layout.config, fused=form != "single",
+                              one_launch_post=form == "fused1")
     impl.initialize_layer(c.rk, c.rv)
     impl.partition_for = lambda meta, s=splits: (s, 0)
     c.meta.merged_lse = torch.full((n, 6), 7.0, device=DEV)
@@ -83,9 +85,10 @@ def _forward(c, form, splits, raw=None):
 def test_fused_step_is_bitwise_the_single_launch_step(lengths, prefixes, splits):
     c = _case(lengths, prefixes, seed=7)
     want = _forward(c, "single", splits)
-    got = _forward(c, "fused", splits)
-    for a, b in zip(want, got):
-        assert torch.equal(a, b)
+    for form in ("fused", "fused1"):
+        got = _forward(c, form, splits)
+        for a, b in zip(want, got):
+            assert torch.equal(a, b), form
 
 
 @pytest.mark.parametrize("lengths,prefixes,partition", [
@@ -100,11 +103,11 @@ def test_token_bounded_fused_step_against_dense_reference(lengths, prefixes, par
     c = _case(lengths, prefixes, seed=13)
     n = c.q.shape[0]
     outs = []
-    for fused in (True, False):
+    for fused, one in ((True, True), (False, False), (True, False)):
         raw = c.raw.clone()
         k_cache, v_cache = _views(raw, c.layout)
         impl = OscarAttentionImpl(6, 256, 1 / 16, 1, c.layout.config, split_policy="mi355x",
-                                  fused=fused)
+                                  fused=fused, one_launch_post=one)
         impl.initialize_layer(c.rk, c.rv)
         impl.partition_for = lambda meta, pt=partition: pt
         c.meta.merged_lse = torch.empty((n, 6), device=DEV)
@@ -112,8 +115,9 @@ def test_token_bounded_fused_step_against_dense_reference(lengths, prefixes, par
         impl.forward(None, c.q, c.k, c.v, (k_cache, v_cache), c.meta, out)
         torch.cuda.synchronize()
         outs.append((out.view(torch.int16).cpu(), c.meta.merged_lse.cpu(), raw.cpu(), out))
-    for a, b in zip(outs[0][:3], outs[1][:3]):
-        assert torch.equal(a, b)
+    for other in outs[1:]:
+        for a, b in zip(outs[0][:3], other[:3]):
+            assert torch.equal(a, b)
     want, want_lse = [], []
     for qi, ki, vi, p in zip(c.qs, c.ks, c.vs, c.prefixes):
         o, l = O.hybrid_reference(bits(qi), bits(ki), bits(vi), p, bits(c.rk), bits(c.rv),
