@@ -1,19 +1,80 @@
-"""Per-layer launch order of the OSCAR INT2 attention path (vLLM-free).
+"""Per-layer launch order of the OSCAR INT2 attention path.
 
-Reference: oscar_ascend/backend.py:67-227 (``OscarAttentionImpl``). The vLLM class plumbing
-(AttentionBackend registration, vllm_config validation) is out of scope; what is kept is the
-forward contract: same arguments, same kernel order, no host reads, the window store last
-(it must follow both attention branches because a long current chunk wraps the ring).
-Initial prefill without history (the reference's Ascend FIA call) is not provided: the
-INT2 path below also serves it, with one split.
+Reference: oscar_ascend/backend.py:13-227. ``OscarAttentionImpl`` keeps the forward contract:
+same arguments, same kernel order, no host reads, the window store last (it must follow both
+attention branches because a long current chunk wraps the ring). ``OscarAttentionBackend``
+and ``validate_vllm_config`` are the vLLM-facing class and checks (backend.py:13-64), written
+against duck-typed vLLM objects so that they import without vLLM. Initial prefill (the
+reference's Ascend FIA call, ``meta.initial_prefill``) runs through the INT2 path below with
+an empty history: the BF16 branch is the causal attention over the request's own tokens.
 """
 
 from __future__ import annotations
+
+import os
 
 import torch
 
 from . import kernels
 from .config import OscarConfig, choose_history_partition, choose_splits
+
+
+class OscarAttentionBackend:
+    """Reference backend.py:13-38: the backend class the plugin routes to."""
+
+    forward_includes_kv_cache_update = True
+
+    @staticmethod
+    def get_name():
+        return "CUSTOM"
+
+    @staticmethod
+    def get_impl_cls():
+        return OscarAttentionImpl
+
+    @staticmethod
+    def get_builder_cls():
+        from .metadata import OscarMetadataBuilder
+
+        return OscarMetadataBuilder
+
+    @staticmethod
+    def get_kv_cache_shape(num_blocks, block_size, num_kv_heads, head_size, cache_dtype_str="auto"):
+        """(K, V) stripes of bf16 [num_blocks, block_size, num_kv_heads, head_size] each: the
+        native paged layout whose K stripe holds the INT2 slots and V stripe the windows."""
+        return (2, num_blocks, block_size, num_kv_heads, head_size)
+
+    @staticmethod
+    def copy_blocks(*args, **kwargs):
+        raise NotImplementedError("OSCAR ring ownership does not support shared/copied request pages")
+
+    @staticmethod
+    def swap_blocks(*args, **kwargs):
+        raise NotImplementedError("OSCAR supports native recompute preemption, not KV swapping")
+
+
+def validate_vllm_config(config):
+    """Reference backend.py:41-64, with the ROCm runner's names: the configurations the INT2
+    path does not support are rejected with the reference's reasons."""
+    if config.cache_config.enable_prefix_caching:
+        raise ValueError("OSCAR requires --no-enable-prefix-caching (BF16 ring owner isolation)")
+    if config.cache_config.cache_dtype not in ("auto", "bfloat16"):
+        raise ValueError("Use --kv-cache-dtype auto with OSCAR_AMD_ENABLED=1")
+    if config.model_config.dtype != torch.bfloat16:
+        raise ValueError("OSCAR target model must use BF16 activation/cache dtype")
+    if getattr(config, "kv_transfer_config", None) is not None:
+        raise ValueError("KV transfer is not supported by this OSCAR layout")
+    pc = config.parallel_config
+    if (getattr(pc, "decode_context_parallel_size", 1) != 1
+            or getattr(pc, "prefill_context_parallel_size", 1) != 1):
+        raise ValueError("OSCAR currently requires PCP=DCP=1")
+    if getattr(pc, "enable_dbo", False):
+        raise ValueError("DBO requires separate metadata buffer sets and is not supported")
+    if os.getenv("VLLM_USE_V2_MODEL_RUNNER", "0") == "1":
+        raise ValueError("This OSCAR adapter targets the v1 model runner")
+    hf = config.model_config.hf_text_config
+    if getattr(hf, "head_dim", None) != 256:
+        raise ValueError("This implementation targets D256 full attention")
 
 
 class OscarAttentionImpl:

@@ -38,6 +38,8 @@ class OscarMetadata:
     max_seq_len: int | None = None
     merged_lse: torch.Tensor | None = None
     total_seq_len: int | None = None  # host-side sum of seq_lens (MI355X split partition)
+    initial_prefill: bool = False  # every request starts here (host scheduler state)
+    query_ends: list | None = None  # cumulative query ends (host), for initial prefill
 
 
 class OscarMetadataBuilder:
@@ -97,9 +99,20 @@ class OscarMetadataBuilder:
                               source_table=common.block_table_tensor, table=self.table,
                               copy_columns=copy_columns)
         seq_cpu = getattr(common, "seq_lens_cpu", None)
+        # Reference metadata.py:120-128: only the scheduler's host state marks an initial
+        # prefill (no device read); its query ends come from the host copy of qstarts.
+        state = getattr(common, "attn_state", None)
+        initial = not dummy and getattr(state, "name", state) == "PrefillNoCache"
+        query_ends = None
+        if initial:
+            qcpu = getattr(common, "query_start_loc_cpu", None)
+            if qcpu is None or getattr(qcpu, "device", None) is None or qcpu.device.type != "cpu":
+                raise ValueError("query_start_loc_cpu must really be on CPU")
+            query_ends = qcpu[1 : nr + 1].tolist()
         return OscarMetadata(
             self.qstarts, self.seqs, self.table, self.slots, self.counts, nr, nt,
             common.max_query_len, self.max_reqs, self.layout, is_dummy=dummy, tasks=self.tasks,
             task_count=self.task_count, max_seq_len=getattr(common, "max_seq_len", None),
             total_seq_len=None if dummy or seq_cpu is None else int(seq_cpu[:nr].sum()),
+            initial_prefill=initial, query_ends=query_ends,
         )
