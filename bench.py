@@ -40,6 +40,9 @@ CONFIGS = {
                desc="ragged MTP: B64, ctx log-uniform [256, 131072], 4 query tokens each"),
     "c5": dict(batch=4, context=262144, qlen=1, ragged=False, splits="mi355x",
                desc="long context: B4 x 262144 ctx, adaptive splits"),
+    # --mode prefill only (initial prefill, SURVEY next row): every token is a query token.
+    "p1": dict(batch=4, context=4096, qlen=4096, ragged=False, splits="reference",
+               desc="initial prefill: B4 x 4096 tokens, GQA 6:1, D256, causal"),
 }
 
 
@@ -56,10 +59,11 @@ def parse_args(argv=None):
     p.add_argument("--no-graph", action="store_true", help="eager launches instead of HIP graphs")
     p.add_argument("--one-launch-post", action="store_true",
                    help="history branch and post-attention in one launch (kernels.history_post)")
-    p.add_argument("--mode", default="step", choices=("step", "history", "copy"),
+    p.add_argument("--mode", default="step", choices=("step", "history", "copy", "prefill"),
                    help="step: full benchmark; history: only the history-attention launches "
                         "(for rocprofv3 counters); copy: a plain device copy of --copy-mib MiB "
-                        "(counter calibration)")
+                        "(counter calibration); prefill: the initial-prefill launch on a "
+                        "prefill config (--config p1)")
     p.add_argument("--copy-mib", type=int, default=1024)
     return p.parse_args(argv)
 
@@ -340,6 +344,41 @@ def read_traffic(kernel, config):
     return None
 
 
+def prefill_measurement(args, w, device):
+    """Initial-prefill launch alone (HIP events): useful causal FLOPs (QK and PV over each
+    request's own tokens, 4 flop per query-key pair and dim) against the bf16 MFMA peak."""
+    import torch
+
+    from oscar_new_amd import kernels
+
+    ntok = w.q.shape[0]
+    if any(p != 0 for p in w.prefixes):
+        raise SystemExit("bench.py --mode prefill needs a config whose requests have no prefix")
+    w.meta.initial_prefill = True
+    _, win = w.layout.tensor_views((w.k_cache, w.v_cache))
+    out = torch.empty(ntok, 6 * 256, dtype=torch.bfloat16, device=device)
+    run = lambda: kernels.prefill_attention(w.q, w.k, w.v, win, w.meta, w.layout, 1 / 16, out)
+    for _ in range(max(1, args.warmup)):
+        run()
+    torch.cuda.synchronize()
+    evs = []
+    for _ in range(args.steps):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        run()
+        b.record()
+        evs.append((a, b))
+    torch.cuda.synchronize()
+    us = statistics.mean(a.elapsed_time(b) for a, b in evs) * 1e3
+    pairs = sum(s * (s + 1) // 2 for s in w.seqs)
+    flops = 4.0 * pairs * 6 * 256
+    print(json.dumps({"mode": "prefill", "config": args.config, "tokens": ntok,
+                      "us": us, "tflops": flops / (us * 1e-6) / 1e12,
+                      "mfma_bf16_peak_tflops": 2500.0,
+                      "frac": flops / (us * 1e-6) / 1e12 / 2500.0}))
+    return 0
+
+
 def main(argv=None):
     args = parse_args(argv)
     if args.gpus != 1:
@@ -377,6 +416,8 @@ def main(argv=None):
     def step(i):
         impls[i].forward(None, w.q, w.k, w.v, layers[i], w.meta, outputs[i])
 
+    if args.mode == "prefill":
+        return prefill_measurement(args, w, device)
     if args.mode == "history":
         qrot = kernels.rotate(w.q, w.rk)
         views = [w.layout.tensor_views(c) for c in layers]

@@ -227,6 +227,27 @@ int oscar_post_attention(const float* history_partials, const float* history_lse
                          void* stream);
 
 /*
+ * prefill_attention -- initial prefill (every request's history empty): replaces the
+ * reference's fused-infer call (oscar_ascend/backend.py:175-193: causal attention of each
+ * request over its own current tokens, output rows past num_actual_tokens zeroed). It runs
+ * the BF16 branch of oscar_attention_partials (raw, one split) and writes its rows straight
+ * to output (bf16 [n, hq*256], 16-byte aligned) with the bits merge_splits + rotate +
+ * merge_paths give a row whose history branch is empty; merged_lse (optional) gets the LSE.
+ * Rows of tokens at or past counts[1] are zeroed (LSE -inf). Arguments as
+ * oscar_attention_partials; key/value rows contiguous and 16-byte aligned.
+ */
+int oscar_prefill_attention(const void* query, int64_t q_s0, int64_t q_s1, const void* key,
+                            int64_t k_s0, int64_t k_s1, const void* value, int64_t v_s0,
+                            int64_t v_s1, const void* window, int64_t window_elems,
+                            const int32_t* qstarts, const int32_t* seq_lens,
+                            const int32_t* block_tables, int64_t table_stride,
+                            int64_t table_columns, const int32_t* counts, const int32_t* tasks,
+                            const int32_t* task_count, int64_t n, int64_t hq, int64_t programs,
+                            int32_t block_n, int32_t query_tile, int32_t max_query_len,
+                            float scale, const oscar_layout* layout, void* output,
+                            float* merged_lse, void* stream);
+
+/*
  * history_post -- the history branch and post_attention in ONE launch (no reference
  * counterpart: it replaces oscar_attention_partials(raw = 0) followed by
  * oscar_post_attention, with the same output and merged_lse bits). The arguments are those of

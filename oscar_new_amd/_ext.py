@@ -89,6 +89,14 @@ SIGNATURES = {
         _P, _I64, _P, _P, _P, _I64, _I64,  # window, elems, qstarts, seq_lens, table, stride, max_reqs
         POINTER(OscarLayout), _P,
     ],
+    "oscar_prefill_attention": [
+        _P, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64,  # query, key, value (+ row strides)
+        _P, _I64,  # window
+        _P, _P, _P, _I64, _I64,  # qstarts, seq_lens, block_tables, stride, columns
+        _P, _P, _P,  # counts, tasks, task_count
+        _I64, _I64, _I64, _I32, _I32, _I32, _F,  # n hq programs bn qt mql scale
+        POINTER(OscarLayout), _P, _P, _P,  # layout, output, merged_lse, stream
+    ],
     "oscar_history_post": [
         _P, _I64, _I64, _I64,  # query (rotated)
         _P, _I64,  # history, bytes

@@ -165,6 +165,19 @@ class OscarAttentionImpl:
         if n == 0:
             return output
 
+        if getattr(meta, "initial_prefill", False):
+            # Reference backend.py:171-193 + 225-226: INT2 store, causal attention over each
+            # request's own tokens (the fused-infer call), then the window store.
+            krot = kernels.rotate(key, self.rk_cols)
+            vrot = kernels.rotate(value, self.rv_cols)
+            kernels.store_int2(krot, vrot, self.history, meta.slot_mapping, meta.counts,
+                               meta.layout)
+            kernels.prefill_attention(query, key, value, self.window, meta, meta.layout,
+                                      self.scale, output.view(n, -1),
+                                      getattr(meta, "merged_lse", None))
+            kernels.store_windows(key, value, self.window, meta, meta.layout)
+            return output
+
         splits, split_tokens = self.partition_for(meta)
         if self.fused:
             # BF16 branch + rotations + INT2 store; then history, merges + window in two

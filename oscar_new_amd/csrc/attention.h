@@ -40,6 +40,10 @@ struct AttnArgs {
   int32_t split_tokens;  // history branch: 0 = kernels.py:368-370 rule, else token-bounded
   FastDiv g_div;  // division by g (query heads per kv head)
   float scale_log2;
+  // BF16 branch written as the layer output (initial prefill, no history): bf16 rows
+  // [n][hq][256] and, when non-null, their LSE [n][hq].
+  uint16_t* direct_out;
+  float* direct_lse;
 };
 
 struct Task {

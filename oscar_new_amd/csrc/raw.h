@@ -87,7 +87,9 @@ constexpr int finish_lds_bytes() {
   return 4 * 16 * kHeadDim * 4 + (2 * 4 + 3) * RT * 16 * 4;
 }
 
-template <int RT>
+// kDirect: the normalized rows go to a.direct_out as bf16 (and the LSE to a.direct_lse): the
+// bits merge_paths gives a row whose history branch is empty.
+template <int RT, bool kDirect = false>
 __device__ void finish(const AttnArgs& a, const Task& t, int head, int split, State<RT>& st,
                        uint8_t* lds) {
   typedef float OutWave[16][kHeadDim];
@@ -153,14 +155,25 @@ __device__ void finish(const AttnArgs& a, const Task& t, int head, int split, St
                           *reinterpret_cast<const f32x4*>(&s_o[1][row16][d]) +
                           *reinterpret_cast<const f32x4*>(&s_o[2][row16][d]) +
                           *reinterpret_cast<const f32x4*>(&s_o[3][row16][d]);
-        *reinterpret_cast<float4*>(a.partials + orow * kHeadDim + d) =
-            make_float4(sum[0] / den, sum[1] / den, sum[2] / den, sum[3] / den);
+        if constexpr (kDirect) {
+          const int64_t out_row = ri.token * a.hq + ri.qhead;
+          *reinterpret_cast<uint2*>(a.direct_out + out_row * kHeadDim + d) =
+              make_uint2(pack_bf16x2(sum[0] / den, sum[1] / den),
+                         pack_bf16x2(sum[2] / den, sum[3] / den));
+        } else {
+          *reinterpret_cast<float4*>(a.partials + orow * kHeadDim + d) =
+              make_float4(sum[0] / den, sum[1] / den, sum[2] / den, sum[3] / den);
+        }
       }
     }
   }
   if (threadIdx.x < RT * 16) {
     const RowInfo ri = row_info(a, t, head, threadIdx.x);
-    if (ri.valid) a.lse[(ri.token * a.hq + ri.qhead) * a.splits + split] = s_lse[threadIdx.x];
+    if constexpr (kDirect) {
+      if (ri.valid && a.direct_lse) a.direct_lse[ri.token * a.hq + ri.qhead] = s_lse[threadIdx.x];
+    } else {
+      if (ri.valid) a.lse[(ri.token * a.hq + ri.qhead) * a.splits + split] = s_lse[threadIdx.x];
+    }
   }
 }
 
@@ -234,7 +247,7 @@ __device__ __forceinline__ void raw_load_block(const AttnArgs& a, const Task& t,
 
 // One workgroup of the BF16 branch: (task, kv head, split).
 // `smem`: finish_lds_bytes<RT>() bytes of 16-byte aligned LDS.
-template <int RT>
+template <int RT, bool kDirect = false>
 __device__ __forceinline__ void raw_block(const AttnArgs& a, int task, int head, int split,
                                           uint8_t* smem) {
   Task t;
@@ -332,7 +345,7 @@ __device__ __forceinline__ void raw_block(const AttnArgs& a, int task, int head,
     }
     if (more) cur = nxt;
   }
-  finish<RT>(a, t, head, split, st, smem);
+  finish<RT, kDirect>(a, t, head, split, st, smem);
 }
 
 }  // namespace oscar

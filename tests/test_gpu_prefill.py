@@ -1,0 +1,67 @@
+"""Initial prefill (reference backend.py:175-193: the fused-infer call, causal attention of each
+request over its own tokens, rows past num_actual_tokens zeroed) through
+kernels.prefill_attention, on MI355X.
+
+* Bit for bit against the general INT2 path of the same step (empty history): output, merged
+  LSE and every cache byte (INT2 slots of the step's tokens, BF16 windows).
+* Against the oracle's dense reference (hybrid_reference with no prefix = causal attention in
+  fp64 over bf16 inputs): the reference test's atol 0.035 / rtol 0.04
+  (tests/test_npu_kernels.py:194), mean-abs <= 2e-3, LSE within 2e-2.
+* Padded rows past the token count: zero output, LSE -inf.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from oscar_new_amd.config import OscarConfig, task_capacity
+from oscar_new_amd import kernels
+from tests._state import bits
+from tests.test_gpu_fused import _case, _forward
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+CASES = [
+    ([1], 0),  # one token
+    ([37, 130, 261], 0),  # ragged requests, several query tiles each
+    ([1500], 0),  # one long prompt: the ring wraps in the window store
+    ([3, 64, 70], 2),  # padded rows past the token count
+]
+
+
+@pytest.mark.parametrize("lengths,pad", CASES)
+def test_prefill_matches_int2_path_and_dense_reference(lengths, pad):
+    c = _case(lengths, [0] * len(lengths), seed=41, cfg=OscarConfig(sink_tokens=4,
+                                                                    recent_tokens=64))
+    print(f"[prefill] lengths {lengths} pad {pad}", flush=True)
+    if pad:
+        c.q = torch.cat([c.q, torch.randn(pad, 6, 256, device=DEV).bfloat16()])
+        c.k = torch.cat([c.k, torch.randn(pad, 1, 256, device=DEV).bfloat16()])
+        c.v = torch.cat([c.v, torch.randn(pad, 1, 256, device=DEV).bfloat16()])
+        qt = c.layout.config.queries_per_tile
+        c.meta.tasks = torch.empty((task_capacity(c.q.shape[0], c.meta.max_num_reqs, qt), 2),
+                                   device=DEV, dtype=torch.int32)
+        kernels.prepare_tasks(c.meta.query_start_loc, c.meta.counts, c.meta.tasks,
+                              c.meta.task_count, c.meta.max_num_reqs, qt)
+    n = c.q.shape[0]
+    c.meta.initial_prefill = False
+    want = _forward(c, "single", 1)
+    c.meta.initial_prefill = True
+    got = _forward(c, "single", 1)
+    for a, b in zip(want, got):
+        assert torch.equal(a, b)
+    out = got[0].view(torch.bfloat16).float().numpy().reshape(n, 6, 256)
+    lse = got[1].numpy()
+    if pad:
+        assert not out[n - pad:].any() and np.isneginf(lse[n - pad:]).all()
+    start = 0
+    for qi, ki, vi in zip(c.qs, c.ks, c.vs):
+        rows = slice(start, start + qi.shape[0])
+        start += qi.shape[0]
+        o, l = O.hybrid_reference(bits(qi), bits(ki), bits(vi), 0, bits(c.rk), bits(c.rv),
+                                  c.layout.config)
+        np.testing.assert_allclose(out[rows], o, atol=0.035, rtol=0.04)
+        assert np.abs(out[rows] - o).mean() <= 2e-3
+        np.testing.assert_allclose(lse[rows], l, atol=2e-2, rtol=0)
