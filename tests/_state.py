@@ -34,13 +34,13 @@ def oracle_geometry(layout):
                       cfg.head_dim, cfg.sink_tokens, cfg.recent_tokens, cfg.speculative_tokens)
 
 
-def make_state(lengths, prefix_lengths, cfg=None, pages=20, max_reqs=8, device="cuda"):
-    layout = CacheLayout(768, config=cfg or OscarConfig())
+def make_state(lengths, prefix_lengths, cfg=None, pages=20, max_reqs=8, device="cuda", page=768,
+               kv_heads=1):
+    layout = CacheLayout(page, kv_heads=kv_heads, config=cfg or OscarConfig())
     conv = pages * CONV_BYTES_PER_PAGE
     stripe = pages * layout.stripe_page_bytes
     raw = torch.full((conv + 2 * stripe,), 0x5A, device=device, dtype=torch.uint8)
-    k = raw[conv : conv + stripe].view(torch.bfloat16).view(-1, 128, 1, 256)
-    v = raw[conv + stripe :].view(torch.bfloat16).view(-1, 128, 1, 256)
+    k, v = native_views(raw, layout, pages)
     history, window = layout.tensor_views((k, v))
     free = list(range(1, pages))
     free = free[::2] + free[1::2]  # non-monotonic physical pages; page 0 never owned
@@ -74,6 +74,17 @@ def make_state(lengths, prefix_lengths, cfg=None, pages=20, max_reqs=8, device="
         task_count=torch.zeros(1, device=device, dtype=torch.int32),
     )
     return layout, raw, history, window, meta, tables
+
+
+def native_views(raw, layout, pages=20):
+    """Native (K, V) cache views [blocks, 128, kv heads, 256] of a make_state byte buffer
+    (conv | K | V)."""
+    stripe = pages * layout.stripe_page_bytes
+    conv = raw.numel() - 2 * stripe
+    shape = (-1, layout.kernel_block_tokens, layout.kv_heads, layout.config.head_dim)
+    k = raw[conv : conv + stripe].view(torch.bfloat16).view(shape)
+    v = raw[conv + stripe :].view(torch.bfloat16).view(shape)
+    return k, v
 
 
 def prepare_prefix(k, v, rk, rv, history, window, meta, tables, layout, prefixes, device="cuda"):
