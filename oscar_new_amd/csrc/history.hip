@@ -573,6 +573,13 @@ __global__ __launch_bounds__(kThreads, 3 - RT) void history_kernel(const AttnArg
 __host__ __device__ constexpr int pair_token(int ga, int e) {
   return 32 * ((e >> 2) & 1) + 16 * (e >> 3) + 4 * ga + (e & 3);
 }
+// LDS record slot of chunk token t in the paired kernel: token bits 2-3 XOR bits 4-5 (its own
+// inverse). With 144-byte records, tokens 16 apart share banks; a transposed V read takes
+// tokens t, t + 16, t + 32 and t + 48 at once, which this map spreads over four bank groups
+// (4-way conflicts become 2-way, the floor for this stride). The DMA places token
+// pair_slot(r) in slot r, so the copy itself is unchanged.
+__host__ __device__ constexpr int pair_slot(int t) { return t ^ (((t >> 4) & 3) << 2); }
+static_assert(pair_slot(pair_slot(45)) == 45 && pair_slot(21) == 17, "pair_slot is an involution");
 
 // kFinish: the two-launch step's history launch (finish.h): the grid has one more z slice
 // (window stores, padded rows), unused split slots are left unwritten (the merge reads only
@@ -613,13 +620,13 @@ __device__ __forceinline__ void history_pair_body(const AttnArgs& a, const Finis
   const int nmine = nchunk > wave ? (nchunk - wave + 3) >> 2 : 0;  // chunks wave + 4 j
   const int kb_first = p_lo >> a.L.bk_shift;
 
-  // ---- DMA plan (as in the general kernel).
+  // ---- DMA plan (as in the general kernel, record slot r holding token pair_slot(r)).
   const uint32_t tok_bytes = static_cast<uint32_t>(a.L.kv_heads) * kSlot;
   uint32_t voff[kDma];
 #pragma unroll
   for (int i = 0; i < kDma; ++i) {
     const int c = 64 * i + lane;
-    voff[i] = static_cast<uint32_t>(c / kPieces) * tok_bytes + 16 * (c % kPieces);
+    voff[i] = static_cast<uint32_t>(pair_slot(c / kPieces)) * tok_bytes + 16 * (c % kPieces);
   }
   const uint32_t my_ring = lds_addr(s_ring) + wave * 2 * kStageBytes;
   const uint32_t in_kb_mask = static_cast<uint32_t>(a.L.bk - 1);
@@ -742,14 +749,25 @@ __device__ __forceinline__ void history_pair_body(const AttnArgs& a, const Finis
     if (nmine > 1) issue(1, 1);
   }
 
-  // ---- per-lane LDS offsets inside a stage (record r starts at kSkew + 144 r)
+  // ---- per-lane LDS offsets inside a stage (token t's record starts at kSkew + 144
+  // pair_slot(t))
   const int side = n >> 3;  // 0: X tokens, 1: Y tokens of each pair tile
-  // QK A operand: token i + 16 (G&1) of the pair tile, code dwords 4b + 2 (G>>1), +1.
-  const int k_off = kSkew + kRec * (n + 16 * (g & 1)) + 8 * (g >> 1);
-  // Scale|zero of this lane's score tokens 32 pt + 16 side + 4 g + v.
-  const int sz_off = kSkew + kRec * (16 * side + 4 * g) + 64;
+  // QK A operand: token i + 16 (G&1) + 32 pt of the pair tile, code dwords 4b + 2 (G>>1), +1.
+  int k_off[2];
+#pragma unroll
+  for (int pt = 0; pt < 2; ++pt)
+    k_off[pt] = kSkew + kRec * pair_slot(n + 16 * (g & 1) + 32 * pt) + 8 * (g >> 1);
+  // Scale|zero of this lane's score tokens 32 h + 16 side + 4 g + v (v < 4: bits 0-1 are
+  // left alone by pair_slot, so v stays an immediate offset).
+  int sz_off[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h)
+    sz_off[h] = kSkew + kRec * pair_slot(32 * h + 16 * side + 4 * g) + 64;
   // Transposed V reads: token rows T(2 (g&1), n) and T(2 (g&1) + 1, n) = T(2 (g&1), n) + 4.
-  const int v_off = kSkew + kRec * pair_token(2 * (g & 1), n) + kVector;
+  int v_off[2];
+#pragma unroll
+  for (int r = 0; r < 2; ++r)
+    v_off[r] = kSkew + kRec * pair_slot(pair_token(2 * (g & 1), n) + 4 * r) + kVector;
 
   float m = -INFINITY, psum = 0.f, zsum = 0.f;
   f32x4 o[16];  // o[2c + par]: rows 4g + v, dim 32c + 2n + par (units of c/2)
@@ -766,8 +784,7 @@ __device__ __forceinline__ void history_pair_body(const AttnArgs& a, const Finis
       i32x8 kf[2];
 #pragma unroll
       for (int pt = 0; pt < 2; ++pt) {
-        const uint32_t* kp =
-            reinterpret_cast<const uint32_t*>(st + k_off + 32 * kRec * pt + 16 * b);
+        const uint32_t* kp = reinterpret_cast<const uint32_t*>(st + k_off[pt] + 16 * b);
         const uint32_t w0 = kp[0], w1 = kp[1];
         kf[pt] = i32x8{even_codes(w0), odd_codes(w0), even_codes(w1), odd_codes(w1), 0, 0, 0, 0};
       }
@@ -779,7 +796,7 @@ __device__ __forceinline__ void history_pair_body(const AttnArgs& a, const Finis
     uint32_t ksz[8], vsz[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      const int off = sz_off + kRec * (32 * (e >> 2) + (e & 3));
+      const int off = sz_off[e >> 2] + kRec * (e & 3);
       ksz[e] = *reinterpret_cast<const uint32_t*>(st + off);
       vsz[e] = *reinterpret_cast<const uint32_t*>(st + off + kVector);
     }
@@ -851,9 +868,10 @@ __device__ __forceinline__ void history_pair_body(const AttnArgs& a, const Finis
     // O += P V over the chunk's 64 tokens, 32 dims (16 dim pairs) per transposed read pair.
 #pragma unroll
     for (int c = 0; c < 8; ++c) {
-      const i32x2 r0 = __builtin_amdgcn_ds_read_tr4_b64_v2i32((lds_i32x2_ptr_t)(st + v_off + 8 * c));
+      const i32x2 r0 =
+          __builtin_amdgcn_ds_read_tr4_b64_v2i32((lds_i32x2_ptr_t)(st + v_off[0] + 8 * c));
       const i32x2 r1 =
-          __builtin_amdgcn_ds_read_tr4_b64_v2i32((lds_i32x2_ptr_t)(st + v_off + 4 * kRec + 8 * c));
+          __builtin_amdgcn_ds_read_tr4_b64_v2i32((lds_i32x2_ptr_t)(st + v_off[1] + 8 * c));
       const i32x8 be = i32x8{even_codes(r0[0]), even_codes(r0[1]), even_codes(r1[0]),
                              even_codes(r1[1]), 0, 0, 0, 0};
       const i32x8 bo = i32x8{odd_codes(r0[0]), odd_codes(r0[1]), odd_codes(r1[0]),
