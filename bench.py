@@ -214,7 +214,8 @@ def split_partial_bytes(w, splits, split_tokens):
 
 
 def time_store(device, args, steps):
-    """rotate + clip-search + INT2 pack of 4096 tokens into permuted pages."""
+    """rotate + clip-search + INT2 pack of 4096 tokens into permuted pages
+    (device time per call from HIP-graph replays)."""
     import torch
 
     from oscar_new_amd import kernels
@@ -247,18 +248,33 @@ def time_store(device, args, steps):
         once()
     kr, vr = kernels.rotate(k, rk), kernels.rotate(v, rv)
     torch.cuda.synchronize()
-    full = []
-    for _ in range(steps):
-        e = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
-        e[0].record()
-        once()
-        e[1].record()
-        kernels.store_int2(kr, vr, history, slots, counts, layout)
-        e[2].record()
-        full.append(e)
-    torch.cuda.synchronize()
-    t_full = statistics.median(x[0].elapsed_time(x[1]) for x in full) * 1e3
-    t_store = statistics.median(x[1].elapsed_time(x[2]) for x in full) * 1e3
+
+    # Device time without host submission gaps: each form is captured `reps` times in one
+    # HIP graph, and the graph's replays are timed with events on the capture stream.
+    reps = 10
+    stream = torch.cuda.Stream()
+
+    def timed(fn):
+        graph = torch.cuda.CUDAGraph()
+        stream.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.graph(graph, stream=stream):
+            for _ in range(reps):
+                fn()
+        torch.cuda.synchronize()
+        with torch.cuda.stream(stream):
+            graph.replay()
+            times = []
+            for _ in range(max(1, steps // reps)):
+                a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                a.record(stream)
+                graph.replay()
+                b.record(stream)
+                times.append((a, b))
+        torch.cuda.synchronize()
+        return statistics.median(a.elapsed_time(b) for a, b in times) * 1e3 / reps
+
+    t_full = timed(once)
+    t_store = timed(lambda: kernels.store_int2(kr, vr, history, slots, counts, layout))
     alg = n * (2 * 512) + 2 * 256 * 256 * 2 + n * 136 + n * 8
     return {
         "workload": "c2: 4096 tokens x 1 kv head, D256, 2% outlier channels x10, seeded QR "

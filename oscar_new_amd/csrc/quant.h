@@ -138,17 +138,51 @@ __device__ __forceinline__ void quantize_store(const float x[4], int mode, float
   if (mode == OSCAR_CLIP_FACTOR) {
     thr = maxabs * factor;
   } else if (mode == OSCAR_CLIP_SEARCH) {
+    // The uniform values of candidate i (threshold, fp16 zero and scale, 1 / scale: the
+    // arithmetic of quantize_clipped) are computed once, by lane i, and read back per
+    // candidate, instead of by every lane for every candidate.
+    const int ci = lane & 7;
+    float fc = search_factor(0);
+#pragma unroll
+    for (int i = 1; i < 8; ++i) fc = ci == i ? search_factor(i) : fc;
+    const float tc = maxabs * fc;
+    const float lo = clamp1(mn, tc), hi = clamp1(mx, tc);
+    float spread = (hi - lo) / 3.0f;
+    spread = spread < 6.103515625e-05f ? 6.103515625e-05f : spread;
+    const float zc = f16_bits_to_float(float_to_f16_bits(lo));
+    const float sc = f16_bits_to_float(float_to_f16_bits(spread));
+    const float rc = 1.0f / sc;
     float best_err = 0.f;
     int best = 0;
+#pragma unroll
     for (int i = 0; i < 8; ++i) {
-      const float t = maxabs * search_factor(i);
-      float xi[4];
-      clamp4(x, t, xi);
-      const Quantized q = quantize_clipped(xi, clamp1(mn, t), clamp1(mx, t));
+      const float t = lane_value(tc, i), zf = lane_value(zc, i), sf = lane_value(sc, i);
+      const float r = lane_value(rc, i);
+      float xi[4], y[4];
+      // Clip (one median-of-three per element: the same value as the min/max pair for the
+      // finite inputs here).
+#pragma unroll
+      for (int e = 0; e < 4; ++e) xi[e] = __builtin_amdgcn_fmed3f(x[e], -t, t);
+      // As quantize_clipped, with the reciprocal product fused into its + 0.5 and a wider
+      // test for the IEEE fallback (any y within 2^-16 of an integer): an estimate that far
+      // from 1, 2 and 3 truncates to the code of the exact quotient, and codes can only be
+      // redone exactly more often, never less.
+      bool near = false;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        y[e] = __builtin_fmaf(xi[e] - zf, r, 0.5f);
+        near |= fabsf(y[e] - rintf(y[e])) < 1.52587890625e-05f;
+      }
+      if (__any(near)) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) y[e] = (xi[e] - zf) / sf + 0.5f;
+      }
       float sq[4];
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const float dec = static_cast<float>(q.code[e]) * q.sf + q.zf;
+        int c = static_cast<int>(y[e]);
+        c = c < 0 ? 0 : (c > 3 ? 3 : c);
+        const float dec = static_cast<float>(c) * sf + zf;
         const float err = x[e] - dec;
         sq[e] = err * err;
       }

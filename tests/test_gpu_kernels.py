@@ -63,6 +63,31 @@ def test_rotation_sizes_contiguous(rows):
     assert (got != want).mean() < 0.02
 
 
+@pytest.mark.parametrize("tokens,heads,layout", [
+    (4096, 1, "rows"),  # the store benchmark's shape, R row-major
+    (1029, 2, "cols"),  # ragged row count, two heads, R column-contiguous
+    (8200, 1, "rows"),  # more 16-row blocks than workgroups: each workgroup loops
+    (700, 3, "strided"),  # strided x (every other head of a [700, 6, 256] buffer)
+])
+def test_rotation_tiled_is_bitwise_the_small_kernel(tokens, heads, layout):
+    # From 1024 rows on, rotate stages R in LDS (rotate_tiled_kernel); slices below that
+    # size take the per-tile kernel. Same operands and k order: the same bits.
+    g = torch.Generator().manual_seed(tokens)
+    r = _qr_bf16(5)
+    if layout == "cols":
+        r = r.T.contiguous().T  # column-contiguous view of the same matrix
+    if layout == "strided":
+        x = torch.randn(tokens, 2 * heads, 256, generator=g).bfloat16().to(DEV)[:, ::2]
+    else:
+        x = torch.randn(tokens, heads, 256, generator=g).bfloat16().to(DEV)
+    assert x.shape[0] * x.shape[1] >= 1024
+    got = kernels.rotate(x, r)
+    step = 1000 // heads
+    want = torch.cat([kernels.rotate(x[i : i + step], r) for i in range(0, tokens, step)])
+    torch.cuda.synchronize()
+    assert torch.equal(got.view(torch.int16), want.view(torch.int16))
+
+
 # ------------------------------------------------------------------ store_int2 / unpack
 
 
@@ -91,6 +116,15 @@ def test_store_bytes_bit_exact_and_sentinels(mode, ratio):
     k[0].zero_()
     k[1].fill_(0.5)
     k[2].fill_(1e-12)
+    # Values on half- and quarter-step grids put (x - zero) / scale + 0.5 exactly on 1, 2
+    # and 3 for many clip thresholds: the quotients the fast path must hand to IEEE division.
+    idx = torch.arange(256)
+    g = torch.Generator().manual_seed(5)
+    for row, (mod, step, off) in enumerate([(7, 0.5, 3), (13, 0.25, 6), (4, 1.0, 0),
+                                            (9, 0.5, 4), (25, 0.125, 12)], start=3):
+        vals = ((idx % mod) - off).float() * step
+        k[row, 0] = vals[torch.randperm(256, generator=g)].bfloat16()
+        v[row, 0] = (-vals).bfloat16()
     kernels.store_int2(k.to(DEV), v.to(DEV), history, meta.slot_mapping, meta.counts, layout)
     expected = O.packed_slots(bits(k), bits(v), cfg)
     history_cpu = history.cpu().numpy()
