@@ -240,7 +240,12 @@ def time_store(device, args, steps):
     slots = (blocks[:, None] * 128 + torch.arange(128)[None]).reshape(-1).to(torch.int64).to(device)
     counts = torch.tensor([1, n], dtype=torch.int32, device=device)
 
-    def once():
+    rk_t, rv_t = rk.T.contiguous(), rv.T.contiguous()
+
+    def once():  # the product's path: rotation and store in one launch
+        kernels.rotate_store_int2(k, v, rk_t, rv_t, history, slots, counts, layout)
+
+    def unfused():  # the reference's sequence: rotate K, rotate V, store_int2
         kernels.store_int2(kernels.rotate(k, rk), kernels.rotate(v, rv), history, slots, counts,
                            layout)
 
@@ -274,6 +279,7 @@ def time_store(device, args, steps):
         return statistics.median(a.elapsed_time(b) for a, b in times) * 1e3 / reps
 
     t_full = timed(once)
+    t_unfused = timed(unfused)
     t_store = timed(lambda: kernels.store_int2(kr, vr, history, slots, counts, layout))
     alg = n * (2 * 512) + 2 * 256 * 256 * 2 + n * 136 + n * 8
     return {
@@ -281,6 +287,9 @@ def time_store(device, args, steps):
                     "rotation, 8-factor MSE clip search, 128-token pages on permuted slots",
         "tokens_per_s": n / (t_full * 1e-6),
         "us_per_call": t_full,
+        "path": "rotate_store_int2 (one launch)",
+        "unfused_us_per_call": t_unfused,
+        "unfused_tokens_per_s": n / (t_unfused * 1e-6),
         "store_kernel_us": t_store,
         "store_kernel_tokens_per_s": n / (t_store * 1e-6),
         "algorithmic_bytes": alg,

@@ -91,6 +91,21 @@ int oscar_store_int2(const void* key_rot, const void* value_rot, int64_t n, void
                      const oscar_layout* layout, const oscar_clip* clip, void* stream);
 
 /*
+ * rotate_store_int2 -- replaces the reference's `store_int2(rotate(key, Rk), rotate(value,
+ * Rv), ...)` sequence (backend.py:171-173; kernels.py:51-66 and 175-202) with one launch:
+ * the same cache bytes as oscar_rotate of K and V followed by oscar_store_int2, without the
+ * rotated rows going through HBM. key/value: bf16 [n][kv_heads][256], row (token, head) at
+ * token * s0 + head * s1 elements (s0, s1 multiples of 8; rows contiguous, 16-byte aligned).
+ * rk_t / rv_t: R_k^T and R_v^T, contiguous bf16 [256][256]. No reference counterpart as one
+ * call.
+ */
+int oscar_rotate_store_int2(const void* key, int64_t k_s0, int64_t k_s1, const void* value,
+                            int64_t v_s0, int64_t v_s1, int64_t n, const void* rk_t,
+                            const void* rv_t, void* history, int64_t history_bytes,
+                            const int64_t* slots, const int32_t* counts,
+                            const oscar_layout* layout, const oscar_clip* clip, void* stream);
+
+/*
  * prepare_tasks -- replaces kernels.py:262-287 `prepare_tasks(qstarts, counts, tasks,
  * task_count, max_reqs, query_tile, num_reqs, source_table, table, copy_columns)`.
  * Writes tasks[i] = (req, q_offset) for every query tile of every request < counts[0]

@@ -54,6 +54,8 @@ SIGNATURES = {
     "oscar_rotate": [_P, _I64, _I64, _I64, _I64, _I64, _I64, _P, _I64, _I64, _P, _P],
     "oscar_store_int2": [_P, _P, _I64, _P, _I64, _P, _P, POINTER(OscarLayout),
                          POINTER(OscarClip), _P],
+    "oscar_rotate_store_int2": [_P, _I64, _I64, _P, _I64, _I64, _I64, _P, _P, _P, _I64, _P, _P,
+                                POINTER(OscarLayout), POINTER(OscarClip), _P],
     "oscar_prepare_tasks": [_P, _P, _P, _P, _I64, _I64, _I32, _I64, _P, _I64, _P, _I64, _I64,
                             _P],
     "oscar_attention_partials": [

@@ -168,10 +168,8 @@ class OscarAttentionImpl:
         if getattr(meta, "initial_prefill", False):
             # Reference backend.py:171-193 + 225-226: INT2 store, causal attention over each
             # request's own tokens (the fused-infer call), then the window store.
-            krot = kernels.rotate(key, self.rk_cols)
-            vrot = kernels.rotate(value, self.rv_cols)
-            kernels.store_int2(krot, vrot, self.history, meta.slot_mapping, meta.counts,
-                               meta.layout)
+            kernels.rotate_store_int2(key, value, self.rk_t, self.rv_t, self.history,
+                                      meta.slot_mapping, meta.counts, meta.layout)
             kernels.prefill_attention(query, key, value, self.window, meta, meta.layout,
                                       self.scale, output.view(n, -1),
                                       getattr(meta, "merged_lse", None))

@@ -11,6 +11,7 @@
 // One wavefront quantizes one 256-element vector; lane l owns elements 4l..4l+3, i.e.
 // exactly packed byte l.
 #include "quant.h"
+#include "rotate.h"
 
 #pragma clang fp contract(off)
 
@@ -51,6 +52,77 @@ __global__ __launch_bounds__(kThreads) void store_int2_kernel(const StoreArgs a)
                       bf16_to_float(raw.y & 0xffffu), bf16_to_float(raw.y >> 16)};
   quantize_store(x, a.mode, is_v ? a.v_ratio : a.k_ratio, is_v ? a.v_factor : a.k_factor,
                  a.history + base + is_v * a.L.vector_bytes);
+}
+
+// ---- rotate_store_int2: the K/V rotation and the INT2 store of many tokens in one launch.
+// Workgroup (16-row block x, K or V by y) of 16 wavefronts: the block's rows are staged once
+// in LDS (16-byte piece p of row r at slot p ^ r), wavefront w computes output columns
+// 16 w .. 16 w + 15 of the block with the operands, MFMA and k order of rotate_kernel (B from
+// the columns of R, i.e. rows of R^T, through L2), the bf16 block is kept in LDS, and
+// wavefront w then clips, quantizes and stores row w as store_int2_kernel does. The rotated
+// rows never go to HBM.
+struct RotateStoreArgs {
+  const uint16_t* x[2];  // K, V: row (token, head) at token * s0 + head * s1, contiguous, 16-B aligned
+  int64_t s0[2], s1[2];
+  const uint16_t* rt[2];  // R_k^T, R_v^T: contiguous [256][256]
+  FastDiv h_div;
+  StoreArgs st;  // rows, history, slots, counts, layout and clip (st.k / st.v unused)
+};
+
+constexpr int kRsWaves = 16;
+
+__device__ __forceinline__ int rs_piece(int row, int piece) { return row * kHeadDim + 8 * (piece ^ row); }
+
+__global__ __launch_bounds__(kRsWaves * kWave) __attribute__((amdgpu_waves_per_eu(8)))
+void rotate_store_kernel(const RotateStoreArgs a) {
+  __shared__ __attribute__((aligned(16))) uint16_t s_x[16 * kHeadDim];
+  __shared__ __attribute__((aligned(16))) uint16_t s_rot[16 * kHeadDim];
+  const StoreArgs& st = a.st;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int n = lane & 15, g = lane >> 4;
+  const int is_v = blockIdx.y;
+  const int64_t r0 = static_cast<int64_t>(blockIdx.x) * 16;
+  const int h = st.L.kv_heads;
+  // This wavefront's store row; its token count and slot are requested with the staging loads.
+  const int64_t row = r0 + wave;
+  const bool in = row < st.rows;
+  const uint32_t token = fastdiv(static_cast<uint32_t>(in ? row : 0), a.h_div);
+  const int head = static_cast<int>((in ? row : 0) - static_cast<int64_t>(token) * h);
+  const bool live = in && static_cast<int64_t>(token) < st.counts[1];
+  const int64_t slot = live ? st.slots[token] : -1;
+  if (tid < 16 * 32) {
+    const int rr = tid >> 5, piece = tid & 31;
+    const int64_t xrow = r0 + rr;
+    u32x4 v = u32x4{0u, 0u, 0u, 0u};
+    if (xrow < st.rows) {
+      const uint32_t xt = fastdiv(static_cast<uint32_t>(xrow), a.h_div);
+      const int64_t xh = xrow - static_cast<int64_t>(xt) * h;
+      v = *reinterpret_cast<const u32x4*>(a.x[is_v] + static_cast<int64_t>(xt) * a.s0[is_v] +
+                                          xh * a.s1[is_v] + 8 * piece);
+    }
+    *reinterpret_cast<u32x4*>(s_x + rs_piece(rr, piece)) = v;
+  }
+  RotateOperands op;
+  rotate_load_b<true>(op, a.rt[is_v] + static_cast<int64_t>(16 * wave + n) * kHeadDim, 1, g);
+  __syncthreads();
+#pragma unroll
+  for (int m = 0; m < 8; ++m) op.a[m] = *reinterpret_cast<const u32x4*>(s_x + rs_piece(n, 4 * m + g));
+  const f32x4 acc = rotate_mfma(op);
+#pragma unroll
+  for (int v = 0; v < 4; ++v)
+    s_rot[(4 * g + v) * kHeadDim + 16 * wave + n] = static_cast<uint16_t>(float_to_bf16(acc[v]));
+  __syncthreads();
+  // Same skips as store_int2_kernel (kernels.py:168-169 and the buffer bound).
+  if (!live || slot < 0) return;
+  const int64_t page = slot / st.L.bp;
+  const int64_t within = slot - page * st.L.bp;
+  const int64_t base = page * st.L.page_bytes + (within * h + head) * st.L.slot_bytes;
+  if (base + 2 * st.L.vector_bytes > st.history_bytes) return;
+  const uint2 raw = *reinterpret_cast<const uint2*>(s_rot + wave * kHeadDim + lane * 4);
+  const float x[4] = {bf16_to_float(raw.x & 0xffffu), bf16_to_float(raw.x >> 16),
+                      bf16_to_float(raw.y & 0xffffu), bf16_to_float(raw.y >> 16)};
+  quantize_store(x, st.mode, is_v ? st.v_ratio : st.k_ratio, is_v ? st.v_factor : st.k_factor,
+                 st.history + base + is_v * st.L.vector_bytes);
 }
 
 struct UnpackArgs {
@@ -129,6 +201,51 @@ extern "C" int oscar_store_int2(const void* key_rot, const void* value_rot, int6
   a.v_factor = clip->v_factor;
   const dim3 grid(static_cast<unsigned>((a.rows + 1) / 2));
   hipLaunchKernelGGL(store_int2_kernel, grid, dim3(kThreads), 0, as_stream(stream), a);
+  return static_cast<int>(hipGetLastError());
+}
+
+extern "C" int oscar_rotate_store_int2(const void* key, int64_t k_s0, int64_t k_s1,
+                                       const void* value, int64_t v_s0, int64_t v_s1, int64_t n,
+                                       const void* rk_t, const void* rv_t, void* history,
+                                       int64_t history_bytes, const int64_t* slots,
+                                       const int32_t* counts, const oscar_layout* layout,
+                                       const oscar_clip* clip, void* stream) {
+  using namespace oscar;
+  if (n < 0 || history_bytes < 0) return OSCAR_E_SHAPE;
+  RotateStoreArgs a{};
+  StoreArgs& st = a.st;
+  const int status = make_layout(layout, &st.L);
+  if (status != OSCAR_OK) return status;
+  if (!clip) return OSCAR_E_NULL;
+  if (clip->mode < OSCAR_CLIP_PERCENTILE || clip->mode > OSCAR_CLIP_SEARCH) return OSCAR_E_SHAPE;
+  if (n == 0) return OSCAR_OK;
+  if (!key || !value || !rk_t || !rv_t || !history || !slots || !counts) return OSCAR_E_NULL;
+  if (n * st.L.kv_heads > 0x7fffffffll) return OSCAR_E_SHAPE;
+  auto aligned16 = [](const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
+  if (!aligned16(key) || !aligned16(value) || !aligned16(rk_t) || !aligned16(rv_t) ||
+      k_s0 % 8 || k_s1 % 8 || v_s0 % 8 || v_s1 % 8 || reinterpret_cast<uintptr_t>(history) % 4)
+    return OSCAR_E_ALIGN;
+  a.x[0] = static_cast<const uint16_t*>(key);
+  a.x[1] = static_cast<const uint16_t*>(value);
+  a.s0[0] = k_s0;
+  a.s1[0] = k_s1;
+  a.s0[1] = v_s0;
+  a.s1[1] = v_s1;
+  a.rt[0] = static_cast<const uint16_t*>(rk_t);
+  a.rt[1] = static_cast<const uint16_t*>(rv_t);
+  a.h_div = make_fastdiv(static_cast<uint32_t>(st.L.kv_heads));
+  st.rows = n * st.L.kv_heads;
+  st.history = static_cast<uint8_t*>(history);
+  st.history_bytes = history_bytes;
+  st.slots = slots;
+  st.counts = counts;
+  st.mode = clip->mode;
+  st.k_ratio = clip->k_ratio;
+  st.v_ratio = clip->v_ratio;
+  st.k_factor = clip->k_factor;
+  st.v_factor = clip->v_factor;
+  const dim3 grid(static_cast<unsigned>((st.rows + 15) / 16), 2);
+  hipLaunchKernelGGL(rotate_store_kernel, grid, dim3(kRsWaves * kWave), 0, as_stream(stream), a);
   return static_cast<int>(hipGetLastError());
 }
 

@@ -141,6 +141,33 @@ def store_int2(key_rot, value_rot, history, slots, counts, layout):
     )
 
 
+def rotate_store_int2(key, value, rk_t, rv_t, history, slots, counts, layout):
+    """``store_int2(rotate(key, Rk), rotate(value, Rv), ...)`` as one launch (the same
+    cache bytes; the rotated rows stay on chip). ``rk_t``/``rv_t`` are R^T as contiguous
+    bf16 [256, 256]; ``key``/``value`` are bf16 [n, kv_heads, 256] with contiguous rows.
+    Reference: backend.py:171-173 (kernels.py:51-66, 175-202)."""
+    _device_check(key, value, rk_t, rv_t, history, slots, counts)
+    n = key.shape[0]
+    if value.shape[0] != n:
+        raise ValueError("key and value must have the same token count")
+    for r in (rk_t, rv_t):
+        if r.dtype != torch.bfloat16 or not r.is_contiguous() or tuple(r.shape) != (256, 256):
+            raise ValueError("rk_t / rv_t must be contiguous bf16 [256, 256] (R transposed)")
+    key, k0, k1 = _row_strides(key, "key")
+    value, v0, v1 = _row_strides(value, "value")
+    if slots.dtype != torch.int64:
+        raise ValueError("slot mapping must be int64")
+    _int32(counts, "counts")
+    _ext.check(
+        _ext.library().oscar_rotate_store_int2(
+            _ptr(key), k0, k1, _ptr(value), v0, v1, n, _ptr(rk_t), _ptr(rv_t), _ptr(history),
+            history.numel() * history.element_size(), _ptr(slots), _ptr(counts),
+            layout_struct(layout), clip_struct(layout.config), _stream(key),
+        ),
+        "rotate_store_int2",
+    )
+
+
 def prepare_tasks(qstarts, counts, tasks, task_count, max_reqs, query_tile, num_reqs=None,
                   source_table=None, table=None, copy_columns=0):
     """Compact (request, query offset) task table on device (reference kernels.py:262-287)."""

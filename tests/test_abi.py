@@ -63,6 +63,26 @@ def test_history_post_host_side_errors():
     assert call(slots=7) == -2  # fewer counters than programs x kv heads
 
 
+def test_rotate_store_host_side_errors():
+    # Fake, never dereferenced addresses: every call below returns before a launch.
+    lib = _ext.library()
+    good = _ext.OscarLayout(256, 1, 768, 128, 160, 68, 4, 128, 132, 0, 393216)
+    clip = _ext.OscarClip(2, 0.96, 0.92, 1.0, 1.0)
+    a = 1 << 20
+
+    def call(key=a, k_s0=256, n=4, rk_t=a, history=a, clip=clip):
+        return lib.oscar_rotate_store_int2(key, k_s0, 256, a, 256, 256, n, rk_t, a, history,
+                                           1 << 24, a, a, good, clip, None)
+
+    assert call(n=0) == 0
+    assert call(n=-1) == -2
+    assert call(rk_t=None) == -1
+    assert call(key=a + 8) == -4  # rows must be 16-byte aligned
+    assert call(k_s0=260) == -4
+    assert call(history=a + 2) == -4
+    assert call(clip=_ext.OscarClip(9, 0.96, 0.92, 1.0, 1.0)) == -2
+
+
 def test_status_strings():
     lib = _ext.library()
     assert lib.oscar_status_string(0) == b"ok"

@@ -139,6 +139,38 @@ def test_store_bytes_bit_exact_and_sentinels(mode, ratio):
     assert np.array_equal(bits(kd), ko) and np.array_equal(bits(vd), vo)
 
 
+@pytest.mark.parametrize("tokens,heads,mode,active", [
+    (4096, 1, "search", 4096),  # the store benchmark's shape
+    (37, 2, "percentile", 30),  # ragged block, two heads, padded tokens past the count
+    (300, 1, "factor", 300),
+])
+def test_rotate_store_is_bitwise_rotate_then_store(tokens, heads, mode, active):
+    # One launch against oscar_rotate (K, V) + oscar_store_int2: every cache byte.
+    g = torch.Generator().manual_seed(tokens + heads)
+    cfg = replace(OscarConfig(), clip_mode=mode, k_clip_ratio=0.96, v_clip_ratio=0.92,
+                  k_clip_factor=0.7, v_clip_factor=0.9)
+    from oscar_new_amd.layout import CacheLayout
+
+    layout = CacheLayout(768, kv_heads=heads, config=cfg)
+    pages = max(2, -(-tokens // 768) + 1)
+    base = torch.full((pages * layout.stripe_page_bytes,), 0x5A, dtype=torch.uint8, device=DEV)
+    k = torch.randn(tokens, 2 * heads, 256, generator=g).bfloat16().to(DEV)[:, ::2]  # strided
+    v = torch.randn(tokens, heads, 256, generator=g).bfloat16().to(DEV)
+    perm = torch.randperm((pages - 1) * 768, generator=g)[:tokens] + 768
+    slots = perm.to(torch.int64).to(DEV)
+    slots[3] = -1  # a masked row
+    counts = torch.tensor([1, active], dtype=torch.int32, device=DEV)
+    rk, rv = _qr_bf16(11), _qr_bf16(12)
+    want = base.clone()
+    kernels.store_int2(kernels.rotate(k, rk), kernels.rotate(v, rv), want, slots, counts, layout)
+    got = base.clone()
+    kernels.rotate_store_int2(k, v, rk.T.contiguous(), rv.T.contiguous(), got, slots, counts,
+                              layout)
+    torch.cuda.synchronize()
+    assert torch.equal(got.cpu(), want.cpu())
+    assert not torch.equal(got.cpu(), base.cpu())
+
+
 def test_store_skips_masked_rows():
     layout, raw, history, _, meta, _ = make_state([800], [760])
     before = history.clone()
