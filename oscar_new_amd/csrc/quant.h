@@ -180,9 +180,10 @@ __device__ __forceinline__ void quantize_store(const float x[4], int mode, float
       float sq[4];
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        int c = static_cast<int>(y[e]);
-        c = c < 0 ? 0 : (c > 3 ? 3 : c);
-        const float dec = static_cast<float>(c) * sf + zf;
+        // The code as a float: truncation toward zero clamped to [0, 3], the value of the
+        // integer code (a -0 here decodes to the same sum: -0 * sf + zf == 0 * sf + zf).
+        const float c = __builtin_amdgcn_fmed3f(truncf(y[e]), 0.0f, 3.0f);
+        const float dec = c * sf + zf;
         const float err = x[e] - dec;
         sq[e] = err * err;
       }
