@@ -1,5 +1,6 @@
 // store_int2: clip + INT2 quantize + pack rotated K/V rows into 160-byte paged slots;
-// unpack: the diagnostic dequant of packed slots.
+// rotate_store_int2: the K/V rotation and the same store in one launch; unpack: the
+// diagnostic dequant of packed slots.
 //
 // Reference: oscar_ascend/kernels.py:69-202 (`_clip_vec`, `_store_vec`, `_store_kernel`,
 // `store_int2`) and kernels.py:205-219, 623-648 (`_load_vec`, `_unpack_kernel`).
