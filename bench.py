@@ -40,7 +40,7 @@ CONFIGS = {
                desc="ragged MTP: B64, ctx log-uniform [256, 131072], 4 query tokens each"),
     "c5": dict(batch=4, context=262144, qlen=1, ragged=False, splits="mi355x",
                desc="long context: B4 x 262144 ctx, adaptive splits"),
-    # --mode prefill only (initial prefill, SURVEY next row): every token is a query token.
+    # --mode prefill only (initial prefill, no cached tokens): every token is a query token.
     "p1": dict(batch=4, context=4096, qlen=4096, ragged=False, splits="reference",
                desc="initial prefill: B4 x 4096 tokens, GQA 6:1, D256, causal"),
 }

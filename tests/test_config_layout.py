@@ -146,7 +146,7 @@ def test_bad_config_rejected():
 
 
 def test_percentile_selection_and_grid_known_values():
-    # design.md: 12 (K, r=0.96) and 22 (V, r=0.92) selection rounds; tests/test_tasks.py:123-124.
+    # Reference docs/design.md: 12 (K, r=0.96) and 22 (V, r=0.92) selection rounds; tests/test_tasks.py:123-124.
     assert percentile_selection(0.96)[:2] == (11, 10)
     assert percentile_selection(0.92)[:2] == (21, 20)
     assert abs(percentile_selection(0.96)[2] - 0.8) < 1e-9
