@@ -39,7 +39,9 @@ CONFIGS = {
     "c4": dict(batch=64, context=131072, qlen=4, ragged=True, splits="mi355x",
                desc="ragged MTP: B64, ctx log-uniform [256, 131072], 4 query tokens each"),
     "c5": dict(batch=4, context=262144, qlen=1, ragged=False, splits="mi355x",
-               desc="long context: B4 x 262144 ctx, adaptive splits"),
+               pool_blocks=300_000,
+               desc="long context: B4 x 262144 ctx, adaptive splits, 128-token blocks scattered "
+                    "over a 300k-block (50k-page, 39 GB) pool"),
     # --mode prefill only (initial prefill, no cached tokens): every token is a query token.
     "p1": dict(batch=4, context=4096, qlen=4096, ragged=False, splits="reference",
                desc="initial prefill: B4 x 4096 tokens, GQA 6:1, D256, causal"),
@@ -52,7 +54,9 @@ def parse_args(argv=None):
     p.add_argument("--steps", type=int, default=200)
     p.add_argument("--warmup", type=int, default=20)
     p.add_argument("--config", default="c3", choices=sorted(CONFIGS))
-    p.add_argument("--layers", type=int, default=4, help="independent KV caches cycled per step")
+    p.add_argument("--layers", type=int, default=None,
+                   help="independent KV caches cycled per step (default 4; 2 when one cache "
+                        "exceeds 16 GB)")
     p.add_argument("--seed", type=int, default=1234)
     p.add_argument("--cpu-sample", type=int, default=2, help="requests timed on the CPU oracle")
     p.add_argument("--no-cpu-baseline", action="store_true")
@@ -112,7 +116,9 @@ def build_workload(args, cfg, device):
     b = len(seqs)
     bpp = layout.blocks_per_page
     pages_per_req = [-(-s // layout.physical_block_tokens) for s in seqs]
-    pool = sum(pages_per_req) + 1  # page 0 never owned
+    # Pages are drawn at random from the pool (page 0 never owned): the owned pages of a
+    # request scatter over the whole pool, as after a long serving run.
+    pool = max(sum(pages_per_req) + 1, -(-cfg.get("pool_blocks", 0) // bpp))
     order = (torch.randperm(pool - 1, generator=gen) + 1).tolist()
     columns = max(pages_per_req) * bpp
     table = torch.zeros((b, columns), dtype=torch.int32)
@@ -423,16 +429,18 @@ def main(argv=None):
     if args.mode == "copy":
         return copy_calibration(args, device)
     cfg = CONFIGS[args.config]
-    print(f"[bench] building {args.config} workload ({args.layers} layers)", file=sys.stderr, flush=True)
+    print(f"[bench] building {args.config} workload", file=sys.stderr, flush=True)
     w = build_workload(args, cfg, device)
+    if args.layers is None:
+        args.layers = 2 if w.k_cache.numel() * 2 > 16 << 30 else 4
     layers = [(w.k_cache, w.v_cache)]
     for _ in range(args.layers - 1):
         layers.append((w.k_cache.clone(), w.v_cache.clone()))
     impls = []
     for _ in layers:
-        impl = OscarAttentionImpl(6, 256, 1 / 16, 1, w.cfg, split_policy=cfg["splits"],
+        impl = OscarAttentionImpl.standalone(6, 256, 1 / 16, 1, w.cfg, split_policy=cfg["splits"],
                                   one_launch_post=args.one_launch_post)
-        impl.initialize_layer(w.rk, w.rv)
+        impl.set_rotations(w.rk, w.rv)
         impls.append(impl)
     ntok = w.q.shape[0]
     outputs = [torch.empty(ntok, 6 * 256, dtype=torch.bfloat16, device=device) for _ in layers]

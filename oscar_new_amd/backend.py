@@ -1,12 +1,20 @@
-"""Per-layer launch order of the OSCAR INT2 attention path.
+"""vLLM attention backend and per-layer launch order of the OSCAR INT2 attention path.
 
-Reference: oscar_ascend/backend.py:13-227. ``OscarAttentionImpl`` keeps the forward contract:
-same arguments, same kernel order, no host reads, the window store last (it must follow both
-attention branches because a long current chunk wraps the ring). ``OscarAttentionBackend``
-and ``validate_vllm_config`` are the vLLM-facing class and checks (backend.py:13-64), written
-against duck-typed vLLM objects so that they import without vLLM. Initial prefill (the
-reference's Ascend FIA call, ``meta.initial_prefill``) runs through the INT2 path below with
-an empty history: the BF16 branch is the causal attention over the request's own tokens.
+Reference: oscar_ascend/backend.py:13-227. Three parts:
+
+* ``OscarAttentionBackend``: the class the platform hook routes FULL decoder attention to
+  (backend.py:13-38): implementation and builder classes, the native two-stripe cache shape,
+  no block copies or swaps.
+* ``validate_vllm_config``: the engine configurations the INT2 layout cannot serve
+  (backend.py:41-64), checked when a layer implementation is built.
+* ``OscarAttentionImpl``: constructed by vLLM with its attention-implementation arguments
+  (backend.py:67-105), given its calibrated rotations after weight loading
+  (``initialize_layer``, backend.py:107-117), and run once per layer step (``forward``,
+  backend.py:125-227: no host reads, the window store after both attention branches).
+
+vLLM is not importable in this image; everything here is written against duck-typed vLLM
+objects, so it imports and is tested without it. ``OscarAttentionImpl.standalone`` builds a
+layer without a vLLM config (benchmarks and tests).
 """
 
 from __future__ import annotations
@@ -20,7 +28,7 @@ from .config import OscarConfig, choose_history_partition, choose_splits
 
 
 class OscarAttentionBackend:
-    """Reference backend.py:13-38: the backend class the plugin routes to."""
+    """Routed backend (reference backend.py:13-38)."""
 
     forward_includes_kv_cache_update = True
 
@@ -40,62 +48,119 @@ class OscarAttentionBackend:
 
     @staticmethod
     def get_kv_cache_shape(num_blocks, block_size, num_kv_heads, head_size, cache_dtype_str="auto"):
-        """(K, V) stripes of bf16 [num_blocks, block_size, num_kv_heads, head_size] each: the
-        native paged layout whose K stripe holds the INT2 slots and V stripe the windows."""
+        """Two native bf16 stripes [num_blocks, block_size, num_kv_heads, head_size]: the K
+        stripe carries the INT2 slots, the V stripe of a request's first page its window."""
         return (2, num_blocks, block_size, num_kv_heads, head_size)
 
     @staticmethod
     def copy_blocks(*args, **kwargs):
-        raise NotImplementedError("OSCAR ring ownership does not support shared/copied request pages")
+        raise NotImplementedError(
+            "OSCAR pages belong to one request (its BF16 window lives in its first page); "
+            "pages cannot be copied or shared")
 
     @staticmethod
     def swap_blocks(*args, **kwargs):
-        raise NotImplementedError("OSCAR supports native recompute preemption, not KV swapping")
+        raise NotImplementedError("OSCAR supports recompute preemption only; KV swapping is "
+                                  "not available")
+
+
+def _config_problems(config):
+    """(rejected, reason) for every engine option the INT2 layout cannot serve."""
+    cache, model, parallel = config.cache_config, config.model_config, config.parallel_config
+    text = getattr(model, "hf_text_config", None)
+    return (
+        (bool(cache.enable_prefix_caching),
+         "OSCAR needs --no-enable-prefix-caching: a request's BF16 ring lives in its own "
+         "first page"),
+        (cache.cache_dtype not in ("auto", "bfloat16"),
+         "OSCAR manages its own KV format; start with --kv-cache-dtype auto"),
+        (model.dtype != torch.bfloat16, "the OSCAR target model must run in bf16"),
+        (getattr(config, "kv_transfer_config", None) is not None,
+         "KV transfer cannot move OSCAR's INT2 pages"),
+        (getattr(parallel, "decode_context_parallel_size", 1) != 1
+         or getattr(parallel, "prefill_context_parallel_size", 1) != 1,
+         "OSCAR runs with PCP=DCP=1 only"),
+        (bool(getattr(parallel, "enable_dbo", False)),
+         "dual-batch overlap would need two metadata buffer sets; DBO is unsupported"),
+        (os.getenv("VLLM_USE_V2_MODEL_RUNNER", "0") == "1",
+         "OSCAR plugs into the v1 model runner; unset VLLM_USE_V2_MODEL_RUNNER"),
+        (getattr(getattr(config, "quant_config", None), "enable_c8_quant", False),
+         "C8 KV quantization replaces the OSCAR layout; W8A8 weights are fine"),
+        (getattr(text, "head_dim", None) != 256, "OSCAR covers D256 full attention only"),
+    )
 
 
 def validate_vllm_config(config):
-    """Reference backend.py:41-64, with the ROCm runner's names: the configurations the INT2
-    path does not support are rejected with the reference's reasons."""
-    if config.cache_config.enable_prefix_caching:
-        raise ValueError("OSCAR requires --no-enable-prefix-caching (BF16 ring owner isolation)")
-    if config.cache_config.cache_dtype not in ("auto", "bfloat16"):
-        raise ValueError("Use --kv-cache-dtype auto with OSCAR_AMD_ENABLED=1")
-    if config.model_config.dtype != torch.bfloat16:
-        raise ValueError("OSCAR target model must use BF16 activation/cache dtype")
-    if getattr(config, "kv_transfer_config", None) is not None:
-        raise ValueError("KV transfer is not supported by this OSCAR layout")
-    pc = config.parallel_config
-    if (getattr(pc, "decode_context_parallel_size", 1) != 1
-            or getattr(pc, "prefill_context_parallel_size", 1) != 1):
-        raise ValueError("OSCAR currently requires PCP=DCP=1")
-    if getattr(pc, "enable_dbo", False):
-        raise ValueError("DBO requires separate metadata buffer sets and is not supported")
-    if os.getenv("VLLM_USE_V2_MODEL_RUNNER", "0") == "1":
-        raise ValueError("This OSCAR adapter targets the v1 model runner")
-    hf = config.model_config.hf_text_config
-    if getattr(hf, "head_dim", None) != 256:
-        raise ValueError("This implementation targets D256 full attention")
+    """Raise ValueError for the first unsupported engine option (reference backend.py:41-64).
+    The reference's Qwen3.5 model-type restriction is not kept: any D256 full-attention
+    decoder is served."""
+    for rejected, reason in _config_problems(config):
+        if rejected:
+            raise ValueError(reason)
+
+
+STANDALONE = object()  # ``vllm_config`` value of a layer built outside any vLLM engine
+
+
+def _current_vllm_config():
+    """The engine config vLLM is constructing layers under, or None without vLLM."""
+    try:
+        from vllm.config import get_current_vllm_config
+    except ImportError:
+        return None
+    return get_current_vllm_config()
 
 
 class OscarAttentionImpl:
-    """Reference: backend.py:67-227. ``split_policy`` "reference" keeps config.py:84-89,
-    "mi355x" fills the 256 CUs (config.choose_splits_mi355x). ``one_launch_post`` runs the
-    history branch and post-attention as one launch (``kernels.history_post``) where it applies;
-    the result is the same bits either way."""
+    """One FULL attention layer (reference backend.py:67-227).
 
-    def __init__(self, num_heads, head_size, scale, num_kv_heads, cfg=None,
-                 split_policy="reference", fused=True, one_launch_post=False):
-        if head_size != 256:
-            raise ValueError("OSCAR requires FULL decoder attention with D256")
+    Constructed by vLLM with the standard implementation arguments. Options that are not
+    vLLM's are keyword-only: ``vllm_config`` (default: the config vLLM is building under),
+    ``oscar_config`` (default: from the environment, with the speculative token count of the
+    vLLM config), ``split_policy`` ("reference": config.py:84-89; "mi355x": fill the 256 CUs
+    with token-bounded splits), ``fused`` (three launches per step instead of the nine single
+    launches; same bits) and ``one_launch_post`` (history branch and post-attention in one
+    launch where it applies; same bits).
+    """
+
+    def __init__(self, num_heads, head_size, scale, num_kv_heads, alibi_slopes=None,
+                 sliding_window=None, kv_cache_dtype="auto", logits_soft_cap=None,
+                 attn_type="decoder", kv_sharing_target_layer_name=None, *, vllm_config=None,
+                 oscar_config=None, split_policy="reference", fused=True, one_launch_post=False,
+                 **kwargs):
+        unsupported = (
+            (alibi_slopes is not None, "ALiBi"),
+            (sliding_window is not None, "sliding-window attention"),
+            (bool(logits_soft_cap), "logits soft-capping"),
+            (kv_sharing_target_layer_name is not None, "cross-layer KV sharing"),
+            (kwargs.get("sinks") is not None, "learned attention sinks"),
+        )
+        for present, feature in unsupported:
+            if present:
+                raise ValueError(f"OSCAR attention does not implement {feature}")
+        if str(getattr(attn_type, "value", attn_type)).lower() != "decoder" or head_size != 256:
+            raise ValueError("OSCAR serves FULL decoder attention with head size 256 only")
         if num_kv_heads <= 0 or num_heads % num_kv_heads:
-            raise ValueError("query heads must be a multiple of kv heads")
+            raise ValueError("the query head count must be a multiple of the KV head count")
         if split_policy not in ("reference", "mi355x"):
             raise ValueError("split_policy must be 'reference' or 'mi355x'")
+        if vllm_config is STANDALONE:
+            vllm_config = None
+        elif vllm_config is None:
+            vllm_config = _current_vllm_config()
+        self.vllm_config = vllm_config
+        if self.vllm_config is not None:
+            validate_vllm_config(self.vllm_config)
+        if oscar_config is None:
+            spec = getattr(self.vllm_config, "speculative_config", None)
+            oscar_config = OscarConfig.from_env(spec.num_speculative_tokens if spec else 0)
+        self.cfg = oscar_config
         self.num_heads = num_heads
         self.num_kv_heads = num_kv_heads
         self.head_size = head_size
         self.scale = float(scale)
-        self.cfg = cfg or OscarConfig.from_env()
+        self.kv_cache_dtype = kv_cache_dtype
+        self.attn_type = attn_type
         self.split_policy = split_policy
         self.fused = fused
         self.one_launch_post = one_launch_post
@@ -103,15 +168,36 @@ class OscarAttentionImpl:
         self.history = self.window = None
         self.cache_identity = None
 
-    def initialize_layer(self, rk, rv):
-        """Install the layer's calibrated K/V rotations (bf16 [256, 256] on the device)."""
+    @classmethod
+    def standalone(cls, num_heads, head_size, scale, num_kv_heads, cfg=None, **options):
+        """A layer outside a vLLM engine (no engine config, no config checks), for benchmarks
+        and tests; ``cfg`` defaults to the environment's with no speculative tokens."""
+        return cls(num_heads, head_size, scale, num_kv_heads, vllm_config=STANDALONE,
+                   oscar_config=cfg, **options)
+
+    def initialize_layer(self, layer):
+        """Load this layer's calibrated K/V rotations (reference backend.py:107-117): the
+        artefacts named by VLLM_OSCAR_K/V_ROTATION_PATH, matched by ``layer.layer_name``'s
+        decoder index, validated on the CPU and copied to the current device as bf16."""
+        from .rotations import get_rotation
+
+        # The layer's own scale buffer sits on its device; otherwise the current GPU.
+        scale = getattr(layer, "_k_scale", None)
+        device = scale.device if torch.is_tensor(scale) else torch.device(
+            "cuda", torch.cuda.current_device())
+        name = layer.layer_name
+        self.set_rotations(get_rotation(self.cfg.k_rotation_path, name, device),
+                           get_rotation(self.cfg.v_rotation_path, name, device))
+
+    def set_rotations(self, rk, rv):
+        """Install K/V rotations directly (bf16 [256, 256] on the device)."""
         for r in (rk, rv):
             if tuple(r.shape) != (256, 256):
                 raise ValueError("rotations must be 256x256")
         self.rk = rk.to(torch.bfloat16).contiguous()
         self.rv = rv.to(torch.bfloat16).contiguous()
-        # x @ R reads R column-wise; a transposed view of R^T stored row-major keeps those
-        # reads contiguous (the inverse rotation's R^T view of rv already is).
+        # x @ R reads R column-wise; R^T stored row-major keeps those reads contiguous. The
+        # inverse rotation's R^T view of rv already is.
         self.rk_t = self.rk.T.contiguous()
         self.rv_t = self.rv.T.contiguous()
         self.rk_cols = self.rk_t.T
@@ -122,93 +208,98 @@ class OscarAttentionImpl:
 
     def partition_for(self, meta):
         """``(splits, split_tokens)`` of the history branch. "reference": config.py:84-89
-        with the reference split rule; "mi355x": ``choose_history_partition`` (reads the
-        host-side ``meta.max_seq_len`` and, when present, ``meta.total_seq_len``)."""
+        with the reference split rule; "mi355x": ``choose_history_partition`` (host-side
+        ``meta.max_seq_len`` and, when present, ``meta.total_seq_len``)."""
         if self.split_policy == "reference":
             return choose_splits(meta.num_reqs, self.num_kv_heads, meta.max_query_len), 0
-        tasks = -(-meta.num_actual_tokens // self.cfg.queries_per_tile) if meta.max_query_len > 1 \
-            else meta.num_reqs
+        tasks = meta.num_reqs if meta.max_query_len <= 1 else \
+            -(-meta.num_actual_tokens // self.cfg.queries_per_tile)
         return choose_history_partition(tasks, self.num_kv_heads, meta.max_query_len,
                                         getattr(meta, "max_seq_len", None),
                                         getattr(meta, "total_seq_len", None))
 
-    def forward(self, layer, query, key, value, kv_cache, attn_metadata, output=None):
-        """Reference: backend.py:125-227 (minus the Ascend prefill call).
+    def _bind_cache(self, kv_cache, layout):
+        identity = (kv_cache[0].data_ptr(), kv_cache[1].data_ptr(), layout)
+        if self.cache_identity != identity:
+            self.history, self.window = layout.tensor_views(kv_cache)
+            self.cache_identity = identity
 
-        ``fused`` (default) runs the step as three launches (``pre_attention``, the history
-        kernel, ``post_attention``) that produce the same bits as the reference order of
-        single launches below.
-        """
+    def forward(self, layer, query, key, value, kv_cache, attn_metadata, output=None,
+                output_scale=None, output_block_scale=None):
+        """One layer step (reference backend.py:125-227); returns ``output``."""
         if output is None:
-            raise ValueError("an attention output buffer is required")
-        if attn_metadata is None:
+            raise ValueError("OSCAR writes into a caller-provided attention output buffer")
+        if output_scale is not None or output_block_scale is not None:
+            raise ValueError("OSCAR does not fuse output quantization")
+        if attn_metadata is None:  # profiling run: nothing scheduled
             return output.zero_()
         if self.rk is None or self.rv is None:
-            raise RuntimeError("OSCAR rotations were not initialized for this layer")
+            raise RuntimeError("this OSCAR layer has no rotations: initialize_layer runs after "
+                               "weight loading")
         if key is None or value is None:
-            raise ValueError("OSCAR requires the current K/V to maintain exact BF16 windows")
+            raise ValueError("OSCAR needs the current K/V: the BF16 window is exact")
         if query.device.type != "cuda":
             raise RuntimeError("OSCAR kernels run on a ROCm GPU")
         meta = attn_metadata
         n = query.shape[0]
-        query = query.view(n, self.num_heads, self.head_size)
-        key = key.view(key.shape[0], self.num_kv_heads, self.head_size)
-        value = value.view(value.shape[0], self.num_kv_heads, self.head_size)
-        if key.shape[0] != n or value.shape[0] != n:
-            raise ValueError("Q/K/V must have matching current-token dimensions")
-        identity = (kv_cache[0].data_ptr(), kv_cache[1].data_ptr(), meta.layout)
-        if self.cache_identity != identity:
-            self.history, self.window = meta.layout.tensor_views(kv_cache)
-            self.cache_identity = identity
+        q = query.view(n, self.num_heads, self.head_size)
+        k = key.view(key.shape[0], self.num_kv_heads, self.head_size)
+        v = value.view(value.shape[0], self.num_kv_heads, self.head_size)
+        if k.shape[0] != n or v.shape[0] != n:
+            raise ValueError("query, key and value must cover the same tokens")
+        self._bind_cache(kv_cache, meta.layout)
         if not output.is_contiguous():
-            raise ValueError("Attention output must be contiguous")
+            raise ValueError("the attention output must be contiguous")
         if n == 0:
             return output
-
+        rows = output.view(n, -1)
+        lse = getattr(meta, "merged_lse", None)
+        layout = meta.layout
         if getattr(meta, "initial_prefill", False):
-            # Reference backend.py:171-193 + 225-226: INT2 store, causal attention over each
-            # request's own tokens (the fused-infer call), then the window store.
-            kernels.rotate_store_int2(key, value, self.rk_t, self.rv_t, self.history,
-                                      meta.slot_mapping, meta.counts, meta.layout)
-            kernels.prefill_attention(query, key, value, self.window, meta, meta.layout,
-                                      self.scale, output.view(n, -1),
-                                      getattr(meta, "merged_lse", None))
-            kernels.store_windows(key, value, self.window, meta, meta.layout)
+            # Every request starts here: INT2 store of all tokens, causal attention over each
+            # request's own tokens (the reference's fused-infer call), then the windows.
+            kernels.rotate_store_int2(k, v, self.rk_t, self.rv_t, self.history,
+                                      meta.slot_mapping, meta.counts, layout)
+            kernels.prefill_attention(q, k, v, self.window, meta, layout, self.scale, rows, lse)
+            kernels.store_windows(k, v, self.window, meta, layout)
             return output
-
         splits, split_tokens = self.partition_for(meta)
         if self.fused:
-            # BF16 branch + rotations + INT2 store; then history, merges + window in two
-            # launches, or (one_launch_post, decode-sized tasks, <= 16 splits) in one.
-            qrot, rp, rl = kernels.pre_attention(query, key, value, self.history, self.window,
-                                                 meta, meta.layout, self.scale, self.rk_t,
-                                                 self.rv_t)
-            if self.one_launch_post and kernels.history_post_supported(
-                    meta, meta.layout, self.num_heads, splits, n):
-                kernels.history_post(qrot, self.history, meta, meta.layout, self.scale, splits, rp,
-                                     rl, self.rv, key, value, self.window, output.view(n, -1),
-                                     getattr(meta, "merged_lse", None), split_tokens=split_tokens)
-                return output
-            hp, hl = kernels.attention_partials(qrot, key, value, self.history, self.window, meta,
-                                                meta.layout, self.scale, splits, raw=False,
-                                                split_tokens=split_tokens)
-            kernels.post_attention(hp, hl, rp, rl, self.rv, key, value, self.window, meta,
-                                   meta.layout, output.view(n, -1), getattr(meta, "merged_lse", None))
-            return output
-
-        krot = kernels.rotate(key, self.rk_cols)
-        vrot = kernels.rotate(value, self.rv_cols)
-        kernels.store_int2(krot, vrot, self.history, meta.slot_mapping, meta.counts, meta.layout)
-        qrot = kernels.rotate(query, self.rk_cols)
-        hp, hl = kernels.attention_partials(qrot, key, value, self.history, self.window, meta,
-                                            meta.layout, self.scale, splits, raw=False,
-                                            split_tokens=split_tokens)
-        hrot, hlogsum = kernels.merge_splits(hp, hl, meta.counts)
-        hout = kernels.rotate(hrot, self.rv.T)
-        rp, rl = kernels.attention_partials(query, key, value, self.history, self.window, meta,
-                                            meta.layout, self.scale, 1, raw=True)
-        kernels.merge_paths(hout, hlogsum, rp, rl, meta.counts, output.view(n, -1),
-                            getattr(meta, "merged_lse", None))
-        # Must follow BOTH attention branches: long current chunks wrap the ring.
-        kernels.store_windows(key, value, self.window, meta, meta.layout)
+            self._fused_step(q, k, v, meta, splits, split_tokens, rows, lse)
+        else:
+            self._single_launch_step(q, k, v, meta, splits, split_tokens, rows, lse)
         return output
+
+    def _fused_step(self, q, k, v, meta, splits, split_tokens, rows, lse):
+        """pre-attention (q rotation, K/V INT2 store, BF16 branch) -> history -> post
+        (split merge, inverse V rotation, path merge, windows); the last two in one launch
+        with ``one_launch_post`` where it applies."""
+        layout = meta.layout
+        qrot, rp, rl = kernels.pre_attention(q, k, v, self.history, self.window, meta, layout,
+                                             self.scale, self.rk_t, self.rv_t)
+        if self.one_launch_post and kernels.history_post_supported(
+                meta, layout, self.num_heads, splits, q.shape[0]):
+            kernels.history_post(qrot, self.history, meta, layout, self.scale, splits, rp, rl,
+                                 self.rv, k, v, self.window, rows, lse, split_tokens=split_tokens)
+            return
+        hp, hl = kernels.attention_partials(qrot, k, v, self.history, self.window, meta, layout,
+                                            self.scale, splits, raw=False,
+                                            split_tokens=split_tokens)
+        kernels.post_attention(hp, hl, rp, rl, self.rv, k, v, self.window, meta, layout, rows,
+                               lse)
+
+    def _single_launch_step(self, q, k, v, meta, splits, split_tokens, rows, lse):
+        """The reference's order of single launches (backend.py:171-226)."""
+        layout = meta.layout
+        kernels.store_int2(kernels.rotate(k, self.rk_cols), kernels.rotate(v, self.rv_cols),
+                           self.history, meta.slot_mapping, meta.counts, layout)
+        hp, hl = kernels.attention_partials(kernels.rotate(q, self.rk_cols), k, v, self.history,
+                                            self.window, meta, layout, self.scale, splits,
+                                            raw=False, split_tokens=split_tokens)
+        merged, merged_lse = kernels.merge_splits(hp, hl, meta.counts)
+        hout = kernels.rotate(merged, self.rv.T)
+        rp, rl = kernels.attention_partials(q, k, v, self.history, self.window, meta, layout,
+                                            self.scale, 1, raw=True)
+        kernels.merge_paths(hout, merged_lse, rp, rl, meta.counts, rows, lse)
+        # Last: a chunk longer than the ring overwrites window slots both branches read.
+        kernels.store_windows(k, v, self.window, meta, layout)

@@ -435,16 +435,25 @@ def prefill_attention(query, key, value, window, meta, layout, scale, output, me
 
 
 _COUNTERS = {}
+DEFAULT_COUNTER_SLOTS = 1 << 16
 
 
-def _finish_counters(device, slots):
-    """Zeroed int32 completion counters of one device, grown on demand (allocate them before a
-    graph capture: a first call outside the capture does). Every history_post launch leaves
-    them zero; launches that overlap on one device (two streams at once) would race on them."""
-    buf = _COUNTERS.get(device)
-    if buf is None or buf.numel() < slots:
-        buf = torch.zeros(max(slots, 4096), dtype=torch.int32, device=device)
-        _COUNTERS[device] = buf
+def finish_counters(meta, device, slots):
+    """The int32 completion counters a ``history_post`` launch uses: the metadata's own
+    (``meta.finish_counters``, sized by the builder from its task capacity) or else one
+    per-device buffer of ``DEFAULT_COUNTER_SLOTS``. Both are allocated once, zeroed, and never
+    replaced (a captured graph keeps their address); every launch leaves them zero. A launch
+    needing more slots than they hold is refused. Launches that overlap on one device (two
+    streams at once) must not share counters."""
+    buf = getattr(meta, "finish_counters", None)
+    if buf is None:
+        buf = _COUNTERS.get(device)
+        if buf is None:
+            buf = torch.zeros(DEFAULT_COUNTER_SLOTS, dtype=torch.int32, device=device)
+            _COUNTERS[device] = buf
+    if buf.numel() < slots:
+        raise ValueError(f"history_post needs {slots} completion counters; the buffer holds "
+                         f"{buf.numel()}")
     return buf
 
 
@@ -490,7 +499,7 @@ def history_post(query, history, meta, layout, scale, splits, raw_partials, raw_
     partials = torch.empty((n, hq, splits, d), dtype=torch.float32, device=query.device)
     lse = torch.empty((n, hq, splits), dtype=torch.float32, device=query.device)
     stream = _stream(query)
-    counters = _finish_counters(query.device, programs * layout.kv_heads)
+    counters = finish_counters(meta, query.device, programs * layout.kv_heads)
     table = _int32(meta.block_tables, "block_tables")
     max_query_len = getattr(meta, "max_query_len", None)
     max_query_len = int(max_query_len) if isinstance(max_query_len, int) else 0

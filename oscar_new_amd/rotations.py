@@ -1,68 +1,101 @@
-"""Strict loading of calibrated K/V rotation artefacts (reference rotations.py:1-53).
+"""Calibrated K/V rotation artefacts: load once, validate, hand each layer its matrix.
 
-Checkpoint formats accepted (as the reference): a [layers, D, D] tensor, or a dict
-``{"layers": {index: matrix | {"rotation": matrix}}}`` / ``{index: ...}``. Files are read with
-``torch.load(weights_only=True)`` only. ``get_rotation`` validates shape, finiteness and
-orthogonality on the checkpoint's fp32 values before the bf16 device copy.
+Behaviour follows oscar_ascend/rotations.py:1-53 (reference); the code is this package's own.
+An artefact is a ``torch.save`` file read with ``weights_only=True`` (nothing in it is
+executed) in one of two shapes:
+
+* a ``[layers, D, D]`` tensor, row ``i`` being decoder layer ``i``'s matrix;
+* a mapping ``{index: matrix}`` or ``{"layers": {index: matrix}}``, where a matrix may also
+  sit under a ``"rotation"`` key of its entry.
+
+Matrices are kept as fp32 on the CPU. A layer's matrix must be D x D, finite and orthogonal
+(every entry of R^T R within 0.015 + 0.015 |I| of the identity, the reference's acceptance
+bound) before its bf16 copy goes to the device.
 """
 
 from __future__ import annotations
 
-import re
 from functools import lru_cache
 
 import torch
 
+ORTHOGONALITY_ATOL = 0.015
+ORTHOGONALITY_RTOL = 0.015
+
 
 def layer_index(name):
-    """Global decoder layer index of a module name (``...layers.<i>...``)."""
-    match = re.search(r"(?:^|\.)layers\.(\d+)(?:\.|$)", name)
-    if match is None:
-        raise ValueError(f"Cannot resolve global decoder layer index: {name}")
-    return int(match.group(1))
+    """Decoder layer index in a module path: the integer component right after ``layers``
+    (``model.layers.12.self_attn.attn`` -> 12)."""
+    parts = name.split(".")
+    for here, after in zip(parts, parts[1:]):
+        if here == "layers" and after.isdigit():
+            return int(after)
+    raise ValueError(f"no decoder layer index ('layers.<i>') in module name {name!r}")
 
 
-def _table(source, path):
-    if torch.is_tensor(source) and source.ndim == 3:
-        items = enumerate(source)
-    elif isinstance(source, dict):
-        items = source.get("layers", source).items()
-    else:
-        raise ValueError(f"Unsupported rotation checkpoint format: {path}")
-    result = {}
-    for key, entry in items:
-        matrix = entry["rotation"] if isinstance(entry, dict) else entry
-        if not torch.is_tensor(matrix):
-            raise ValueError(f"Invalid matrix for layer {key} in {path}")
-        result[int(key)] = matrix.float().contiguous()
-    return result
+def _entries(source):
+    """(index, matrix) pairs of a loaded artefact, in either accepted shape."""
+    if torch.is_tensor(source):
+        if source.ndim != 3:
+            raise ValueError(f"a rotation tensor must be [layers, D, D], got {tuple(source.shape)}")
+        return list(enumerate(source))
+    if isinstance(source, dict):
+        table = source["layers"] if "layers" in source else source
+        if isinstance(table, dict):
+            return [(key, entry.get("rotation") if isinstance(entry, dict) else entry)
+                    for key, entry in table.items()]
+    raise ValueError("unrecognized rotation artefact: expected a [layers, D, D] tensor or a "
+                     "{layer: matrix} mapping")
 
 
 @lru_cache(maxsize=4)
 def load_checkpoint(path):
+    """``{layer index: fp32 CPU matrix}`` of the artefact at ``path`` (cached)."""
     if not path:
-        raise ValueError("Calibrated D256 K/V rotation paths are required")
-    return _table(torch.load(path, map_location="cpu", weights_only=True), path)
+        raise ValueError("no rotation artefact given: set VLLM_OSCAR_K_ROTATION_PATH and "
+                         "VLLM_OSCAR_V_ROTATION_PATH to the calibrated D256 K/V rotations")
+    source = torch.load(path, map_location="cpu", weights_only=True)
+    table = {}
+    try:
+        entries = _entries(source)
+    except ValueError as err:
+        raise ValueError(f"{path}: {err}") from None
+    for key, matrix in entries:
+        if not torch.is_tensor(matrix):
+            raise ValueError(f"{path}: layer {key} holds no matrix")
+        table[int(key)] = matrix.detach().to(torch.float32).contiguous()
+    return table
+
+
+def check_rotation(matrix, dim=256, what="rotation"):
+    """Raise ValueError unless ``matrix`` is a finite, orthogonal dim x dim matrix."""
+    if tuple(matrix.shape) != (dim, dim):
+        raise ValueError(f"{what}: expected {dim}x{dim}, got {tuple(matrix.shape)}")
+    if not bool(torch.isfinite(matrix).all()):
+        raise ValueError(f"{what}: contains NaN or infinite entries")
+    m = matrix.to(torch.float32)
+    eye = torch.eye(dim, dtype=torch.float32)
+    excess = (m.T @ m - eye).abs() - (ORTHOGONALITY_ATOL + ORTHOGONALITY_RTOL * eye)
+    if float(excess.max()) > 0:
+        raise ValueError(f"{what}: R^T R departs from the identity by more than "
+                         f"{ORTHOGONALITY_ATOL} (+{ORTHOGONALITY_RTOL} on the diagonal)")
 
 
 def get_rotation(path, name, device, dim=256):
-    """The layer's rotation as contiguous bf16 on ``device`` (reference rotations.py:36-53)."""
+    """Validated rotation of module ``name``'s layer from the artefact at ``path``, as a
+    contiguous bf16 matrix on ``device`` (reference rotations.py:36-53)."""
     index = layer_index(name)
     table = load_checkpoint(path)
     if index not in table:
-        raise ValueError(f"Missing rotation for {name} (layer {index}) in {path}")
+        raise ValueError(f"{path} has no rotation for layer {index} ({name})")
     matrix = table[index]
-    if tuple(matrix.shape) != (dim, dim):
-        raise ValueError(f"Expected D{dim} rotation for {name}; got {tuple(matrix.shape)}")
-    if not torch.isfinite(matrix).all():
-        raise ValueError(f"Nonfinite rotation for {name}")
-    identity = torch.eye(dim, dtype=matrix.dtype)
-    if not torch.allclose(matrix.T @ matrix, identity, atol=0.015, rtol=0.015):
-        raise ValueError(f"Rotation for {name} is not orthogonal")
+    # Validation runs on the artefact's own fp32 values, before the bf16 conversion.
+    check_rotation(matrix, dim, f"layer {index} rotation in {path}")
     return matrix.to(device=device, dtype=torch.bfloat16).contiguous()
 
 
 def save_rotations(path, rotations):
-    """Write ``{layer index: [D, D] matrix}`` in the format ``load_checkpoint`` reads."""
-    torch.save({"layers": {int(k): {"rotation": v.detach().float().cpu().contiguous()}
-                           for k, v in rotations.items()}}, path)
+    """Write ``{layer index: D x D matrix}`` as an artefact ``load_checkpoint`` reads."""
+    layers = {int(i): {"rotation": r.detach().to(torch.float32).cpu().contiguous()}
+              for i, r in rotations.items()}
+    torch.save({"layers": layers}, path)

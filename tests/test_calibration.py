@@ -100,22 +100,28 @@ def test_rotation_artefacts_round_trip_and_rejections(tmp_path):
     r = R.get_rotation(str(path), "model.layers.3.self_attn", "cpu")
     assert r.dtype == torch.bfloat16 and r.shape == (256, 256)
     torch.testing.assert_close(r.float(), good[3].float(), atol=1e-2, rtol=0)
-    with pytest.raises(ValueError, match="Missing"):
+    with pytest.raises(ValueError, match="no rotation for layer 4"):
         R.get_rotation(str(path), "model.layers.4.self_attn", "cpu")
     stacked = tmp_path / "stack.pt"
     torch.save(torch.stack([torch.eye(256), 2 * torch.eye(256)]), stacked)
     assert R.get_rotation(str(stacked), "layers.0", "cpu").shape == (256, 256)
-    with pytest.raises(ValueError, match="orthogonal"):
+    with pytest.raises(ValueError, match="departs from the identity"):
         R.get_rotation(str(stacked), "layers.1", "cpu")
+    # The acceptance bound is 0.015 off the diagonal and 0.03 on it (the reference's).
+    nearly = torch.eye(256) * (1.014 ** 0.5)
+    R.check_rotation(nearly)
+    with pytest.raises(ValueError):
+        R.check_rotation(torch.eye(256) * (1.031 ** 0.5))
     bad = tmp_path / "bad.pt"
     torch.save({"layers": {0: torch.eye(128), 1: torch.full((256, 256), float("inf"))}}, bad)
-    with pytest.raises(ValueError, match="D256"):
+    with pytest.raises(ValueError, match="expected 256x256"):
         R.get_rotation(str(bad), "layers.0", "cpu")
-    with pytest.raises(ValueError, match="Nonfinite"):
+    with pytest.raises(ValueError, match="NaN or infinite"):
         R.get_rotation(str(bad), "layers.1", "cpu")
     odd = tmp_path / "odd.pt"
     torch.save([torch.eye(256)], odd)
-    with pytest.raises(ValueError, match="Unsupported"):
+    with pytest.raises(ValueError, match="unrecognized rotation artefact"):
         R.load_checkpoint(str(odd))
-    with pytest.raises(ValueError, match="required"):
+    with pytest.raises(ValueError, match="VLLM_OSCAR_K_ROTATION_PATH"):
         R.load_checkpoint("")
+    assert R.layer_index("layers.2") == 2 and R.layer_index("a.layers.x.layers.5.b") == 5

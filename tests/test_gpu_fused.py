@@ -16,7 +16,7 @@ import oracle as O
 from oscar_new_amd import kernels
 from oscar_new_amd.backend import OscarAttentionImpl
 from oscar_new_amd.config import OscarConfig
-from tests._state import bits, make_state, prepare_prefix
+from tests._state import bits, check_step_against_cache, make_state, prepare_prefix
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -43,7 +43,7 @@ def _case(lengths, prefixes, seed, cfg=None):
     kernels.prepare_tasks(meta.query_start_loc, meta.counts, meta.tasks, meta.task_count,
                           meta.max_num_reqs, layout.config.queries_per_tile)
     return SimpleNamespace(layout=layout, raw=raw, meta=meta, rk=rk, rv=rv, ks=ks, vs=vs, qs=qs,
-                           q=q, k=k, v=v, prefixes=prefixes)
+                           q=q, k=k, v=v, prefixes=prefixes, tables=tables)
 
 
 def _views(raw, layout, pages=20):
@@ -70,9 +70,9 @@ def _forward(c, form, splits, raw=None):
     n = c.q.shape[0]
     raw = c.raw.clone() if raw is None else raw
     k_cache, v_cache = _views(raw, c.layout)
-    impl = OscarAttentionImpl(6, 256, 1 / 16, 1, c.layout.config, fused=form != "single",
+    impl = OscarAttentionImpl.standalone(6, 256, 1 / 16, 1, c.layout.config, fused=form != "single",
                               one_launch_post=form == "fused1")
-    impl.initialize_layer(c.rk, c.rv)
+    impl.set_rotations(c.rk, c.rv)
     impl.partition_for = lambda meta, s=splits: (s, 0)
     c.meta.merged_lse = torch.full((n, 6), 7.0, device=DEV)
     out = torch.full((n, 6 * 256), 3.0, device=DEV, dtype=torch.bfloat16)
@@ -106,9 +106,9 @@ def test_token_bounded_fused_step_against_dense_reference(lengths, prefixes, par
     for fused, one in ((True, True), (False, False), (True, False)):
         raw = c.raw.clone()
         k_cache, v_cache = _views(raw, c.layout)
-        impl = OscarAttentionImpl(6, 256, 1 / 16, 1, c.layout.config, split_policy="mi355x",
+        impl = OscarAttentionImpl.standalone(6, 256, 1 / 16, 1, c.layout.config, split_policy="mi355x",
                                   fused=fused, one_launch_post=one)
-        impl.initialize_layer(c.rk, c.rv)
+        impl.set_rotations(c.rk, c.rv)
         impl.partition_for = lambda meta, pt=partition: pt
         c.meta.merged_lse = torch.empty((n, 6), device=DEV)
         out = torch.empty((n, 6 * 256), device=DEV, dtype=torch.bfloat16)
@@ -118,6 +118,8 @@ def test_token_bounded_fused_step_against_dense_reference(lengths, prefixes, par
     for other in outs[1:]:
         for a, b in zip(outs[0][:3], other[:3]):
             assert torch.equal(a, b)
+    check_step_against_cache(outs[0][3], outs[0][1], c.raw, c.layout, c.tables, lengths,
+                             prefixes, c.qs, c.ks, c.vs, c.rk, c.rv)
     want, want_lse = [], []
     for qi, ki, vi, p in zip(c.qs, c.ks, c.vs, c.prefixes):
         o, l = O.hybrid_reference(bits(qi), bits(ki), bits(vi), p, bits(c.rk), bits(c.rv),
@@ -140,8 +142,8 @@ def test_fused_step_replays_in_a_graph():
     n = c.q.shape[0]
     raw_graph, raw_eager = c.raw.clone(), c.raw.clone()
     kg, vg = _views(raw_graph, c.layout)
-    impl = OscarAttentionImpl(6, 256, 1 / 16, 1, c.layout.config, fused=True)
-    impl.initialize_layer(c.rk, c.rv)
+    impl = OscarAttentionImpl.standalone(6, 256, 1 / 16, 1, c.layout.config, fused=True)
+    impl.set_rotations(c.rk, c.rv)
     impl.partition_for = lambda meta: (8, 0)
     lse = c.meta.merged_lse = torch.empty((n, 6), device=DEV)
     out = torch.empty((n, 6 * 256), device=DEV, dtype=torch.bfloat16)
@@ -174,12 +176,16 @@ def test_fused_step_against_dense_reference(lengths, prefixes, splits):
     c = _case(lengths, prefixes, seed=11)
     n = c.q.shape[0]
     k_cache, v_cache = _views(c.raw, c.layout)
-    impl = OscarAttentionImpl(6, 256, 1 / 16, 1, c.layout.config, fused=True)
-    impl.initialize_layer(c.rk, c.rv)
+    impl = OscarAttentionImpl.standalone(6, 256, 1 / 16, 1, c.layout.config, fused=True)
+    impl.set_rotations(c.rk, c.rv)
     impl.partition_for = lambda meta, s=splits: (s, 0)
     c.meta.merged_lse = torch.empty((n, 6), device=DEV)
     out = torch.empty((n, 6 * 256), device=DEV, dtype=torch.bfloat16)
+    before = c.raw.clone()  # the step's window store may overwrite ring slots it read
     impl.forward(None, c.q, c.k, c.v, (k_cache, v_cache), c.meta, out)
+    torch.cuda.synchronize()
+    check_step_against_cache(out, c.meta.merged_lse, before, c.layout, c.tables, lengths,
+                             prefixes, c.qs, c.ks, c.vs, c.rk, c.rv)
     want, want_lse = [], []
     for qi, ki, vi, p in zip(c.qs, c.ks, c.vs, c.prefixes):
         o, l = O.hybrid_reference(bits(qi), bits(ki), bits(vi), p, bits(c.rk), bits(c.rv),
@@ -250,8 +256,8 @@ def test_fused_step_masks_padded_tokens_and_dummy_runs():
                           c.meta.max_num_reqs, 4)
     before = c.raw.clone()
     k_cache, v_cache = _views(c.raw, c.layout)
-    impl = OscarAttentionImpl(6, 256, 1 / 16, 1, c.layout.config, fused=True)
-    impl.initialize_layer(c.rk, c.rv)
+    impl = OscarAttentionImpl.standalone(6, 256, 1 / 16, 1, c.layout.config, fused=True)
+    impl.set_rotations(c.rk, c.rv)
     c.meta.merged_lse = torch.empty((n, 6), device=DEV)
     out = torch.full((n, 6 * 256), 3.0, device=DEV, dtype=torch.bfloat16)
     impl.forward(None, c.q, c.k, c.v, (k_cache, v_cache), c.meta, out)

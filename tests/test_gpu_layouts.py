@@ -52,8 +52,8 @@ def _case(page, lengths, prefixes, seed):
 def _step(c, fused, one_launch, splits):
     layout, raw0, meta, rk, rv, _, _, _, q, k, v = c
     raw = raw0.clone()
-    impl = OscarAttentionImpl(HQ, 256, 1 / 16, H, CFG, fused=fused, one_launch_post=one_launch)
-    impl.initialize_layer(rk, rv)
+    impl = OscarAttentionImpl.standalone(HQ, 256, 1 / 16, H, CFG, fused=fused, one_launch_post=one_launch)
+    impl.set_rotations(rk, rv)
     impl.partition_for = lambda meta: (splits, 0)
     n = q.shape[0]
     meta.merged_lse = torch.full((n, HQ), 7.0, device=DEV)
