@@ -33,7 +33,8 @@ enum oscar_status {
   OSCAR_E_SHAPE = -2,       /* sizes/strides inconsistent or unsupported */
   OSCAR_E_LAYOUT = -3,      /* cache geometry invalid */
   OSCAR_E_ALIGN = -4,       /* pointer or stride alignment not supported */
-  OSCAR_E_UNSUPPORTED = -5  /* valid request outside this build's coverage */
+  OSCAR_E_UNSUPPORTED = -5, /* valid request outside this build's coverage */
+  OSCAR_E_SCRATCH = -6      /* request larger than the fixed scratch of a no-alloc entry */
 };
 
 /* Cache geometry (reference: oscar_ascend/layout.py:9-44, config.py:45-63). */
@@ -288,6 +289,38 @@ int oscar_history_post(const void* query, int64_t q_s0, int64_t q_s1, int64_t q_
                        const void* key, int64_t k_s0, int64_t k_s1, const void* value,
                        int64_t v_s0, int64_t v_s1, void* window, int64_t window_elems,
                        int64_t max_reqs, void* stream);
+
+/*
+ * history_post_noalloc -- oscar_history_post without caller scratch: the split partials, their
+ * LSEs and the completion counters live in a fixed device array of this library
+ * (OSCAR_NOALLOC_SCRATCH_BYTES per GPU, held until the process ends), so the call allocates
+ * nothing and needs no workspace argument. No counterpart in the reference: it is for callers
+ * that cannot allocate device memory (code under graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc). Arguments and results are those of oscar_history_post without
+ * partials, lse, counters and counter_slots; the output and merged_lse bits are the same.
+ * Limits: oscar_noalloc_scratch_bytes(n, hq, splits) <= OSCAR_NOALLOC_SCRATCH_BYTES and
+ * programs * kv_heads <= 16384, else OSCAR_E_SCRATCH (nothing launched). The first call on a
+ * device resolves the array's address and clears its counters on `stream`. Every call on a GPU
+ * shares that GPU's array: calls that overlap on one GPU (concurrent streams) race.
+ */
+#define OSCAR_NOALLOC_SCRATCH_BYTES (32ll << 20)
+
+int64_t oscar_noalloc_scratch_bytes(int64_t n, int64_t hq, int32_t splits);
+
+int oscar_history_post_noalloc(const void* query, int64_t q_s0, int64_t q_s1, int64_t q_s2,
+                               const void* history, int64_t history_bytes,
+                               const int32_t* qstarts, const int32_t* seq_lens,
+                               const int32_t* block_tables, int64_t table_stride,
+                               int64_t table_columns, const int32_t* counts,
+                               const int32_t* tasks, const int32_t* task_count, int64_t n,
+                               int64_t hq, int64_t programs, int32_t splits, int32_t block_n,
+                               int32_t query_tile, int32_t max_query_len, float scale,
+                               int32_t split_tokens, const oscar_layout* layout,
+                               const float* raw_partials, const float* raw_lse, const void* rv,
+                               void* output, float* merged_lse, const void* key, int64_t k_s0,
+                               int64_t k_s1, const void* value, int64_t v_s0, int64_t v_s1,
+                               void* window, int64_t window_elems, int64_t max_reqs,
+                               void* stream);
 
 #ifdef __cplusplus
 }

@@ -111,7 +111,21 @@ SIGNATURES = {
         _P, _I64, _I64, _P, _I64, _I64,  # key, value (+ row strides)
         _P, _I64, _I64, _P,  # window, elems, max_reqs, stream
     ],
+    "oscar_history_post_noalloc": [
+        _P, _I64, _I64, _I64,  # query (rotated)
+        _P, _I64,  # history, bytes
+        _P, _P, _P, _I64, _I64,  # qstarts, seq_lens, block_tables, stride, columns
+        _P, _P, _P,  # counts, tasks, task_count
+        _I64, _I64, _I64, _I32, _I32, _I32, _I32, _F, _I32,  # n hq programs splits bn qt mql scale st
+        POINTER(OscarLayout),  # layout
+        _P, _P, _P, _P, _P,  # raw partials, raw lse, rv, output, merged_lse
+        _P, _I64, _I64, _P, _I64, _I64,  # key, value (+ row strides)
+        _P, _I64, _I64, _P,  # window, elems, max_reqs, stream
+    ],
+    "oscar_noalloc_scratch_bytes": [_I64, _I64, _I32],
 }
+RESTYPES = {"oscar_noalloc_scratch_bytes": c_int64}
+NOALLOC_SCRATCH_BYTES = 32 << 20  # OSCAR_NOALLOC_SCRATCH_BYTES
 
 _lib = None
 
@@ -130,7 +144,7 @@ def library():
     for name, argtypes in SIGNATURES.items():
         fn = getattr(lib, name)
         fn.argtypes = argtypes
-        fn.restype = c_int32
+        fn.restype = RESTYPES.get(name, c_int32)
     lib.oscar_status_string.argtypes = [c_int32]
     lib.oscar_status_string.restype = ctypes.c_char_p
     _lib = lib

@@ -51,6 +51,8 @@ extern "C" const char* oscar_status_string(int status) {
     case OSCAR_E_LAYOUT: return "invalid cache layout";
     case OSCAR_E_ALIGN: return "pointer or stride alignment not supported";
     case OSCAR_E_UNSUPPORTED: return "request outside this build's coverage";
+    case OSCAR_E_SCRATCH:
+      return "request exceeds the fixed scratch array of an allocation-free entry point";
     default: break;
   }
   if (status > 0) return hipGetErrorString(static_cast<hipError_t>(status));

@@ -14,7 +14,8 @@ ROOT = Path(__file__).resolve().parents[1]
 
 def declared_symbols():
     text = (ROOT / "include" / "oscar_hip.h").read_text()
-    return sorted(set(re.findall(r"^\s*(?:int|const char\*)\s+(oscar_\w+)\s*\(", text, re.M)))
+    return sorted(set(re.findall(r"^\s*(?:int|int64_t|const char\*)\s+(oscar_\w+)\s*\(", text,
+                                 re.M)))
 
 
 def test_header_and_binding_agree():
