@@ -63,6 +63,8 @@ def parse_args(argv=None):
     p.add_argument("--no-graph", action="store_true", help="eager launches instead of HIP graphs")
     p.add_argument("--one-launch-post", action="store_true",
                    help="history branch and post-attention in one launch (kernels.history_post)")
+    p.add_argument("--layer-step", action="store_true",
+                   help="the one-launch layer step (kernels.layer_step) instead of three launches")
     p.add_argument("--mode", default="step", choices=("step", "history", "copy", "prefill"),
                    help="step: full benchmark; history: only the history-attention launches "
                         "(for rocprofv3 counters); copy: a plain device copy of --copy-mib MiB "
@@ -439,7 +441,8 @@ def main(argv=None):
     impls = []
     for _ in layers:
         impl = OscarAttentionImpl.standalone(6, 256, 1 / 16, 1, w.cfg, split_policy=cfg["splits"],
-                                  one_launch_post=args.one_launch_post)
+                                             one_launch_post=args.one_launch_post,
+                                             layer_step=args.layer_step)
         impl.set_rotations(w.rk, w.rv)
         impls.append(impl)
     ntok = w.q.shape[0]
@@ -580,6 +583,7 @@ def main(argv=None):
             "splits": splits, "split_tokens": split_tokens, "layers_cycled": len(layers),
             "hip_graph": graphs is not None, "seed": args.seed,
             "one_launch_post": bool(args.one_launch_post),
+            "layer_step": bool(args.layer_step),
         },
         "us_per_layer_step": us_step,
         "gpu_us_per_layer_step": gpu_ms / args.steps * 1e3,

@@ -291,6 +291,38 @@ int oscar_history_post(const void* query, int64_t q_s0, int64_t q_s1, int64_t q_
                        int64_t max_reqs, void* stream);
 
 /*
+ * layer_step -- one FULL-attention layer step in ONE launch (no reference counterpart: it
+ * replaces the whole sequence of backend.py:171-226 -- rotate K, V and q, store_int2, the
+ * history and BF16 attention branches, merge_splits, rotate(hrot, Rv.T), merge_paths and
+ * store_windows -- for decode and MTP-verification steps). query/key/value: the step's
+ * UNROTATED bf16 rows (row strides in elements, multiples of 8, rows 16-byte aligned);
+ * history/window: the K/V stripe views (both written: the INT2 slots of the step's tokens and
+ * the windows); rk_t / rv_t: R_k^T and R_v^T, contiguous bf16 [256][256]; rv: R_v row-major.
+ * Scratch: partials / lse (fp32 [n, hq, splits, 256] / [n, hq, splits]), raw_partials /
+ * raw_lse (fp32 [n, hq, 4, 256] / [n, hq, 4]) and counters (int32 [counter_slots >= programs *
+ * kv_heads], zero before the first call, left zero by every call; calls that overlap on one
+ * device must not share them). output: bf16 [n, hq * 256]; merged_lse optional fp32 [n, hq].
+ * The INT2 bytes and window bytes are those of the single entry points; the output and merged
+ * LSE agree with them within rounding (the BF16 branch is merged from up to four splits).
+ * Coverage (else OSCAR_E_UNSUPPORTED: use the three fused launches): query rows per task
+ * (max_query_len * hq / kv_heads) <= 8, 1 <= max_query_len <= query_tile <= 4 (one task per
+ * request), splits <= 16.
+ */
+int oscar_layer_step(const void* query, int64_t q_s0, int64_t q_s1, const void* key, int64_t k_s0,
+                     int64_t k_s1, const void* value, int64_t v_s0, int64_t v_s1, void* history,
+                     int64_t history_bytes, void* window, int64_t window_elems,
+                     const int32_t* qstarts, const int32_t* seq_lens, const int32_t* block_tables,
+                     int64_t table_stride, int64_t table_columns, const int32_t* counts,
+                     const int32_t* tasks, const int32_t* task_count, const int64_t* slots,
+                     int64_t n, int64_t hq, int64_t programs, int32_t splits, int32_t block_n,
+                     int32_t query_tile, int32_t max_query_len, float scale,
+                     int32_t split_tokens, const void* rk_t, const void* rv_t, const void* rv,
+                     const oscar_clip* clip, const oscar_layout* layout, float* partials,
+                     float* lse, float* raw_partials, float* raw_lse, int32_t* counters,
+                     int64_t counter_slots, void* output, float* merged_lse, int64_t max_reqs,
+                     void* stream);
+
+/*
  * history_post_noalloc -- oscar_history_post without caller scratch: the split partials, their
  * LSEs and the completion counters live in a fixed device array of this library
  * (OSCAR_NOALLOC_SCRATCH_BYTES per GPU, held until the process ends), so the call allocates

@@ -111,6 +111,16 @@ SIGNATURES = {
         _P, _I64, _I64, _P, _I64, _I64,  # key, value (+ row strides)
         _P, _I64, _I64, _P,  # window, elems, max_reqs, stream
     ],
+    "oscar_layer_step": [
+        _P, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64,  # query, key, value (+ row strides)
+        _P, _I64, _P, _I64,  # history, bytes, window, elems
+        _P, _P, _P, _I64, _I64,  # qstarts, seq_lens, block_tables, stride, columns
+        _P, _P, _P, _P,  # counts, tasks, task_count, slots
+        _I64, _I64, _I64, _I32, _I32, _I32, _I32, _F, _I32,  # n hq programs splits bn qt mql scale st
+        _P, _P, _P, POINTER(OscarClip), POINTER(OscarLayout),  # rk_t, rv_t, rv, clip, layout
+        _P, _P, _P, _P, _P, _I64,  # partials, lse, raw partials, raw lse, counters, slots
+        _P, _P, _I64, _P,  # output, merged_lse, max_reqs, stream
+    ],
     "oscar_history_post_noalloc": [
         _P, _I64, _I64, _I64,  # query (rotated)
         _P, _I64,  # history, bytes

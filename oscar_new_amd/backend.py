@@ -119,15 +119,19 @@ class OscarAttentionImpl:
     ``oscar_config`` (default: from the environment, with the speculative token count of the
     vLLM config), ``split_policy`` ("reference": config.py:84-89; "mi355x": fill the 256 CUs
     with token-bounded splits), ``fused`` (three launches per step instead of the nine single
-    launches; same bits) and ``one_launch_post`` (history branch and post-attention in one
-    launch where it applies; same bits).
+    launches; same bits), ``layer_step`` (opt-in: the whole step in one launch where it
+    applies, the INT2 and window bytes of the other forms and the output within rounding of
+    them; slower than three launches on MI355X today, because its latency-bound parts wait
+    behind the INT2 stream's memory traffic) and
+    ``one_launch_post`` (history branch and post-attention in one launch where it applies and
+    the one-launch step does not; same bits as three launches).
     """
 
     def __init__(self, num_heads, head_size, scale, num_kv_heads, alibi_slopes=None,
                  sliding_window=None, kv_cache_dtype="auto", logits_soft_cap=None,
                  attn_type="decoder", kv_sharing_target_layer_name=None, *, vllm_config=None,
                  oscar_config=None, split_policy="reference", fused=True, one_launch_post=False,
-                 **kwargs):
+                 layer_step=False, **kwargs):
         unsupported = (
             (alibi_slopes is not None, "ALiBi"),
             (sliding_window is not None, "sliding-window attention"),
@@ -164,6 +168,7 @@ class OscarAttentionImpl:
         self.split_policy = split_policy
         self.fused = fused
         self.one_launch_post = one_launch_post
+        self.layer_step = layer_step
         self.rk = self.rv = self.rk_cols = self.rv_cols = self.rk_t = self.rv_t = None
         self.history = self.window = None
         self.cache_identity = None
@@ -271,10 +276,16 @@ class OscarAttentionImpl:
         return output
 
     def _fused_step(self, q, k, v, meta, splits, split_tokens, rows, lse):
-        """pre-attention (q rotation, K/V INT2 store, BF16 branch) -> history -> post
-        (split merge, inverse V rotation, path merge, windows); the last two in one launch
-        with ``one_launch_post`` where it applies."""
+        """The whole step in one launch (``layer_step``, where it applies), else pre-attention
+        (q rotation, K/V INT2 store, BF16 branch) -> history -> post (split merge, inverse V
+        rotation, path merge, windows), the last two in one launch with ``one_launch_post``."""
         layout = meta.layout
+        if self.layer_step and kernels.layer_step_supported(meta, layout, self.num_heads, splits,
+                                                            q.shape[0]):
+            kernels.layer_step(q, k, v, self.history, self.window, meta, layout, self.scale,
+                               splits, self.rk_t, self.rv_t, self.rv, rows, lse,
+                               split_tokens=split_tokens)
+            return
         qrot, rp, rl = kernels.pre_attention(q, k, v, self.history, self.window, meta, layout,
                                              self.scale, self.rk_t, self.rv_t)
         if self.one_launch_post and kernels.history_post_supported(

@@ -34,6 +34,7 @@
 #include "attention.h"
 #include "dma.h"
 #include "finish.h"
+#include "layer.h"
 
 namespace oscar {
 namespace {
@@ -581,16 +582,25 @@ __host__ __device__ constexpr int pair_token(int ga, int e) {
 __host__ __device__ constexpr int pair_slot(int t) { return t ^ (((t >> 4) & 3) << 2); }
 static_assert(pair_slot(pair_slot(45)) == 45 && pair_slot(21) == 17, "pair_slot is an involution");
 
-// kFinish: the two-launch step's history launch (finish.h): the grid has one more z slice
+// kMode 0: the history branch alone (attention_partials).
+// kMode 1: the two-launch step's history launch (finish.h): the grid has one more z slice
 // (window stores, padded rows), unused split slots are left unwritten (the merge reads only
 // the task's splits), and the workgroup that completes a (task, head) finishes its rows.
-template <bool kFinish>
-__device__ __forceinline__ void history_pair_body(const AttnArgs& a, const FinishArgs* fin) {
-  if constexpr (kFinish) {
+// kMode 2: the one-launch layer step (layer.h): as 1, and the workgroups also rotate the query
+// (a.query is the unrotated query), store the step's INT2 slots, share the BF16 branch, and
+// the finisher stores the windows; padded rows are cleared by split 0 of each program.
+template <int kMode>
+__device__ __forceinline__ void history_pair_body(const AttnArgs& a, const FinishArgs* fin,
+                                                  const LayerArgs* lay) {
+  constexpr bool kFinish = kMode >= 1;
+  if constexpr (kMode == 1) {
     if (static_cast<int>(blockIdx.z) == a.splits) {
       finish_extra(*fin, blockIdx.y);
       return;
     }
+  }
+  if constexpr (kMode == 2) {
+    if (blockIdx.y == 0 && blockIdx.z == 0) clear_padded_rows(*fin, blockIdx.x);
   }
   __shared__ __attribute__((aligned(16))) uint8_t s_ring[kRingBytes];
   __shared__ uint32_t s_off[kTableCache];
@@ -599,6 +609,14 @@ __device__ __forceinline__ void history_pair_body(const AttnArgs& a, const Finis
                 "query rows and operand images fit wavefront 3's stages");
   static_assert(4 * 8 * 256 * 4 <= kRingBytes, "the epilogue merge fits the ring");
   static_assert(kFinishLdsBytes <= kRingBytes, "the finisher fits the ring");
+  static_assert(kLayerRingBytes <= kRingBytes, "the layer-step finisher fits the ring");
+  static_assert(16 * kStageRowBytes + 4 * 2 * 8 * 16 * 4 <= 2 * kStageBytes,
+                "the layer step's 16-row staging tile and operand images fit wavefront 3's stages");
+
+  // Layer step: R_k^T operands of the query rotation are requested first (they depend on
+  // nothing), so that they arrive with the task metadata.
+  u32x4 rb[4][8];
+  if constexpr (kMode == 2) load_rt_tiles(lay->rk_t, rb);
 
   Task t;
   if (!read_task(a, t, blockIdx.x)) return;
@@ -649,8 +667,20 @@ __device__ __forceinline__ void history_pair_body(const AttnArgs& a, const Finis
   };
 
   // ---- query rows -> LDS (wavefront 3's stages): piece p of row r at r * 32 + (p ^ r).
+  // Layer step: 16 staged rows, the query rows 0..7 and, in the workgroups that store them,
+  // the current key rows (8..11) and value rows (12..15) of the task's tokens.
   uint8_t* q_lds = s_ring + 6 * kStageBytes;
-  uint32_t* q_img = reinterpret_cast<uint32_t*>(q_lds + 8 * 512);  // [b][term][r][h][d]
+  // The FP8 operand images [b][term][r][h][d]: after the staged rows, or, in the layer step,
+  // in the finisher's LDS (free until the end), so that they outlive wavefront 3's stages.
+  __shared__ __attribute__((aligned(16))) uint8_t s_fin[kMode == 2 ? kLayerFinBytes : 16];
+  static_assert(kMode != 2 || 4 * 2 * 8 * 16 * 4 <= kLayerFinBytes, "images fit s_fin");
+  uint32_t* q_img = reinterpret_cast<uint32_t*>(kMode == 2 ? s_fin : q_lds + 8 * 512);
+  bool stores_k = false, stores_v = false;
+  const int nraw = min(kRawSplits, nsplit);
+  if constexpr (kMode == 2) {
+    stores_k = split == 4 % nsplit;
+    stores_v = split == 5 % nsplit;
+  }
   {
     const int slot = wave * 64 + lane;
     const int row = slot >> 5, piece = (slot & 31) ^ row;
@@ -658,6 +688,19 @@ __device__ __forceinline__ void history_pair_body(const AttnArgs& a, const Finis
     const uint16_t* src =
         ri.valid ? a.query + ri.token * a.qs0 + ri.qhead * a.qs1 + 8 * piece : a.query;
     dma_dwordx4(src, lds_addr(q_lds) + 1024 * wave);
+    if constexpr (kMode == 2) {
+      // Rows 8 + i (keys) and 12 + i (values) of current token i < min(qlen, 4).
+      const int row2 = 8 + row, i = row & 3;
+      const bool is_v = row >= 4;
+      const bool want = (is_v ? stores_v : stores_k) && i < t.qlen;
+      const int64_t token = static_cast<int64_t>(t.qstart) + t.qoff + i;
+      const int piece2 = (slot & 31) ^ (row2 & 31);
+      const uint16_t* src2 =
+          want ? (is_v ? a.value + token * a.vs0 + head * a.vs1
+                       : a.key + token * a.ks0 + head * a.ks1) + 8 * piece2
+               : a.query;
+      dma_dwordx4(src2, lds_addr(q_lds) + 4096 + 1024 * wave);
+    }
   }
   if (nchunk > 0) {
     const int nkb = min(((p_hi - 1) >> a.L.bk_shift) - kb_first + 1, kTableCache);
@@ -669,6 +712,29 @@ __device__ __forceinline__ void history_pair_body(const AttnArgs& a, const Finis
   if (wave < 3) {
     if (nmine > 0) issue(0, 0);
     if (nmine > 1) issue(1, 1);
+  }
+
+  // ---- layer step: rotate the staged rows in place (rows 0..7 and the key rows by R_k, the
+  // value rows by R_v), the bits of the rotate entry point. The BF16 branch's wavefront keeps
+  // the unrotated query rows (its B operand) in registers.
+  const bool raw_wave = kMode == 2 && wave == 3 && split < nraw;
+  u32x4 qraw[8];
+  if constexpr (kMode == 2) {
+    u32x4 aop[8];
+    load_stage_a(q_lds, aop);
+#pragma unroll
+    for (int m = 0; m < 8; ++m) {
+      qraw[m] = u32x4{0u, 0u, 0u, 0u};
+      if (raw_wave && n < 8)
+        qraw[m] = *reinterpret_cast<const u32x4*>(q_lds + n * 512 + 16 * ((8 * g + m) ^ n));
+    }
+    barrier_lds();  // every operand is in registers; the rotated rows replace the staged ones
+    rotate_stage(aop, rb, q_lds, 0, stores_k ? 12 : 8);
+    if (stores_v) {
+      load_rt_tiles(lay->rv_t, rb);
+      rotate_stage(aop, rb, q_lds, 12, 16);
+    }
+    barrier_lds();
   }
 
   // ---- row statistics (every wavefront, redundantly): lane l reduces row l / 8 over dims
@@ -728,7 +794,7 @@ __device__ __forceinline__ void history_pair_body(const AttnArgs& a, const Finis
   }
   barrier_lds();
   i32x8 qb[4][kQTerms];
-  {
+  auto load_qb = [&]() {
     const bool live = (n < 8) == (g < 2);
     const int h = g & 1;
 #pragma unroll
@@ -742,11 +808,42 @@ __device__ __forceinline__ void history_pair_body(const AttnArgs& a, const Finis
                                    (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]}
                            : i32x8{0, 0, 0, 0, 0, 0, 0, 0};
       }
+  };
+  // The layer step loads them after its BF16-branch share (fewer registers live there).
+  if constexpr (kMode != 2) load_qb();
+  // Layer step: wavefront i keeps the rotated key / value row of current token i (if this
+  // workgroup stores it) before wavefront 3's stages are reused.
+  const int kv_rows = min(t.qlen, 4);
+  const bool do_k = stores_k && wave < kv_rows, do_v = stores_v && wave < kv_rows;
+  float kx[4], vx[4];
+  if constexpr (kMode == 2) {
+    if (do_k) stage_row_floats(q_lds, 8 + wave, kx);
+    if (do_v) stage_row_floats(q_lds, 12 + wave, vx);
   }
   barrier_lds();  // everyone is done with wavefront 3's stages
   if (wave == 3) {
     if (nmine > 0) issue(0, 0);
     if (nmine > 1) issue(1, 1);
+  }
+  if constexpr (kMode == 2) {
+    // INT2 store of the step's own key / value rows (store_int2 semantics), then this split's
+    // share of the BF16 branch, while the first chunks are in flight.
+    const int64_t token = static_cast<int64_t>(t.qstart) + t.qoff + wave;
+    if (do_k) store_int2_row(a, *lay, token, head, false, kx);
+    if (do_v) store_int2_row(a, *lay, token, head, true, vx);
+    if (raw_wave) {
+      const int first_blk =
+          a.table_columns > 0 ? a.table[static_cast<int64_t>(t.req) * a.table_stride] : -1;
+      RawTask r;
+      r.high = t.sink_len + t.prefix - t.recent_begin;
+      r.win = -1;
+      if (first_blk >= 0) {
+        const int64_t owner = fastdiv(static_cast<uint32_t>(first_blk), a.L.bpp_div);
+        r.win = owner * (a.L.page_bytes / 2) + static_cast<int64_t>(head) * kHeadDim;
+      }
+      raw_share(a, *lay, t, r, head, split, nraw, qraw);
+    }
+    load_qb();
   }
 
   // ---- per-lane LDS offsets inside a stage (token t's record starts at kSkew + 144
@@ -979,12 +1076,20 @@ __device__ __forceinline__ void history_pair_body(const AttnArgs& a, const Finis
   if constexpr (kFinish) {
     __shared__ int s_flag;
     int32_t* counter = fin->counters + static_cast<int64_t>(blockIdx.x) * a.L.kv_heads + head;
-    if (finish_arrive(counter, nsplit, &s_flag)) finish_task8(*fin, a, t, head, nsplit, s_ring);
+    if (finish_arrive(counter, nsplit, &s_flag)) {
+      if constexpr (kMode == 1) {
+        finish_task8(*fin, a, t, head, nsplit, s_ring);
+      } else {
+        finish_layer8(*fin, *lay, a, t, head, nsplit, nraw, s_ring, s_fin);
+        // Every split of the task, and so every read of its window, is done.
+        store_window_request(fin->p.win, t.req, head);
+      }
+    }
   }
 }
 
 __global__ __launch_bounds__(kThreads, 2) void history_pair_kernel(const AttnArgs a) {
-  history_pair_body<false>(a, nullptr);
+  history_pair_body<0>(a, nullptr, nullptr);
 }
 
 struct HistoryFinishArgs {
@@ -993,7 +1098,17 @@ struct HistoryFinishArgs {
 };
 
 __global__ __launch_bounds__(kThreads, 2) void history_pair_finish_kernel(const HistoryFinishArgs h) {
-  history_pair_body<true>(h.a, &h.f);
+  history_pair_body<1>(h.a, &h.f, nullptr);
+}
+
+struct LayerStepArgs {
+  AttnArgs a;
+  FinishArgs f;
+  LayerArgs l;
+};
+
+__global__ __launch_bounds__(kThreads, 2) void layer_step_kernel(const LayerStepArgs h) {
+  history_pair_body<2>(h.a, &h.f, &h.l);
 }
 
 }  // namespace
@@ -1005,6 +1120,15 @@ hipError_t launch_history(const AttnArgs& a, dim3 grid, int rows, hipStream_t st
     hipLaunchKernelGGL(history_kernel<1>, grid, dim3(kThreads), 0, stream, a);
   else
     hipLaunchKernelGGL(history_kernel<2>, grid, dim3(kThreads), 0, stream, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_layer_step(const AttnArgs& a, const FinishArgs& f, const LayerArgs& l,
+                             hipStream_t stream) {
+  const LayerStepArgs h{a, f, l};
+  const dim3 grid(static_cast<unsigned>(f.programs), static_cast<unsigned>(a.L.kv_heads),
+                  static_cast<unsigned>(a.splits));
+  hipLaunchKernelGGL(layer_step_kernel, grid, dim3(kThreads), 0, stream, h);
   return hipGetLastError();
 }
 

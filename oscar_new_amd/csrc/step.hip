@@ -20,6 +20,7 @@
 #include "finish.h"
 #include "post.h"
 #include "quant.h"
+#include "layer.h"
 #include "raw.h"
 
 namespace oscar {
@@ -373,4 +374,62 @@ extern "C" int oscar_history_post(
   f.counters = counters;
   f.programs = static_cast<int32_t>(programs);
   return static_cast<int>(launch_history_finish(a, f, as_stream(stream)));
+}
+
+extern "C" int oscar_layer_step(
+    const void* query, int64_t q_s0, int64_t q_s1, const void* key, int64_t k_s0, int64_t k_s1,
+    const void* value, int64_t v_s0, int64_t v_s1, void* history, int64_t history_bytes,
+    void* window, int64_t window_elems, const int32_t* qstarts, const int32_t* seq_lens,
+    const int32_t* block_tables, int64_t table_stride, int64_t table_columns,
+    const int32_t* counts, const int32_t* tasks, const int32_t* task_count, const int64_t* slots,
+    int64_t n, int64_t hq, int64_t programs, int32_t splits, int32_t block_n, int32_t query_tile,
+    int32_t max_query_len, float scale, int32_t split_tokens, const void* rk_t, const void* rv_t,
+    const void* rv, const oscar_clip* clip, const oscar_layout* layout, float* partials,
+    float* lse, float* raw_partials, float* raw_lse, int32_t* counters, int64_t counter_slots,
+    void* output, float* merged_lse, int64_t max_reqs, void* stream) {
+  using namespace oscar;
+  AttnArgs a;
+  int64_t qrows = 0;
+  int st = make_attn_args(query, q_s0, q_s1, 1, key, k_s0, k_s1, 1, value, v_s0, v_s1, 1, history,
+                          history_bytes, window, window_elems, qstarts, seq_lens, block_tables,
+                          table_stride, table_columns, counts, tasks, task_count, n, hq, programs,
+                          splits, block_n, query_tile, max_query_len, scale, 0, split_tokens, layout,
+                          partials, lse, &a, &qrows);
+  if (st != OSCAR_OK) return st;
+  // One task per request (every request's tokens in one query tile), <= 8 query rows per task,
+  // <= 16 splits (the one-round merges of the finisher).
+  if (qrows > 8 || splits > kWaveMergeSplits || max_query_len < 1 || max_query_len > query_tile ||
+      query_tile > 4)
+    return OSCAR_E_UNSUPPORTED;
+  if (!clip) return OSCAR_E_NULL;
+  if (clip->mode < OSCAR_CLIP_PERCENTILE || clip->mode > OSCAR_CLIP_SEARCH) return OSCAR_E_SHAPE;
+  FinishArgs f{};
+  st = make_post_args(partials, lse, splits, raw_partials, raw_lse, counts, rv, n, hq, output,
+                      merged_lse, key, k_s0, k_s1, value, v_s0, v_s1, window, window_elems,
+                      qstarts, seq_lens, block_tables, table_stride, max_reqs, layout, &f.p);
+  if (st != OSCAR_OK || n == 0) return st;
+  if (!slots || !rk_t || !rv_t || !counters) return OSCAR_E_NULL;
+  if (!aligned16(key) || !aligned16(value) || !aligned16(rk_t) || !aligned16(rv_t) ||
+      !aligned16(raw_partials) || k_s0 % 8 || k_s1 % 8 || v_s0 % 8 || v_s1 % 8 ||
+      reinterpret_cast<uintptr_t>(counters) % 4 || reinterpret_cast<uintptr_t>(history) % 4)
+    return OSCAR_E_ALIGN;
+  if (counter_slots < programs * a.L.kv_heads) return OSCAR_E_SHAPE;
+  // The finisher reads the split rows through 32-bit buffer offsets.
+  if (n * hq * splits * kHeadDim * 4 >= (1ll << 32) || n * hq * kRawSplits * kHeadDim * 4 >= (1ll << 32))
+    return OSCAR_E_UNSUPPORTED;
+  f.counters = counters;
+  f.programs = static_cast<int32_t>(programs);
+  LayerArgs l{};
+  l.rk_t = static_cast<const uint16_t*>(rk_t);
+  l.rv_t = static_cast<const uint16_t*>(rv_t);
+  l.history = static_cast<uint8_t*>(history);
+  l.slots = slots;
+  l.mode = clip->mode;
+  l.k_ratio = clip->k_ratio;
+  l.v_ratio = clip->v_ratio;
+  l.k_factor = clip->k_factor;
+  l.v_factor = clip->v_factor;
+  l.raw_part = raw_partials;
+  l.raw_lse = raw_lse;
+  return static_cast<int>(launch_layer_step(a, f, l, as_stream(stream)));
 }

@@ -26,6 +26,8 @@ __all__ = [
     "dequant_inverse_rotate",
     "pre_attention",
     "post_attention",
+    "history_post",
+    "layer_step",
     "layout_struct",
     "clip_struct",
 ]
@@ -520,6 +522,75 @@ def history_post(query, history, meta, layout, scale, splits, raw_partials, raw_
             window.numel(), meta.max_num_reqs, stream,
         ),
         "history_post",
+    )
+
+
+RAW_SPLITS = 4  # BF16-branch partials per row in layer_step
+
+
+def layer_step_supported(meta, layout, hq, splits, tokens=None):
+    """Whether ``layer_step`` covers this step: one task per request (1 <= max_query_len <=
+    query_tile <= 4), <= 8 query rows per task, <= 16 splits, split rows below 4 GiB."""
+    cfg = layout.config
+    mql = getattr(meta, "max_query_len", None)
+    qt = cfg.queries_per_tile
+    if not isinstance(mql, int) or not 1 <= mql <= qt or qt > 4:
+        return False
+    rows = mql * (hq // layout.kv_heads)
+    small = tokens is None or tokens * hq * splits * cfg.head_dim * 4 < 1 << 32
+    return rows <= 8 and 1 <= splits <= 16 and small
+
+
+def layer_step(query, key, value, history, window, meta, layout, scale, splits, rk_t, rv_t, rv,
+               output, merged_lse=None, split_tokens=0):
+    """One layer step in ONE launch (no reference counterpart): the work of backend.py:171-226
+    (rotations, INT2 store, both attention branches, merges, inverse V rotation, window store)
+    with the INT2 and window bytes of the single entry points and the output within rounding
+    of them. ``query``/``key``/``value`` are the unrotated rows; ``rk_t``/``rv_t`` are R^T and
+    ``rv`` is R_v, contiguous bf16 [256, 256]. Requires ``layer_step_supported``."""
+    _device_check(query, key, value, history, window, rk_t, rv_t, rv, output, merged_lse)
+    n, hq, d = query.shape
+    if not output.is_contiguous():
+        raise ValueError("Attention output must be contiguous")
+    if n == 0:
+        return
+    if not layer_step_supported(meta, layout, hq, splits, n):
+        raise ValueError("layer_step covers one task per request, <= 8 query rows per task and "
+                         "<= 16 splits")
+    for r in (rk_t, rv_t, rv):
+        if r.dtype != torch.bfloat16 or not r.is_contiguous() or tuple(r.shape) != (d, d):
+            raise ValueError("rk_t / rv_t / rv must be contiguous bf16 [256, 256]")
+    cfg = layout.config
+    programs = attention_programs(n, meta.max_num_reqs, cfg.queries_per_tile)
+    if meta.tasks.shape[0] < programs:
+        raise ValueError(f"task table holds {meta.tasks.shape[0]} rows; the grid needs {programs}")
+    if meta.slot_mapping.dtype != torch.int64:
+        raise ValueError("slot mapping must be int64")
+    query, q0, q1 = _row_strides(query, "query")
+    key, k0, k1 = _row_strides(key, "key")
+    value, v0, v1 = _row_strides(value, "value")
+    dev = query.device
+    partials = torch.empty((n, hq, splits, d), dtype=torch.float32, device=dev)
+    lse = torch.empty((n, hq, splits), dtype=torch.float32, device=dev)
+    raw_partials = torch.empty((n, hq, RAW_SPLITS, d), dtype=torch.float32, device=dev)
+    raw_lse = torch.empty((n, hq, RAW_SPLITS), dtype=torch.float32, device=dev)
+    counters = finish_counters(meta, dev, programs * layout.kv_heads)
+    table = _int32(meta.block_tables, "block_tables")
+    _ext.check(
+        _ext.library().oscar_layer_step(
+            _ptr(query), q0, q1, _ptr(key), k0, k1, _ptr(value), v0, v1,
+            _ptr(history), history.numel() * history.element_size(), _ptr(window), window.numel(),
+            _ptr(_int32(meta.query_start_loc, "query_start_loc")),
+            _ptr(_int32(meta.seq_lens, "seq_lens")), _ptr(table), table.stride(0), table.shape[1],
+            _ptr(_int32(meta.counts, "counts")), _ptr(_int32(meta.tasks, "tasks")),
+            _ptr(_int32(meta.task_count, "task_count")), _ptr(meta.slot_mapping),
+            n, hq, programs, splits, cfg.block_n, cfg.queries_per_tile, int(meta.max_query_len),
+            float(scale), int(split_tokens), _ptr(rk_t), _ptr(rv_t), _ptr(rv), clip_struct(cfg),
+            layout_struct(layout), _ptr(partials), _ptr(lse), _ptr(raw_partials), _ptr(raw_lse),
+            _ptr(counters), counters.numel(), _ptr(output), _ptr(merged_lse), meta.max_num_reqs,
+            _stream(query),
+        ),
+        "layer_step",
     )
 
 

@@ -7,9 +7,10 @@ rotations are QR factors of seeded Gaussians (fp32, then bf16). "Page size 128" 
 at least 2 x window = 144 tokens for the BF16 window (layout.py:15-28), so the physical page
 stays 768 tokens as in every other config.
 
-The step runs three ways: the reference order of single launches (backend.py:171-226), the
-fused three-launch layer step and the one-launch history + post form. All three must give
-the same bits. They are checked against
+The step runs four ways: the reference order of single launches (backend.py:171-226), the
+fused three-launch layer step and the two-launch history + post form, which must give the
+same bits, and the one-launch layer step, which must write the same cache bytes and an
+output within the bounds below of theirs. They are checked against
 
 * ``O.cached_decode_reference`` (the device cache read back: INT2 history dequantized and
   inverse-rotated, BF16 window, current K/V; dense fp64 attention) with scale-aware bounds:
@@ -65,18 +66,27 @@ def test_c1_decode_step_matches_oracle():
 
     merged = torch.empty(1, HQ, device=DEV)
     single = run_attention(qd, kd, vd, rk_d, rv_d, hist, window, meta, layout, splits, merged)
+    cache = raw.clone()
     forms = {}
-    for one_launch in (False, True):
-        impl = OscarAttentionImpl.standalone(HQ, 256, 1 / 16, 1, cfg, one_launch_post=one_launch)
+    for one_launch, layer in ((False, False), (True, False), (False, True)):
+        impl = OscarAttentionImpl.standalone(HQ, 256, 1 / 16, 1, cfg, one_launch_post=one_launch,
+                                             layer_step=layer)
         impl.set_rotations(rk_d, rv_d)
         meta.merged_lse = torch.empty(1, HQ, device=DEV)
         out = torch.empty(1, HQ * 256, dtype=torch.bfloat16, device=DEV)
-        impl.forward(None, qd, kd, vd, native_views(raw, layout), meta, out)
-        forms[one_launch] = (out, meta.merged_lse)
+        step_cache = cache.clone()
+        impl.forward(None, qd, kd, vd, native_views(step_cache, layout), meta, out)
+        forms[(one_launch, layer)] = (out, meta.merged_lse, step_cache)
     torch.cuda.synchronize()
-    for out, lse in forms.values():
-        assert torch.equal(out.view(1, HQ, 256), single), "fused forms differ from single launches"
-        assert torch.equal(lse, merged)
+    for (one_launch, layer), (out, lse, step_cache) in forms.items():
+        assert torch.equal(step_cache, cache), "the step rewrote different cache bytes"
+        if layer:
+            assert_scaled_close(out.view(1, HQ, 256).float().cpu().numpy(),
+                                single.float().cpu().numpy(), "one-launch step")
+            assert_lse_close(lse.cpu().numpy(), merged.cpu().numpy(), "one-launch LSE", atol=1e-3)
+        else:
+            assert torch.equal(out.view(1, HQ, 256), single), "fused forms differ"
+            assert torch.equal(lse, merged)
 
     got = single.float().cpu().numpy()
     got_lse = merged.cpu().numpy()

@@ -1,9 +1,13 @@
-"""The fused layer step (pre_attention, history kernel, post_attention) against the reference
-order of single launches (oscar_ascend/backend.py:171-226) and against the dense oracle.
+"""The fused layer step (pre_attention, history kernel, post_attention), its two-launch form
+(history + post in one launch) and the one-launch layer step against the reference order of
+single launches (oscar_ascend/backend.py:171-226) and against the dense oracle.
 
-The fused launches run the same device code as the single entry points, so the comparison
-with the single-launch path is bit for bit: attention output, merged LSE, every byte of the
-K stripe (INT2 slots + untouched padding) and of the V stripe (BF16 windows).
+The three- and two-launch forms run the same device code as the single entry points, so the
+comparison with the single-launch path is bit for bit: attention output, merged LSE, every byte
+of the K stripe (INT2 slots + untouched padding) and of the V stripe (BF16 windows). The
+one-launch layer step writes the same cache bytes (bit for bit) and merges the BF16 branch
+from up to four splits, so its output is checked with the scale-aware bounds against the
+single-launch output and against the cache read back.
 """
 
 from types import SimpleNamespace
@@ -16,7 +20,8 @@ import oracle as O
 from oscar_new_amd import kernels
 from oscar_new_amd.backend import OscarAttentionImpl
 from oscar_new_amd.config import OscarConfig
-from tests._state import bits, check_step_against_cache, make_state, prepare_prefix
+from tests._state import (assert_lse_close, assert_scaled_close, bits, check_step_against_cache,
+                          make_state, prepare_prefix)
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -65,13 +70,15 @@ CASES = [
 
 
 def _forward(c, form, splits, raw=None):
-    """One layer step in `form` ("single", "fused" or "fused1": history + post in one launch
-    where it applies) on a copy of the cache."""
+    """One layer step in `form` ("single"; "fused": three launches; "fused1": history + post
+    in one launch where it applies; "layer": the one-launch step where it applies) on a copy
+    of the cache."""
     n = c.q.shape[0]
     raw = c.raw.clone() if raw is None else raw
     k_cache, v_cache = _views(raw, c.layout)
-    impl = OscarAttentionImpl.standalone(6, 256, 1 / 16, 1, c.layout.config, fused=form != "single",
-                              one_launch_post=form == "fused1")
+    impl = OscarAttentionImpl.standalone(6, 256, 1 / 16, 1, c.layout.config,
+                                         fused=form != "single", one_launch_post=form == "fused1",
+                                         layer_step=form == "layer")
     impl.set_rotations(c.rk, c.rv)
     impl.partition_for = lambda meta, s=splits: (s, 0)
     c.meta.merged_lse = torch.full((n, 6), 7.0, device=DEV)
@@ -91,6 +98,24 @@ def test_fused_step_is_bitwise_the_single_launch_step(lengths, prefixes, splits)
             assert torch.equal(a, b), form
 
 
+@pytest.mark.parametrize("lengths,prefixes,splits", CASES + [
+    ([1300, 700, 2500, 40], [1299, 699, 2499, 39], 5),  # decode, fewer splits than raw shares
+    ([3000, 1500], [2999, 1499], 1),  # one split: it stores K, V and the whole BF16 branch
+])
+def test_layer_step_writes_the_same_cache_and_a_close_output(lengths, prefixes, splits):
+    c = _case(lengths, prefixes, seed=17)
+    want = _forward(c, "single", splits)
+    got = _forward(c, "layer", splits)
+    assert torch.equal(want[2], got[2]), "cache bytes"
+    n = c.q.shape[0]
+    a = want[0].view(torch.bfloat16).float().numpy()
+    b = got[0].view(torch.bfloat16).float().numpy()
+    assert_scaled_close(b, a, "layer step vs single launches")
+    assert_lse_close(got[1].numpy(), want[1].numpy(), "layer step merged LSE", atol=1e-3)
+    check_step_against_cache(got[0].view(torch.bfloat16).reshape(n, -1), got[1], c.raw,
+                             c.layout, c.tables, lengths, prefixes, c.qs, c.ks, c.vs, c.rk, c.rv)
+
+
 @pytest.mark.parametrize("lengths,prefixes,partition", [
     ([6000, 1500, 300], [5999, 1499, 299], (6, 1024)),
     ([6000, 1500, 300], [5999, 1499, 299], (40, 256)),  # workgroup-per-row merge
@@ -106,8 +131,9 @@ def test_token_bounded_fused_step_against_dense_reference(lengths, prefixes, par
     for fused, one in ((True, True), (False, False), (True, False)):
         raw = c.raw.clone()
         k_cache, v_cache = _views(raw, c.layout)
-        impl = OscarAttentionImpl.standalone(6, 256, 1 / 16, 1, c.layout.config, split_policy="mi355x",
-                                  fused=fused, one_launch_post=one)
+        impl = OscarAttentionImpl.standalone(6, 256, 1 / 16, 1, c.layout.config,
+                                             split_policy="mi355x", fused=fused,
+                                             one_launch_post=one, layer_step=False)
         impl.set_rotations(c.rk, c.rv)
         impl.partition_for = lambda meta, pt=partition: pt
         c.meta.merged_lse = torch.empty((n, 6), device=DEV)
@@ -134,15 +160,20 @@ def test_token_bounded_fused_step_against_dense_reference(lengths, prefixes, par
                                rtol=0)
 
 
-def test_fused_step_replays_in_a_graph():
+@pytest.mark.parametrize("lengths,prefixes,form", [
+    ([900, 517], [896, 516], "fused"),  # MTP: three launches
+    ([1300, 700, 2500], [1299, 699, 2499], "layer"),  # decode: the one-launch step
+])
+def test_fused_step_replays_in_a_graph(lengths, prefixes, form):
     # Reference tests/test_npu_kernels.py:197-245 through the fused step: a captured step
-    # replayed with new queries on a reset cache matches the eager single-launch step every
-    # time.
-    c = _case([900, 517], [896, 516], seed=21, cfg=OscarConfig(sink_tokens=4, recent_tokens=64))
+    # replayed with new queries on a reset cache matches the eager step of the same form
+    # every time (the three-launch form is also the single-launch step's bits).
+    c = _case(lengths, prefixes, seed=21, cfg=OscarConfig(sink_tokens=4, recent_tokens=64))
     n = c.q.shape[0]
     raw_graph, raw_eager = c.raw.clone(), c.raw.clone()
     kg, vg = _views(raw_graph, c.layout)
-    impl = OscarAttentionImpl.standalone(6, 256, 1 / 16, 1, c.layout.config, fused=True)
+    impl = OscarAttentionImpl.standalone(6, 256, 1 / 16, 1, c.layout.config, fused=True,
+                                         layer_step=form == "layer")
     impl.set_rotations(c.rk, c.rv)
     impl.partition_for = lambda meta: (8, 0)
     lse = c.meta.merged_lse = torch.empty((n, 6), device=DEV)
@@ -164,7 +195,7 @@ def test_fused_step_replays_in_a_graph():
         torch.cuda.synchronize()
         got = (out.view(torch.int16).cpu(), lse.cpu(), raw_graph.cpu())
         c.meta.merged_lse = lse
-        want = _forward(c, "single", 8, raw=raw_eager)
+        want = _forward(c, "single" if form == "fused" else form, 8, raw=raw_eager)
         for a, b in zip(want, got):
             assert torch.equal(a, b), replay
         _ = (c.q * 2).sum().item()  # eager work between replays

@@ -18,7 +18,8 @@ import oracle as O
 from oscar_new_amd import kernels
 from oscar_new_amd.backend import OscarAttentionImpl
 from oscar_new_amd.config import OscarConfig
-from tests._state import bits, make_state, native_views, prepare_prefix
+from tests._state import (assert_lse_close, assert_scaled_close, bits, make_state, native_views,
+                          prepare_prefix)
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -49,10 +50,11 @@ def _case(page, lengths, prefixes, seed):
         cat(vs, prefixes)
 
 
-def _step(c, fused, one_launch, splits):
+def _step(c, fused, one_launch, splits, layer=False):
     layout, raw0, meta, rk, rv, _, _, _, q, k, v = c
     raw = raw0.clone()
-    impl = OscarAttentionImpl.standalone(HQ, 256, 1 / 16, H, CFG, fused=fused, one_launch_post=one_launch)
+    impl = OscarAttentionImpl.standalone(HQ, 256, 1 / 16, H, CFG, fused=fused,
+                                         one_launch_post=one_launch, layer_step=layer)
     impl.set_rotations(rk, rv)
     impl.partition_for = lambda meta: (splits, 0)
     n = q.shape[0]
@@ -76,6 +78,13 @@ def test_other_pages_and_two_kv_heads(page, lengths, prefixes, splits):
         got = _step(c, fused, one, splits)
         for a, b in zip(want, got):
             assert torch.equal(a, b), (fused, one)
+    # The one-launch step (decode here; MTP with 6 query heads per KV head falls back): same
+    # cache bytes, output and LSE within the scale-aware bounds.
+    layer = _step(c, True, False, splits, layer=True)
+    assert torch.equal(layer[2], want[2])
+    assert_scaled_close(layer[0].view(torch.bfloat16).float().numpy(),
+                        want[0].view(torch.bfloat16).float().numpy(), "layer step")
+    assert_lse_close(layer[1].numpy(), want[1].numpy(), "layer step LSE", atol=1e-3)
     _, _, _, rk, rv, ks, vs, qs, q, _, _ = c
     out = want[0].view(torch.bfloat16).float().numpy().reshape(q.shape[0], HQ, 256)
     lse = want[1].numpy()

@@ -13,7 +13,8 @@ each of the three device paths that store windows:
 
 * ``kernels.store_windows`` (the single entry point);
 * the fused layer step (``post_attention``'s window workgroups);
-* the one-launch history + post step (the window slice of its grid).
+* the two-launch history + post step (the window slice of its grid);
+* the one-launch layer step (the workgroup that completes a task stores its window).
 
 The single entry point must also leave the K stripe untouched.
 """
@@ -92,15 +93,15 @@ def test_window_bytes_match_oracle_through_ring_wraps_and_rollbacks():
         assert torch.equal(got_k.view(torch.int16), k_stripe), \
             f"store_windows wrote the K stripe, step {index}"
 
-        for one_launch in (False, True):
+        for one_launch, layer in ((False, False), (True, False), (False, True)):
             fused = raw.clone()
             impl = OscarAttentionImpl.standalone(HQ, 256, 1 / 16, H, cfg,
-                                                 one_launch_post=one_launch)
+                                                 one_launch_post=one_launch, layer_step=layer)
             impl.set_rotations(eye, eye)
             out = torch.empty(n, HQ * 256, dtype=torch.bfloat16, device=DEV)
             impl.forward(None, q, k, v, native_views(fused, layout), meta, out)
             torch.cuda.synchronize()
             got_v = native_views(fused, layout)[1]
             assert np.array_equal(bits(got_v).reshape(-1), want), \
-                f"fused step (one launch {one_launch}), step {index}"
+                f"fused step (one-launch post {one_launch}, layer step {layer}), step {index}"
         raw = fused  # the next step sees this step's INT2 slots and windows
