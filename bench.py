@@ -58,7 +58,9 @@ def parse_args(argv=None):
                    help="independent KV caches cycled per step (default 4; 2 when one cache "
                         "exceeds 16 GB)")
     p.add_argument("--seed", type=int, default=1234)
-    p.add_argument("--cpu-sample", type=int, default=2, help="requests timed on the CPU oracle")
+    p.add_argument("--cpu-sample", type=int, default=0,
+                   help="requests timed on the CPU baseline (0: a seeded sample of about "
+                        "2**18 context tokens)")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-graph", action="store_true", help="eager launches instead of HIP graphs")
     p.add_argument("--one-launch-post", action="store_true",
@@ -305,57 +307,155 @@ def time_store(device, args, steps):
     }
 
 
+CPU_RUNS, CPU_WARMUP = 5, 1
+CPU_SAMPLE_TOKENS = 1 << 18  # context tokens of the sampled requests per timed run
+
+
+def cpu_threads():
+    """Host threads for the CPU baseline: the job's share (OMP_NUM_THREADS) or every core."""
+    import torch
+
+    torch.set_num_threads(int(os.environ.get("OMP_NUM_THREADS") or 0) or os.cpu_count() or 1)
+    return torch.get_num_threads()
+
+
+def median_run(fn, runs=CPU_RUNS, warmup=CPU_WARMUP):
+    """Median wall seconds of ``runs`` timed calls after ``warmup`` untimed ones."""
+    for _ in range(warmup):
+        fn()
+    times = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return statistics.median(times)
+
+
+def cpu_c1_decode(seed):
+    """c1 (B1, Hq 2 / Hkv 1, ctx 512, 4 sink + 64 recent) decode step on the torch float32
+    restatement, over a cache of slot images packed by that restatement: (us, description)."""
+    import torch
+
+    import oracle as O
+    from oracle import cpu_torch as T
+
+    gen = torch.Generator().manual_seed(seed)
+    geo = O.Geometry(768, 1, 128, 256, 4, 64, 3)
+    seq, pages = 512, 2
+    history = torch.zeros(pages * geo.stripe_page_bytes, dtype=torch.uint8)
+    window = torch.randn(pages * geo.stripe_page_bytes // 2, generator=gen).bfloat16()
+    k = torch.randn(seq, 1, 256, generator=gen)
+    v = torch.randn(seq, 1, 256, generator=gen)
+    k[..., :4] *= 8.0  # 4 outlier channels x8
+    rk = torch.linalg.qr(torch.randn(256, 256, generator=gen))[0].bfloat16()
+    rv = torch.linalg.qr(torch.randn(256, 256, generator=gen))[0].bfloat16()
+    images = T.quantize_pack(T.rotate(k.bfloat16(), rk), T.rotate(v.bfloat16(), rv))
+    table = list(range(geo.blocks_per_page, 2 * geo.blocks_per_page))
+    history.view(pages, -1)[1, : seq * 160] = images.reshape(-1)
+    q = torch.randn(1, 2, 256, generator=gen).bfloat16()
+    cur_k, cur_v = k[-1:].bfloat16(), v[-1:].bfloat16()
+    sec = median_run(lambda: T.decode_step(history, window, table, seq, q, cur_k, cur_v, rk, rv,
+                                           geo, scale=1 / 16), runs=21, warmup=3)
+    return sec * 1e6, "c1: B1 x 512 ctx, Hq 2 / Hkv 1, 4 sink + 64 recent, median of 21 after 3"
+
+
+def cpu_c2_store(seed):
+    """c2 quantize+pack of 4096 tokens (rotate K and V, 8-factor MSE clip search, INT2 pack
+    into 160-byte slot images) on the torch float32 restatement: tokens/s."""
+    import torch
+
+    from oracle import cpu_torch as T
+
+    gen = torch.Generator().manual_seed(seed)
+    n = 4096
+    k = torch.randn(n, 1, 256, generator=gen)
+    v = torch.randn(n, 1, 256, generator=gen)
+    hot = torch.randperm(256, generator=gen)[:5]  # 2 % outlier channels x10
+    k[..., hot] *= 10.0
+    rk = torch.linalg.qr(torch.randn(256, 256, generator=gen))[0].bfloat16()
+    rv = torch.linalg.qr(torch.randn(256, 256, generator=gen))[0].bfloat16()
+    kb, vb = k.bfloat16(), v.bfloat16()
+    sec = median_run(lambda: T.quantize_pack(T.rotate(kb, rk), T.rotate(vb, rv), "search"))
+    return n / sec
+
+
 def cpu_baseline(w, args, outputs):
-    """CPU oracle (numpy) on a bounded sample of requests of layer 0, plus parity."""
+    """CPU baseline on the host cores: the torch float32 restatement of the decode step
+    (oracle/cpu_torch.py: INT2 history dequantized and inverse-rotated, BF16 window and current
+    rows, dense float32 softmax) over a seeded sample of the workload's requests read back
+    from the device cache, median of 5 timed runs after 1 warm-up, scaled to the whole batch
+    by context tokens; beside it c1's decode step and c2's quantize+pack tokens/s. Also the
+    sample's parity against the GPU output."""
     import numpy as np
     import torch
 
     import oracle as O
+    from oracle import cpu_torch as T
 
+    cores = cpu_threads()
     geo = O.Geometry(w.layout.physical_block_tokens, 1, 128, 256, w.cfg.sink_tokens,
                      w.cfg.recent_tokens, w.cfg.speculative_tokens)
-    history = w.k_cache.view(torch.uint8).view(-1).cpu().numpy()
-    window = w.v_cache.view(torch.int16).view(-1).cpu().numpy().view(np.uint16)
+    rk, rv = w.rk.cpu(), w.rv.cpu()
+    q, k, v = w.q.cpu(), w.k.cpu(), w.v.cpu()
+    order = torch.randperm(len(w.seqs), generator=torch.Generator().manual_seed(args.seed))
+    sample, tokens = [], 0
+    for r in order.tolist():
+        if args.cpu_sample and len(sample) >= args.cpu_sample:
+            break
+        if not args.cpu_sample and sample and tokens >= CPU_SAMPLE_TOKENS:
+            break
+        sample.append(r)
+        tokens += w.seqs[r]
+    # Host copy of the sample's own pages only (the pool can be tens of GB), blocks renumbered.
+    bpp = geo.blocks_per_page
+    rows = {r: w.table[r, : -(-w.seqs[r] // 128)].tolist() for r in sample}
+    pages = sorted({b // bpp for row in rows.values() for b in row})
+    renumber = {p: i for i, p in enumerate(pages)}
+    tables = {r: np.array([renumber[b // bpp] * bpp + b % bpp for b in row], np.int64)
+              for r, row in rows.items()}
+    idx = torch.tensor(pages, device=w.k_cache.device)
+    npool = w.k_cache.shape[0] // bpp
+    history = w.k_cache.view(torch.uint8).reshape(npool, -1).index_select(0, idx).reshape(-1).cpu()
+    window = w.v_cache.reshape(npool, -1).index_select(0, idx).reshape(-1).cpu()
+    got = outputs.float().cpu().reshape(-1, 6, 256)
+    got_lse = w.meta.merged_lse.cpu()
+    results = {}
 
-    def bits(t):
-        return t.detach().cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
-
-    rk, rv = bits(w.rk), bits(w.rv)
-    sample = list(range(min(args.cpu_sample, len(w.seqs))))
-    got = outputs.float().cpu().numpy().reshape(-1, 6, 256)
-    got_lse = w.meta.merged_lse.cpu().numpy()
-    errs, lse_errs, times = [], [], []
-    for rep in range(3):
-        t0 = time.perf_counter()
+    def run():
         for r in sample:
             rows = slice(r * w.qlen, (r + 1) * w.qlen)
-            out, lse = O.cached_decode_reference(history, window, w.table[r].numpy(), w.seqs[r],
-                                                 bits(w.q[rows]), bits(w.k[rows]), bits(w.v[rows]),
-                                                 rk, rv, geo, scale=1 / 16)
-            if rep == 0:
-                errs.append(np.abs(got[rows] - out))
-                lse_errs.append(np.abs(got_lse[rows] - lse))
-        times.append(time.perf_counter() - t0)
-    per_req = statistics.median(times) / len(sample)
-    try:
-        from threadpoolctl import threadpool_info
+            results[r] = T.decode_step(history, window, tables[r], w.seqs[r], q[rows],
+                                       k[rows], v[rows], rk, rv, geo, scale=1 / 16)
 
-        cores = max((i.get("num_threads", 1) for i in threadpool_info()), default=1)
-    except Exception:  # pragma: no cover
-        cores = os.cpu_count() or 1
-    err = np.concatenate([e.reshape(-1) for e in errs])
-    lerr = np.concatenate([e.reshape(-1) for e in lse_errs])
+    sec = median_run(run)
+    scale = sum(w.seqs) / tokens
+    num = den = max_abs = lse_err = 0.0
+    for r in sample:
+        rows = slice(r * w.qlen, (r + 1) * w.qlen)
+        want, want_lse = results[r]
+        diff = got[rows] - want
+        num += float((diff * diff).sum())
+        den += float((want * want).sum())
+        max_abs = max(max_abs, float(diff.abs().max()))
+        lse_err = max(lse_err, float((got_lse[rows] - want_lse).abs().max()))
+    c1_us, c1_desc = cpu_c1_decode(args.seed)
     cpu = {
-        "value": per_req * len(w.seqs) * 1e6,
+        "value": sec * scale * 1e6,
         "unit": "us/layer-step",
         "cores": int(cores),
         "kind": "port",
-        "sample": f"{len(sample)} of {len(w.seqs)} requests of layer 0 (numpy oracle "
-                  f"cached_decode_reference: INT2 dequant + inverse rotation + dense fp64 "
-                  f"attention), median of 3, scaled x{len(w.seqs) / len(sample):g}",
+        "sample": f"{len(sample)} of {len(w.seqs)} requests ({tokens} of {sum(w.seqs)} context "
+                  f"tokens) of layer 0, torch float32 restatement (oracle/cpu_torch.py: INT2 "
+                  f"dequant + inverse rotation + dense float32 attention), median of "
+                  f"{CPU_RUNS} runs after {CPU_WARMUP} warm-up, scaled x{scale:.3g} by tokens",
+        "c1_us_per_step": c1_us,
+        "c1_sample": c1_desc,
+        "c2_store_tokens_per_s": cpu_c2_store(args.seed),
+        "c2_sample": "c2: 4096 tokens x 1 kv head, rotate K and V + 8-factor MSE clip search + "
+                     f"INT2 pack, median of {CPU_RUNS} runs after {CPU_WARMUP} warm-up",
     }
-    parity = {"requests": len(sample), "max_abs": float(err.max()), "mean_abs": float(err.mean()),
-              "lse_max_abs": float(lerr.max())}
+    parity = {"requests": len(sample), "rel_l2": math.sqrt(num / max(den, 1e-30)),
+              "max_abs": max_abs, "lse_max_abs": lse_err}
     return cpu, parity
 
 
@@ -555,7 +655,8 @@ def main(argv=None):
         rows = ntok * 6
         hist_alg += partial_bytes + rows * (1024 + 4) + rows * (512 + 4) + 256 * 256 * 2
         hist_alg += 2 * 2 * ntok * 512
-    hist_kernel = "history_pair_finish_kernel" if one_launch else "history_pair_kernel"
+    hist_kernel = ("history_pair_finish_kernel" if one_launch
+                   else kernels.history_kernel_name(w.meta, w.layout, 6))
     print(f"[bench] step {us_step:.1f} us, history kernel {hist_us:.1f} us", file=sys.stderr,
           flush=True)
 

@@ -354,6 +354,54 @@ int oscar_history_post_noalloc(const void* query, int64_t q_s0, int64_t q_s1, in
                                void* window, int64_t window_elems, int64_t max_reqs,
                                void* stream);
 
+/* ---------------------------------------------------------------- calibration (startup) */
+
+/*
+ * accumulate_gram -- covariance += sum over rows r = (token, head) of w_r x_r x_r^T
+ * (oscar_ascend/calibration_kernels.py:14-70, accumulate_gram). x: [n, heads, dim] bf16
+ * (x_fp32 = 0) or fp32 (x_fp32 = 1), element strides s_t, s_h, s_d; weights: fp32 [n * heads]
+ * (row index token * heads + head) or NULL for 1; covariance: fp32 [dim, dim] row-major,
+ * updated in place. dim a multiple of 32. Deterministic (fixed summation order).
+ */
+int oscar_accumulate_gram(const void* x, int32_t x_fp32, int64_t n, int64_t heads, int64_t dim,
+                          int64_t s_t, int64_t s_h, int64_t s_d, const float* weights,
+                          float* covariance, void* stream);
+
+/*
+ * sst_weights -- weights[t] = max(k_t^T C_q k_t, 0) for the n key rows of one KV head, and
+ * *total_weight += their sum (calibration_kernels.py:73-126, sst_weights). key: bf16 or fp32
+ * [n, 1, 256] with element strides s_t (token) and s_d; q_covariance: fp32 [256, 256].
+ */
+int oscar_sst_weights(const void* key, int32_t key_fp32, int64_t n, int64_t dim, int64_t s_t,
+                      int64_t s_d, const float* q_covariance, float* weights,
+                      float* total_weight, void* stream);
+
+/*
+ * normalize -- out = x / max(denominator, 1e-30) over count fp32 values; the denominator is
+ * *denominator when that pointer is non-NULL (a device scalar), else `value`
+ * (calibration_kernels.py:129-156, normalize).
+ */
+int oscar_normalize(const float* x, int64_t count, const float* denominator, float value,
+                    float* out, void* stream);
+
+/*
+ * calibrated_rotations -- eigen-decomposition of `batch` symmetric fp32 [256, 256] covariances
+ * by cyclic round-robin Jacobi sweeps, then R = U H Pbr per matrix
+ * (calibration_kernels.py:159-327, calibrated_rotations): eigenvalues fp32 [batch, 256]
+ * ascending, rotations fp32 [batch, 256, 256]. Sweeps stop per matrix once the relative
+ * off-diagonal residual (max |off-diagonal| / max |diagonal|, checked every second sweep and
+ * after the last) is below `tolerance`, or after max_sweeps (<= 64). info: fp32 [batch, 2] =
+ * (sweeps run, last residual; +inf for a non-finite matrix) -- the caller reads it back and
+ * rejects non-converged results. workspace: >= oscar_calibration_workspace_bytes(batch,
+ * max_sweeps) bytes of device memory, 16-byte aligned. Three launches, no host round trip.
+ */
+int64_t oscar_calibration_workspace_bytes(int32_t batch, int32_t max_sweeps);
+
+int oscar_calibrated_rotations(const float* covariances, int32_t batch, int32_t dim,
+                               int32_t max_sweeps, float tolerance, void* workspace,
+                               int64_t workspace_bytes, float* rotations, float* eigenvalues,
+                               float* info, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -133,8 +133,14 @@ SIGNATURES = {
         _P, _I64, _I64, _P,  # window, elems, max_reqs, stream
     ],
     "oscar_noalloc_scratch_bytes": [_I64, _I64, _I32],
+    # calibration (startup): gram, attention weights, normalize, eigensolver + U H Pbr
+    "oscar_accumulate_gram": [_P, _I32, _I64, _I64, _I64, _I64, _I64, _I64, _P, _P, _P],
+    "oscar_sst_weights": [_P, _I32, _I64, _I64, _I64, _I64, _P, _P, _P, _P],
+    "oscar_normalize": [_P, _I64, _P, _F, _P, _P],
+    "oscar_calibration_workspace_bytes": [_I32, _I32],
+    "oscar_calibrated_rotations": [_P, _I32, _I32, _I32, _F, _P, _I64, _P, _P, _P, _P],
 }
-RESTYPES = {"oscar_noalloc_scratch_bytes": c_int64}
+RESTYPES = {"oscar_noalloc_scratch_bytes": c_int64, "oscar_calibration_workspace_bytes": c_int64}
 NOALLOC_SCRATCH_BYTES = 32 << 20  # OSCAR_NOALLOC_SCRATCH_BYTES
 
 _lib = None

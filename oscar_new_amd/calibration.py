@@ -1,16 +1,12 @@
-"""Calibration math of the K/V rotations (reference calibration_kernels.py:250-327 and
-tests/test_calibration_math.py): the attention-weighted covariances, their eigenvectors and
-the rotation R = U H Pbr.
+"""Calibration math of the K/V rotations on the GPU (reference
+``oscar_ascend/calibration_kernels.py``): streamed covariance sums, the attention weights of
+the V covariance, normalization, and the batched Jacobi eigensolver that turns each
+covariance into the rotation R = U H Pbr.
 
-* Covariances (test_calibration_math.py:70-91): K uses the query covariance as is; V is
-  weighted per token by w_t = k_t^T C_q k_t, accumulated in chunks as
-  sum_t w_t v_t v_t^T / sum_t w_t (``WeightedCovariance``), equal to the one-shot form.
-* Eigenvectors: ``torch.linalg.eigh`` (LAPACK / rocSOLVER) replaces the reference's cyclic
-  Jacobi sweeps on the NPU; the eigenpairs are sorted ascending as the reference sorts them.
-  Calibration runs once per model, off the decode path.
-* Composition (calibration_kernels.py:270-284): each row of U goes through the in-place
-  Walsh-Hadamard butterfly, scaled by 1/sqrt(D), and element i lands in column
-  bit_reverse(D - 1 - i) (the descending-eigenvalue bit-reversal permutation Pbr).
+Startup-only work: the decode path only applies the resulting matrices. Every function runs
+the HIP library (``csrc/calibrate.hip``); there is no CPU path. The covariance objectives:
+K uses the query covariance C_q as is; V is weighted per token by w_t = max(k_t^T C_q k_t, 0),
+accumulated as sum_t w_t v_t v_t^T and divided by sum_t w_t.
 """
 
 from __future__ import annotations
@@ -19,80 +15,137 @@ import math
 
 import torch
 
+from . import _ext
+from .kernels import _device_check, _ptr, _stream
 
-def hadamard_rows(x):
-    """Rows of ``x`` [.., D] times the orthonormal Sylvester Hadamard matrix H_D (butterflies)."""
-    y = x.clone()
-    dim = y.shape[-1]
-    if dim & (dim - 1):
-        raise ValueError("Hadamard size must be a power of two")
-    idx = torch.arange(dim, device=y.device)
-    for bit in range(dim.bit_length() - 1):
-        partner = y[..., idx ^ (1 << bit)]
-        low = (idx & (1 << bit)) == 0
-        y = torch.where(low, y + partner, partner - y)
-    return y / math.sqrt(dim)
+__all__ = ["accumulate_gram", "sst_weights", "normalize", "calibrated_rotations"]
+
+DIM = 256
 
 
-def bit_reverse(i, bits):
-    return int(f"{i:0{bits}b}"[::-1], 2)
+def _input_flag(t, name):
+    if t.dtype == torch.bfloat16:
+        return 0
+    if t.dtype == torch.float32:
+        return 1
+    raise ValueError(f"{name} must be bfloat16 or float32, got {t.dtype}")
 
 
-def compose_rotation(u_ascending):
-    """R = U H Pbr for eigenvectors sorted by ascending eigenvalue (columns of ``u``)."""
-    dim = u_ascending.shape[-1]
-    bits = dim.bit_length() - 1
-    y = hadamard_rows(u_ascending)
-    dest = torch.tensor([bit_reverse(dim - 1 - i, bits) for i in range(dim)], device=y.device)
-    r = torch.empty_like(y)
-    r[..., dest] = y
-    return r
+def _fp32_matrix(t, name, shape):
+    if t.dtype != torch.float32 or tuple(t.shape) != tuple(shape) or not t.is_contiguous():
+        raise ValueError(f"{name} must be a contiguous float32 tensor of shape {tuple(shape)}")
 
 
-def eigenpairs(covariance):
-    """Eigenvalues ascending and matching eigenvectors (columns) of a symmetric matrix."""
-    values, vectors = torch.linalg.eigh(covariance.double())
-    order = values.argsort()
-    return vectors[:, order], values[order]
+def accumulate_gram(x, covariance, weights=None):
+    """covariance += sum over rows (token, head) of w x x^T (calibration_kernels.py:59-70).
+
+    ``x``: [n, heads, dim] bf16 or fp32 (any strides); ``covariance``: fp32 [dim, dim],
+    updated in place; ``weights``: optional fp32 [n * heads] (row token * heads + head).
+    """
+    _device_check(x, covariance, weights)
+    n, heads, dim = x.shape
+    flag = _input_flag(x, "x")
+    _fp32_matrix(covariance, "covariance", (dim, dim))
+    if weights is not None and (weights.dtype != torch.float32 or weights.numel() != n * heads
+                                or not weights.is_contiguous()):
+        raise ValueError("weights must be a contiguous float32 tensor with one value per row")
+    _ext.check(
+        _ext.library().oscar_accumulate_gram(
+            _ptr(x), flag, n, heads, dim, *x.stride(), _ptr(weights), _ptr(covariance),
+            _stream(x)),
+        "accumulate_gram",
+    )
+    return covariance
 
 
-def calibrated_rotation(covariance):
-    """The rotation of one covariance, its eigenvalues and the reconstruction residual."""
-    if not torch.isfinite(covariance).all():
-        raise RuntimeError("Nonfinite calibration covariance; rotations not published")
-    u, values = eigenpairs(covariance)
-    rotation = compose_rotation(u)
-    residual = (u @ torch.diag(values) @ u.T - covariance.double()).abs().max().item()
-    return rotation.float(), values.float(), residual
+def sst_weights(key, q_covariance, total_weight):
+    """Per-token weights max(k^T C_q k, 0) of the keys of one KV head, and
+    ``total_weight += their sum`` (calibration_kernels.py:109-126).
+
+    ``key``: [n, 1, 256] bf16 or fp32; ``q_covariance``: fp32 [256, 256]; ``total_weight``:
+    fp32 scalar tensor on the device. Returns fp32 [n].
+    """
+    _device_check(key, q_covariance, total_weight)
+    n, heads, dim = key.shape
+    if heads != 1:
+        raise ValueError(f"sst_weights takes the keys of one KV head ([n, 1, {DIM}]); got "
+                         f"{heads} heads")
+    if dim != DIM:
+        raise ValueError(f"the calibration weights are built for head_dim {DIM}, got {dim}")
+    flag = _input_flag(key, "key")
+    _fp32_matrix(q_covariance, "q_covariance", (DIM, DIM))
+    if total_weight.dtype != torch.float32 or total_weight.numel() != 1:
+        raise ValueError("total_weight must be a float32 scalar tensor")
+    weights = torch.empty(n, dtype=torch.float32, device=key.device)
+    _ext.check(
+        _ext.library().oscar_sst_weights(
+            _ptr(key), flag, n, dim, key.stride(0), key.stride(2), _ptr(q_covariance),
+            _ptr(weights), _ptr(total_weight), _stream(key)),
+        "sst_weights",
+    )
+    return weights
 
 
-class WeightedCovariance:
-    """Streaming sum_t w_t x_t x_t^T / sum_t w_t over chunks of rows x [T, D] and weights [T]."""
-
-    def __init__(self, dim, device="cpu"):
-        self.total = torch.zeros((dim, dim), dtype=torch.float64, device=device)
-        self.weight = 0.0
-
-    def update(self, rows, weights=None):
-        rows = rows.double()
-        w = torch.ones(rows.shape[0], dtype=torch.float64, device=rows.device) if weights is None \
-            else weights.double()
-        self.total += rows.T @ (rows * w[:, None])
-        self.weight += float(w.sum())
-
-    def finalize(self):
-        if not self.weight > 0:
-            raise RuntimeError("No calibration tokens were observed")
-        return self.total / self.weight
-
-
-def query_covariance(q):
-    """Per-layer query covariance over tokens and query heads: q [T, Hq, D]."""
-    flat = q.reshape(-1, q.shape[-1]).double()
-    return flat.T @ flat / flat.shape[0]
+def normalize(x, denominator):
+    """x / max(denominator, 1e-30) (calibration_kernels.py:145-156); ``denominator`` is a
+    number or an fp32 scalar tensor on the device (read there, no host sync)."""
+    _device_check(x)
+    if x.dtype != torch.float32 or not x.is_contiguous():
+        raise ValueError("normalize takes a contiguous float32 tensor")
+    out = torch.empty_like(x)
+    if isinstance(denominator, torch.Tensor):
+        _device_check(denominator)
+        if denominator.dtype != torch.float32 or denominator.numel() != 1:
+            raise ValueError("a tensor denominator must be a float32 scalar")
+        den, value = _ptr(denominator), 1.0
+    else:
+        den, value = None, float(denominator)
+    _ext.check(
+        _ext.library().oscar_normalize(_ptr(x), x.numel(), den, value, _ptr(out), _stream(x)),
+        "normalize",
+    )
+    return out
 
 
-def key_weights(k, qcov):
-    """Attention weight of each key row, w_t = k_t^T C_q k_t (k [T, D])."""
-    k = k.double()
-    return (k @ qcov * k).sum(-1)
+def calibrated_rotations(covariances, max_sweeps=12, tolerance=1e-6):
+    """Batched eigen-decomposition and R = U H Pbr (calibration_kernels.py:287-327).
+
+    ``covariances``: fp32 [batch, 256, 256] on the device. Returns ``(rotations fp32 [batch,
+    256, 256], eigenvalues fp32 [batch, 256] ascending, {"sweeps", "relative_off_diagonal"})``.
+    All sweeps run on the device; only the per-matrix (sweeps, residual) pairs are read back
+    at the end. Raises RuntimeError for a non-finite covariance or when the residual is not
+    below ``tolerance`` after ``max_sweeps`` sweeps (nothing is returned then).
+    """
+    _device_check(covariances)
+    if covariances.dim() != 3 or covariances.dtype != torch.float32:
+        raise ValueError("covariances must be float32 [batch, 256, 256]")
+    batch, dim, last = covariances.shape
+    if dim != DIM or last != DIM:
+        raise ValueError(f"the eigensolver is built for {DIM} x {DIM} covariances, got "
+                         f"{dim} x {last}")
+    if not 1 <= max_sweeps <= 64:
+        raise ValueError("max_sweeps must be in [1, 64]")
+    lib = _ext.library()
+    cov = covariances.contiguous()
+    size = lib.oscar_calibration_workspace_bytes(batch, max_sweeps)
+    workspace = torch.empty(size, dtype=torch.uint8, device=cov.device)
+    rotations = torch.empty_like(cov)
+    eigenvalues = torch.empty((batch, DIM), dtype=torch.float32, device=cov.device)
+    info = torch.empty((batch, 2), dtype=torch.float32, device=cov.device)
+    _ext.check(
+        lib.oscar_calibrated_rotations(_ptr(cov), batch, dim, max_sweeps, float(tolerance),
+                                       _ptr(workspace), size, _ptr(rotations),
+                                       _ptr(eigenvalues), _ptr(info), _stream(cov)),
+        "calibrated_rotations",
+    )
+    done = info.cpu()
+    residual = float(done[:, 1].max())
+    sweeps = int(done[:, 0].max())
+    if not math.isfinite(residual):
+        raise RuntimeError("calibration covariance holds NaN or infinite values; no rotation "
+                           "is produced")
+    if not residual < tolerance:
+        raise RuntimeError(f"Jacobi sweeps stopped at relative off-diagonal {residual:.3e} "
+                           f"(tolerance {tolerance:g}) after {sweeps} sweeps; no rotation is "
+                           "produced")
+    return rotations, eigenvalues, {"sweeps": sweeps, "relative_off_diagonal": residual}

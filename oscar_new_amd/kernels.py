@@ -459,15 +459,28 @@ def finish_counters(meta, device, slots):
     return buf
 
 
+def history_rows(meta, layout, hq):
+    """Query rows per history task: query tokens per task (``meta.max_query_len`` when it is
+    below the tile) times the query heads of one KV head."""
+    mql = getattr(meta, "max_query_len", None)
+    qt = layout.config.queries_per_tile
+    return (mql if isinstance(mql, int) and 0 < mql < qt else qt) * (hq // layout.kv_heads)
+
+
+def history_kernel_name(meta, layout, hq):
+    """The history-branch kernel ``attention_partials`` launches for this batch: the paired
+    kernel up to 8 rows per task, then the one-tile and two-tile kernels."""
+    rows = history_rows(meta, layout, hq)
+    if rows <= 8:
+        return "history_pair_kernel"
+    return "history_kernel<1>" if rows <= 16 else "history_kernel<2>"
+
+
 def history_post_supported(meta, layout, hq, splits, tokens=None):
     """Whether ``history_post`` covers this launch: <= 8 query rows per task, <= 16 splits,
     split rows below 4 GiB (``tokens``: the launch's query rows n, when known)."""
-    cfg = layout.config
-    mql = getattr(meta, "max_query_len", None)
-    qt = cfg.queries_per_tile
-    rows = (mql if isinstance(mql, int) and 0 < mql < qt else qt) * (hq // layout.kv_heads)
-    small = tokens is None or tokens * hq * splits * cfg.head_dim * 4 < 1 << 32
-    return rows <= 8 and 1 <= splits <= 16 and small
+    small = tokens is None or tokens * hq * splits * layout.config.head_dim * 4 < 1 << 32
+    return history_rows(meta, layout, hq) <= 8 and 1 <= splits <= 16 and small
 
 
 def history_post(query, history, meta, layout, scale, splits, raw_partials, raw_lse, rv, key,

@@ -1,10 +1,12 @@
-"""Rotation artefacts and calibration math (reference rotations.py, calibration_kernels.py:250-327,
-tests/test_calibration_math.py), CPU.
+"""Rotation artefacts and the CPU calibration oracle (reference rotations.py,
+calibration_kernels.py:159-327, tests/test_calibration_math.py), CPU.
 
-Pins: the butterfly Hadamard against the recursive Sylvester matrix; the bit-reversed scatter
-against the explicit permutation-matrix product (and a hand-worked D = 4 case); eigenpairs by
-reconstruction and against a diagonal covariance's known answer; R orthogonal; the streaming
-weighted covariance against the one-shot normalization of the reference test.
+Pins of ``oracle/calibration_oracle.py``: the butterfly Hadamard against the recursive
+Sylvester matrix; the bit-reversed scatter against the explicit permutation-matrix product
+(and a hand-worked D = 4 case); the round-robin schedule covers every pair once per sweep;
+the Jacobi eigenpairs against LAPACK (torch.linalg.eigh), by reconstruction and against a
+diagonal covariance's known answer; R orthogonal; the streaming weighted covariance against
+the one-shot normalization of the reference test.
 """
 
 import math
@@ -12,7 +14,7 @@ import math
 import pytest
 import torch
 
-from oscar_new_amd import calibration as C
+from oracle import calibration_oracle as C
 from oscar_new_amd import rotations as R
 
 
@@ -58,16 +60,51 @@ def test_eigenpairs_reconstruct_and_sort_ascending():
     g = torch.Generator().manual_seed(3)
     x = torch.randn(300, 256, dtype=torch.float64, generator=g)
     cov = x.T @ x / 300
-    rotation, values, residual = C.calibrated_rotation(cov)
-    assert residual < 1e-9 and bool((values[1:] >= values[:-1]).all())
-    torch.testing.assert_close(rotation.double().T @ rotation.double(),
-                               torch.eye(256, dtype=torch.float64), atol=1e-5, rtol=0)
+    u, values = C.eigenpairs(cov)
+    assert bool((values[1:] >= values[:-1]).all())
+    torch.testing.assert_close(u @ torch.diag(values) @ u.T, cov, atol=1e-9, rtol=0)
+    rotation = C.compose_rotation(u)
+    torch.testing.assert_close(rotation.T @ rotation, torch.eye(256, dtype=torch.float64),
+                               atol=1e-9, rtol=0)
     diag = torch.diag(torch.tensor([3.0, 1.0, 2.0, 0.5], dtype=torch.float64))
     u, vals = C.eigenpairs(diag)
     torch.testing.assert_close(vals, torch.tensor([0.5, 1.0, 2.0, 3.0], dtype=torch.float64))
     torch.testing.assert_close(u.abs(), torch.eye(4, dtype=torch.float64)[:, [3, 1, 2, 0]])
-    with pytest.raises(RuntimeError, match="Nonfinite"):
-        C.calibrated_rotation(torch.full((4, 4), float("nan")))
+
+
+@pytest.mark.parametrize("dim", [4, 16, 256])
+def test_round_robin_schedule_covers_every_pair_once_per_sweep(dim):
+    seen = set()
+    for r in range(dim - 1):
+        p, q = C.round_pairs(dim, r)
+        assert len(set(p.tolist()) | set(q.tolist())) == dim  # disjoint pairs cover 0..dim-1
+        seen.update(tuple(sorted(pq)) for pq in zip(p.tolist(), q.tolist()))
+    assert len(seen) == dim * (dim - 1) // 2
+
+
+def test_jacobi_matches_lapack_and_reconstructs():
+    g = torch.Generator().manual_seed(14)
+    x = torch.randn(48, 16, dtype=torch.float64, generator=g)
+    cov = x.T @ x
+    u, values = C.jacobi_eigh(cov)
+    torch.testing.assert_close(values, torch.linalg.eigvalsh(cov), atol=1e-9, rtol=1e-10)
+    # Rotations stop once |a_pq| <= 1e-8 (|a_pp| + |a_qq|), which bounds the reconstruction.
+    torch.testing.assert_close(u @ torch.diag(values) @ u.T, cov, atol=1e-5, rtol=1e-6)
+    ref, _ = C.eigenpairs(cov)
+    signs = torch.sign((u * ref).sum(0))
+    torch.testing.assert_close(u * signs, ref, atol=1e-6, rtol=0)
+    torch.testing.assert_close(C.jacobi_eigh(torch.diag(torch.tensor([3.0, 1.0, 2.0])))[1],
+                               torch.tensor([1.0, 2.0, 3.0], dtype=torch.float64))
+
+
+def test_gram_and_key_weights_against_direct_sums():
+    g = torch.Generator().manual_seed(2)
+    x = torch.randn(5, 3, 8, dtype=torch.float64, generator=g)
+    w = torch.rand(15, dtype=torch.float64, generator=g)
+    direct = sum(w[i] * torch.outer(x.reshape(15, 8)[i], x.reshape(15, 8)[i]) for i in range(15))
+    torch.testing.assert_close(C.gram(x, w), direct)
+    qcov = -torch.eye(8, dtype=torch.float64)  # negative quadratic forms clamp to zero
+    assert (C.key_weights(x[:, 0], qcov) == 0).all()
 
 
 def test_streaming_weighted_covariance_matches_one_shot_normalization():
