@@ -65,6 +65,9 @@ def parse_args(argv=None):
     p.add_argument("--no-graph", action="store_true", help="eager launches instead of HIP graphs")
     p.add_argument("--one-launch-post", action="store_true",
                    help="history branch and post-attention in one launch (kernels.history_post)")
+    p.add_argument("--no-overlap", action="store_true",
+                   help="pre-attention (q rotation, BF16 branch, INT2 store) as its own "
+                        "launch instead of q rotation + history launch carrying the rest")
     p.add_argument("--layer-step", action="store_true",
                    help="the one-launch layer step (kernels.layer_step) instead of three launches")
     p.add_argument("--mode", default="step", choices=("step", "history", "copy", "prefill"),
@@ -542,6 +545,7 @@ def main(argv=None):
     for _ in layers:
         impl = OscarAttentionImpl.standalone(6, 256, 1 / 16, 1, w.cfg, split_policy=cfg["splits"],
                                              one_launch_post=args.one_launch_post,
+                                             overlap=not args.no_overlap,
                                              layer_step=args.layer_step)
         impl.set_rotations(w.rk, w.rv)
         impls.append(impl)
@@ -684,6 +688,7 @@ def main(argv=None):
             "splits": splits, "split_tokens": split_tokens, "layers_cycled": len(layers),
             "hip_graph": graphs is not None, "seed": args.seed,
             "one_launch_post": bool(args.one_launch_post),
+            "overlap": not args.no_overlap,
             "layer_step": bool(args.layer_step),
         },
         "us_per_layer_step": us_step,

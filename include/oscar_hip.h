@@ -209,7 +209,10 @@ int oscar_unpack(const void* history, int64_t history_bytes, const int64_t* slot
  * oscar_rotate of query by Rk) and the INT2 slots of the current tokens (exactly as
  * oscar_store_int2 of the rotated K/V). rk_t / rv_t: R_k^T and R_v^T, contiguous bf16
  * [256][256] (rk_t[c][k] = R_k[k][c]). query/key/value rows must be contiguous and 16-byte
- * aligned (row strides in elements, multiples of 8).
+ * aligned (row strides in elements, multiples of 8). qrot == NULL leaves the q rotation out
+ * (the caller rotates q itself, e.g. with oscar_rotate on another stream, so that the history
+ * launch can start while this one runs: the history branch never reads the slots written
+ * here).
  */
 int oscar_pre_attention(const void* query, int64_t q_s0, int64_t q_s1, const void* key,
                         int64_t k_s0, int64_t k_s1, const void* value, int64_t v_s0, int64_t v_s1,
@@ -262,6 +265,32 @@ int oscar_prefill_attention(const void* query, int64_t q_s0, int64_t q_s1, const
                             int32_t block_n, int32_t query_tile, int32_t max_query_len,
                             float scale, const oscar_layout* layout, void* output,
                             float* merged_lse, void* stream);
+
+/*
+ * history_pre -- the history branch (oscar_attention_partials with raw = 0) and the BF16 branch
+ * plus K/V INT2 store of oscar_pre_attention (its q rotation excluded) in ONE launch: the
+ * pre-attention work runs as extra workgroups dispatched ahead of the history splits, so it
+ * leaves the step's critical path. No reference counterpart as one call: it replaces
+ * backend.py:171-173 (rotate K/V, store_int2) and 211-222 (BF16 branch) beside the history
+ * attention_partials of backend.py:195-205. query_rot: the rotated query (as for
+ * oscar_attention_partials); query/key/value/window/rk_t/rv_t/slots/clip/raw_partials/raw_lse:
+ * as for oscar_pre_attention; partials/lse/splits/split_tokens: as for
+ * oscar_attention_partials. All outputs have the bits of those two calls. Coverage: query rows
+ * per task (min(query_tile, max_query_len) * hq / kv_heads) <= 8, else OSCAR_E_UNSUPPORTED.
+ */
+int oscar_history_pre(const void* query_rot, int64_t r_s0, int64_t r_s1, int64_t r_s2,
+                      const void* query, int64_t q_s0, int64_t q_s1, const void* key,
+                      int64_t k_s0, int64_t k_s1, const void* value, int64_t v_s0, int64_t v_s1,
+                      void* history, int64_t history_bytes, const void* window,
+                      int64_t window_elems, const int32_t* qstarts, const int32_t* seq_lens,
+                      const int32_t* block_tables, int64_t table_stride, int64_t table_columns,
+                      const int32_t* counts, const int32_t* tasks, const int32_t* task_count,
+                      int64_t n, int64_t hq, int64_t programs, int32_t splits, int32_t block_n,
+                      int32_t query_tile, int32_t max_query_len, float scale,
+                      int32_t split_tokens, const void* rk_t, const void* rv_t,
+                      const int64_t* slots, const oscar_clip* clip, const oscar_layout* layout,
+                      float* partials, float* lse, float* raw_partials, float* raw_lse,
+                      void* stream);
 
 /*
  * history_post -- the history branch and post_attention in ONE launch (no reference

@@ -124,14 +124,16 @@ class OscarAttentionImpl:
     them; slower than three launches on MI355X today, because its latency-bound parts wait
     behind the INT2 stream's memory traffic) and
     ``one_launch_post`` (history branch and post-attention in one launch where it applies and
-    the one-launch step does not; same bits as three launches).
+    the one-launch step does not; same bits as three launches) and ``overlap`` (default on:
+    where it applies, the three launches are the q rotation, the history launch carrying the
+    BF16 branch and the K/V INT2 store as extra workgroups, and post-attention; same bits).
     """
 
     def __init__(self, num_heads, head_size, scale, num_kv_heads, alibi_slopes=None,
                  sliding_window=None, kv_cache_dtype="auto", logits_soft_cap=None,
                  attn_type="decoder", kv_sharing_target_layer_name=None, *, vllm_config=None,
                  oscar_config=None, split_policy="reference", fused=True, one_launch_post=False,
-                 layer_step=False, **kwargs):
+                 layer_step=False, overlap=True, **kwargs):
         unsupported = (
             (alibi_slopes is not None, "ALiBi"),
             (sliding_window is not None, "sliding-window attention"),
@@ -169,6 +171,7 @@ class OscarAttentionImpl:
         self.fused = fused
         self.one_launch_post = one_launch_post
         self.layer_step = layer_step
+        self.overlap = overlap
         self.rk = self.rv = self.rk_cols = self.rv_cols = self.rk_t = self.rv_t = None
         self.history = self.window = None
         self.cache_identity = None
@@ -285,6 +288,18 @@ class OscarAttentionImpl:
             kernels.layer_step(q, k, v, self.history, self.window, meta, layout, self.scale,
                                splits, self.rk_t, self.rv_t, self.rv, rows, lse,
                                split_tokens=split_tokens)
+            return
+        if (self.overlap and not self.one_launch_post
+                and kernels.history_pre_supported(meta, layout, self.num_heads)):
+            # q rotation, then one launch holding the history branch and, dispatched ahead of
+            # it, the BF16 branch and the INT2 store (the history branch never reads the slots
+            # the store writes), then post-attention.
+            qrot = kernels.rotate(q, self.rk_cols)
+            hp, hl, rp, rl = kernels.history_pre(qrot, q, k, v, self.history, self.window, meta,
+                                                 layout, self.scale, splits, self.rk_t,
+                                                 self.rv_t, split_tokens=split_tokens)
+            kernels.post_attention(hp, hl, rp, rl, self.rv, k, v, self.window, meta, layout,
+                                   rows, lse)
             return
         qrot, rp, rl = kernels.pre_attention(q, k, v, self.history, self.window, meta, layout,
                                              self.scale, self.rk_t, self.rv_t)

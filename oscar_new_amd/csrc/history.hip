@@ -35,6 +35,7 @@
 #include "dma.h"
 #include "finish.h"
 #include "layer.h"
+#include "pre.h"
 
 namespace oscar {
 namespace {
@@ -589,10 +590,14 @@ static_assert(pair_slot(pair_slot(45)) == 45 && pair_slot(21) == 17, "pair_slot 
 // kMode 2: the one-launch layer step (layer.h): as 1, and the workgroups also rotate the query
 // (a.query is the unrotated query), store the step's INT2 slots, share the BF16 branch, and
 // the finisher stores the windows; padded rows are cleared by split 0 of each program.
+// kMode 3: as 0, behind `role_slices` z slices of pre-attention roles (pre.h: the BF16 branch
+// and the K/V INT2 store of the step), which dispatch first and run beside the history stream.
 template <int kMode>
 __device__ __forceinline__ void history_pair_body(const AttnArgs& a, const FinishArgs* fin,
-                                                  const LayerArgs* lay) {
-  constexpr bool kFinish = kMode >= 1;
+                                                  const LayerArgs* lay,
+                                                  const PreArgs* pre = nullptr,
+                                                  int role_slices = 0) {
+  constexpr bool kFinish = kMode == 1 || kMode == 2;
   if constexpr (kMode == 1) {
     if (static_cast<int>(blockIdx.z) == a.splits) {
       finish_extra(*fin, blockIdx.y);
@@ -612,6 +617,21 @@ __device__ __forceinline__ void history_pair_body(const AttnArgs& a, const Finis
   static_assert(kLayerRingBytes <= kRingBytes, "the layer-step finisher fits the ring");
   static_assert(16 * kStageRowBytes + 4 * 2 * 8 * 16 * 4 <= 2 * kStageBytes,
                 "the layer step's 16-row staging tile and operand images fit wavefront 3's stages");
+  static_assert(finish_lds_bytes<1>() <= kRingBytes && 16 * kHeadDim * 2 <= kRingBytes,
+                "the pre-attention roles fit the ring");
+  if constexpr (kMode == 3) {
+    const int z = blockIdx.z;
+    if (z < role_slices) {
+      if (z == 0) {
+        raw_block<1, false, true>(pre->attn, blockIdx.x, blockIdx.y, 0, s_ring);
+      } else {
+        const int r = ((z - 1) * static_cast<int>(gridDim.x) + static_cast<int>(blockIdx.x)) *
+                          static_cast<int>(gridDim.y) + static_cast<int>(blockIdx.y);
+        if (r < pre->kv_wgs) kv_store_role(*pre, r, s_ring);
+      }
+      return;
+    }
+  }
 
   // Layer step: R_k^T operands of the query rotation are requested first (they depend on
   // nothing), so that they arrive with the task metadata.
@@ -620,7 +640,7 @@ __device__ __forceinline__ void history_pair_body(const AttnArgs& a, const Finis
 
   Task t;
   if (!read_task(a, t, blockIdx.x)) return;
-  const int head = blockIdx.y, split = blockIdx.z;
+  const int head = blockIdx.y, split = static_cast<int>(blockIdx.z) - role_slices;
   const int length = t.recent_begin - t.sink_len;
   const int nsplit = history_splits(a, length);
   if (split >= nsplit) {
@@ -1111,6 +1131,16 @@ __global__ __launch_bounds__(kThreads, 2) void layer_step_kernel(const LayerStep
   history_pair_body<2>(h.a, &h.f, &h.l);
 }
 
+struct HistoryPreArgs {
+  AttnArgs a;
+  PreArgs p;
+  int32_t role_slices;
+};
+
+__global__ __launch_bounds__(kThreads, 2) void history_pre_kernel(const HistoryPreArgs h) {
+  history_pair_body<3>(h.a, nullptr, nullptr, &h.p, h.role_slices);
+}
+
 }  // namespace
 
 hipError_t launch_history(const AttnArgs& a, dim3 grid, int rows, hipStream_t stream) {
@@ -1120,6 +1150,13 @@ hipError_t launch_history(const AttnArgs& a, dim3 grid, int rows, hipStream_t st
     hipLaunchKernelGGL(history_kernel<1>, grid, dim3(kThreads), 0, stream, a);
   else
     hipLaunchKernelGGL(history_kernel<2>, grid, dim3(kThreads), 0, stream, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_history_pre(const AttnArgs& a, const PreArgs& p, int role_slices, dim3 grid,
+                              hipStream_t stream) {
+  const HistoryPreArgs h{a, p, role_slices};
+  hipLaunchKernelGGL(history_pre_kernel, grid, dim3(kThreads), 0, stream, h);
   return hipGetLastError();
 }
 

@@ -1,0 +1,110 @@
+// Pre-attention pieces shared by the fused launches: the arguments of the BF16 branch, the q
+// rotation and the K/V INT2 store of one step, the 16-row rotation tile, and the K/V store
+// role. step.hip runs them as the pre-attention launch; history.hip can run the BF16 branch and
+// the store as extra workgroups of the history launch.
+#pragma once
+
+#include "quant.h"
+#include "raw.h"
+
+namespace oscar {
+
+struct PreArgs {
+  AttnArgs attn;          // BF16 branch: unrotated query, key, value, window, metadata
+  const uint16_t* rk_t;   // R_k^T, contiguous: rk_t[c][k] = R_k[k][c]
+  const uint16_t* rv_t;   // R_v^T, contiguous
+  uint16_t* qrot;         // [n, hq, 256]
+  int64_t q_rows;         // n * hq
+  int64_t kv_rows;        // n * H
+  uint8_t* history;
+  int64_t history_bytes;
+  const int64_t* slots;
+  int32_t mode;
+  float k_ratio, v_ratio, k_factor, v_factor;
+  FastDiv h_div, hq_div;    // division by H and by hq
+  int32_t raw_wgs, kv_wgs;  // role boundaries in blockIdx.x
+};
+
+// Rotation of rows [16 tile, +16) by R (given as R^T rows) into a [16][256] bf16 LDS tile
+// (kv) or into `out` (q). Wavefront w computes columns 64w .. 64w + 63.
+__device__ __forceinline__ void rotate_rows16(const uint16_t* x, int64_t xs0, int64_t xs1,
+                                              FastDiv h_div, int64_t h, int64_t rows,
+                                              int64_t tile, const uint16_t* rt, uint16_t* lds_tile,
+                                              uint16_t* out) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int n = lane & 15, g = lane >> 4;
+  const int64_t row = tile * 16 + n;
+  const uint16_t* xp = nullptr;
+  if (row < rows) {
+    const uint32_t token = fastdiv(static_cast<uint32_t>(row), h_div);
+    xp = x + static_cast<int64_t>(token) * xs0 + (row - static_cast<int64_t>(token) * h) * xs1;
+  }
+  // Every operand (the A rows and the four column tiles of R) is requested before the first
+  // MFMA: one round of memory latency.
+  RotateOperands op;
+  u32x4 rb[4][8];
+  rotate_load_a<true>(op, xp, 1, g);
+#pragma unroll
+  for (int ct = 0; ct < 4; ++ct) {
+    rotate_load_b<true>(op, rt + static_cast<int64_t>(64 * wave + 16 * ct + n) * kHeadDim, 1, g);
+#pragma unroll
+    for (int m = 0; m < 8; ++m) rb[ct][m] = op.b[m];
+  }
+#pragma unroll
+  for (int ct = 0; ct < 4; ++ct) {
+    const int col = 64 * wave + 16 * ct + n;
+    const f32x4 acc = rotate_mfma(op.a, rb[ct]);
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int r = 4 * g + v;
+      const uint16_t bits = static_cast<uint16_t>(float_to_bf16(acc[v]));
+      if (lds_tile) {
+        lds_tile[r * kHeadDim + col] = bits;
+      } else if (tile * 16 + r < rows) {
+        out[(tile * 16 + r) * kHeadDim + col] = bits;
+      }
+    }
+  }
+}
+
+// K or V rows of quad r (K: r even, V: r odd): four workgroups share a 16-row rotation tile
+// (each computes it) and each clips/quantizes/packs four of its rows, one per wavefront, into
+// their slots. The row's token count and slot are requested before the rotation. `smem`:
+// 16 x 256 bf16 of 16-byte aligned LDS.
+__device__ __forceinline__ void kv_store_role(const PreArgs& p, int r, uint8_t* smem) {
+  const AttnArgs& a = p.attn;
+  const FastDiv h_div = p.h_div;
+  const int is_v = r & 1;
+  const int64_t quad = r >> 1, tile = quad >> 2;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int rr = 4 * static_cast<int>(quad & 3) + wave;
+  const int64_t row = tile * 16 + rr;
+  const bool in = row < p.kv_rows;
+  const uint32_t token = fastdiv(static_cast<uint32_t>(in ? row : 0), h_div);
+  const int head = static_cast<int>((in ? row : 0) - static_cast<int64_t>(token) * a.L.kv_heads);
+  const bool live = in && static_cast<int64_t>(token) < a.counts[1];
+  const int64_t slot = live ? p.slots[token] : -1;  // in flight beside the rotation loads
+  uint16_t* tile_lds = reinterpret_cast<uint16_t*>(smem);
+  rotate_rows16(is_v ? a.value : a.key, is_v ? a.vs0 : a.ks0, is_v ? a.vs1 : a.ks1, h_div,
+                a.L.kv_heads, p.kv_rows, tile, is_v ? p.rv_t : p.rk_t, tile_lds, nullptr);
+  __syncthreads();
+  // Same skips as store_int2 (kernels.py:168-169 and the buffer bound).
+  if (!live || slot < 0) return;
+  const int64_t page = slot / a.L.bp;
+  const int64_t within = slot - page * a.L.bp;
+  const int64_t base = page * a.L.page_bytes + (within * a.L.kv_heads + head) * a.L.slot_bytes;
+  if (base + 2 * a.L.vector_bytes > p.history_bytes) return;
+  const uint2 raw = *reinterpret_cast<const uint2*>(tile_lds + rr * kHeadDim + lane * 4);
+  const float x[4] = {bf16_to_float(raw.x & 0xffffu), bf16_to_float(raw.x >> 16),
+                      bf16_to_float(raw.y & 0xffffu), bf16_to_float(raw.y >> 16)};
+  quantize_store(x, p.mode, is_v ? p.v_ratio : p.k_ratio, is_v ? p.v_factor : p.k_factor,
+                 p.history + base + is_v * a.L.vector_bytes);
+}
+
+// The history launch with the pre-attention roles (history.hip): grid (programs, H,
+// role_slices + splits); z-slice 0 runs the BF16 branch of (task, kv head) (lean form, one
+// split), z-slices 1 .. role_slices - 1 the K/V store quads, the rest the history splits.
+hipError_t launch_history_pre(const AttnArgs& a, const PreArgs& p, int role_slices, dim3 grid,
+                              hipStream_t stream);
+
+}  // namespace oscar

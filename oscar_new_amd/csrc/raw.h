@@ -218,36 +218,51 @@ struct RawBlock {
   bool live[8];
 };
 
-__device__ __forceinline__ void raw_load_block(const AttnArgs& a, const Task& t, const RawTask& r,
-                                               int head, int t0, int end, int g, int n,
-                                               RawBlock& b) {
+__device__ __forceinline__ void raw_load_k(const AttnArgs& a, const Task& t, const RawTask& r,
+                                           int head, int t0, int end, int g, int n,
+                                           u32x4 (&kd)[2][8]) {
   const uint16_t* kp[2];
   int kpos;
 #pragma unroll
   for (int tt = 0; tt < 2; ++tt) kp[tt] = raw_token(a, t, r, head, t0 + 16 * tt + n, end, 0, kpos);
-  const uint16_t* vp[8];
-#pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    vp[e] = raw_token(a, t, r, head, t0 + tau(g, e), end, 1, b.pos[e]);
-    b.live[e] = vp[e] != nullptr;
-  }
 #pragma unroll
   for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
     for (int m = 0; m < 8; ++m)
-      b.kd[tt][m] = kp[tt] ? *reinterpret_cast<const u32x4*>(kp[tt] + 64 * g + 8 * m)
-                           : u32x4{0u, 0u, 0u, 0u};
+      kd[tt][m] = kp[tt] ? *reinterpret_cast<const u32x4*>(kp[tt] + 64 * g + 8 * m)
+                         : u32x4{0u, 0u, 0u, 0u};
+}
+
+__device__ __forceinline__ void raw_load_v(const AttnArgs& a, const Task& t, const RawTask& r,
+                                           int head, int t0, int end, int g, int n,
+                                           u32x4 (&vd)[8][2], int (&pos)[8], bool (&live)[8]) {
+  const uint16_t* vp[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
-    b.vd[e][0] = vp[e] ? *reinterpret_cast<const u32x4*>(vp[e] + 16 * n) : u32x4{0u, 0u, 0u, 0u};
-    b.vd[e][1] = vp[e] ? *reinterpret_cast<const u32x4*>(vp[e] + 16 * n + 8)
-                       : u32x4{0u, 0u, 0u, 0u};
+    vp[e] = raw_token(a, t, r, head, t0 + tau(g, e), end, 1, pos[e]);
+    live[e] = vp[e] != nullptr;
+  }
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    vd[e][0] = vp[e] ? *reinterpret_cast<const u32x4*>(vp[e] + 16 * n) : u32x4{0u, 0u, 0u, 0u};
+    vd[e][1] = vp[e] ? *reinterpret_cast<const u32x4*>(vp[e] + 16 * n + 8)
+                     : u32x4{0u, 0u, 0u, 0u};
   }
 }
 
+__device__ __forceinline__ void raw_load_block(const AttnArgs& a, const Task& t, const RawTask& r,
+                                               int head, int t0, int end, int g, int n,
+                                               RawBlock& b) {
+  raw_load_k(a, t, r, head, t0, end, g, n, b.kd);
+  raw_load_v(a, t, r, head, t0, end, g, n, b.vd, b.pos, b.live);
+}
+
 // One workgroup of the BF16 branch: (task, kv head, split).
-// `smem`: finish_lds_bytes<RT>() bytes of 16-byte aligned LDS.
-template <int RT, bool kDirect = false>
+// `smem`: finish_lds_bytes<RT>() bytes of 16-byte aligned LDS. kLean: the block's K rows are
+// loaded, scored, and only then its V rows (no prefetch; fewer registers, for a workgroup
+// role inside a launch whose other roles need two workgroups per CU). Same arithmetic, same
+// bits as the prefetching form.
+template <int RT, bool kDirect = false, bool kLean = false>
 __device__ __forceinline__ void raw_block(const AttnArgs& a, int task, int head, int split,
                                           uint8_t* smem) {
   Task t;
@@ -291,14 +306,15 @@ __device__ __forceinline__ void raw_block(const AttnArgs& a, int task, int head,
   // are requested before the current block is computed, so a wavefront with two blocks (a
   // decode step's 133 BF16 tokens over four wavefronts) still waits one memory round trip.
   // (Two row tiles (RT = 2) leave no registers for the second block: loaded in turn.)
-  constexpr bool kPrefetch = RT == 1;
+  constexpr bool kPrefetch = RT == 1 && !kLean;
   RawBlock cur, nxt;
   int t0 = begin + kBlock * wave;
   if (kPrefetch && t0 < end) raw_load_block(a, t, r, head, t0, end, g, n, cur);
   for (; t0 < end; t0 += 4 * kBlock) {
     const bool more = kPrefetch && t0 + 4 * kBlock < end;
     if (more) raw_load_block(a, t, r, head, t0 + 4 * kBlock, end, g, n, nxt);
-    if (!kPrefetch) raw_load_block(a, t, r, head, t0, end, g, n, cur);
+    if (!kPrefetch && !kLean) raw_load_block(a, t, r, head, t0, end, g, n, cur);
+    if (kLean) raw_load_k(a, t, r, head, t0, end, g, n, cur.kd);
     f32x4 sc[RT][2];
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt)
@@ -311,6 +327,7 @@ __device__ __forceinline__ void raw_block(const AttnArgs& a, int task, int head,
 #pragma unroll
         for (int rt = 0; rt < RT; ++rt)
           sc[rt][tt] = mfma16x16x32(cur.kd[tt][m], qb[rt][m], sc[rt][tt]);
+    if (kLean) raw_load_v(a, t, r, head, t0, end, g, n, cur.vd, cur.pos, cur.live);
     float s2[RT][8];
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt)

@@ -19,70 +19,11 @@
 //     backend.py:225-226 requires.
 #include "finish.h"
 #include "post.h"
-#include "quant.h"
+#include "pre.h"
 #include "layer.h"
-#include "raw.h"
 
 namespace oscar {
 namespace {
-
-struct PreArgs {
-  AttnArgs attn;          // BF16 branch: unrotated query, key, value, window, metadata
-  const uint16_t* rk_t;   // R_k^T, contiguous: rk_t[c][k] = R_k[k][c]
-  const uint16_t* rv_t;   // R_v^T, contiguous
-  uint16_t* qrot;         // [n, hq, 256]
-  int64_t q_rows;         // n * hq
-  int64_t kv_rows;        // n * H
-  uint8_t* history;
-  int64_t history_bytes;
-  const int64_t* slots;
-  int32_t mode;
-  float k_ratio, v_ratio, k_factor, v_factor;
-  FastDiv h_div, hq_div;    // division by H and by hq
-  int32_t raw_wgs, kv_wgs;  // role boundaries in blockIdx.x
-};
-
-// Rotation of rows [16 tile, +16) by R (given as R^T rows) into a [16][256] bf16 LDS tile
-// (kv) or into `out` (q). Wavefront w computes columns 64w .. 64w + 63.
-__device__ __forceinline__ void rotate_rows16(const uint16_t* x, int64_t xs0, int64_t xs1,
-                                              FastDiv h_div, int64_t h, int64_t rows,
-                                              int64_t tile, const uint16_t* rt, uint16_t* lds_tile,
-                                              uint16_t* out) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int n = lane & 15, g = lane >> 4;
-  const int64_t row = tile * 16 + n;
-  const uint16_t* xp = nullptr;
-  if (row < rows) {
-    const uint32_t token = fastdiv(static_cast<uint32_t>(row), h_div);
-    xp = x + static_cast<int64_t>(token) * xs0 + (row - static_cast<int64_t>(token) * h) * xs1;
-  }
-  // Every operand (the A rows and the four column tiles of R) is requested before the first
-  // MFMA: one round of memory latency.
-  RotateOperands op;
-  u32x4 rb[4][8];
-  rotate_load_a<true>(op, xp, 1, g);
-#pragma unroll
-  for (int ct = 0; ct < 4; ++ct) {
-    rotate_load_b<true>(op, rt + static_cast<int64_t>(64 * wave + 16 * ct + n) * kHeadDim, 1, g);
-#pragma unroll
-    for (int m = 0; m < 8; ++m) rb[ct][m] = op.b[m];
-  }
-#pragma unroll
-  for (int ct = 0; ct < 4; ++ct) {
-    const int col = 64 * wave + 16 * ct + n;
-    const f32x4 acc = rotate_mfma(op.a, rb[ct]);
-#pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      const int r = 4 * g + v;
-      const uint16_t bits = static_cast<uint16_t>(float_to_bf16(acc[v]));
-      if (lds_tile) {
-        lds_tile[r * kHeadDim + col] = bits;
-      } else if (tile * 16 + r < rows) {
-        out[(tile * 16 + r) * kHeadDim + col] = bits;
-      }
-    }
-  }
-}
 
 template <int RT>
 __global__ __launch_bounds__(kThreads) void pre_attention_kernel(const PreArgs p) {
@@ -98,37 +39,8 @@ __global__ __launch_bounds__(kThreads) void pre_attention_kernel(const PreArgs p
     raw_block<RT>(a, task, head, 0, smem);
     return;
   }
-  const FastDiv h_div = p.h_div;
   if (bid < p.raw_wgs + p.kv_wgs) {
-    // K or V rows: four workgroups share a 16-row rotation tile (each computes it) and each
-    // clips/quantizes/packs four of its rows, one per wavefront, into their slots. The
-    // row's token count and slot are requested before the rotation.
-    const int r = bid - p.raw_wgs;
-    const int is_v = r & 1;
-    const int64_t quad = r >> 1, tile = quad >> 2;
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int rr = 4 * static_cast<int>(quad & 3) + wave;
-    const int64_t row = tile * 16 + rr;
-    const bool in = row < p.kv_rows;
-    const uint32_t token = fastdiv(static_cast<uint32_t>(in ? row : 0), h_div);
-    const int head = static_cast<int>((in ? row : 0) - static_cast<int64_t>(token) * a.L.kv_heads);
-    const bool live = in && static_cast<int64_t>(token) < a.counts[1];
-    const int64_t slot = live ? p.slots[token] : -1;  // in flight beside the rotation loads
-    uint16_t* tile_lds = reinterpret_cast<uint16_t*>(smem);
-    rotate_rows16(is_v ? a.value : a.key, is_v ? a.vs0 : a.ks0, is_v ? a.vs1 : a.ks1, h_div,
-                  a.L.kv_heads, p.kv_rows, tile, is_v ? p.rv_t : p.rk_t, tile_lds, nullptr);
-    __syncthreads();
-    // Same skips as store_int2 (kernels.py:168-169 and the buffer bound).
-    if (!live || slot < 0) return;
-    const int64_t page = slot / a.L.bp;
-    const int64_t within = slot - page * a.L.bp;
-    const int64_t base = page * a.L.page_bytes + (within * a.L.kv_heads + head) * a.L.slot_bytes;
-    if (base + 2 * a.L.vector_bytes > p.history_bytes) return;
-    const uint2 raw = *reinterpret_cast<const uint2*>(tile_lds + rr * kHeadDim + lane * 4);
-    const float x[4] = {bf16_to_float(raw.x & 0xffffu), bf16_to_float(raw.x >> 16),
-                        bf16_to_float(raw.y & 0xffffu), bf16_to_float(raw.y >> 16)};
-    quantize_store(x, p.mode, is_v ? p.v_ratio : p.k_ratio, is_v ? p.v_factor : p.k_factor,
-                   p.history + base + is_v * a.L.vector_bytes);
+    kv_store_role(p, bid - p.raw_wgs, smem);
     return;
   }
   // q tile: rotated rows straight to qrot.
@@ -160,17 +72,24 @@ namespace {
 bool aligned16(const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; }
 }  // namespace
 
-extern "C" int oscar_pre_attention(
-    const void* query, int64_t q_s0, int64_t q_s1, const void* key, int64_t k_s0, int64_t k_s1,
-    const void* value, int64_t v_s0, int64_t v_s1, const void* window, int64_t window_elems,
-    const int32_t* qstarts, const int32_t* seq_lens, const int32_t* block_tables,
-    int64_t table_stride, int64_t table_columns, const int32_t* counts, const int32_t* tasks,
-    const int32_t* task_count, int64_t n, int64_t hq, int64_t programs, int32_t block_n,
-    int32_t query_tile, int32_t max_query_len, float scale, const void* rk_t, const void* rv_t,
-    void* history, int64_t history_bytes, const int64_t* slots, const oscar_clip* clip,
-    const oscar_layout* layout, float* raw_partials, float* raw_lse, void* qrot, void* stream) {
-  using namespace oscar;
-  PreArgs p{};
+namespace oscar {
+namespace {
+
+// The checks and fields of one pre-attention launch (all roles; grid sizes in raw_wgs and
+// kv_wgs, the q tiles follow when qrot is set). OSCAR_OK with *p filled and *qrows = query rows
+// per task, or the entry point's error code (OSCAR_OK with nothing filled when n == 0).
+int make_pre_args(const void* query, int64_t q_s0, int64_t q_s1, const void* key, int64_t k_s0,
+                  int64_t k_s1, const void* value, int64_t v_s0, int64_t v_s1, const void* window,
+                  int64_t window_elems, const int32_t* qstarts, const int32_t* seq_lens,
+                  const int32_t* block_tables, int64_t table_stride, int64_t table_columns,
+                  const int32_t* counts, const int32_t* tasks, const int32_t* task_count,
+                  int64_t n, int64_t hq, int64_t programs, int32_t block_n, int32_t query_tile,
+                  int32_t max_query_len, float scale, const void* rk_t, const void* rv_t,
+                  void* history, int64_t history_bytes, const int64_t* slots,
+                  const oscar_clip* clip, const oscar_layout* layout, float* raw_partials,
+                  float* raw_lse, void* qrot, PreArgs* out, int64_t* qrows_out) {
+  PreArgs& p = *out;
+  p = PreArgs{};
   AttnArgs& a = p.attn;
   const int st = make_layout(layout, &a.L);
   if (st != OSCAR_OK) return st;
@@ -184,14 +103,15 @@ extern "C" int oscar_pre_attention(
   const int64_t qrows = (max_query_len > 0 && max_query_len < query_tile ? max_query_len
                                                                          : query_tile) * g;
   if (qrows > 32) return OSCAR_E_UNSUPPORTED;
+  *qrows_out = qrows;
   if (n == 0) return OSCAR_OK;
   if (!query || !key || !value || !window || !qstarts || !seq_lens || !block_tables || !counts ||
       !tasks || !task_count || !rk_t || !rv_t || !history || !slots || !raw_partials ||
-      !raw_lse || !qrot)
+      !raw_lse)
     return OSCAR_E_NULL;
   if (q_s0 % 8 || q_s1 % 8 || k_s0 % 8 || k_s1 % 8 || v_s0 % 8 || v_s1 % 8 || !aligned16(query) ||
       !aligned16(key) || !aligned16(value) || !aligned16(window) || !aligned16(rk_t) ||
-      !aligned16(rv_t) || !aligned16(raw_partials) || !aligned16(qrot) ||
+      !aligned16(rv_t) || !aligned16(raw_partials) || (qrot && !aligned16(qrot)) ||
       reinterpret_cast<uintptr_t>(history) % 4)
     return OSCAR_E_ALIGN;
   a.query = static_cast<const uint16_t*>(query);
@@ -240,7 +160,32 @@ extern "C" int oscar_pre_attention(
   p.hq_div = make_fastdiv(static_cast<uint32_t>(hq));
   p.raw_wgs = static_cast<int32_t>(programs * h);
   p.kv_wgs = static_cast<int32_t>(2 * 4 * ((p.kv_rows + 15) / 16));
-  const int64_t q_wgs = (p.q_rows + 15) / 16;
+  return OSCAR_OK;
+}
+
+}  // namespace
+}  // namespace oscar
+
+extern "C" int oscar_pre_attention(
+    const void* query, int64_t q_s0, int64_t q_s1, const void* key, int64_t k_s0, int64_t k_s1,
+    const void* value, int64_t v_s0, int64_t v_s1, const void* window, int64_t window_elems,
+    const int32_t* qstarts, const int32_t* seq_lens, const int32_t* block_tables,
+    int64_t table_stride, int64_t table_columns, const int32_t* counts, const int32_t* tasks,
+    const int32_t* task_count, int64_t n, int64_t hq, int64_t programs, int32_t block_n,
+    int32_t query_tile, int32_t max_query_len, float scale, const void* rk_t, const void* rv_t,
+    void* history, int64_t history_bytes, const int64_t* slots, const oscar_clip* clip,
+    const oscar_layout* layout, float* raw_partials, float* raw_lse, void* qrot, void* stream) {
+  using namespace oscar;
+  PreArgs p;
+  int64_t qrows = 0;
+  const int st = make_pre_args(query, q_s0, q_s1, key, k_s0, k_s1, value, v_s0, v_s1, window,
+                               window_elems, qstarts, seq_lens, block_tables, table_stride,
+                               table_columns, counts, tasks, task_count, n, hq, programs, block_n,
+                               query_tile, max_query_len, scale, rk_t, rv_t, history,
+                               history_bytes, slots, clip, layout, raw_partials, raw_lse, qrot,
+                               &p, &qrows);
+  if (st != OSCAR_OK || n == 0) return st;
+  const int64_t q_wgs = qrot ? (p.q_rows + 15) / 16 : 0;  // NULL qrot: no q rotation role
   const dim3 grid(static_cast<unsigned>(p.raw_wgs + p.kv_wgs + q_wgs));
   hipStream_t s = as_stream(stream);
   if (qrows <= 16)
@@ -248,6 +193,44 @@ extern "C" int oscar_pre_attention(
   else
     hipLaunchKernelGGL(pre_attention_kernel<2>, grid, dim3(kThreads), 0, s, p);
   return static_cast<int>(hipGetLastError());
+}
+
+extern "C" int oscar_history_pre(
+    const void* query_rot, int64_t r_s0, int64_t r_s1, int64_t r_s2, const void* query,
+    int64_t q_s0, int64_t q_s1, const void* key, int64_t k_s0, int64_t k_s1, const void* value,
+    int64_t v_s0, int64_t v_s1, void* history, int64_t history_bytes, const void* window,
+    int64_t window_elems, const int32_t* qstarts, const int32_t* seq_lens,
+    const int32_t* block_tables, int64_t table_stride, int64_t table_columns,
+    const int32_t* counts, const int32_t* tasks, const int32_t* task_count, int64_t n,
+    int64_t hq, int64_t programs, int32_t splits, int32_t block_n, int32_t query_tile,
+    int32_t max_query_len, float scale, int32_t split_tokens, const void* rk_t,
+    const void* rv_t, const int64_t* slots, const oscar_clip* clip, const oscar_layout* layout,
+    float* partials, float* lse, float* raw_partials, float* raw_lse, void* stream) {
+  using namespace oscar;
+  PreArgs p;
+  int64_t qrows = 0;
+  int st = make_pre_args(query, q_s0, q_s1, key, k_s0, k_s1, value, v_s0, v_s1, window,
+                         window_elems, qstarts, seq_lens, block_tables, table_stride,
+                         table_columns, counts, tasks, task_count, n, hq, programs, block_n,
+                         query_tile, max_query_len, scale, rk_t, rv_t, history, history_bytes,
+                         slots, clip, layout, raw_partials, raw_lse, nullptr, &p, &qrows);
+  if (st != OSCAR_OK) return st;
+  if (qrows > 8) return OSCAR_E_UNSUPPORTED;
+  AttnArgs a;
+  int64_t hrows = 0;
+  st = make_attn_args(query_rot, r_s0, r_s1, r_s2, nullptr, 0, 0, 1, nullptr, 0, 0, 1, history,
+                      history_bytes, window, window_elems, qstarts, seq_lens, block_tables,
+                      table_stride, table_columns, counts, tasks, task_count, n, hq, programs,
+                      splits, block_n, query_tile, max_query_len, scale, 0, split_tokens, layout,
+                      partials, lse, &a, &hrows);
+  if (st != OSCAR_OK || n == 0) return st;
+  // Role slices in front of the history splits (dispatched first): slice 0 is the BF16
+  // branch of (task, kv head); the next ones hold the K/V store quads.
+  const int64_t per_slice = programs * a.L.kv_heads;
+  const int role_slices = 1 + static_cast<int>((p.kv_wgs + per_slice - 1) / per_slice);
+  const dim3 grid(static_cast<unsigned>(programs), static_cast<unsigned>(a.L.kv_heads),
+                  static_cast<unsigned>(splits + role_slices));
+  return static_cast<int>(launch_history_pre(a, p, role_slices, grid, as_stream(stream)));
 }
 
 namespace oscar {

@@ -28,6 +28,8 @@ __all__ = [
     "post_attention",
     "history_post",
     "layer_step",
+    "history_pre",
+    "history_pre_supported",
     "layout_struct",
     "clip_struct",
 ]
@@ -481,6 +483,71 @@ def history_post_supported(meta, layout, hq, splits, tokens=None):
     split rows below 4 GiB (``tokens``: the launch's query rows n, when known)."""
     small = tokens is None or tokens * hq * splits * layout.config.head_dim * 4 < 1 << 32
     return history_rows(meta, layout, hq) <= 8 and 1 <= splits <= 16 and small
+
+
+def history_pre_supported(meta, layout, hq):
+    """Whether ``history_pre`` covers this batch: <= 8 query rows per task (the paired history
+    kernel and a one-tile BF16 branch)."""
+    return history_rows(meta, layout, hq) <= 8
+
+
+def history_pre(query_rot, query, key, value, history, window, meta, layout, scale, splits,
+                rk_t, rv_t, split_tokens=0):
+    """The history branch and the pre-attention work other than the q rotation (BF16 branch,
+    K/V INT2 store) in one launch, the latter as workgroups dispatched ahead of the history
+    splits (no reference counterpart as one call; it replaces ``attention_partials(qrot, ...,
+    raw=False)`` plus ``pre_attention`` without its q rotation, with their bits).
+
+    ``query_rot``: the rotated query; ``query``/``key``/``value``: the step's unrotated rows.
+    Returns ``(partials [n, hq, splits, 256], lse [n, hq, splits], raw_partials
+    [n, hq, 1, 256], raw_lse [n, hq, 1])``, all fp32.
+    """
+    _device_check(query_rot, query, key, value, history, window, rk_t, rv_t)
+    n, hq, d = query.shape
+    cfg = layout.config
+    if not history_pre_supported(meta, layout, hq):
+        raise ValueError("history_pre covers <= 8 query rows per task")
+    if split_tokens < 0:
+        raise ValueError("split_tokens must be >= 0")
+    dev = query.device
+    partials = torch.empty((n, hq, splits, d), dtype=torch.float32, device=dev)
+    lse = torch.empty((n, hq, splits), dtype=torch.float32, device=dev)
+    raw_partials = torch.empty((n, hq, 1, d), dtype=torch.float32, device=dev)
+    raw_lse = torch.empty((n, hq, 1), dtype=torch.float32, device=dev)
+    if n == 0:
+        return partials, lse, raw_partials, raw_lse
+    programs = attention_programs(n, meta.max_num_reqs, cfg.queries_per_tile)
+    if meta.tasks.shape[0] < programs:
+        raise ValueError(f"task table holds {meta.tasks.shape[0]} rows; the grid needs {programs}")
+    for r in (rk_t, rv_t):
+        if r.dtype != torch.bfloat16 or not r.is_contiguous() or tuple(r.shape) != (d, d):
+            raise ValueError("rk_t / rv_t must be contiguous bf16 [256, 256] (R transposed)")
+    query_rot = _rows_contiguous(query_rot)
+    query, q0, q1 = _row_strides(query, "query")
+    key, k0, k1 = _row_strides(key, "key")
+    value, v0, v1 = _row_strides(value, "value")
+    if meta.slot_mapping.dtype != torch.int64:
+        raise ValueError("slot mapping must be int64")
+    table = _int32(meta.block_tables, "block_tables")
+    max_query_len = getattr(meta, "max_query_len", None)
+    max_query_len = int(max_query_len) if isinstance(max_query_len, int) else 0
+    _ext.check(
+        _ext.library().oscar_history_pre(
+            _ptr(query_rot), *query_rot.stride(), _ptr(query), q0, q1, _ptr(key), k0, k1,
+            _ptr(value), v0, v1, _ptr(history), history.numel() * history.element_size(),
+            _ptr(window), window.numel(),
+            _ptr(_int32(meta.query_start_loc, "query_start_loc")),
+            _ptr(_int32(meta.seq_lens, "seq_lens")), _ptr(table), table.stride(0), table.shape[1],
+            _ptr(_int32(meta.counts, "counts")), _ptr(_int32(meta.tasks, "tasks")),
+            _ptr(_int32(meta.task_count, "task_count")),
+            n, hq, programs, splits, cfg.block_n, cfg.queries_per_tile, max_query_len,
+            float(scale), int(split_tokens), _ptr(rk_t), _ptr(rv_t), _ptr(meta.slot_mapping),
+            clip_struct(cfg), layout_struct(layout), _ptr(partials), _ptr(lse),
+            _ptr(raw_partials), _ptr(raw_lse), _stream(query),
+        ),
+        "history_pre",
+    )
+    return partials, lse, raw_partials, raw_lse
 
 
 def history_post(query, history, meta, layout, scale, splits, raw_partials, raw_lse, rv, key,

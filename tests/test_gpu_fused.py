@@ -70,15 +70,16 @@ CASES = [
 
 
 def _forward(c, form, splits, raw=None):
-    """One layer step in `form` ("single"; "fused": three launches; "fused1": history + post
-    in one launch where it applies; "layer": the one-launch step where it applies) on a copy
-    of the cache."""
+    """One layer step in `form` ("single"; "fused": q rotation, history launch carrying the
+    BF16 branch and INT2 store, post-attention; "fused_serial": pre-attention, history,
+    post-attention; "fused1": history + post in one launch where it applies; "layer": the
+    one-launch step where it applies) on a copy of the cache."""
     n = c.q.shape[0]
     raw = c.raw.clone() if raw is None else raw
     k_cache, v_cache = _views(raw, c.layout)
     impl = OscarAttentionImpl.standalone(6, 256, 1 / 16, 1, c.layout.config,
                                          fused=form != "single", one_launch_post=form == "fused1",
-                                         layer_step=form == "layer")
+                                         layer_step=form == "layer", overlap=form != "fused_serial")
     impl.set_rotations(c.rk, c.rv)
     impl.partition_for = lambda meta, s=splits: (s, 0)
     c.meta.merged_lse = torch.full((n, 6), 7.0, device=DEV)
@@ -92,7 +93,7 @@ def _forward(c, form, splits, raw=None):
 def test_fused_step_is_bitwise_the_single_launch_step(lengths, prefixes, splits):
     c = _case(lengths, prefixes, seed=7)
     want = _forward(c, "single", splits)
-    for form in ("fused", "fused1"):
+    for form in ("fused", "fused_serial", "fused1"):
         got = _forward(c, form, splits)
         for a, b in zip(want, got):
             assert torch.equal(a, b), form
@@ -246,6 +247,39 @@ def test_pre_attention_matches_single_entry_points():
                                                 1 / 16, 1, True)
     torch.cuda.synchronize()
     assert torch.equal(qrot.view(torch.int16), q_ref.view(torch.int16))
+    assert torch.equal(rp, rp_ref)
+    assert torch.equal(rl, rl_ref)
+    assert torch.equal(hist_a, hist_b)
+
+
+@pytest.mark.parametrize("lengths,prefixes,split_tokens", [
+    ([1804, 2601], [1803, 2600], 0),  # decode: one query row group per task
+    ([69, 263, 1804, 40], [67, 261, 1802, 38], 0),  # two-token MTP (12 rows: > 8, refused)
+    ([6000, 300, 4000], [5999, 299, 3999], 512),  # token-bounded splits
+])
+def test_history_pre_matches_single_entry_points(lengths, prefixes, split_tokens):
+    c = _case(lengths, prefixes, seed=4)
+    meta, layout = c.meta, c.layout
+    splits = 8
+    hist_a, win_a = layout.tensor_views(_views(c.raw.clone(), layout))
+    hist_b, win_b = layout.tensor_views(_views(c.raw.clone(), layout))
+    rk_t, rv_t = c.rk.T.contiguous(), c.rv.T.contiguous()
+    qrot = kernels.rotate(c.q, rk_t.T)
+    if not kernels.history_pre_supported(meta, layout, 6):
+        with pytest.raises(ValueError):
+            kernels.history_pre(qrot, c.q, c.k, c.v, hist_a, win_a, meta, layout, 1 / 16, splits,
+                                rk_t, rv_t)
+        return
+    hp, hl, rp, rl = kernels.history_pre(qrot, c.q, c.k, c.v, hist_a, win_a, meta, layout, 1 / 16,
+                                         splits, rk_t, rv_t, split_tokens=split_tokens)
+    hp_ref, hl_ref = kernels.attention_partials(qrot, c.k, c.v, hist_b, win_b, meta, layout,
+                                                1 / 16, splits, False, split_tokens=split_tokens)
+    _, rp_ref, rl_ref = kernels.pre_attention(c.q, c.k, c.v, hist_b, win_b, meta, layout, 1 / 16,
+                                              rk_t, rv_t)
+    torch.cuda.synchronize()
+    live = hl_ref > -float("inf")  # split slots a token-bounded request does not use
+    assert torch.equal(hl, hl_ref)
+    assert torch.equal(hp[live], hp_ref[live])
     assert torch.equal(rp, rp_ref)
     assert torch.equal(rl, rl_ref)
     assert torch.equal(hist_a, hist_b)
