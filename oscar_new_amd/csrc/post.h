@@ -156,15 +156,80 @@ __device__ __forceinline__ void post_rows_map(const PostArgs& p, RowOf row_of, i
       [&](int, int64_t row, int col, uint16_t bits) { p.out[row * kHeadDim + col] = bits; });
 }
 
-// Rows [row0, min(row0 + R, row_end, p.rows)) (the post-attention launch).
+// Rows [row0, min(row0 + R, p.rows)) (R <= 4, one per wavefront) for the 64 output columns
+// of `quarter`: wavefront w merges row w into LDS, then rotates the merged rows back for column
+// tile w of the quarter (16 columns) and merges them with the BF16 branch. The four quarter
+// workgroups of a row group each merge the same rows (the same bits) and read a quarter of
+// R_v, so that no workgroup streams all of R_v: a latency-bound workgroup's reads are limited
+// by its own outstanding requests, not by the memory system. Each output element takes the
+// arithmetic of rotate_merge (same operands, same MFMA k order, same path merge).
+// kMode: the split merge of the launch (merge_mode): one round or a scan per wavefront-row,
+// or (R = 1) the four wavefronts merging the row together, as the other post paths do.
 template <int R, int kMode>
-__device__ __forceinline__ void post_rows(const PostArgs& p, int64_t row0, int64_t row_end,
-                                          uint16_t (*s_h)[kHeadDim], float* s_l,
-                                          GroupMergeLds* group_lds) {
-  const int64_t end = min(row_end, p.rows);
-  post_rows_map<R, kMode>(
-      p, [=](int r) { return row0 + r < end ? row0 + r : static_cast<int64_t>(-1); }, p.splits,
-      s_h, s_l, group_lds);
+__device__ __forceinline__ void post_rows_quarter(const PostArgs& p, int64_t row0, int quarter,
+                                                  uint16_t (*s_h)[kHeadDim], float* s_l,
+                                                  GroupMergeLds* group_lds) {
+  static_assert(R >= 1 && R <= 4, "one merged row per wavefront");
+  static_assert(kMode != kMergeScanGroup || R == 1, "a workgroup-row merge serves one row");
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int n = lane & 15, g = lane >> 4;
+  const int64_t end = min(row0 + R, p.rows);
+  const int col = 64 * quarter + 16 * wave + n;
+  RotateOperands op;
+  rotate_load_b<true>(op, p.rv + static_cast<int64_t>(col) * kHeadDim, 1, g);
+  u32x4 rb[8];
+#pragma unroll
+  for (int m = 0; m < 8; ++m) rb[m] = op.b[m];
+  const int active = p.counts[1];
+  // BF16-branch value and LSE of this lane's rows 4g + v at column `col`.
+  int64_t row[4];
+  bool valid[4];
+  float bv[4], lb[4];
+#pragma unroll
+  for (int v = 0; v < 4; ++v) {
+    const int r = 4 * g + v;
+    row[v] = r < R && row0 + r < end ? row0 + r : -1;
+    const int64_t lrow = row[v] >= 0 ? row[v] : 0;
+    valid[v] = row[v] >= 0 && row[v] / p.hq < active;
+    const float l = p.rl[lrow];
+    const float x = p.rp[lrow * kHeadDim + col];
+    lb[v] = valid[v] ? l : -INFINITY;
+    bv[v] = valid[v] ? x : 0.f;
+  }
+  if constexpr (kMode == kMergeScanGroup) {
+    const bool in = row0 < end;
+    const SplitMerge m = merge_splits_row_group(p.hp + (in ? row0 : 0) * p.splits * kHeadDim,
+                                                p.hl + (in ? row0 : 0) * p.splits, p.splits,
+                                                in && row0 / p.hq < active, group_lds);
+    if (wave == 0) {
+      *reinterpret_cast<uint2*>(&s_h[0][lane * 4]) = merge_splits_out(m);
+      if (lane == 0) s_l[0] = merge_splits_lse(m);
+    }
+  } else if (wave < R) {
+    const int64_t r = row0 + wave;
+    const bool in = r < end;
+    const float* part = p.hp + (in ? r : 0) * p.splits * kHeadDim;
+    const float* ls = p.hl + (in ? r : 0) * p.splits;
+    const bool live = in && r / p.hq < active;
+    const SplitMerge m = kMode == kMergeOneRound
+                             ? merge_splits_row(part, ls, p.splits, live, lane)
+                             : merge_splits_row_scan(part, ls, p.splits, live, lane);
+    *reinterpret_cast<uint2*>(&s_h[wave][lane * 4]) = merge_splits_out(m);
+    if (lane == 0) s_l[wave] = merge_splits_lse(m);
+  }
+  __syncthreads();
+  rotate_load_a<true>(op, n < R ? &s_h[n][0] : nullptr, 1, g);
+  const f32x4 acc = rotate_mfma(op.a, rb);
+#pragma unroll
+  for (int v = 0; v < 4; ++v) {
+    const int r = 4 * g + v;
+    if (r >= R || row[v] < 0) continue;
+    const PathWeights w = path_weights(valid[v] ? s_l[r] : -INFINITY, lb[v]);
+    const float av = valid[v] ? bf16_to_float(float_to_bf16(acc[v])) : 0.f;
+    p.out[row[v] * kHeadDim + col] =
+        static_cast<uint16_t>(float_to_bf16(path_merge(w, av, bv[v])));
+    if (p.merged_lse && quarter == 0 && wave == 0 && n == 0) p.merged_lse[row[v]] = path_lse(w);
+  }
 }
 
 }  // namespace oscar

@@ -25,6 +25,8 @@
 namespace oscar {
 namespace {
 
+constexpr int kPostQuarterRows = 2;  // rows per column-quarter post-attention workgroup
+
 template <int RT>
 __global__ __launch_bounds__(kThreads) void pre_attention_kernel(const PreArgs p) {
   constexpr int kRawLds = finish_lds_bytes<RT>();
@@ -48,19 +50,25 @@ __global__ __launch_bounds__(kThreads) void pre_attention_kernel(const PreArgs p
   rotate_rows16(a.query, a.qs0, a.qs1, p.hq_div, a.hq, p.q_rows, tile, p.rk_t, nullptr, p.qrot);
 }
 
-// Workgroups [0, merge_wgs): R (token, query head) rows each (R = 4: one wavefront per row for
-// the split merge; R = 1 above 16 splits: the four wavefronts merge the row together). The
-// remaining workgroups store the window of one request each; both branches have read the
+// More than 16 splits. Workgroups [0, merge_wgs): R (token, query head) rows each (R = 4: a
+// scanned split merge per wavefront-row; R = 1: the four wavefronts merge the row together).
+// The remaining workgroups store the window of one request each; both branches have read the
 // window before this launch, and the merges do not touch it.
+// Grid (merge_wgs + requests, 4): workgroup (x, y < 4) serves R rows (merge_mode's rule: R = 1
+// for a workgroup-row merge) for output columns [64 y, 64 y + 64); the window workgroups are
+// those of y = 0; both branches have read the window before this launch, and the merges do
+// not touch it.
 template <int R, int kMode>
 __global__ __launch_bounds__(kThreads) void post_attention_kernel(const PostArgs p) {
   __shared__ __attribute__((aligned(16))) uint16_t s_h[R][kHeadDim];  // merged history rows
   __shared__ float s_l[R];
   __shared__ GroupMergeLds group_lds;
   if (static_cast<int>(blockIdx.x) < p.merge_wgs) {
-    post_rows<R, kMode>(p, static_cast<int64_t>(blockIdx.x) * R, p.rows, s_h, s_l, &group_lds);
+    post_rows_quarter<R, kMode>(p, static_cast<int64_t>(blockIdx.x) * R, blockIdx.y, s_h, s_l,
+                                &group_lds);
     return;
   }
+  if (blockIdx.y != 0) return;
   const int req = static_cast<int>(blockIdx.x) - p.merge_wgs;
   for (int head = 0; head < p.win.L.kv_heads; ++head) store_window_request(p.win, req, head);
 }
@@ -308,15 +316,18 @@ extern "C" int oscar_post_attention(
                                 table_stride, max_reqs, layout, &p);
   if (st != OSCAR_OK || n == 0) return st;
   const int mode = merge_mode(p.rows, splits);
-  const int64_t merge_wgs = mode == kMergeScanGroup ? p.rows : (p.rows + 3) / 4;
-  if (merge_wgs + p.win_requests > 0x7fffffffll) return OSCAR_E_SHAPE;
-  p.merge_wgs = static_cast<int32_t>(merge_wgs);
-  const dim3 grid(static_cast<unsigned>(merge_wgs + p.win_requests));
+  const int rows_per_wg = mode == kMergeScanGroup ? 1 : kPostQuarterRows;
+  const int64_t groups = (p.rows + rows_per_wg - 1) / rows_per_wg;
+  if (groups + p.win_requests > 0x7fffffffll) return OSCAR_E_SHAPE;
+  p.merge_wgs = static_cast<int32_t>(groups);
+  const dim3 grid(static_cast<unsigned>(groups + p.win_requests), 4);
   hipStream_t s = as_stream(stream);
   if (mode == kMergeOneRound)
-    hipLaunchKernelGGL((post_attention_kernel<4, kMergeOneRound>), grid, dim3(kThreads), 0, s, p);
+    hipLaunchKernelGGL((post_attention_kernel<kPostQuarterRows, kMergeOneRound>), grid,
+                       dim3(kThreads), 0, s, p);
   else if (mode == kMergeScanWave)
-    hipLaunchKernelGGL((post_attention_kernel<4, kMergeScanWave>), grid, dim3(kThreads), 0, s, p);
+    hipLaunchKernelGGL((post_attention_kernel<kPostQuarterRows, kMergeScanWave>), grid,
+                       dim3(kThreads), 0, s, p);
   else
     hipLaunchKernelGGL((post_attention_kernel<1, kMergeScanGroup>), grid, dim3(kThreads), 0, s, p);
   return static_cast<int>(hipGetLastError());
