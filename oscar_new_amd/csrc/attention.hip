@@ -4,11 +4,7 @@
 // Reference: oscar_ascend/kernels.py:290-482 (`_attention_kernel` with IS_RAW true: raw
 // positions = sink + recent window + causal current tokens, kernels.py:421-470).
 //
-// MI355X design: a workgroup is 4 independent wavefronts on bf16 MFMA
-// (v_mfma_f32_16x16x32_bf16); each owns every 4th 32-token block of the split and keeps its
-// own online-softmax state, merged once through LDS at the end. Scores are computed
-// transposed (S^T = K Q^T), so the MFMA output layout (lane holds 4 consecutive tokens of
-// one query row) is the A-operand layout of the P*V MFMA with no shuffle in between.
+// The BF16 branch's row arithmetic and workgroup layout are raw.h's.
 #include "raw.h"
 
 namespace oscar {
@@ -16,8 +12,7 @@ namespace {
 
 template <int RT>
 __global__ __launch_bounds__(kThreads) void raw_kernel(const AttnArgs a) {
-  __shared__ __attribute__((aligned(16))) uint8_t smem[finish_lds_bytes<RT>()];
-  raw_block<RT>(a, blockIdx.x, blockIdx.y, blockIdx.z, smem);
+  raw_block<RT>(a, blockIdx.x, blockIdx.y, blockIdx.z);
 }
 
 // Initial prefill: grid (programs, kv heads, 2). Slice 0 is the BF16 branch of each task
@@ -26,9 +21,8 @@ __global__ __launch_bounds__(kThreads) void raw_kernel(const AttnArgs a) {
 // output[num_actual_tokens:].
 template <int RT>
 __global__ __launch_bounds__(kThreads) void prefill_kernel(const AttnArgs a) {
-  __shared__ __attribute__((aligned(16))) uint8_t smem[finish_lds_bytes<RT>()];
   if (blockIdx.z == 0) {
-    raw_block<RT, true>(a, blockIdx.x, blockIdx.y, 0, smem);
+    raw_block<RT, true>(a, blockIdx.x, blockIdx.y, 0);
     return;
   }
   if (blockIdx.y != 0) return;

@@ -617,13 +617,12 @@ __device__ __forceinline__ void history_pair_body(const AttnArgs& a, const Finis
   static_assert(kLayerRingBytes <= kRingBytes, "the layer-step finisher fits the ring");
   static_assert(16 * kStageRowBytes + 4 * 2 * 8 * 16 * 4 <= 2 * kStageBytes,
                 "the layer step's 16-row staging tile and operand images fit wavefront 3's stages");
-  static_assert(finish_lds_bytes<1>() <= kRingBytes && 16 * kHeadDim * 2 <= kRingBytes,
-                "the pre-attention roles fit the ring");
+  static_assert(16 * kHeadDim * 2 <= kRingBytes, "the K/V store role's tile fits the ring");
   if constexpr (kMode == 3) {
     const int z = blockIdx.z;
     if (z < role_slices) {
       if (z == 0) {
-        raw_block<1, false, true>(pre->attn, blockIdx.x, blockIdx.y, 0, s_ring);
+        raw_block<1, false, true>(pre->attn, blockIdx.x, blockIdx.y, 0);
       } else {
         const int r = ((z - 1) * static_cast<int>(gridDim.x) + static_cast<int>(blockIdx.x)) *
                           static_cast<int>(gridDim.y) + static_cast<int>(blockIdx.y);

@@ -1,14 +1,23 @@
 // The BF16 branch of the split-KV attention (sink, recent ring and current tokens), shared by
-// the attention_partials entry point and the fused pre-attention kernel.
+// the attention_partials entry point, the fused pre-attention launch, the history launch's
+// pre-attention roles and (row for row) the initial-prefill kernel.
 //
 // Reference: oscar_ascend/kernels.py:290-482 (`_attention_kernel` with IS_RAW true: raw
 // positions = sink + recent window + causal current tokens, kernels.py:421-470).
 //
-// MI355X design: a workgroup is 4 independent wavefronts on bf16 MFMA
-// (v_mfma_f32_16x16x32_bf16); each owns every 4th 32-token block of the split and keeps its
-// own online-softmax state, merged once through LDS at the end. Scores are computed
-// transposed (S^T = K Q^T), so the MFMA output layout (lane holds 4 consecutive tokens of
-// one query row) is the A-operand layout of the P*V MFMA with no shuffle in between.
+// Row arithmetic (what every path reproduces bit for bit): each query row streams the split's
+// 32-token blocks in order through one online softmax on bf16 MFMA (v_mfma_f32_16x16x32_bf16):
+// scores S^T = K Q^T (16-token tiles, k in eight 32-dim steps), a lazy running max (a row moves
+// its max only when a block's row maximum passes it by 2^8), p = 2^(s - m) packed to bf16, and
+// P*V accumulated in fp32; the row sum is reduced across its four lane groups at the end.
+// Scores come out transposed, so the MFMA output layout (lane holds 4 consecutive tokens of
+// one query row) is the A-operand layout of the P*V MFMA with no shuffle in between. A row's
+// bits depend only on its own query, the keys and values, not on which rows share its tile,
+// its wavefront or its workgroup.
+//
+// Decode workgroup: 4 wavefronts over the same rows and blocks, wavefront w accumulating the
+// 64 output dims 16 n + 4 w + {0..3} (n = lane & 15) of every row; each computes the scores
+// itself (the same bits in every wavefront), so no merge of wavefront states is needed.
 #pragma once
 
 #include "attention.h"
@@ -16,7 +25,7 @@
 namespace oscar {
 
 constexpr float kRescale = 8.0f;  // lazy-max slack, log2 units
-constexpr int kBlock = 32;        // tokens per wavefront iteration
+constexpr int kBlock = 32;        // tokens per block
 
 // Per-lane token of element e of the PV k-group g: 4 consecutive tokens of each 16-token
 // QK tile, matching the transposed-score output layout.
@@ -24,29 +33,33 @@ __device__ __forceinline__ int tau(int g, int e) { return e < 4 ? 4 * g + e : 12
 
 // ---------------------------------------------------------------- softmax state
 
-template <int RT>
+// kTiles P*V accumulator tiles per row tile: tile j of lane (n, g) holds rows 4 g + v, one
+// output dim each (the caller's dim map; 16 tiles: dims 16 n + j).
+template <int RT, int kTiles = 16>
 struct State {
-  float m[RT];      // running max (log2 units) of query row n + 16 rt
-  float psum[RT];   // sum p over this lane's tokens
-  f32x4 o[RT][16];  // PV accumulators: tile j holds dims 16n + j
+  float m[RT];          // running max (log2 units) of query row n + 16 rt
+  float psum[RT];       // sum p over this lane's tokens
+  f32x4 o[RT][kTiles];  // P*V accumulators
 };
 
-template <int RT>
-__device__ __forceinline__ void state_init(State<RT>& st) {
+template <int RT, int kTiles>
+__device__ __forceinline__ void state_init(State<RT, kTiles>& st) {
 #pragma unroll
   for (int rt = 0; rt < RT; ++rt) {
     st.m[rt] = -INFINITY;
     st.psum[rt] = 0.f;
 #pragma unroll
-    for (int t = 0; t < 16; ++t) st.o[rt][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int t = 0; t < kTiles; ++t) st.o[rt][t] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
 }
 
-// Lazy running max. Each lane first checks its own 8 scores against m + 2^8 (no cross-lane
-// traffic); only if some lane of the wavefront sees a larger score is the row max reduced
-// across the 4 lane groups and the accumulators rescaled. Between updates p <= 2^8.
+// Lazy running max, per row. Each lane first checks its own 8 scores of the block against
+// m + 2^8 (no cross-lane traffic); only if some lane of the wavefront sees a larger score are
+// the block's row maxima reduced across the 4 lane groups, and then exactly the rows whose
+// block maximum passes m + 2^8 move m to it and rescale their sum and accumulators (the other
+// rows multiply by exactly 1). Between updates p <= 2^8.
 template <int RT, int kTiles>
-__device__ __forceinline__ void update_max(State<RT>& st, const float (&s2)[RT][8], int g) {
+__device__ __forceinline__ void update_max(State<RT, kTiles>& st, const float (&s2)[RT][8], int g) {
   float lm[RT];
   bool need = false;
 #pragma unroll
@@ -63,8 +76,9 @@ __device__ __forceinline__ void update_max(State<RT>& st, const float (&s2)[RT][
       float v = lm[rt];
       v = fmaxf(v, __shfl_xor(v, 16, kWave));
       v = fmaxf(v, __shfl_xor(v, 32, kWave));
-      const float mn = fmaxf(st.m[rt], v);
-      const float alpha = mn == -INFINITY ? 1.0f : exp2f(st.m[rt] - mn);
+      const float mo = st.m[rt];
+      const float mn = v > mo + kRescale ? v : mo;
+      const float alpha = mn == mo ? 1.0f : (mn == -INFINITY ? 1.0f : exp2f(mo - mn));
       st.m[rt] = mn;
       st.psum[rt] *= alpha;
 #pragma unroll
@@ -77,104 +91,50 @@ __device__ __forceinline__ void update_max(State<RT>& st, const float (&s2)[RT][
   }
 }
 
-// ---------------------------------------------------------------- epilogue
-
-// Merge the 4 wavefront states through LDS and write normalized partials + LSE: per row tile,
-// every wavefront publishes its scaled accumulators at once, then each thread sums one
-// (row, 16 dims) over the four wavefronts in wavefront order.
-template <int RT>
-constexpr int finish_lds_bytes() {
-  return 4 * 16 * kHeadDim * 4 + (2 * 4 + 3) * RT * 16 * 4;
+// The block's scores of row tile rt to log2 units with the causal / range mask, then the
+// lazy max, p, the lane's sum and the bf16 P operand (lane (n, g): row n, tokens tau(g, e)).
+template <int RT, int kTiles>
+__device__ __forceinline__ void block_softmax(State<RT, kTiles>& st, const f32x4 (&sc)[RT][2],
+                                              const bool (&ok)[RT][8], float scale_log2, int g,
+                                              u32x4 (&ap)[RT]) {
+  float s2[RT][8];
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) s2[rt][e] = ok[rt][e] ? sc[rt][e >> 2][e & 3] * scale_log2 : -INFINITY;
+  update_max(st, s2, g);
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt) {
+    float p[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      p[e] = s2[rt][e] == -INFINITY ? 0.f : exp2f(s2[rt][e] - st.m[rt]);
+      st.psum[rt] += p[e];
+    }
+#pragma unroll
+    for (int f = 0; f < 4; ++f) ap[rt][f] = pack_bf16x2(p[2 * f], p[2 * f + 1]);
+  }
 }
 
-// kDirect: the normalized rows go to a.direct_out as bf16 (and the LSE to a.direct_lse): the
-// bits merge_paths gives a row whose history branch is empty.
-template <int RT, bool kDirect = false>
-__device__ void finish(const AttnArgs& a, const Task& t, int head, int split, State<RT>& st,
-                       uint8_t* lds) {
-  typedef float OutWave[16][kHeadDim];
-  OutWave* s_o = reinterpret_cast<OutWave*>(lds);
-  typedef float StatWave[RT * 16];
-  StatWave* s_m = reinterpret_cast<StatWave*>(lds + 4 * 16 * kHeadDim * 4);
-  StatWave* s_p = s_m + 4;
-  float* s_max = reinterpret_cast<float*>(s_p + 4);
-  float* s_den = s_max + RT * 16;
-  float* s_lse = s_den + RT * 16;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int n = lane & 15, g = lane >> 4;
+// B operand of P*V for output dim 16 n + j: the bf16 values of dim j of this lane's eight
+// tokens, as token pairs (vd2[e]: dims 2 d, 2 d + 1 of the lane's dword d = j / 2 of token e).
+__device__ __forceinline__ u32x4 pv_operand(const uint32_t (&vd2)[8], int j) {
+  const uint32_t sel = (j & 1) ? 0x07060302u : 0x05040100u;
+  u32x4 bv;
 #pragma unroll
-  for (int rt = 0; rt < RT; ++rt) {
-    st.psum[rt] += __shfl_xor(st.psum[rt], 16, kWave);
-    st.psum[rt] += __shfl_xor(st.psum[rt], 32, kWave);
-    if (g == 0) {
-      s_m[wave][n + 16 * rt] = st.m[rt];
-      s_p[wave][n + 16 * rt] = st.psum[rt];
-    }
-  }
-  __syncthreads();
-  if (threadIdx.x < RT * 16) {
-    const int row = threadIdx.x;
-    float mx = -INFINITY;
-#pragma unroll
-    for (int w = 0; w < 4; ++w) mx = fmaxf(mx, s_m[w][row]);
-    float den = 0.f;
-#pragma unroll
-    for (int w = 0; w < 4; ++w)
-      if (s_m[w][row] != -INFINITY) den += exp2f(s_m[w][row] - mx) * s_p[w][row];
-    s_max[row] = mx;
-    s_den[row] = den;
-    s_lse[row] = den > 0.f ? (mx + log2f(den)) * kLn2 : -INFINITY;
-  }
-  __syncthreads();
-#pragma unroll
-  for (int rt = 0; rt < RT; ++rt) {
-    if (rt > 0) __syncthreads();  // the previous tile's sums have been read
-    // Lane (g, n) holds dims 16n + tile of rows 4g + v.
-#pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      const int row = 16 * rt + 4 * g + v;
-      const float mw = s_m[wave][row];
-      const float f = mw == -INFINITY ? 0.f : exp2f(mw - s_max[row]);
-#pragma unroll
-      for (int c = 0; c < 4; ++c)
-        *reinterpret_cast<f32x4*>(&s_o[wave][4 * g + v][16 * n + 4 * c]) =
-            f32x4{st.o[rt][4 * c][v] * f, st.o[rt][4 * c + 1][v] * f, st.o[rt][4 * c + 2][v] * f,
-                  st.o[rt][4 * c + 3][v] * f};
-    }
-    __syncthreads();
-    const int row16 = threadIdx.x >> 4, dq = threadIdx.x & 15;
-    const int row = 16 * rt + row16;
-    const RowInfo ri = row_info(a, t, head, row);
-    if (ri.valid) {
-      const float den = fmaxf(s_den[row], 1.0e-30f);
-      const int64_t orow = (ri.token * a.hq + ri.qhead) * a.splits + split;
-#pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        const int d = 16 * dq + 4 * c;
-        const f32x4 sum = *reinterpret_cast<const f32x4*>(&s_o[0][row16][d]) +
-                          *reinterpret_cast<const f32x4*>(&s_o[1][row16][d]) +
-                          *reinterpret_cast<const f32x4*>(&s_o[2][row16][d]) +
-                          *reinterpret_cast<const f32x4*>(&s_o[3][row16][d]);
-        if constexpr (kDirect) {
-          const int64_t out_row = ri.token * a.hq + ri.qhead;
-          *reinterpret_cast<uint2*>(a.direct_out + out_row * kHeadDim + d) =
-              make_uint2(pack_bf16x2(sum[0] / den, sum[1] / den),
-                         pack_bf16x2(sum[2] / den, sum[3] / den));
-        } else {
-          *reinterpret_cast<float4*>(a.partials + orow * kHeadDim + d) =
-              make_float4(sum[0] / den, sum[1] / den, sum[2] / den, sum[3] / den);
-        }
-      }
-    }
-  }
-  if (threadIdx.x < RT * 16) {
-    const RowInfo ri = row_info(a, t, head, threadIdx.x);
-    if constexpr (kDirect) {
-      if (ri.valid && a.direct_lse) a.direct_lse[ri.token * a.hq + ri.qhead] = s_lse[threadIdx.x];
-    } else {
-      if (ri.valid) a.lse[(ri.token * a.hq + ri.qhead) * a.splits + split] = s_lse[threadIdx.x];
-    }
-  }
+  for (int f = 0; f < 4; ++f) bv[f] = __builtin_amdgcn_perm(vd2[2 * f + 1], vd2[2 * f], sel);
+  return bv;
+}
+
+// The row's normalizer and natural-log LSE from the lane's sum (all 4 lane groups of row n
+// hold the full sum after the reduction) and max.
+__device__ __forceinline__ float row_sum(float psum) {
+  psum += __shfl_xor(psum, 16, kWave);
+  psum += __shfl_xor(psum, 32, kWave);
+  return psum;
+}
+__device__ __forceinline__ float row_lse(float mx, float den) {
+  return den > 0.f ? (mx + log2f(den)) * kLn2 : -INFINITY;
 }
 
 // ---------------------------------------------------------------- raw (BF16) branch
@@ -209,15 +169,8 @@ __device__ __forceinline__ const uint16_t* raw_token(const AttnArgs& a, const Ta
   return a.window + off;
 }
 
-// K rows of the block's two 16-token score tiles (A operands) and V rows of this lane's eight
-// tokens (B operands of P*V), with the positions that mask them.
-struct RawBlock {
-  u32x4 kd[2][8];
-  u32x4 vd[8][2];
-  int pos[8];
-  bool live[8];
-};
-
+// K rows of the block's two 16-token score tiles (A operands: lane (n, g), k-step m holds dims
+// 64 g + 8 m .. + 7 of token 16 tt + n).
 __device__ __forceinline__ void raw_load_k(const AttnArgs& a, const Task& t, const RawTask& r,
                                            int head, int t0, int end, int g, int n,
                                            u32x4 (&kd)[2][8]) {
@@ -233,9 +186,11 @@ __device__ __forceinline__ void raw_load_k(const AttnArgs& a, const Task& t, con
                          : u32x4{0u, 0u, 0u, 0u};
 }
 
+// V dims 16 n + 4 w .. + 3 of this lane's eight tokens (two dwords each), with the positions
+// that mask them.
 __device__ __forceinline__ void raw_load_v(const AttnArgs& a, const Task& t, const RawTask& r,
-                                           int head, int t0, int end, int g, int n,
-                                           u32x4 (&vd)[8][2], int (&pos)[8], bool (&live)[8]) {
+                                           int head, int t0, int end, int g, int n, int w,
+                                           uint2 (&vq)[8], int (&pos)[8], bool (&live)[8]) {
   const uint16_t* vp[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
@@ -243,28 +198,24 @@ __device__ __forceinline__ void raw_load_v(const AttnArgs& a, const Task& t, con
     live[e] = vp[e] != nullptr;
   }
 #pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    vd[e][0] = vp[e] ? *reinterpret_cast<const u32x4*>(vp[e] + 16 * n) : u32x4{0u, 0u, 0u, 0u};
-    vd[e][1] = vp[e] ? *reinterpret_cast<const u32x4*>(vp[e] + 16 * n + 8)
-                     : u32x4{0u, 0u, 0u, 0u};
-  }
+  for (int e = 0; e < 8; ++e)
+    vq[e] = vp[e] ? *reinterpret_cast<const uint2*>(vp[e] + 16 * n + 4 * w) : make_uint2(0u, 0u);
 }
 
-__device__ __forceinline__ void raw_load_block(const AttnArgs& a, const Task& t, const RawTask& r,
-                                               int head, int t0, int end, int g, int n,
-                                               RawBlock& b) {
-  raw_load_k(a, t, r, head, t0, end, g, n, b.kd);
-  raw_load_v(a, t, r, head, t0, end, g, n, b.vd, b.pos, b.live);
-}
+struct RawBlock {
+  u32x4 kd[2][8];
+  uint2 vq[8];
+  int pos[8];
+  bool live[8];
+};
 
-// One workgroup of the BF16 branch: (task, kv head, split).
-// `smem`: finish_lds_bytes<RT>() bytes of 16-byte aligned LDS. kLean: the block's K rows are
-// loaded, scored, and only then its V rows (no prefetch; fewer registers, for a workgroup
-// role inside a launch whose other roles need two workgroups per CU). Same arithmetic, same
-// bits as the prefetching form.
+// One workgroup of the BF16 branch: (task, kv head, split). Wavefront w writes output dims
+// 16 n + 4 w .. + 3 of every row. kDirect: the normalized rows go to a.direct_out as bf16 (and
+// the LSE to a.direct_lse): the bits merge_paths gives a row whose history branch is empty.
+// kLean: the block's K rows are loaded and scored before its V rows, with no prefetch (fewer
+// registers, for a role inside a launch that must keep two workgroups per CU); same bits.
 template <int RT, bool kDirect = false, bool kLean = false>
-__device__ __forceinline__ void raw_block(const AttnArgs& a, int task, int head, int split,
-                                          uint8_t* smem) {
+__device__ __forceinline__ void raw_block(const AttnArgs& a, int task, int head, int split) {
   Task t;
   if (!read_task(a, t, task)) return;
   // The owner page (block-table column 0) is requested together with the request's
@@ -299,22 +250,26 @@ __device__ __forceinline__ void raw_block(const AttnArgs& a, int task, int head,
       for (int m = 0; m < 8; ++m) qb[rt][m] = *reinterpret_cast<const u32x4*>(qp + 8 * m);
     }
   }
-  State<RT> st;
+  State<RT, 4> st;
   state_init(st);
 
-  // A wavefront's blocks are t0 = begin + 32 w, + 128, ...; the K/V rows of the next block
-  // are requested before the current block is computed, so a wavefront with two blocks (a
-  // decode step's 133 BF16 tokens over four wavefronts) still waits one memory round trip.
-  // (Two row tiles (RT = 2) leave no registers for the second block: loaded in turn.)
+  // The K/V rows of the next block are requested before the current block is computed
+  // (kLean: none; two row tiles: none, for registers).
   constexpr bool kPrefetch = RT == 1 && !kLean;
   RawBlock cur, nxt;
-  int t0 = begin + kBlock * wave;
-  if (kPrefetch && t0 < end) raw_load_block(a, t, r, head, t0, end, g, n, cur);
-  for (; t0 < end; t0 += 4 * kBlock) {
-    const bool more = kPrefetch && t0 + 4 * kBlock < end;
-    if (more) raw_load_block(a, t, r, head, t0 + 4 * kBlock, end, g, n, nxt);
-    if (!kPrefetch && !kLean) raw_load_block(a, t, r, head, t0, end, g, n, cur);
-    if (kLean) raw_load_k(a, t, r, head, t0, end, g, n, cur.kd);
+  int t0 = begin;
+  if (kPrefetch && t0 < end) {
+    raw_load_k(a, t, r, head, t0, end, g, n, cur.kd);
+    raw_load_v(a, t, r, head, t0, end, g, n, wave, cur.vq, cur.pos, cur.live);
+  }
+  for (; t0 < end; t0 += kBlock) {
+    const bool more = kPrefetch && t0 + kBlock < end;
+    if (more) {
+      raw_load_k(a, t, r, head, t0 + kBlock, end, g, n, nxt.kd);
+      raw_load_v(a, t, r, head, t0 + kBlock, end, g, n, wave, nxt.vq, nxt.pos, nxt.live);
+    }
+    if (!kPrefetch) raw_load_k(a, t, r, head, t0, end, g, n, cur.kd);
+    if (!kPrefetch && !kLean) raw_load_v(a, t, r, head, t0, end, g, n, wave, cur.vq, cur.pos, cur.live);
     f32x4 sc[RT][2];
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt)
@@ -327,42 +282,58 @@ __device__ __forceinline__ void raw_block(const AttnArgs& a, int task, int head,
 #pragma unroll
         for (int rt = 0; rt < RT; ++rt)
           sc[rt][tt] = mfma16x16x32(cur.kd[tt][m], qb[rt][m], sc[rt][tt]);
-    if (kLean) raw_load_v(a, t, r, head, t0, end, g, n, cur.vd, cur.pos, cur.live);
-    float s2[RT][8];
+    if (kLean) raw_load_v(a, t, r, head, t0, end, g, n, wave, cur.vq, cur.pos, cur.live);
+    bool ok[RT][8];
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const bool ok = cur.live[e] && cur.pos[e] <= t.prefix + qi_row[rt];
-        s2[rt][e] = ok ? sc[rt][e >> 2][e & 3] * a.scale_log2 : -INFINITY;
-      }
-    update_max<RT, 16>(st, s2, g);
+      for (int e = 0; e < 8; ++e) ok[rt][e] = cur.live[e] && cur.pos[e] <= t.prefix + qi_row[rt];
     u32x4 ap[RT];
+    block_softmax(st, sc, ok, a.scale_log2, g, ap);
 #pragma unroll
-    for (int rt = 0; rt < RT; ++rt) {
-      float p[8];
+    for (int jj = 0; jj < 4; ++jj) {
+      uint32_t vd2[8];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        p[e] = s2[rt][e] == -INFINITY ? 0.f : exp2f(s2[rt][e] - st.m[rt]);
-        st.psum[rt] += p[e];
-      }
+      for (int e = 0; e < 8; ++e) vd2[e] = (jj >> 1) ? cur.vq[e].y : cur.vq[e].x;
+      const u32x4 bv = pv_operand(vd2, jj);
 #pragma unroll
-      for (int f = 0; f < 4; ++f) ap[rt][f] = pack_bf16x2(p[2 * f], p[2 * f + 1]);
-    }
-#pragma unroll
-    for (int tile = 0; tile < 16; ++tile) {
-      const uint32_t sel = (tile & 1) ? 0x07060302u : 0x05040100u;
-      u32x4 bv;
-#pragma unroll
-      for (int f = 0; f < 4; ++f)
-        bv[f] = __builtin_amdgcn_perm(cur.vd[2 * f + 1][tile >> 3][(tile & 7) >> 1],
-                                      cur.vd[2 * f][tile >> 3][(tile & 7) >> 1], sel);
-#pragma unroll
-      for (int rt = 0; rt < RT; ++rt) st.o[rt][tile] = mfma16x16x32(ap[rt], bv, st.o[rt][tile]);
+      for (int rt = 0; rt < RT; ++rt) st.o[rt][jj] = mfma16x16x32(ap[rt], bv, st.o[rt][jj]);
     }
     if (more) cur = nxt;
   }
-  finish<RT, kDirect>(a, t, head, split, st, smem);
+  // Normalize: lane (n, g) holds rows 4 g + v, dims 16 n + 4 wave + jj.
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt) {
+    const float den_n = row_sum(st.psum[rt]);
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int row = 16 * rt + 4 * g + v;
+      const float den = fmaxf(__shfl(den_n, 4 * g + v, kWave), 1.0e-30f);
+      const RowInfo ri = row_info(a, t, head, row);
+      if (!ri.valid) continue;
+      const int d = 16 * n + 4 * wave;
+      const float o0 = st.o[rt][0][v] / den, o1 = st.o[rt][1][v] / den;
+      const float o2 = st.o[rt][2][v] / den, o3 = st.o[rt][3][v] / den;
+      if constexpr (kDirect) {
+        const int64_t out_row = ri.token * a.hq + ri.qhead;
+        *reinterpret_cast<uint2*>(a.direct_out + out_row * kHeadDim + d) =
+            make_uint2(pack_bf16x2(o0, o1), pack_bf16x2(o2, o3));
+      } else {
+        const int64_t orow = (ri.token * a.hq + ri.qhead) * a.splits + split;
+        *reinterpret_cast<float4*>(a.partials + orow * kHeadDim + d) = make_float4(o0, o1, o2, o3);
+      }
+    }
+    // LSE of row n (wavefront 0, lane group 0).
+    if (wave == 0 && g == 0) {
+      const RowInfo ri = row_info(a, t, head, n + 16 * rt);
+      const float lse = row_lse(st.m[rt], den_n);
+      if constexpr (kDirect) {
+        if (ri.valid && a.direct_lse) a.direct_lse[ri.token * a.hq + ri.qhead] = lse;
+      } else {
+        if (ri.valid) a.lse[(ri.token * a.hq + ri.qhead) * a.splits + split] = lse;
+      }
+    }
+  }
 }
 
 }  // namespace oscar

@@ -29,16 +29,14 @@ constexpr int kPostQuarterRows = 2;  // rows per column-quarter post-attention w
 
 template <int RT>
 __global__ __launch_bounds__(kThreads) void pre_attention_kernel(const PreArgs p) {
-  constexpr int kRawLds = finish_lds_bytes<RT>();
-  constexpr int kTileLds = 16 * kHeadDim * 2;
-  __shared__ __attribute__((aligned(16))) uint8_t smem[kRawLds > kTileLds ? kRawLds : kTileLds];
+  __shared__ __attribute__((aligned(16))) uint8_t smem[16 * kHeadDim * 2];  // K/V rotation tile
   const int bid = blockIdx.x;
   const AttnArgs& a = p.attn;
   if (bid < p.raw_wgs) {
     // BF16 branch: workgroup (task, kv head), one split.
     const int h = a.L.kv_heads;
     const int task = bid / h, head = bid - task * h;
-    raw_block<RT>(a, task, head, 0, smem);
+    raw_block<RT>(a, task, head, 0);
     return;
   }
   if (bid < p.raw_wgs + p.kv_wgs) {
