@@ -248,23 +248,23 @@ int oscar_post_attention(const float* history_partials, const float* history_lse
 /*
  * prefill_attention -- initial prefill (every request's history empty): replaces the
  * reference's fused-infer call (oscar_ascend/backend.py:175-193: causal attention of each
- * request over its own current tokens, output rows past num_actual_tokens zeroed). It runs
- * the BF16 branch of oscar_attention_partials (raw, one split) and writes its rows straight
- * to output (bf16 [n, hq*256], 16-byte aligned) with the bits merge_splits + rotate +
- * merge_paths give a row whose history branch is empty; merged_lse (optional) gets the LSE.
- * Rows of tokens at or past counts[1] are zeroed (LSE -inf). Arguments as
- * oscar_attention_partials; key/value rows contiguous and 16-byte aligned.
+ * request over its own current tokens, output rows past num_actual_tokens zeroed). A flash
+ * kernel: 128 (query, head) rows per workgroup share each 32-token K/V block through LDS. Each
+ * row has the bits the BF16 branch of oscar_attention_partials (raw, one split) followed by
+ * merge_splits + rotate + merge_paths gives a row whose history branch is empty; output: bf16
+ * [n, hq*256] (16-byte aligned), merged_lse (optional): fp32 [n, hq]. query: bf16 [n][hq][256],
+ * key/value: bf16 [n][kv_heads][256] (row strides in elements, multiples of 8; rows 16-byte
+ * aligned). qstarts [max_reqs + 1], seq_lens [max_reqs], counts [2] (live requests, tokens) as
+ * for the other entry points; max_query_len: host bound on query tokens per request (0 =
+ * unknown: n). Rows of tokens at or past counts[1] are zeroed (LSE -inf). A request whose
+ * seq_len differs from its query tokens has history and is not served: its rows are NaN.
  */
 int oscar_prefill_attention(const void* query, int64_t q_s0, int64_t q_s1, const void* key,
                             int64_t k_s0, int64_t k_s1, const void* value, int64_t v_s0,
-                            int64_t v_s1, const void* window, int64_t window_elems,
-                            const int32_t* qstarts, const int32_t* seq_lens,
-                            const int32_t* block_tables, int64_t table_stride,
-                            int64_t table_columns, const int32_t* counts, const int32_t* tasks,
-                            const int32_t* task_count, int64_t n, int64_t hq, int64_t programs,
-                            int32_t block_n, int32_t query_tile, int32_t max_query_len,
-                            float scale, const oscar_layout* layout, void* output,
-                            float* merged_lse, void* stream);
+                            int64_t v_s1, const int32_t* qstarts, const int32_t* seq_lens,
+                            const int32_t* counts, int64_t n, int64_t hq, int64_t max_reqs,
+                            int32_t max_query_len, float scale, const oscar_layout* layout,
+                            void* output, float* merged_lse, void* stream);
 
 /*
  * history_pre -- the history branch (oscar_attention_partials with raw = 0) and the BF16 branch

@@ -93,10 +93,8 @@ SIGNATURES = {
     ],
     "oscar_prefill_attention": [
         _P, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64,  # query, key, value (+ row strides)
-        _P, _I64,  # window
-        _P, _P, _P, _I64, _I64,  # qstarts, seq_lens, block_tables, stride, columns
-        _P, _P, _P,  # counts, tasks, task_count
-        _I64, _I64, _I64, _I32, _I32, _I32, _F,  # n hq programs bn qt mql scale
+        _P, _P, _P,  # qstarts, seq_lens, counts
+        _I64, _I64, _I64, _I32, _F,  # n, hq, max_reqs, max_query_len, scale
         POINTER(OscarLayout), _P, _P, _P,  # layout, output, merged_lse, stream
     ],
     "oscar_history_post": [

@@ -15,26 +15,6 @@ __global__ __launch_bounds__(kThreads) void raw_kernel(const AttnArgs a) {
   raw_block<RT>(a, blockIdx.x, blockIdx.y, blockIdx.z);
 }
 
-// Initial prefill: grid (programs, kv heads, 2). Slice 0 is the BF16 branch of each task
-// written straight to the output (the request's own tokens, causal); slice 1 clears the rows
-// of tokens x, x + programs, ... at or past the token count (head 0), as the reference zeroes
-// output[num_actual_tokens:].
-template <int RT>
-__global__ __launch_bounds__(kThreads) void prefill_kernel(const AttnArgs a) {
-  if (blockIdx.z == 0) {
-    raw_block<RT, true>(a, blockIdx.x, blockIdx.y, 0);
-    return;
-  }
-  if (blockIdx.y != 0) return;
-  const int active = a.counts[1];
-  for (int64_t tok = blockIdx.x; tok < a.n; tok += gridDim.x) {
-    if (tok < active) continue;
-    uint16_t* out = a.direct_out + tok * a.hq * kHeadDim;
-    for (int e = threadIdx.x; e < a.hq * kHeadDim; e += kThreads) out[e] = 0;
-    if (a.direct_lse && threadIdx.x < a.hq) a.direct_lse[tok * a.hq + threadIdx.x] = -INFINITY;
-  }
-}
-
 }  // namespace
 }  // namespace oscar
 
@@ -154,35 +134,3 @@ extern "C" int oscar_attention_partials(
   return static_cast<int>(hipGetLastError());
 }
 
-extern "C" int oscar_prefill_attention(
-    const void* query, int64_t q_s0, int64_t q_s1, const void* key, int64_t k_s0, int64_t k_s1,
-    const void* value, int64_t v_s0, int64_t v_s1, const void* window, int64_t window_elems,
-    const int32_t* qstarts, const int32_t* seq_lens, const int32_t* block_tables,
-    int64_t table_stride, int64_t table_columns, const int32_t* counts, const int32_t* tasks,
-    const int32_t* task_count, int64_t n, int64_t hq, int64_t programs, int32_t block_n,
-    int32_t query_tile, int32_t max_query_len, float scale, const oscar_layout* layout,
-    void* output, float* merged_lse, void* stream) {
-  using namespace oscar;
-  if (n > 0 && !output) return OSCAR_E_NULL;
-  if (reinterpret_cast<uintptr_t>(output) % 16) return OSCAR_E_ALIGN;
-  AttnArgs a;
-  int64_t qrows = 0;
-  // The output doubles as the (unused) partial buffer of the argument checks.
-  float* out_f = static_cast<float*>(output);
-  const int st = make_attn_args(query, q_s0, q_s1, 1, key, k_s0, k_s1, 1, value, v_s0, v_s1, 1,
-                                nullptr, 0, window, window_elems, qstarts, seq_lens, block_tables,
-                                table_stride, table_columns, counts, tasks, task_count, n, hq,
-                                programs, 1, block_n, query_tile, max_query_len, scale, 1, 0,
-                                layout, out_f, out_f, &a, &qrows);
-  if (st != OSCAR_OK || n == 0) return st;
-  if (!(scale > 0.f) || !(scale < INFINITY)) return OSCAR_E_UNSUPPORTED;
-  a.direct_out = static_cast<uint16_t*>(output);
-  a.direct_lse = merged_lse;
-  const dim3 grid(static_cast<unsigned>(programs), static_cast<unsigned>(a.L.kv_heads), 2);
-  hipStream_t s = as_stream(stream);
-  if (qrows <= 16)
-    hipLaunchKernelGGL(prefill_kernel<1>, grid, dim3(kThreads), 0, s, a);
-  else
-    hipLaunchKernelGGL(prefill_kernel<2>, grid, dim3(kThreads), 0, s, a);
-  return static_cast<int>(hipGetLastError());
-}

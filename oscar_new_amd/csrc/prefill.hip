@@ -1,0 +1,285 @@
+// Initial prefill: causal attention of each request over its own tokens (no history), the
+// replacement of the reference's fused-infer call (oscar_ascend/backend.py:175-193).
+//
+// Flash layout for MI355X: a workgroup serves 128 consecutive (query, head) rows of one request
+// and one KV head (wavefront w: row tiles 2 w, 2 w + 1 of 16 rows, all 256 output dims) and
+// streams the request's keys and values in 32-token blocks that its four wavefronts share:
+// each block is copied into LDS once by direct-to-LDS loads (two stages, the next block in
+// flight while the current one is computed), so the K/V bytes a workgroup reads serve all of
+// its 128 rows. The arithmetic of every row is the BF16 branch's (raw.h: the same MFMA
+// operands and k order, the same lazy max, p, sums and normalization), so the output, the LSE
+// and the bits are those of the decode path (attention_partials raw + merges) for a request
+// without history. Blocks past a workgroup's last query are not read (they are masked for
+// every row). Workgroups run the longest spans (the last rows of a request) first. Requests
+// with cached tokens (seq_len != query tokens) are not initial prefills: their rows are
+// written as NaN (output and LSE), never silently wrong.
+#include "dma.h"
+#include "raw.h"
+
+namespace oscar {
+namespace {
+
+constexpr int kPrefillRT = 2;                        // row tiles per wavefront
+constexpr int kSpanRows = 4 * 16 * kPrefillRT;       // 128 rows per workgroup
+constexpr int kRowBytes = kHeadDim * 2;              // 512 bytes per K or V row
+constexpr int kBlockBytes = kBlock * kRowBytes;      // 16 KiB per K or V block
+constexpr int kStageBytesP = 2 * kBlockBytes;        // K then V
+constexpr int kDmaPerWave = kStageBytesP / 1024 / 4;  // 1 KiB per DMA, 8 per wavefront
+
+// LDS position of 16-byte chunk c of block row t: chunks are XOR-swizzled by the row's low four
+// bits, so that the 16 lanes of a K read (16 rows, one chunk) and of a V read (one row, 16
+// chunk pairs) each touch 16 different bank groups.
+__device__ __forceinline__ uint32_t chunk_pos(int t, int c) { return c ^ (t & 15); }
+
+struct PrefillArgs {
+  const uint16_t* query;
+  int64_t qs0, qs1;
+  const uint16_t* key;
+  int64_t ks0, ks1;
+  const uint16_t* value;
+  int64_t vs0, vs1;
+  const int32_t* qstarts;
+  const int32_t* seq_lens;
+  const int32_t* counts;
+  int64_t n;
+  int32_t g, hq, kv_heads;
+  FastDiv g_div;
+  float scale_log2;
+  uint16_t* out;
+  float* lse;
+};
+
+// Copies block b of (K, V) rows into `stage`: wavefront w issues DMAs 8 w .. 8 w + 7, DMA i
+// covering K (i < 16) or V rows 2 (i mod 16), + 1. Lane l writes row t = 2 (i mod 16) + l / 32
+// at position l mod 32, fetching the chunk chunk_pos maps there. Every lane issues its copy
+// (the stage waits count 8 DMAs per wavefront): rows at or past the request's token count copy
+// its last row instead; they are masked for every query row, so their p is exactly 0 and their
+// products add exact zeros, as the decode path's zero rows do.
+__device__ __forceinline__ void prefill_copy_block(const PrefillArgs& a, int64_t qstart, int qlen,
+                                                   int head, int b, uint8_t* stage) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+  for (int k = 0; k < kDmaPerWave; ++k) {
+    const int i = kDmaPerWave * wave + k;
+    const int is_v = i >> 4;
+    const int t = 2 * (i & 15) + (lane >> 5);
+    const int key = min(kBlock * b + t, qlen - 1);
+    const int c = static_cast<int>(chunk_pos(t, lane & 31));
+    const uint16_t* row = is_v ? a.value + (qstart + key) * a.vs0 + head * a.vs1
+                               : a.key + (qstart + key) * a.ks0 + head * a.ks1;
+    dma_dwordx4(row + 8 * c, lds_addr(stage + is_v * kBlockBytes + (i & 15) * 1024));
+  }
+}
+
+__global__ __launch_bounds__(kThreads) void prefill_flash_kernel(const PrefillArgs a) {
+  __shared__ __attribute__((aligned(16))) uint8_t s_kv[2][kStageBytesP];
+  const int req = blockIdx.y, head = blockIdx.z;
+  const int span = static_cast<int>(gridDim.x) - 1 - static_cast<int>(blockIdx.x);
+  if (req >= a.counts[0]) return;
+  const int64_t qstart = a.qstarts[req];
+  const int64_t qend = min(static_cast<int64_t>(a.qstarts[req + 1]),
+                           static_cast<int64_t>(a.counts[1]));
+  const int qlen = static_cast<int>(qend - qstart);
+  if (qlen <= 0) return;
+  const int rows_req = qlen * a.g;
+  const int row0 = span * kSpanRows;
+  if (row0 >= rows_req) return;
+  const int row_end = min(row0 + kSpanRows, rows_req);
+  const bool history = a.seq_lens[req] != qlen;  // not an initial prefill: rows are NaN
+  const int q_last = static_cast<int>(fastdiv(static_cast<uint32_t>(row_end - 1), a.g_div));
+  const int nblk = history ? 0 : q_last / kBlock + 1;
+  const int lane = threadIdx.x & 63;
+  const int wave = uniform(threadIdx.x >> 6);
+  const int n = lane & 15, g = lane >> 4;
+
+  if (nblk > 0) prefill_copy_block(a, qstart, qlen, head, 0, s_kv[0]);
+
+  // Query rows of this wavefront's tiles: row16 = row0 + 16 (2 w + rt) + n.
+  u32x4 qb[kPrefillRT][8];
+  int qi_row[kPrefillRT];
+#pragma unroll
+  for (int rt = 0; rt < kPrefillRT; ++rt) {
+    const int row = row0 + 16 * (kPrefillRT * wave + rt) + n;
+    const int qi = static_cast<int>(fastdiv(static_cast<uint32_t>(row), a.g_div));
+    qi_row[rt] = row < row_end ? qi : -1;
+#pragma unroll
+    for (int m = 0; m < 8; ++m) qb[rt][m] = u32x4{0u, 0u, 0u, 0u};
+    if (row < row_end) {
+      const int qhead = head * a.g + (row - qi * a.g);
+      const uint16_t* qp = a.query + (qstart + qi) * a.qs0 + qhead * a.qs1 + 64 * g;
+#pragma unroll
+      for (int m = 0; m < 8; ++m) qb[rt][m] = *reinterpret_cast<const u32x4*>(qp + 8 * m);
+    }
+  }
+  State<kPrefillRT, 16> st;
+  state_init(st);
+
+  for (int b = 0; b < nblk; ++b) {
+    const uint8_t* stage = s_kv[b & 1];
+    if (b + 1 < nblk) {
+      prefill_copy_block(a, qstart, qlen, head, b + 1, s_kv[(b + 1) & 1]);
+      OSCAR_WAIT_VM(kDmaPerWave);
+    } else {
+      OSCAR_WAIT_VM(0);
+    }
+    barrier_lds();  // block b landed (every wavefront's copies)
+    // Scores: A = K rows 16 tt + n, chunk 8 g + m.
+    f32x4 sc[kPrefillRT][2];
+#pragma unroll
+    for (int rt = 0; rt < kPrefillRT; ++rt)
+#pragma unroll
+      for (int tt = 0; tt < 2; ++tt) sc[rt][tt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int m = 0; m < 8; ++m) {
+#pragma unroll
+      for (int tt = 0; tt < 2; ++tt) {
+        const int t = 16 * tt + n;
+        const u32x4 kd = *reinterpret_cast<const u32x4*>(
+            stage + t * kRowBytes + 16 * chunk_pos(t, 8 * g + m));
+#pragma unroll
+        for (int rt = 0; rt < kPrefillRT; ++rt) sc[rt][tt] = mfma16x16x32(kd, qb[rt][m], sc[rt][tt]);
+      }
+    }
+    bool ok[kPrefillRT][8];
+#pragma unroll
+    for (int rt = 0; rt < kPrefillRT; ++rt)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int key = kBlock * b + tau(g, e);
+        ok[rt][e] = key < qlen && key <= qi_row[rt];
+      }
+    u32x4 ap[kPrefillRT];
+    block_softmax(st, sc, ok, a.scale_log2, g, ap);
+    // P*V: V dims 16 n .. 16 n + 15 of this lane's tokens, in two 8-dim halves.
+    const uint8_t* vst = stage + kBlockBytes;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      u32x4 vd[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int t = tau(g, e);
+        vd[e] = *reinterpret_cast<const u32x4*>(vst + t * kRowBytes + 16 * chunk_pos(t, 2 * n + h));
+      }
+#pragma unroll
+      for (int j8 = 0; j8 < 8; ++j8) {
+        const int j = 8 * h + j8;
+        uint32_t vd2[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) vd2[e] = vd[e][j8 >> 1];
+        const u32x4 bv = pv_operand(vd2, j);
+#pragma unroll
+        for (int rt = 0; rt < kPrefillRT; ++rt) st.o[rt][j] = mfma16x16x32(ap[rt], bv, st.o[rt][j]);
+      }
+    }
+    barrier_lds();  // every wavefront is done with this stage before it is refilled
+  }
+
+  // Normalize and store: lane (n, g) holds rows 4 g + v of each tile, dims 16 n + j.
+#pragma unroll
+  for (int rt = 0; rt < kPrefillRT; ++rt) {
+    const float den_n = row_sum(st.psum[rt]);
+    const int tile_row = row0 + 16 * (kPrefillRT * wave + rt);
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int row = tile_row + 4 * g + v;
+      const float den = fmaxf(__shfl(den_n, 4 * g + v, kWave), 1.0e-30f);
+      if (row >= row_end) continue;
+      const int qi = static_cast<int>(fastdiv(static_cast<uint32_t>(row), a.g_div));
+      const int qhead = head * a.g + (row - qi * a.g);
+      uint32_t w[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k)
+        w[k] = history ? 0x7fc07fc0u
+                       : pack_bf16x2(st.o[rt][2 * k][v] / den, st.o[rt][2 * k + 1][v] / den);
+      uint16_t* dst = a.out + ((qstart + qi) * a.hq + qhead) * kHeadDim + 16 * n;
+      *reinterpret_cast<u32x4*>(dst) = u32x4{w[0], w[1], w[2], w[3]};
+      *reinterpret_cast<u32x4*>(dst + 8) = u32x4{w[4], w[5], w[6], w[7]};
+    }
+    if (g == 0 && a.lse) {
+      const int row = tile_row + n;
+      if (row < row_end) {
+        const int qi = static_cast<int>(fastdiv(static_cast<uint32_t>(row), a.g_div));
+        const int qhead = head * a.g + (row - qi * a.g);
+        a.lse[(qstart + qi) * a.hq + qhead] = history ? NAN : row_lse(st.m[rt], den_n);
+      }
+    }
+  }
+}
+
+// Rows of tokens at or past counts[1]: zero output, LSE -inf (the reference zeroes
+// output[num_actual_tokens:]).
+__global__ __launch_bounds__(kThreads) void prefill_clear_kernel(const PrefillArgs a) {
+  const int64_t active = a.counts[1];
+  const int64_t total = a.n * a.hq;
+  for (int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6); row < total;
+       row += static_cast<int64_t>(gridDim.x) * 4) {
+    if (row / a.hq < active) continue;
+    const int lane = threadIdx.x & 63;
+    *reinterpret_cast<uint2*>(a.out + row * kHeadDim + 4 * lane) = make_uint2(0u, 0u);
+    if (a.lse && lane == 0) a.lse[row] = -INFINITY;
+  }
+}
+
+bool aligned16(const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; }
+
+}  // namespace
+}  // namespace oscar
+
+extern "C" int oscar_prefill_attention(
+    const void* query, int64_t q_s0, int64_t q_s1, const void* key, int64_t k_s0, int64_t k_s1,
+    const void* value, int64_t v_s0, int64_t v_s1, const int32_t* qstarts,
+    const int32_t* seq_lens, const int32_t* counts, int64_t n, int64_t hq, int64_t max_reqs,
+    int32_t max_query_len, float scale, const oscar_layout* layout, void* output,
+    float* merged_lse, void* stream) {
+  using namespace oscar;
+  Layout L;
+  const int st = make_layout(layout, &L);
+  if (st != OSCAR_OK) return st;
+  const int64_t h = L.kv_heads;
+  if (n < 0 || hq <= 0 || hq % h || max_reqs < 1 || max_reqs > 65535 || max_query_len < 0 ||
+      n * hq > 0x7fffffffll)
+    return OSCAR_E_SHAPE;
+  if (!(scale > 0.f) || !(scale < INFINITY)) return OSCAR_E_UNSUPPORTED;
+  if (n == 0) return OSCAR_OK;
+  if (!query || !key || !value || !qstarts || !seq_lens || !counts || !output) return OSCAR_E_NULL;
+  if (q_s0 % 8 || q_s1 % 8 || k_s0 % 8 || k_s1 % 8 || v_s0 % 8 || v_s1 % 8 || !aligned16(query) ||
+      !aligned16(key) || !aligned16(value) || !aligned16(output))
+    return OSCAR_E_ALIGN;
+  const int64_t g = hq / h;
+  PrefillArgs a{};
+  a.query = static_cast<const uint16_t*>(query);
+  a.qs0 = q_s0;
+  a.qs1 = q_s1;
+  a.key = static_cast<const uint16_t*>(key);
+  a.ks0 = k_s0;
+  a.ks1 = k_s1;
+  a.value = static_cast<const uint16_t*>(value);
+  a.vs0 = v_s0;
+  a.vs1 = v_s1;
+  a.qstarts = qstarts;
+  a.seq_lens = seq_lens;
+  a.counts = counts;
+  a.n = n;
+  a.g = static_cast<int32_t>(g);
+  a.hq = static_cast<int32_t>(hq);
+  a.kv_heads = static_cast<int32_t>(h);
+  a.g_div = make_fastdiv(static_cast<uint32_t>(g));
+  a.scale_log2 = scale * kLog2e;
+  a.out = static_cast<uint16_t*>(output);
+  a.lse = merged_lse;
+  // Spans per request: its rows (query tokens x g) in 128-row groups; a request never has more
+  // query tokens than max_query_len (when given) or n.
+  const int64_t qmax = max_query_len > 0 && max_query_len < n ? max_query_len : n;
+  const int64_t spans = (qmax * g + kSpanRows - 1) / kSpanRows;
+  if (spans > 0x7fffffffll) return OSCAR_E_SHAPE;
+  hipStream_t s = as_stream(stream);
+  hipLaunchKernelGGL(prefill_flash_kernel,
+                     dim3(static_cast<unsigned>(spans), static_cast<unsigned>(max_reqs),
+                          static_cast<unsigned>(h)),
+                     dim3(kThreads), 0, s, a);
+  const int64_t clear = (n * hq + 3) / 4;
+  hipLaunchKernelGGL(prefill_clear_kernel,
+                     dim3(static_cast<unsigned>(clear < 1024 ? clear : 1024)), dim3(kThreads), 0,
+                     s, a);
+  return static_cast<int>(hipGetLastError());
+}

@@ -404,33 +404,26 @@ def prefill_attention(query, key, value, window, meta, layout, scale, output, me
     """Initial prefill (every request's history empty): causal attention of each request over
     its own current tokens, written to ``output`` (contiguous bf16 [n, hq * 256]); rows past
     the token count are zeroed. Replaces the reference's fused-infer call
-    (backend.py:175-193) with the BF16 branch of ``attention_partials`` and the bits the
-    INT2 path gives when the history is empty."""
+    (backend.py:175-193) with a flash kernel whose rows have the bits the INT2 path's BF16
+    branch gives when the history is empty. ``window`` is not read (kept for the call's
+    shape); requests with cached tokens get NaN rows."""
     _device_check(query, key, value, window, output, merged_lse)
     n, hq, d = query.shape
     if not output.is_contiguous():
         raise ValueError("Attention output must be contiguous")
     if n == 0:
         return output
-    cfg = layout.config
-    programs = attention_programs(n, meta.max_num_reqs, cfg.queries_per_tile)
-    if meta.tasks.shape[0] < programs:
-        raise ValueError(f"task table holds {meta.tasks.shape[0]} rows; the grid needs {programs}")
     query, q0, q1 = _row_strides(query, "query")
     key, k0, k1 = _row_strides(key, "key")
     value, v0, v1 = _row_strides(value, "value")
-    table = _int32(meta.block_tables, "block_tables")
     max_query_len = getattr(meta, "max_query_len", None)
     max_query_len = int(max_query_len) if isinstance(max_query_len, int) else 0
     _ext.check(
         _ext.library().oscar_prefill_attention(
             _ptr(query), q0, q1, _ptr(key), k0, k1, _ptr(value), v0, v1,
-            _ptr(window), window.numel(),
             _ptr(_int32(meta.query_start_loc, "query_start_loc")),
-            _ptr(_int32(meta.seq_lens, "seq_lens")), _ptr(table), table.stride(0), table.shape[1],
-            _ptr(_int32(meta.counts, "counts")), _ptr(_int32(meta.tasks, "tasks")),
-            _ptr(_int32(meta.task_count, "task_count")), n, hq, programs, cfg.block_n,
-            cfg.queries_per_tile, max_query_len, float(scale), layout_struct(layout),
+            _ptr(_int32(meta.seq_lens, "seq_lens")), _ptr(_int32(meta.counts, "counts")),
+            n, hq, int(meta.max_num_reqs), max_query_len, float(scale), layout_struct(layout),
             _ptr(output), _ptr(merged_lse), _stream(query),
         ),
         "prefill_attention",

@@ -65,3 +65,24 @@ def test_prefill_matches_int2_path_and_dense_reference(lengths, pad):
         np.testing.assert_allclose(out[rows], o, atol=0.035, rtol=0.04)
         assert np.abs(out[rows] - o).mean() <= 2e-3
         np.testing.assert_allclose(lse[rows], l, atol=2e-2, rtol=0)
+
+
+@pytest.mark.parametrize("lengths,max_query_len", [
+    ([2048, 1100, 9], True),  # many 32-token blocks and 128-row spans, a span crossing queries
+    ([300, 5], False),  # max_query_len unknown: spans sized by the token count
+])
+def test_long_prefill_is_bitwise_the_int2_path(lengths, max_query_len):
+    # The flash kernel's spans share K/V blocks across 128 rows; every row must still carry the
+    # BF16 branch's bits (the general path runs that branch per 4-query task).
+    c = _case(lengths, [0] * len(lengths), seed=43, cfg=OscarConfig(sink_tokens=4,
+                                                                    recent_tokens=64))
+    print(f"[prefill] lengths {lengths}", flush=True)
+    if not max_query_len:
+        c.meta.max_query_len = None
+    c.meta.initial_prefill = False
+    want = _forward(c, "single", 1)
+    c.meta.initial_prefill = True
+    got = _forward(c, "single", 1)
+    for a, b in zip(want, got):
+        assert torch.equal(a, b)
+    assert torch.isfinite(got[0].view(torch.bfloat16).float()).all()
