@@ -1,11 +1,11 @@
 // Initial prefill: causal attention of each request over its own tokens (no history), the
 // replacement of the reference's fused-infer call (oscar_ascend/backend.py:175-193).
 //
-// Flash layout for MI355X: a workgroup serves 128 consecutive (query, head) rows of one request
-// and one KV head (wavefront w: row tiles 2 w, 2 w + 1 of 16 rows, all 256 output dims) and
+// Flash layout for MI355X: a workgroup of 8 wavefronts serves 128 consecutive (query, head) rows
+// of one request and one KV head (wavefront w: rows 16 w .. 16 w + 15, all 256 output dims) and
 // streams the request's keys and values in 32-token blocks that its four wavefronts share:
-// each block is copied into LDS once by direct-to-LDS loads (two stages, the next block in
-// flight while the current one is computed), so the K/V bytes a workgroup reads serve all of
+// each block is copied into LDS once by direct-to-LDS loads (four stages: three blocks in
+// flight while one is computed), so the K/V bytes a workgroup reads serve all of
 // its 128 rows. The arithmetic of every row is the BF16 branch's (raw.h: the same MFMA
 // operands and k order, the same lazy max, p, sums and normalization), so the output, the LSE
 // and the bits are those of the decode path (attention_partials raw + merges) for a request
@@ -19,17 +19,21 @@
 namespace oscar {
 namespace {
 
-constexpr int kPrefillRT = 2;                        // row tiles per wavefront
-constexpr int kSpanRows = 4 * 16 * kPrefillRT;       // 128 rows per workgroup
+constexpr int kWavesP = 8;                           // wavefronts per workgroup
+constexpr int kThreadsP = kWavesP * kWave;
+constexpr int kPrefillRT = 1;                        // row tiles per wavefront
+constexpr int kSpanRows = kWavesP * 16 * kPrefillRT;  // 128 rows per workgroup
 constexpr int kRowBytes = kHeadDim * 2;              // 512 bytes per K or V row
 constexpr int kBlockBytes = kBlock * kRowBytes;      // 16 KiB per K or V block
 constexpr int kStageBytesP = 2 * kBlockBytes;        // K then V
-constexpr int kDmaPerWave = kStageBytesP / 1024 / 4;  // 1 KiB per DMA, 8 per wavefront
+constexpr int kDmaPerWave = kStageBytesP / 1024 / kWavesP;  // 1 KiB per DMA, 4 per wavefront
+constexpr int kStagesP = 4;                          // blocks in LDS: 3 in flight beside one
 
 // LDS position of 16-byte chunk c of block row t: chunks are XOR-swizzled by the row's low four
-// bits, so that the 16 lanes of a K read (16 rows, one chunk) and of a V read (one row, 16
-// chunk pairs) each touch 16 different bank groups.
-__device__ __forceinline__ uint32_t chunk_pos(int t, int c) { return c ^ (t & 15); }
+// bits and their own bit 4 (into bit 0), so that the 16 lanes of a K read (16 rows, one chunk)
+// and of a V read (one row, chunks 2 n + h) each touch 16 different bank groups (chunk
+// positions distinct modulo 16).
+__device__ __forceinline__ uint32_t chunk_pos(int t, int c) { return c ^ (t & 15) ^ ((c >> 4) & 1); }
 
 struct PrefillArgs {
   const uint16_t* query;
@@ -49,30 +53,37 @@ struct PrefillArgs {
   float* lse;
 };
 
-// Copies block b of (K, V) rows into `stage`: wavefront w issues DMAs 8 w .. 8 w + 7, DMA i
+// Copies block b of (K, V) rows into `stage`: wavefront w issues DMAs 4 w .. 4 w + 3, DMA i
 // covering K (i < 16) or V rows 2 (i mod 16), + 1. Lane l writes row t = 2 (i mod 16) + l / 32
 // at position l mod 32, fetching the chunk chunk_pos maps there. Every lane issues its copy
-// (the stage waits count 8 DMAs per wavefront): rows at or past the request's token count copy
+// (the stage waits count 4 DMAs per wavefront): rows at or past the request's token count copy
 // its last row instead; they are masked for every query row, so their p is exactly 0 and their
-// products add exact zeros, as the decode path's zero rows do.
-__device__ __forceinline__ void prefill_copy_block(const PrefillArgs& a, int64_t qstart, int qlen,
-                                                   int head, int b, uint8_t* stage) {
+// products add exact zeros, as the decode path's zero rows do. `kb`/`vb`: the request's row 0
+// of this head's keys and values; `kstride`/`vstride`: bytes per token.
+__device__ __forceinline__ void prefill_copy_block(const uint8_t* kb, const uint8_t* vb,
+                                                   uint32_t kstride, uint32_t vstride, int qlen,
+                                                   int b, uint8_t* stage) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int last = qlen - 1 - kBlock * b;  // rows past it copy the request's last row
+  const int64_t block_row = static_cast<int64_t>(kBlock) * b;
+  const uint8_t* kbase = kb + block_row * kstride;
+  const uint8_t* vbase = vb + block_row * vstride;
 #pragma unroll
   for (int k = 0; k < kDmaPerWave; ++k) {
-    const int i = kDmaPerWave * wave + k;
-    const int is_v = i >> 4;
+    const int i = kDmaPerWave * wave + k;  // is_v = i >> 4 is wave-uniform (waves 4..7: V)
     const int t = 2 * (i & 15) + (lane >> 5);
-    const int key = min(kBlock * b + t, qlen - 1);
-    const int c = static_cast<int>(chunk_pos(t, lane & 31));
-    const uint16_t* row = is_v ? a.value + (qstart + key) * a.vs0 + head * a.vs1
-                               : a.key + (qstart + key) * a.ks0 + head * a.ks1;
-    dma_dwordx4(row + 8 * c, lds_addr(stage + is_v * kBlockBytes + (i & 15) * 1024));
+    const uint32_t row = static_cast<uint32_t>(min(t, last));
+    const uint32_t chunk = 16u * chunk_pos(t, lane & 31);
+    const uint32_t lds = lds_addr(stage + (i >> 4) * kBlockBytes + (i & 15) * 1024);
+    if (i >> 4)
+      dma_x4(vbase, row * vstride + chunk, lds);
+    else
+      dma_x4(kbase, row * kstride + chunk, lds);
   }
 }
 
-__global__ __launch_bounds__(kThreads) void prefill_flash_kernel(const PrefillArgs a) {
-  __shared__ __attribute__((aligned(16))) uint8_t s_kv[2][kStageBytesP];
+__global__ __launch_bounds__(kThreadsP) void prefill_flash_kernel(const PrefillArgs a) {
+  __shared__ __attribute__((aligned(16))) uint8_t s_kv[kStagesP][kStageBytesP];
   const int req = blockIdx.y, head = blockIdx.z;
   const int span = static_cast<int>(gridDim.x) - 1 - static_cast<int>(blockIdx.x);
   if (req >= a.counts[0]) return;
@@ -92,9 +103,13 @@ __global__ __launch_bounds__(kThreads) void prefill_flash_kernel(const PrefillAr
   const int wave = uniform(threadIdx.x >> 6);
   const int n = lane & 15, g = lane >> 4;
 
-  if (nblk > 0) prefill_copy_block(a, qstart, qlen, head, 0, s_kv[0]);
+  const uint8_t* kb = reinterpret_cast<const uint8_t*>(a.key + qstart * a.ks0 + head * a.ks1);
+  const uint8_t* vb = reinterpret_cast<const uint8_t*>(a.value + qstart * a.vs0 + head * a.vs1);
+  const uint32_t kstride = static_cast<uint32_t>(a.ks0 * 2), vstride = static_cast<uint32_t>(a.vs0 * 2);
+  for (int b = 0; b < kStagesP - 1 && b < nblk; ++b)
+    prefill_copy_block(kb, vb, kstride, vstride, qlen, b, s_kv[b]);
 
-  // Query rows of this wavefront's tiles: row16 = row0 + 16 (2 w + rt) + n.
+  // Query rows of this wavefront's tile: row16 = row0 + 16 w + n.
   u32x4 qb[kPrefillRT][8];
   int qi_row[kPrefillRT];
 #pragma unroll
@@ -115,13 +130,22 @@ __global__ __launch_bounds__(kThreads) void prefill_flash_kernel(const PrefillAr
   state_init(st);
 
   for (int b = 0; b < nblk; ++b) {
-    const uint8_t* stage = s_kv[b & 1];
-    if (b + 1 < nblk) {
-      prefill_copy_block(a, qstart, qlen, head, b + 1, s_kv[(b + 1) & 1]);
+    const uint8_t* stage = s_kv[b % kStagesP];
+    // Block b + 3 goes to the stage block b - 1 used (every wavefront left it at the barrier
+    // closing the previous iteration); then wait for block b: the blocks issued after it stay
+    // in flight.
+    if (b + kStagesP - 1 < nblk)
+      prefill_copy_block(kb, vb, kstride, vstride, qlen, b + kStagesP - 1,
+                         s_kv[(b + kStagesP - 1) % kStagesP]);
+    const int after = min(nblk - 1 - b, kStagesP - 1);
+    if (after >= 3)
+      OSCAR_WAIT_VM(3 * kDmaPerWave);
+    else if (after == 2)
+      OSCAR_WAIT_VM(2 * kDmaPerWave);
+    else if (after == 1)
       OSCAR_WAIT_VM(kDmaPerWave);
-    } else {
+    else
       OSCAR_WAIT_VM(0);
-    }
     barrier_lds();  // block b landed (every wavefront's copies)
     // Scores: A = K rows 16 tt + n, chunk 8 g + m.
     f32x4 sc[kPrefillRT][2];
@@ -276,7 +300,7 @@ extern "C" int oscar_prefill_attention(
   hipLaunchKernelGGL(prefill_flash_kernel,
                      dim3(static_cast<unsigned>(spans), static_cast<unsigned>(max_reqs),
                           static_cast<unsigned>(h)),
-                     dim3(kThreads), 0, s, a);
+                     dim3(kThreadsP), 0, s, a);
   const int64_t clear = (n * hq + 3) / 4;
   hipLaunchKernelGGL(prefill_clear_kernel,
                      dim3(static_cast<unsigned>(clear < 1024 ? clear : 1024)), dim3(kThreads), 0,

@@ -54,13 +54,22 @@ __device__ __forceinline__ void state_init(State<RT, kTiles>& st) {
 }
 
 // Lazy running max, per row. Each lane first checks its own 8 scores of the block against
-// m + 2^8 (no cross-lane traffic); only if some lane of the wavefront sees a larger score are
-// the block's row maxima reduced across the 4 lane groups, and then exactly the rows whose
-// block maximum passes m + 2^8 move m to it and rescale their sum and accumulators (the other
-// rows multiply by exactly 1). Between updates p <= 2^8.
+// m + 2^8 (block_need, no cross-lane traffic); only if some lane of the wavefront sees a larger
+// score are the block's row maxima reduced across the 4 lane groups (block_rescale), and then
+// exactly the rows whose block maximum passes m + 2^8 move m to it and rescale their sum and
+// accumulators (the other rows multiply by exactly 1). Between updates p <= 2^8.
+template <int RT>
+__device__ __forceinline__ void block_scores(const f32x4 (&sc)[RT][2], const bool (&ok)[RT][8],
+                                             float scale_log2, float (&s2)[RT][8]) {
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) s2[rt][e] = ok[rt][e] ? sc[rt][e >> 2][e & 3] * scale_log2 : -INFINITY;
+}
+
 template <int RT, int kTiles>
-__device__ __forceinline__ void update_max(State<RT, kTiles>& st, const float (&s2)[RT][8], int g) {
-  float lm[RT];
+__device__ __forceinline__ bool block_need(const State<RT, kTiles>& st, const float (&s2)[RT][8],
+                                           float (&lm)[RT]) {
   bool need = false;
 #pragma unroll
   for (int rt = 0; rt < RT; ++rt) {
@@ -70,39 +79,40 @@ __device__ __forceinline__ void update_max(State<RT, kTiles>& st, const float (&
     lm[rt] = v;
     need |= v > st.m[rt] + kRescale;
   }
-  if (__any(need)) {
+  return need;
+}
+
+template <int RT, int kTiles>
+__device__ __forceinline__ void block_rescale(State<RT, kTiles>& st, const float (&lm)[RT], int g) {
 #pragma unroll
-    for (int rt = 0; rt < RT; ++rt) {
-      float v = lm[rt];
-      v = fmaxf(v, __shfl_xor(v, 16, kWave));
-      v = fmaxf(v, __shfl_xor(v, 32, kWave));
-      const float mo = st.m[rt];
-      const float mn = v > mo + kRescale ? v : mo;
-      const float alpha = mn == mo ? 1.0f : (mn == -INFINITY ? 1.0f : exp2f(mo - mn));
-      st.m[rt] = mn;
-      st.psum[rt] *= alpha;
+  for (int rt = 0; rt < RT; ++rt) {
+    float v = lm[rt];
+    v = fmaxf(v, __shfl_xor(v, 16, kWave));
+    v = fmaxf(v, __shfl_xor(v, 32, kWave));
+    const float mo = st.m[rt];
+    const float mn = v > mo + kRescale ? v : mo;
+    const float alpha = mn == mo ? 1.0f : (mn == -INFINITY ? 1.0f : exp2f(mo - mn));
+    st.m[rt] = mn;
+    st.psum[rt] *= alpha;
 #pragma unroll
-      for (int v4 = 0; v4 < 4; ++v4) {
-        const float av = __shfl(alpha, 4 * g + v4, kWave);
+    for (int v4 = 0; v4 < 4; ++v4) {
+      const float av = __shfl(alpha, 4 * g + v4, kWave);
 #pragma unroll
-        for (int t = 0; t < kTiles; ++t) st.o[rt][t][v4] *= av;
-      }
+      for (int t = 0; t < kTiles; ++t) st.o[rt][t][v4] *= av;
     }
   }
 }
 
-// The block's scores of row tile rt to log2 units with the causal / range mask, then the
-// lazy max, p, the lane's sum and the bf16 P operand (lane (n, g): row n, tokens tau(g, e)).
 template <int RT, int kTiles>
-__device__ __forceinline__ void block_softmax(State<RT, kTiles>& st, const f32x4 (&sc)[RT][2],
-                                              const bool (&ok)[RT][8], float scale_log2, int g,
-                                              u32x4 (&ap)[RT]) {
-  float s2[RT][8];
-#pragma unroll
-  for (int rt = 0; rt < RT; ++rt)
-#pragma unroll
-    for (int e = 0; e < 8; ++e) s2[rt][e] = ok[rt][e] ? sc[rt][e >> 2][e & 3] * scale_log2 : -INFINITY;
-  update_max(st, s2, g);
+__device__ __forceinline__ void update_max(State<RT, kTiles>& st, const float (&s2)[RT][8], int g) {
+  float lm[RT];
+  if (__any(block_need(st, s2, lm))) block_rescale(st, lm, g);
+}
+
+// p = 2^(s - m), the lane's sum and the bf16 P operand (lane (n, g): row n, tokens tau(g, e)).
+template <int RT, int kTiles>
+__device__ __forceinline__ void block_p(State<RT, kTiles>& st, const float (&s2)[RT][8],
+                                        u32x4 (&ap)[RT]) {
 #pragma unroll
   for (int rt = 0; rt < RT; ++rt) {
     float p[8];
@@ -114,6 +124,18 @@ __device__ __forceinline__ void block_softmax(State<RT, kTiles>& st, const f32x4
 #pragma unroll
     for (int f = 0; f < 4; ++f) ap[rt][f] = pack_bf16x2(p[2 * f], p[2 * f + 1]);
   }
+}
+
+// The block's scores of row tile rt to log2 units with the causal / range mask, then the
+// lazy max, p, the lane's sum and the bf16 P operand.
+template <int RT, int kTiles>
+__device__ __forceinline__ void block_softmax(State<RT, kTiles>& st, const f32x4 (&sc)[RT][2],
+                                              const bool (&ok)[RT][8], float scale_log2, int g,
+                                              u32x4 (&ap)[RT]) {
+  float s2[RT][8];
+  block_scores(sc, ok, scale_log2, s2);
+  update_max(st, s2, g);
+  block_p(st, s2, ap);
 }
 
 // B operand of P*V for output dim 16 n + j: the bf16 values of dim j of this lane's eight
