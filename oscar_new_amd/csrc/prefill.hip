@@ -128,6 +128,28 @@ __global__ __launch_bounds__(kThreadsP) void prefill_flash_kernel(const PrefillA
   }
   State<kPrefillRT, 16> st;
   state_init(st);
+  // Blocks whose every key is below this wavefront's first query and the request's end need
+  // no mask.
+  const int qi_first = static_cast<int>(
+      fastdiv(static_cast<uint32_t>(row0 + 16 * kPrefillRT * wave), a.g_div));
+  const int full_below = min(qi_first, qlen - 1);  // last key every row of the wave sees
+  // Per-lane LDS offsets of the operands within a stage: K rows 16 tt + n, chunk 8 g + m;
+  // V (at + kBlockBytes) rows tau(g, e), chunk 2 n + h.
+  uint32_t koff[2][8], voff[2][8];
+#pragma unroll
+  for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+    for (int m = 0; m < 8; ++m) {
+      const int t = 16 * tt + n;
+      koff[tt][m] = t * kRowBytes + 16 * chunk_pos(t, 8 * g + m);
+    }
+#pragma unroll
+  for (int h = 0; h < 2; ++h)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int t = tau(g, e);
+      voff[h][e] = kBlockBytes + t * kRowBytes + 16 * chunk_pos(t, 2 * n + h);
+    }
 
   for (int b = 0; b < nblk; ++b) {
     const uint8_t* stage = s_kv[b % kStagesP];
@@ -157,33 +179,34 @@ __global__ __launch_bounds__(kThreadsP) void prefill_flash_kernel(const PrefillA
     for (int m = 0; m < 8; ++m) {
 #pragma unroll
       for (int tt = 0; tt < 2; ++tt) {
-        const int t = 16 * tt + n;
-        const u32x4 kd = *reinterpret_cast<const u32x4*>(
-            stage + t * kRowBytes + 16 * chunk_pos(t, 8 * g + m));
+        const u32x4 kd = *reinterpret_cast<const u32x4*>(stage + koff[tt][m]);
 #pragma unroll
         for (int rt = 0; rt < kPrefillRT; ++rt) sc[rt][tt] = mfma16x16x32(kd, qb[rt][m], sc[rt][tt]);
       }
     }
-    bool ok[kPrefillRT][8];
+    float s2[kPrefillRT][8];
+    if (kBlock * b + kBlock - 1 <= full_below) {
+      block_scores_full(sc, a.scale_log2, s2);
+    } else {
+      bool ok[kPrefillRT][8];
 #pragma unroll
-    for (int rt = 0; rt < kPrefillRT; ++rt)
+      for (int rt = 0; rt < kPrefillRT; ++rt)
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const int key = kBlock * b + tau(g, e);
-        ok[rt][e] = key < qlen && key <= qi_row[rt];
-      }
+        for (int e = 0; e < 8; ++e) {
+          const int key = kBlock * b + tau(g, e);
+          ok[rt][e] = key < qlen && key <= qi_row[rt];
+        }
+      block_scores(sc, ok, a.scale_log2, s2);
+    }
+    update_max(st, s2, g);
     u32x4 ap[kPrefillRT];
-    block_softmax(st, sc, ok, a.scale_log2, g, ap);
+    block_p(st, s2, ap);
     // P*V: V dims 16 n .. 16 n + 15 of this lane's tokens, in two 8-dim halves.
-    const uint8_t* vst = stage + kBlockBytes;
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       u32x4 vd[8];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const int t = tau(g, e);
-        vd[e] = *reinterpret_cast<const u32x4*>(vst + t * kRowBytes + 16 * chunk_pos(t, 2 * n + h));
-      }
+      for (int e = 0; e < 8; ++e) vd[e] = *reinterpret_cast<const u32x4*>(stage + voff[h][e]);
 #pragma unroll
       for (int j8 = 0; j8 < 8; ++j8) {
         const int j = 8 * h + j8;

@@ -31,6 +31,10 @@ constexpr int kBlock = 32;        // tokens per block
 // QK tile, matching the transposed-score output layout.
 __device__ __forceinline__ int tau(int g, int e) { return e < 4 ? 4 * g + e : 12 + 4 * g + e; }
 
+// 2^x by the hardware instruction (v_exp_f32; results below 2^-126 flush to zero): the p and
+// rescale factors of the BF16 branch, whose bf16 P operand cannot hold smaller values anyway.
+__device__ __forceinline__ float exp2_hw(float x) { return __builtin_amdgcn_exp2f(x); }
+
 // ---------------------------------------------------------------- softmax state
 
 // kTiles P*V accumulator tiles per row tile: tile j of lane (n, g) holds rows 4 g + v, one
@@ -67,6 +71,16 @@ __device__ __forceinline__ void block_scores(const f32x4 (&sc)[RT][2], const boo
     for (int e = 0; e < 8; ++e) s2[rt][e] = ok[rt][e] ? sc[rt][e >> 2][e & 3] * scale_log2 : -INFINITY;
 }
 
+// Scores of a block every row sees in full (no mask).
+template <int RT>
+__device__ __forceinline__ void block_scores_full(const f32x4 (&sc)[RT][2], float scale_log2,
+                                                  float (&s2)[RT][8]) {
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) s2[rt][e] = sc[rt][e >> 2][e & 3] * scale_log2;
+}
+
 template <int RT, int kTiles>
 __device__ __forceinline__ bool block_need(const State<RT, kTiles>& st, const float (&s2)[RT][8],
                                            float (&lm)[RT]) {
@@ -91,7 +105,7 @@ __device__ __forceinline__ void block_rescale(State<RT, kTiles>& st, const float
     v = fmaxf(v, __shfl_xor(v, 32, kWave));
     const float mo = st.m[rt];
     const float mn = v > mo + kRescale ? v : mo;
-    const float alpha = mn == mo ? 1.0f : (mn == -INFINITY ? 1.0f : exp2f(mo - mn));
+    const float alpha = mn == mo ? 1.0f : (mn == -INFINITY ? 1.0f : exp2_hw(mo - mn));
     st.m[rt] = mn;
     st.psum[rt] *= alpha;
 #pragma unroll
@@ -118,7 +132,7 @@ __device__ __forceinline__ void block_p(State<RT, kTiles>& st, const float (&s2)
     float p[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      p[e] = s2[rt][e] == -INFINITY ? 0.f : exp2f(s2[rt][e] - st.m[rt]);
+      p[e] = s2[rt][e] == -INFINITY ? 0.f : exp2_hw(s2[rt][e] - st.m[rt]);
       st.psum[rt] += p[e];
     }
 #pragma unroll
