@@ -4,8 +4,8 @@
 // Flash layout for MI355X: a workgroup of 8 wavefronts serves 128 consecutive (query, head) rows
 // of one request and one KV head (wavefront w: rows 16 w .. 16 w + 15, all 256 output dims) and
 // streams the request's keys and values in 32-token blocks that its four wavefronts share:
-// each block is copied into LDS once by direct-to-LDS loads (four stages: three blocks in
-// flight while one is computed), so the K/V bytes a workgroup reads serve all of
+// each block is copied into LDS once by direct-to-LDS loads (four stages: two blocks in flight
+// while one is computed, one barrier per block), so the K/V bytes a workgroup reads serve all of
 // its 128 rows. The arithmetic of every row is the BF16 branch's (raw.h: the same MFMA
 // operands and k order, the same lazy max, p, sums and normalization), so the output, the LSE
 // and the bits are those of the decode path (attention_partials raw + merges) for a request
@@ -27,13 +27,14 @@ constexpr int kRowBytes = kHeadDim * 2;              // 512 bytes per K or V row
 constexpr int kBlockBytes = kBlock * kRowBytes;      // 16 KiB per K or V block
 constexpr int kStageBytesP = 2 * kBlockBytes;        // K then V
 constexpr int kDmaPerWave = kStageBytesP / 1024 / kWavesP;  // 1 KiB per DMA, 4 per wavefront
-constexpr int kStagesP = 4;                          // blocks in LDS: 3 in flight beside one
+constexpr int kStagesP = 4;                          // blocks in LDS
+constexpr int kAheadP = 2;                           // blocks in flight beyond the current one
 
-// LDS position of 16-byte chunk c of block row t: chunks are XOR-swizzled by the row's low four
-// bits and their own bit 4 (into bit 0), so that the 16 lanes of a K read (16 rows, one chunk)
-// and of a V read (one row, chunks 2 n + h) each touch 16 different bank groups (chunk
-// positions distinct modulo 16).
-__device__ __forceinline__ uint32_t chunk_pos(int t, int c) { return c ^ (t & 15) ^ ((c >> 4) & 1); }
+// LDS position of 16-byte chunk c of block row t: the chunk's low three bits are XOR-swizzled by
+// the row's low three bits and the chunk's own bits 3-4, so that each group of 8 lanes the LDS
+// serves together (a ds_read_b128 moves 128 bytes a clock) touches 8 different bank quads, both
+// in a K read (8 rows, one chunk) and in a V read (one row, chunks 2 n + h). An involution.
+__device__ __forceinline__ uint32_t chunk_pos(int t, int c) { return c ^ (t & 7) ^ ((c >> 3) & 3); }
 
 struct PrefillArgs {
   const uint16_t* query;
@@ -106,7 +107,7 @@ __global__ __launch_bounds__(kThreadsP) void prefill_flash_kernel(const PrefillA
   const uint8_t* kb = reinterpret_cast<const uint8_t*>(a.key + qstart * a.ks0 + head * a.ks1);
   const uint8_t* vb = reinterpret_cast<const uint8_t*>(a.value + qstart * a.vs0 + head * a.vs1);
   const uint32_t kstride = static_cast<uint32_t>(a.ks0 * 2), vstride = static_cast<uint32_t>(a.vs0 * 2);
-  for (int b = 0; b < kStagesP - 1 && b < nblk; ++b)
+  for (int b = 0; b <= kAheadP && b < nblk; ++b)
     prefill_copy_block(kb, vb, kstride, vstride, qlen, b, s_kv[b]);
 
   // Query rows of this wavefront's tile: row16 = row0 + 16 w + n.
@@ -153,16 +154,16 @@ __global__ __launch_bounds__(kThreadsP) void prefill_flash_kernel(const PrefillA
 
   for (int b = 0; b < nblk; ++b) {
     const uint8_t* stage = s_kv[b % kStagesP];
-    // Block b + 3 goes to the stage block b - 1 used (every wavefront left it at the barrier
-    // closing the previous iteration); then wait for block b: the blocks issued after it stay
-    // in flight.
-    if (b + kStagesP - 1 < nblk)
-      prefill_copy_block(kb, vb, kstride, vstride, qlen, b + kStagesP - 1,
-                         s_kv[(b + kStagesP - 1) % kStagesP]);
-    const int after = min(nblk - 1 - b, kStagesP - 1);
-    if (after >= 3)
-      OSCAR_WAIT_VM(3 * kDmaPerWave);
-    else if (after == 2)
+    // Block b + 2 goes to the stage of block b - 2: every wavefront finished computing that
+    // block before it reached the barrier of block b - 1, which this wavefront has passed.
+    // Then wait for block b (the blocks issued after it stay in flight) and the barrier that
+    // makes every wavefront's copies of it visible; it is the only barrier of a block.
+    static_assert(kAheadP + 2 <= kStagesP, "the stage refilled is two blocks old");
+    if (b + kAheadP < nblk)
+      prefill_copy_block(kb, vb, kstride, vstride, qlen, b + kAheadP,
+                         s_kv[(b + kAheadP) % kStagesP]);
+    const int after = min(nblk - 1 - b, kAheadP);
+    if (after >= 2)
       OSCAR_WAIT_VM(2 * kDmaPerWave);
     else if (after == 1)
       OSCAR_WAIT_VM(kDmaPerWave);
@@ -218,7 +219,6 @@ __global__ __launch_bounds__(kThreadsP) void prefill_flash_kernel(const PrefillA
         for (int rt = 0; rt < kPrefillRT; ++rt) st.o[rt][j] = mfma16x16x32(ap[rt], bv, st.o[rt][j]);
       }
     }
-    barrier_lds();  // every wavefront is done with this stage before it is refilled
   }
 
   // Normalize and store: lane (n, g) holds rows 4 g + v of each tile, dims 16 n + j.
