@@ -4,7 +4,7 @@
 // Flash layout for MI355X: a workgroup of 8 wavefronts serves 128 consecutive (query, head) rows
 // of one request and one KV head (wavefront w: rows 16 w .. 16 w + 15, all 256 output dims) and
 // streams the request's keys and values in 32-token blocks that its four wavefronts share:
-// each block is copied into LDS once by direct-to-LDS loads (four stages: two blocks in flight
+// each block is copied into LDS once by direct-to-LDS loads (three stages, one block in flight
 // while one is computed, one barrier per block), so the K/V bytes a workgroup reads serve all of
 // its 128 rows. The arithmetic of every row is the BF16 branch's (raw.h: the same MFMA
 // operands and k order, the same lazy max, p, sums and normalization), so the output, the LSE
@@ -27,8 +27,14 @@ constexpr int kRowBytes = kHeadDim * 2;              // 512 bytes per K or V row
 constexpr int kBlockBytes = kBlock * kRowBytes;      // 16 KiB per K or V block
 constexpr int kStageBytesP = 2 * kBlockBytes;        // K then V
 constexpr int kDmaPerWave = kStageBytesP / 1024 / kWavesP;  // 1 KiB per DMA, 4 per wavefront
-constexpr int kStagesP = 4;                          // blocks in LDS
-constexpr int kAheadP = 2;                           // blocks in flight beyond the current one
+constexpr int kStagesP = 3;                          // K/V blocks in LDS
+constexpr int kAheadP = 1;                           // blocks in flight beyond the current one
+// Paired V (the P*V B operands, built once per block by the whole workgroup): row r(d) of dim
+// d holds 16 dwords, dword 4 g + f = (V[tau(g, 2 f + 1)][d] << 16) | V[tau(g, 2 f)][d]; rows
+// are 80 bytes apart and ordered r(16 n + j) = 16 j + n, so that the 8 lanes n = 0..7 of a
+// read (rows 16 n + j, one 16-byte column) hit 8 different bank quads.
+constexpr int kPairRowBytes = 80;
+constexpr int kPairBytes = kHeadDim * kPairRowBytes;  // 20 KiB per block
 
 // LDS position of 16-byte chunk c of block row t: the chunk's low three bits are XOR-swizzled by
 // the row's low three bits and the chunk's own bits 3-4, so that each group of 8 lanes the LDS
@@ -85,6 +91,7 @@ __device__ __forceinline__ void prefill_copy_block(const uint8_t* kb, const uint
 
 __global__ __launch_bounds__(kThreadsP) void prefill_flash_kernel(const PrefillArgs a) {
   __shared__ __attribute__((aligned(16))) uint8_t s_kv[kStagesP][kStageBytesP];
+  __shared__ __attribute__((aligned(16))) uint8_t s_pair[2][kPairBytes];
   const int req = blockIdx.y, head = blockIdx.z;
   const int span = static_cast<int>(gridDim.x) - 1 - static_cast<int>(blockIdx.x);
   if (req >= a.counts[0]) return;
@@ -134,9 +141,8 @@ __global__ __launch_bounds__(kThreadsP) void prefill_flash_kernel(const PrefillA
   const int qi_first = static_cast<int>(
       fastdiv(static_cast<uint32_t>(row0 + 16 * kPrefillRT * wave), a.g_div));
   const int full_below = min(qi_first, qlen - 1);  // last key every row of the wave sees
-  // Per-lane LDS offsets of the operands within a stage: K rows 16 tt + n, chunk 8 g + m;
-  // V (at + kBlockBytes) rows tau(g, e), chunk 2 n + h.
-  uint32_t koff[2][8], voff[2][8];
+  // Per-lane LDS offsets of the K operands within a stage: rows 16 tt + n, chunk 8 g + m.
+  uint32_t koff[2][8];
 #pragma unroll
   for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
@@ -144,32 +150,57 @@ __global__ __launch_bounds__(kThreadsP) void prefill_flash_kernel(const PrefillA
       const int t = 16 * tt + n;
       koff[tt][m] = t * kRowBytes + 16 * chunk_pos(t, 8 * g + m);
     }
+  // Pairing: lane l of wavefront w takes token pair q = l % 16 (tokens t0, t0 + 1 with
+  // t0 = tau(q / 4, 2 (q % 4))) and 8-dim chunk c = 8 (l / 16) + w of the block's V rows; dim
+  // 8 c + j goes to row r = 16 ((8 c + j) % 16) + (8 c + j) / 16 = 128 (c % 2) + 16 j + c / 2.
+  // (The two 16-lane halves of a write then fall on disjoint banks: their rows are 4 apart.)
+  const int pq = lane & 15, pc = 8 * (lane >> 4) + wave;
+  const int pt0 = tau(pq >> 2, 2 * (pq & 3));
+  const uint32_t pair_src0 = kBlockBytes + pt0 * kRowBytes + 16 * chunk_pos(pt0, pc);
+  const uint32_t pair_src1 = kBlockBytes + (pt0 + 1) * kRowBytes + 16 * chunk_pos(pt0 + 1, pc);
+  const uint32_t pair_dst = (128 * (pc & 1) + (pc >> 1)) * kPairRowBytes + 4 * pq;
+  // P*V operand of lane (n, g), dim tile j: row 16 j + n, dwords 4 g .. 4 g + 3.
+  const uint32_t pv_off = n * kPairRowBytes + 16 * g;
+  auto pair_block = [&](const uint8_t* stage, uint8_t* pairs) {
+    const u32x4 x0 = *reinterpret_cast<const u32x4*>(stage + pair_src0);
+    const u32x4 x1 = *reinterpret_cast<const u32x4*>(stage + pair_src1);
 #pragma unroll
-  for (int h = 0; h < 2; ++h)
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const int t = tau(g, e);
-      voff[h][e] = kBlockBytes + t * kRowBytes + 16 * chunk_pos(t, 2 * n + h);
+    for (int j = 0; j < 8; ++j) {
+      const uint32_t sel = (j & 1) ? 0x07060302u : 0x05040100u;
+      *reinterpret_cast<uint32_t*>(pairs + pair_dst + 16 * j * kPairRowBytes) =
+          __builtin_amdgcn_perm(x1[j >> 1], x0[j >> 1], sel);
     }
+  };
+  auto pv_block = [&](const uint8_t* pairs, const u32x4 (&ap)[kPrefillRT]) {
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const u32x4 bv = *reinterpret_cast<const u32x4*>(pairs + pv_off + 16 * j * kPairRowBytes);
+#pragma unroll
+      for (int rt = 0; rt < kPrefillRT; ++rt) st.o[rt][j] = mfma16x16x32(ap[rt], bv, st.o[rt][j]);
+    }
+  };
+  u32x4 ap_prev[kPrefillRT];
 
   for (int b = 0; b < nblk; ++b) {
     const uint8_t* stage = s_kv[b % kStagesP];
-    // Block b + 2 goes to the stage of block b - 2: every wavefront finished computing that
-    // block before it reached the barrier of block b - 1, which this wavefront has passed.
-    // Then wait for block b (the blocks issued after it stay in flight) and the barrier that
-    // makes every wavefront's copies of it visible; it is the only barrier of a block.
+    // Block b + 1 goes to the stage of block b - 2: every wavefront finished with that block
+    // (scores, pairing) before it reached the barrier of block b - 1, which this wavefront has
+    // passed. Then wait for block b (the block issued after it stays in flight) and the
+    // barrier that makes every wavefront's copies of it, and the pairs of block b - 1, visible;
+    // it is the only barrier of a block.
     static_assert(kAheadP + 2 <= kStagesP, "the stage refilled is two blocks old");
     if (b + kAheadP < nblk)
       prefill_copy_block(kb, vb, kstride, vstride, qlen, b + kAheadP,
                          s_kv[(b + kAheadP) % kStagesP]);
     const int after = min(nblk - 1 - b, kAheadP);
-    if (after >= 2)
-      OSCAR_WAIT_VM(2 * kDmaPerWave);
-    else if (after == 1)
+    if (after >= 1)
       OSCAR_WAIT_VM(kDmaPerWave);
     else
       OSCAR_WAIT_VM(0);
-    barrier_lds();  // block b landed (every wavefront's copies)
+    barrier_lds();  // block b landed, pairs of block b - 1 written
+    // P*V of block b - 1 first: the accumulators take it before block b's lazy max may
+    // rescale them, the order of the one-block-at-a-time stream.
+    if (b > 0) pv_block(s_pair[(b - 1) & 1], ap_prev);
     // Scores: A = K rows 16 tt + n, chunk 8 g + m.
     f32x4 sc[kPrefillRT][2];
 #pragma unroll
@@ -200,25 +231,13 @@ __global__ __launch_bounds__(kThreadsP) void prefill_flash_kernel(const PrefillA
       block_scores(sc, ok, a.scale_log2, s2);
     }
     update_max(st, s2, g);
-    u32x4 ap[kPrefillRT];
-    block_p(st, s2, ap);
-    // P*V: V dims 16 n .. 16 n + 15 of this lane's tokens, in two 8-dim halves.
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      u32x4 vd[8];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) vd[e] = *reinterpret_cast<const u32x4*>(stage + voff[h][e]);
-#pragma unroll
-      for (int j8 = 0; j8 < 8; ++j8) {
-        const int j = 8 * h + j8;
-        uint32_t vd2[8];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) vd2[e] = vd[e][j8 >> 1];
-        const u32x4 bv = pv_operand(vd2, j);
-#pragma unroll
-        for (int rt = 0; rt < kPrefillRT; ++rt) st.o[rt][j] = mfma16x16x32(ap[rt], bv, st.o[rt][j]);
-      }
-    }
+    block_p(st, s2, ap_prev);
+    // Pairs of block b (into the buffer block b - 2 used, read before the barrier above).
+    pair_block(stage, s_pair[b & 1]);
+  }
+  if (nblk > 0) {
+    barrier_lds();  // the last block's pairs
+    pv_block(s_pair[(nblk - 1) & 1], ap_prev);
   }
 
   // Normalize and store: lane (n, g) holds rows 4 g + v of each tile, dims 16 n + j.
