@@ -10,7 +10,7 @@
 // operands and k order, the same lazy max, p, sums and normalization), so the output, the LSE
 // and the bits are those of the decode path (attention_partials raw + merges) for a request
 // without history. Blocks past a workgroup's last query are not read (they are masked for
-// every row). Workgroups run the longest spans (the last rows of a request) first. Requests
+// every row). Workgroups run the longest spans (the last rows of requests) first. Requests
 // with cached tokens (seq_len != query tokens) are not initial prefills: their rows are
 // written as NaN (output and LSE), never silently wrong.
 #include "dma.h"
@@ -92,8 +92,8 @@ __device__ __forceinline__ void prefill_copy_block(const uint8_t* kb, const uint
 __global__ __launch_bounds__(kThreadsP) void prefill_flash_kernel(const PrefillArgs a) {
   __shared__ __attribute__((aligned(16))) uint8_t s_kv[kStagesP][kStageBytesP];
   __shared__ __attribute__((aligned(16))) uint8_t s_pair[2][kPairBytes];
-  const int req = blockIdx.y, head = blockIdx.z;
-  const int span = static_cast<int>(gridDim.x) - 1 - static_cast<int>(blockIdx.x);
+  const int req = blockIdx.x, head = blockIdx.z;
+  const int span = static_cast<int>(gridDim.y) - 1 - static_cast<int>(blockIdx.y);
   if (req >= a.counts[0]) return;
   const int64_t qstart = a.qstarts[req];
   const int64_t qend = min(static_cast<int64_t>(a.qstarts[req + 1]),
@@ -339,8 +339,11 @@ extern "C" int oscar_prefill_attention(
   const int64_t spans = (qmax * g + kSpanRows - 1) / kSpanRows;
   if (spans > 0x7fffffffll) return OSCAR_E_SHAPE;
   hipStream_t s = as_stream(stream);
+  // Requests vary fastest: the workgroups of the longest spans of every request dispatch
+  // first (a longest-first order of the whole batch), and consecutive workgroups, which the
+  // dispatcher spreads over the XCDs, keep each XCD on few requests (their K/V stay in its L2).
   hipLaunchKernelGGL(prefill_flash_kernel,
-                     dim3(static_cast<unsigned>(spans), static_cast<unsigned>(max_reqs),
+                     dim3(static_cast<unsigned>(max_reqs), static_cast<unsigned>(spans),
                           static_cast<unsigned>(h)),
                      dim3(kThreadsP), 0, s, a);
   const int64_t clear = (n * hq + 3) / 4;
