@@ -179,7 +179,14 @@ __global__ __launch_bounds__(kThreadsP) void prefill_flash_kernel(const PrefillA
       for (int rt = 0; rt < kPrefillRT; ++rt) st.o[rt][j] = mfma16x16x32(ap[rt], bv, st.o[rt][j]);
     }
   };
+  // P of the block before the first: zero, with zeroed pairs, so that every iteration runs
+  // the previous block's P*V (adding exact zeros the first time) without a branch, and the
+  // scores and P*V MFMAs of an iteration interleave.
   u32x4 ap_prev[kPrefillRT];
+#pragma unroll
+  for (int rt = 0; rt < kPrefillRT; ++rt) ap_prev[rt] = u32x4{0u, 0u, 0u, 0u};
+  for (int i = threadIdx.x; i < 2 * kPairBytes / 16; i += kThreadsP)
+    reinterpret_cast<u32x4*>(&s_pair[0][0])[i] = u32x4{0u, 0u, 0u, 0u};
 
   for (int b = 0; b < nblk; ++b) {
     const uint8_t* stage = s_kv[b % kStagesP];
@@ -198,10 +205,10 @@ __global__ __launch_bounds__(kThreadsP) void prefill_flash_kernel(const PrefillA
     else
       OSCAR_WAIT_VM(0);
     barrier_lds();  // block b landed, pairs of block b - 1 written
-    // P*V of block b - 1 first: the accumulators take it before block b's lazy max may
-    // rescale them, the order of the one-block-at-a-time stream.
-    if (b > 0) pv_block(s_pair[(b - 1) & 1], ap_prev);
-    // Scores: A = K rows 16 tt + n, chunk 8 g + m.
+    // P*V of block b - 1 (the accumulators take it before block b's lazy max may rescale
+    // them, the order of the one-block-at-a-time stream) interleaved with block b's scores
+    // S^T = K Q^T (A = K rows 16 tt + n, chunk 8 g + m): two P*V tiles per score k-step.
+    const uint8_t* pairs = s_pair[(b + 1) & 1];  // block b - 1's
     f32x4 sc[kPrefillRT][2];
 #pragma unroll
     for (int rt = 0; rt < kPrefillRT; ++rt)
@@ -214,6 +221,11 @@ __global__ __launch_bounds__(kThreadsP) void prefill_flash_kernel(const PrefillA
         const u32x4 kd = *reinterpret_cast<const u32x4*>(stage + koff[tt][m]);
 #pragma unroll
         for (int rt = 0; rt < kPrefillRT; ++rt) sc[rt][tt] = mfma16x16x32(kd, qb[rt][m], sc[rt][tt]);
+        const int j = 2 * m + tt;
+        const u32x4 bv = *reinterpret_cast<const u32x4*>(pairs + pv_off + 16 * j * kPairRowBytes);
+#pragma unroll
+        for (int rt = 0; rt < kPrefillRT; ++rt)
+          st.o[rt][j] = mfma16x16x32(ap_prev[rt], bv, st.o[rt][j]);
       }
     }
     float s2[kPrefillRT][8];
@@ -337,7 +349,7 @@ extern "C" int oscar_prefill_attention(
   // query tokens than max_query_len (when given) or n.
   const int64_t qmax = max_query_len > 0 && max_query_len < n ? max_query_len : n;
   const int64_t spans = (qmax * g + kSpanRows - 1) / kSpanRows;
-  if (spans > 0x7fffffffll) return OSCAR_E_SHAPE;
+  if (spans > 65535) return OSCAR_E_SHAPE;  // grid y
   hipStream_t s = as_stream(stream);
   // Requests vary fastest: the workgroups of the longest spans of every request dispatch
   // first (a longest-first order of the whole batch), and consecutive workgroups, which the
