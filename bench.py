@@ -70,11 +70,13 @@ def parse_args(argv=None):
                         "launch instead of q rotation + history launch carrying the rest")
     p.add_argument("--layer-step", action="store_true",
                    help="the one-launch layer step (kernels.layer_step) instead of three launches")
-    p.add_argument("--mode", default="step", choices=("step", "history", "copy", "prefill"),
+    p.add_argument("--mode", default="step",
+                   choices=("step", "history", "copy", "prefill", "store"),
                    help="step: full benchmark; history: only the history-attention launches "
                         "(for rocprofv3 counters); copy: a plain device copy of --copy-mib MiB "
                         "(counter calibration); prefill: the initial-prefill launch on a "
-                        "prefill config (--config p1)")
+                        "prefill config (--config p1); store: the c2 store forms, plain "
+                        "launches (for rocprofv3 counters)")
     p.add_argument("--copy-mib", type=int, default=1024)
     return p.parse_args(argv)
 
@@ -226,9 +228,10 @@ def split_partial_bytes(w, splits, split_tokens):
 # ------------------------------------------------------------------ measurements
 
 
-def time_store(device, args, steps):
+def time_store(device, args, steps, eager=False):
     """rotate + clip-search + INT2 pack of 4096 tokens into permuted pages
-    (device time per call from HIP-graph replays)."""
+    (device time per call from HIP-graph replays). ``eager``: only run each form ``steps``
+    times with plain launches (for rocprofv3 counters) and return None."""
     import torch
 
     from oscar_new_amd import kernels
@@ -266,6 +269,13 @@ def time_store(device, args, steps):
         once()
     kr, vr = kernels.rotate(k, rk), kernels.rotate(v, rv)
     torch.cuda.synchronize()
+    if eager:
+        for _ in range(steps):
+            once()
+        for _ in range(steps):
+            unfused()
+        torch.cuda.synchronize()
+        return None
 
     # Device time without host submission gaps: each form is captured `reps` times in one
     # HIP graph, and the graph's replays are timed with events on the capture stream.
@@ -533,6 +543,10 @@ def main(argv=None):
     torch.cuda.set_device(device)
     if args.mode == "copy":
         return copy_calibration(args, device)
+    if args.mode == "store":
+        time_store(device, args, args.steps, eager=True)
+        print(json.dumps({"mode": "store", "calls_per_form": args.steps}))
+        return 0
     cfg = CONFIGS[args.config]
     print(f"[bench] building {args.config} workload", file=sys.stderr, flush=True)
     w = build_workload(args, cfg, device)

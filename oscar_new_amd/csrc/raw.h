@@ -21,6 +21,7 @@
 #pragma once
 
 #include "attention.h"
+#include "dma.h"
 
 namespace oscar {
 
@@ -205,6 +206,46 @@ __device__ __forceinline__ const uint16_t* raw_token(const AttnArgs& a, const Ta
   return a.window + off;
 }
 
+// raw_token for K and V at once: the position of raw index ns, or INT_MAX if the index holds
+// no token (no V row; raw_token's nullptr), and both row pointers (nullptr where raw_token
+// gives nullptr).
+__device__ __forceinline__ int raw_row(const AttnArgs& a, const Task& t, const RawTask& r,
+                                       int head, int ns, int end, const uint16_t*& kp,
+                                       const uint16_t*& vp) {
+  kp = vp = nullptr;
+  if (ns < 0 || ns >= end) return 0x7fffffff;
+  int pos;
+  if (ns < t.sink_len)
+    pos = ns;
+  else if (ns < r.high)
+    pos = t.recent_begin + ns - t.sink_len;
+  else
+    pos = t.prefix + ns - r.high;
+  if (pos >= t.prefix) {
+    const int64_t ci = static_cast<int64_t>(t.qstart) + pos - t.prefix;
+    if (ci < 0 || ci >= a.n) return 0x7fffffff;
+    kp = a.key + ci * a.ks0 + head * a.ks1;
+    vp = a.value + ci * a.vs0 + head * a.vs1;
+    return pos;
+  }
+  if (r.win < 0 || pos < 0) return 0x7fffffff;
+  const uint32_t lap = fastdiv(static_cast<uint32_t>(pos), a.L.ring_div);
+  const int wi = pos < a.L.sink ? pos : a.L.sink + pos - static_cast<int>(lap) * a.L.ring;
+  const int64_t off = r.win + static_cast<int64_t>(wi) * 2 * a.L.kv_heads * kHeadDim;
+  const int64_t voff = off + static_cast<int64_t>(a.L.kv_heads) * kHeadDim;
+  if (off + kHeadDim <= a.window_elems) kp = a.window + off;
+  if (voff + kHeadDim > a.window_elems) return 0x7fffffff;
+  vp = a.window + voff;
+  return pos;
+}
+
+__device__ __forceinline__ const uint16_t* shfl_ptr(const uint16_t* p, int src) {
+  const uint64_t v = reinterpret_cast<uint64_t>(p);
+  const uint32_t lo = __shfl(static_cast<uint32_t>(v), src, kWave);
+  const uint32_t hi = __shfl(static_cast<uint32_t>(v >> 32), src, kWave);
+  return reinterpret_cast<const uint16_t*>((static_cast<uint64_t>(hi) << 32) | lo);
+}
+
 // K rows of the block's two 16-token score tiles (A operands: lane (n, g), k-step m holds dims
 // 64 g + 8 m .. + 7 of token 16 tt + n).
 __device__ __forceinline__ void raw_load_k(const AttnArgs& a, const Task& t, const RawTask& r,
@@ -245,47 +286,127 @@ struct RawBlock {
   bool live[8];
 };
 
-// One workgroup of the BF16 branch: (task, kv head, split). Wavefront w writes output dims
-// 16 n + 4 w .. + 3 of every row. kDirect: the normalized rows go to a.direct_out as bf16 (and
-// the LSE to a.direct_lse): the bits merge_paths gives a row whose history branch is empty.
-// kLean: the block's K rows are loaded and scored before its V rows, with no prefetch (fewer
-// registers, for a role inside a launch that must keep two workgroups per CU); same bits.
-template <int RT, bool kDirect = false, bool kLean = false>
-__device__ __forceinline__ void raw_block(const AttnArgs& a, int task, int head, int split) {
+// Task, query rows and block range of one BF16-branch workgroup (task, kv head, split).
+template <int RT>
+struct RawSetup {
   Task t;
-  if (!read_task(a, t, task)) return;
+  RawTask r;
+  int begin, end;
+  u32x4 qb[RT][8];  // unrotated query as B operand of S^T = K Q^T: k-step m, d = 64 g + 8 m ..
+  int qi_row[RT];
+};
+
+template <int RT>
+__device__ __forceinline__ bool raw_setup(const AttnArgs& a, int task, int head, int split,
+                                          int n, int g, RawSetup<RT>& s) {
+  if (!read_task(a, s.t, task)) return false;
+  const Task& t = s.t;
   // The owner page (block-table column 0) is requested together with the request's
   // metadata rows: both depend only on the task row.
   const int first = a.table_columns > 0 ? a.table[static_cast<int64_t>(t.req) * a.table_stride]
                                         : -1;
-  RawTask r;
-  r.high = t.sink_len + t.prefix - t.recent_begin;
-  r.win = -1;
+  s.r.high = t.sink_len + t.prefix - t.recent_begin;
+  s.r.win = -1;
   if (first >= 0) {
     const int64_t owner = fastdiv(static_cast<uint32_t>(first), a.L.bpp_div);
-    r.win = owner * (a.L.page_bytes / 2) + static_cast<int64_t>(head) * kHeadDim;
+    s.r.win = owner * (a.L.page_bytes / 2) + static_cast<int64_t>(head) * kHeadDim;
   }
-  int begin, end;
-  split_range(r.high + t.qlen, a.block_n, a.splits, split, begin, end);
-  const int lane = threadIdx.x & 63;
-  const int wave = uniform(threadIdx.x >> 6);
-  const int n = lane & 15, g = lane >> 4;
-
-  // Unrotated query as B operand of S^T = K Q^T; k-step m covers d = 64g + 8m .. +7.
-  u32x4 qb[RT][8];
-  int qi_row[RT];
+  split_range(s.r.high + t.qlen, a.block_n, a.splits, split, s.begin, s.end);
 #pragma unroll
   for (int rt = 0; rt < RT; ++rt) {
     const RowInfo ri = row_info(a, t, head, n + 16 * rt);
-    qi_row[rt] = ri.qi;
+    s.qi_row[rt] = ri.qi;
 #pragma unroll
-    for (int m = 0; m < 8; ++m) qb[rt][m] = u32x4{0u, 0u, 0u, 0u};
+    for (int m = 0; m < 8; ++m) s.qb[rt][m] = u32x4{0u, 0u, 0u, 0u};
     if (ri.valid) {
       const uint16_t* qp = a.query + ri.token * a.qs0 + ri.qhead * a.qs1 + 64 * g;
 #pragma unroll
-      for (int m = 0; m < 8; ++m) qb[rt][m] = *reinterpret_cast<const u32x4*>(qp + 8 * m);
+      for (int m = 0; m < 8; ++m) s.qb[rt][m] = *reinterpret_cast<const u32x4*>(qp + 8 * m);
     }
   }
+  return true;
+}
+
+// Everything of a block after its scores: causal / range mask, online softmax, P*V into the
+// wavefront's 4 output tiles (dims 16 n + 4 w + jj).
+template <int RT>
+__device__ __forceinline__ void raw_block_tail(State<RT, 4>& st, const f32x4 (&sc)[RT][2],
+                                               const RawSetup<RT>& s, const uint2 (&vq)[8],
+                                               const int (&pos)[8], const bool (&live)[8],
+                                               float scale_log2, int g) {
+  bool ok[RT][8];
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) ok[rt][e] = live[e] && pos[e] <= s.t.prefix + s.qi_row[rt];
+  u32x4 ap[RT];
+  block_softmax(st, sc, ok, scale_log2, g, ap);
+#pragma unroll
+  for (int jj = 0; jj < 4; ++jj) {
+    uint32_t vd2[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) vd2[e] = (jj >> 1) ? vq[e].y : vq[e].x;
+    const u32x4 bv = pv_operand(vd2, jj);
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) st.o[rt][jj] = mfma16x16x32(ap[rt], bv, st.o[rt][jj]);
+  }
+}
+
+// Normalized rows and LSEs of the workgroup: lane (n, g) of wavefront w holds rows 4 g + v,
+// dims 16 n + 4 w + jj.
+template <int RT, bool kDirect>
+__device__ __forceinline__ void raw_finish(const AttnArgs& a, const RawSetup<RT>& s, int head,
+                                           int split, const State<RT, 4>& st, int n, int g,
+                                           int wave) {
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt) {
+    const float den_n = row_sum(st.psum[rt]);
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int row = 16 * rt + 4 * g + v;
+      const float den = fmaxf(__shfl(den_n, 4 * g + v, kWave), 1.0e-30f);
+      const RowInfo ri = row_info(a, s.t, head, row);
+      if (!ri.valid) continue;
+      const int d = 16 * n + 4 * wave;
+      const float o0 = st.o[rt][0][v] / den, o1 = st.o[rt][1][v] / den;
+      const float o2 = st.o[rt][2][v] / den, o3 = st.o[rt][3][v] / den;
+      if constexpr (kDirect) {
+        const int64_t out_row = ri.token * a.hq + ri.qhead;
+        *reinterpret_cast<uint2*>(a.direct_out + out_row * kHeadDim + d) =
+            make_uint2(pack_bf16x2(o0, o1), pack_bf16x2(o2, o3));
+      } else {
+        const int64_t orow = (ri.token * a.hq + ri.qhead) * a.splits + split;
+        *reinterpret_cast<float4*>(a.partials + orow * kHeadDim + d) = make_float4(o0, o1, o2, o3);
+      }
+    }
+    // LSE of row n (wavefront 0, lane group 0).
+    if (wave == 0 && g == 0) {
+      const RowInfo ri = row_info(a, s.t, head, n + 16 * rt);
+      const float lse = row_lse(st.m[rt], den_n);
+      if constexpr (kDirect) {
+        if (ri.valid && a.direct_lse) a.direct_lse[ri.token * a.hq + ri.qhead] = lse;
+      } else {
+        if (ri.valid) a.lse[(ri.token * a.hq + ri.qhead) * a.splits + split] = lse;
+      }
+    }
+  }
+}
+
+// One workgroup of the BF16 branch: (task, kv head, split). Wavefront w writes output dims
+// 16 n + 4 w .. + 3 of every row. kDirect: the normalized rows go to a.direct_out as bf16 (and
+// the LSE to a.direct_lse): the bits merge_paths gives a row whose history branch is empty.
+// kLean: the block's K rows are loaded and scored before its V rows, with no prefetch (fewer
+// registers); same bits.
+template <int RT, bool kDirect = false, bool kLean = false>
+__device__ __forceinline__ void raw_block(const AttnArgs& a, int task, int head, int split) {
+  const int lane = threadIdx.x & 63;
+  const int wave = uniform(threadIdx.x >> 6);
+  const int n = lane & 15, g = lane >> 4;
+  RawSetup<RT> s;
+  if (!raw_setup(a, task, head, split, n, g, s)) return;
+  const Task& t = s.t;
+  const RawTask& r = s.r;
+  const int end = s.end;
   State<RT, 4> st;
   state_init(st);
 
@@ -293,7 +414,7 @@ __device__ __forceinline__ void raw_block(const AttnArgs& a, int task, int head,
   // (kLean: none; two row tiles: none, for registers).
   constexpr bool kPrefetch = RT == 1 && !kLean;
   RawBlock cur, nxt;
-  int t0 = begin;
+  int t0 = s.begin;
   if (kPrefetch && t0 < end) {
     raw_load_k(a, t, r, head, t0, end, g, n, cur.kd);
     raw_load_v(a, t, r, head, t0, end, g, n, wave, cur.vq, cur.pos, cur.live);
@@ -317,59 +438,117 @@ __device__ __forceinline__ void raw_block(const AttnArgs& a, int task, int head,
       for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
         for (int rt = 0; rt < RT; ++rt)
-          sc[rt][tt] = mfma16x16x32(cur.kd[tt][m], qb[rt][m], sc[rt][tt]);
+          sc[rt][tt] = mfma16x16x32(cur.kd[tt][m], s.qb[rt][m], sc[rt][tt]);
     if (kLean) raw_load_v(a, t, r, head, t0, end, g, n, wave, cur.vq, cur.pos, cur.live);
-    bool ok[RT][8];
+    raw_block_tail(st, sc, s, cur.vq, cur.pos, cur.live, a.scale_log2, g);
+    if (more) cur = nxt;
+  }
+  raw_finish<RT, kDirect>(a, s, head, split, st, n, g, wave);
+}
+
+// LDS ring of the staged BF16 branch: a slot holds one 32-token block, K rows then V rows
+// (16 KiB each). K row i (token t0 + i) at 512 i with its 16-byte piece p at slot p ^ (i & 7),
+// so that the eight lanes of a 128-bit read group (rows n .. n + 7, one piece) fall on eight
+// different bank quads; V row i at 16 KiB + 512 i, plain.
+constexpr int kRawHalfBytes = kBlock * kHeadDim * 2;
+constexpr int kRawSlotBytes = 2 * kRawHalfBytes;
+// Slots where the launch has the LDS to spare (4 x 32 KiB).
+constexpr int kRawSlots = 4;
+
+// DMA of block t0's K and V rows into `slot`: 2 x 16 KiB, 4 x 1 KiB per wavefront each.
+// Lane l resolves row l % 32 once (raw_row) and the DMA lanes fetch their rows' pointers
+// from it. Every lane issues (a row without a token copies the query row; its score and P
+// are masked and its V operand is replaced by zeros), so every wavefront counts 8 loads per
+// block.
+__device__ __forceinline__ void raw_stage_block(const AttnArgs& a, const Task& t,
+                                                const RawTask& r, int head, int t0, int end,
+                                                int wave, int lane, uint32_t slot) {
+  const uint16_t *kp, *vp;
+  raw_row(a, t, r, head, t0 + (lane & 31), end, kp, vp);
+  kp = kp ? kp : a.query;
+  vp = vp ? vp : a.query;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int seg = 4 * i + wave;
+    const int row = 2 * seg + (lane >> 5), piece = lane & 31;
+    dma_dwordx4(shfl_ptr(kp, row) + 8 * (piece ^ (row & 7)), slot + 1024 * seg);
+    dma_dwordx4(shfl_ptr(vp, row) + 8 * piece, slot + kRawHalfBytes + 1024 * seg);
+  }
+}
+
+// Wait until at most `ahead` blocks (8 loads each) of this wavefront are still in flight,
+// then meet the workgroup: every wavefront's share of the oldest block has landed.
+__device__ __forceinline__ void raw_wait_blocks(int ahead) {
+  switch (ahead) {
+    case 0: asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory"); break;
+    case 1: asm volatile("s_waitcnt vmcnt(8)\n\ts_barrier" ::: "memory"); break;
+    case 2: asm volatile("s_waitcnt vmcnt(16)\n\ts_barrier" ::: "memory"); break;
+    default: asm volatile("s_waitcnt vmcnt(24)\n\ts_barrier" ::: "memory"); break;
+  }
+}
+
+// The BF16 branch with each block's K and V rows staged in an LDS ring of `slots` (<= 4)
+// slots by DMA, up to `slots` blocks in flight. The arithmetic is raw_block's, block for
+// block: the same bits. The block loop is not unrolled: a launch runs this code cold, so its
+// size, not its instruction count, sets the time of the first block. Every thread of the
+// workgroup calls this; `lds` holds slots x 32 KiB.
+template <int RT, bool kDirect = false>
+__device__ __forceinline__ void raw_block_staged(const AttnArgs& a, int task, int head, int split,
+                                                 uint8_t* lds, int slots) {
+  const int lane = threadIdx.x & 63;
+  const int wave = uniform(threadIdx.x >> 6);
+  const int n = lane & 15, g = lane >> 4;
+  RawSetup<RT> s;
+  if (!raw_setup(a, task, head, split, n, g, s)) return;
+  State<RT, 4> st;
+  state_init(st);
+  const uint32_t base = lds_addr(lds);
+  const int nblk = s.begin < s.end ? cdiv(s.end - s.begin, kBlock) : 0;
+  int issued = 0;
+#pragma unroll 1
+  for (int b = 0; b < nblk; ++b) {
+    // Top the ring up (all slots at the first block, then the slot block b - 1 freed).
+#pragma unroll 1
+    for (; issued < nblk && issued < b + slots; ++issued)
+      raw_stage_block(a, s.t, s.r, head, s.begin + kBlock * issued, s.end, wave, lane,
+                      base + kRawSlotBytes * (issued % slots));
+    raw_wait_blocks(issued - b - 1);
+    const int t0 = s.begin + kBlock * b;
+    const uint8_t* slot = lds + kRawSlotBytes * (b % slots);
+    f32x4 sc[RT][2];
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
-      for (int e = 0; e < 8; ++e) ok[rt][e] = cur.live[e] && cur.pos[e] <= t.prefix + qi_row[rt];
-    u32x4 ap[RT];
-    block_softmax(st, sc, ok, a.scale_log2, g, ap);
+      for (int tt = 0; tt < 2; ++tt) sc[rt][tt] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int jj = 0; jj < 4; ++jj) {
-      uint32_t vd2[8];
+    for (int m = 0; m < 8; ++m)
 #pragma unroll
-      for (int e = 0; e < 8; ++e) vd2[e] = (jj >> 1) ? cur.vq[e].y : cur.vq[e].x;
-      const u32x4 bv = pv_operand(vd2, jj);
+      for (int tt = 0; tt < 2; ++tt) {
+        const u32x4 kd = *reinterpret_cast<const u32x4*>(
+            slot + (16 * tt + n) * 512 + 16 * ((8 * g + m) ^ (n & 7)));
 #pragma unroll
-      for (int rt = 0; rt < RT; ++rt) st.o[rt][jj] = mfma16x16x32(ap[rt], bv, st.o[rt][jj]);
-    }
-    if (more) cur = nxt;
-  }
-  // Normalize: lane (n, g) holds rows 4 g + v, dims 16 n + 4 wave + jj.
-#pragma unroll
-  for (int rt = 0; rt < RT; ++rt) {
-    const float den_n = row_sum(st.psum[rt]);
-#pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      const int row = 16 * rt + 4 * g + v;
-      const float den = fmaxf(__shfl(den_n, 4 * g + v, kWave), 1.0e-30f);
-      const RowInfo ri = row_info(a, t, head, row);
-      if (!ri.valid) continue;
-      const int d = 16 * n + 4 * wave;
-      const float o0 = st.o[rt][0][v] / den, o1 = st.o[rt][1][v] / den;
-      const float o2 = st.o[rt][2][v] / den, o3 = st.o[rt][3][v] / den;
-      if constexpr (kDirect) {
-        const int64_t out_row = ri.token * a.hq + ri.qhead;
-        *reinterpret_cast<uint2*>(a.direct_out + out_row * kHeadDim + d) =
-            make_uint2(pack_bf16x2(o0, o1), pack_bf16x2(o2, o3));
-      } else {
-        const int64_t orow = (ri.token * a.hq + ri.qhead) * a.splits + split;
-        *reinterpret_cast<float4*>(a.partials + orow * kHeadDim + d) = make_float4(o0, o1, o2, o3);
+        for (int rt = 0; rt < RT; ++rt) sc[rt][tt] = mfma16x16x32(kd, s.qb[rt][m], sc[rt][tt]);
       }
+    // Positions of the block's rows (lane l: row l % 32); INT_MAX marks a row without a
+    // token, which fails every mask as raw_block's `live` does.
+    const uint16_t *kp_unused, *vp_unused;
+    const int row_pos = raw_row(a, s.t, s.r, head, t0 + (lane & 31), s.end, kp_unused, vp_unused);
+    int pos[8];
+    bool live[8];
+    uint2 vq[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int tok = tau(g, e);
+      pos[e] = __shfl(row_pos, tok, kWave);
+      live[e] = pos[e] != 0x7fffffff;
+      const uint2 v = *reinterpret_cast<const uint2*>(slot + kRawHalfBytes + tok * 512 +
+                                                      32 * n + 8 * wave);
+      vq[e] = live[e] ? v : make_uint2(0u, 0u);
     }
-    // LSE of row n (wavefront 0, lane group 0).
-    if (wave == 0 && g == 0) {
-      const RowInfo ri = row_info(a, t, head, n + 16 * rt);
-      const float lse = row_lse(st.m[rt], den_n);
-      if constexpr (kDirect) {
-        if (ri.valid && a.direct_lse) a.direct_lse[ri.token * a.hq + ri.qhead] = lse;
-      } else {
-        if (ri.valid) a.lse[(ri.token * a.hq + ri.qhead) * a.splits + split] = lse;
-      }
-    }
+    raw_block_tail(st, sc, s, vq, pos, live, a.scale_log2, g);
+    if (issued < nblk) barrier_lds();  // every wavefront has read the slot refilled next
   }
+  raw_finish<RT, kDirect>(a, s, head, split, st, n, g, wave);
 }
 
 }  // namespace oscar

@@ -29,14 +29,16 @@ constexpr int kPostQuarterRows = 2;  // rows per column-quarter post-attention w
 
 template <int RT>
 __global__ __launch_bounds__(kThreads) void pre_attention_kernel(const PreArgs p) {
-  __shared__ __attribute__((aligned(16))) uint8_t smem[16 * kHeadDim * 2];  // K/V rotation tile
+  // K/V rotation tile of the store role, or the BF16 branch's K stages.
+  __shared__ __attribute__((aligned(16))) uint8_t smem[kRawSlots * kRawSlotBytes];
+  static_assert(16 * kHeadDim * 2 <= kRawSlots * kRawSlotBytes, "the store tile fits");
   const int bid = blockIdx.x;
   const AttnArgs& a = p.attn;
   if (bid < p.raw_wgs) {
     // BF16 branch: workgroup (task, kv head), one split.
     const int h = a.L.kv_heads;
     const int task = bid / h, head = bid - task * h;
-    raw_block<RT>(a, task, head, 0);
+    raw_block_staged<RT>(a, task, head, 0, smem, kRawSlots);
     return;
   }
   if (bid < p.raw_wgs + p.kv_wgs) {
