@@ -467,12 +467,20 @@ __device__ __forceinline__ void raw_stage_block(const AttnArgs& a, const Task& t
   raw_row(a, t, r, head, t0 + (lane & 31), end, kp, vp);
   kp = kp ? kp : a.query;
   vp = vp ? vp : a.query;
+  // All eight sources first (the shuffles complete together), then the eight DMAs.
+  const uint16_t* src[8];
+  const int piece = lane & 31;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int row = 2 * (4 * i + wave) + (lane >> 5);
+    src[2 * i] = shfl_ptr(kp, row) + 8 * (piece ^ (row & 7));
+    src[2 * i + 1] = shfl_ptr(vp, row) + 8 * piece;
+  }
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int seg = 4 * i + wave;
-    const int row = 2 * seg + (lane >> 5), piece = lane & 31;
-    dma_dwordx4(shfl_ptr(kp, row) + 8 * (piece ^ (row & 7)), slot + 1024 * seg);
-    dma_dwordx4(shfl_ptr(vp, row) + 8 * piece, slot + kRawHalfBytes + 1024 * seg);
+    dma_dwordx4(src[2 * i], slot + 1024 * seg);
+    dma_dwordx4(src[2 * i + 1], slot + kRawHalfBytes + 1024 * seg);
   }
 }
 
@@ -500,6 +508,13 @@ __device__ __forceinline__ void raw_block_staged(const AttnArgs& a, int task, in
   const int n = lane & 15, g = lane >> 4;
   RawSetup<RT> s;
   if (!raw_setup(a, task, head, split, n, g, s)) return;
+  // The query rows have landed before the ring's DMAs are issued: the compiler counts only
+  // its own loads, so a wait for them placed inside the block loop would also wait for the
+  // DMA of later blocks.
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+    for (int m = 0; m < 8; ++m) asm volatile("" ::"v"(s.qb[rt][m]));
   State<RT, 4> st;
   state_init(st);
   const uint32_t base = lds_addr(lds);
