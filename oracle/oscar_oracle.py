@@ -455,6 +455,17 @@ def _row_softmax(scores: np.ndarray, values: np.ndarray):
     return (p @ values) / den, m + math.log(den)
 
 
+def _chunk_cut(h, lo, length, chunk=64):
+    """History index of a token-bounded split boundary: history index h (position lo + h)
+    moved down to the chunk grid of absolute positions, the ends kept (this build's rule,
+    csrc/attention.h history_positions)."""
+    if h <= 0:
+        return 0
+    if h >= length:
+        return length
+    return max(lo, (lo + h) // chunk * chunk) - lo
+
+
 def attention_partials(q_bits, k_bits, v_bits, history, window, qstarts, seq_lens, table,
                        counts, tasks, task_count, geometry: Geometry, scale, splits, raw,
                        block_n=32, query_tile=4, programs=None, split_tokens=0):
@@ -466,8 +477,10 @@ def attention_partials(q_bits, k_bits, v_bits, history, window, qstarts, seq_len
     Rows not written by a live task stay NaN. Split ranges follow kernels.py:368-370.
     ``split_tokens`` > 0 (history only; this build's token-bounded rule, no reference
     counterpart): a request of ``length`` history tokens uses
-    ``min(splits, max(1, ceil(length / split_tokens)))`` splits with the same range rule; the
-    split slots above that get LSE -inf and keep NaN partials (never written).
+    ``min(splits, max(1, ceil(length / split_tokens)))`` splits with the same range rule,
+    except that every inner boundary moves down to the 64-token grid of absolute positions
+    (``_chunk_cut``); the split slots above that get LSE -inf and keep NaN partials (never
+    written).
     """
     n, hq, d = q_bits.shape
     h = geometry.kv_heads
@@ -551,6 +564,9 @@ def attention_partials(q_bits, k_bits, v_bits, history, window, qstarts, seq_len
                         continue
                     begin = split * tps * block_n
                     end = min((split + 1) * tps * block_n, length)
+                    if split_tokens and not raw:
+                        begin = _chunk_cut(begin, lo, length)
+                        end = _chunk_cut(end, lo, length)
                     sel = slice(begin, max(begin, end))
                     sc = keys[sel] @ q[token, qhead] * float(np.float32(scale))
                     mask = positions[sel] <= prefix + qi

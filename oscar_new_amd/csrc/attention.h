@@ -88,6 +88,33 @@ __device__ __forceinline__ int history_splits(const AttnArgs& a, int length) {
   return min(a.splits, max(1, cdiv(max(length, 0), a.split_tokens)));
 }
 
+// Absolute positions [p_lo, p_hi) of history split `split` of a task with `length` history
+// tokens (positions sink_len .. sink_len + length). The reference rule (split_tokens 0):
+// split_range's history-relative ranges (kernels.py:368-370) moved up by sink_len. The
+// token-bounded rule (split_tokens > 0, no reference counterpart) moves every inner boundary
+// down to the 64-token chunk grid of absolute positions: with a 4-token sink the reference
+// boundaries sit 4 tokens past a chunk boundary, so each split would touch 33 chunks of 64
+// (the chunk on each boundary read by both of its splits, one of the four wavefronts
+// streaming 9 chunks while the others stream 8); aligned, a full split is exactly 32.
+__device__ __forceinline__ void history_positions(const AttnArgs& a, const Task& t, int length,
+                                                  int nsplit, int split, int& p_lo, int& p_hi) {
+  int begin, end;
+  split_range(length, a.block_n, nsplit, split, begin, end);
+  if (a.split_tokens <= 0) {
+    p_lo = max(t.sink_len + begin, 0);
+    p_hi = t.sink_len + end;
+    return;
+  }
+  const int lo = t.sink_len, hi = t.sink_len + max(length, 0);
+  auto cut = [&](int h) {
+    if (h <= 0) return lo;
+    if (h >= length) return hi;
+    return max(lo, (lo + h) & ~63);
+  };
+  p_lo = cut(begin);
+  p_hi = cut(end);
+}
+
 struct RowInfo {
   bool valid;
   int qi, qhead;

@@ -159,9 +159,8 @@ __global__ __launch_bounds__(kThreads, 3 - RT) void history_kernel(const AttnArg
     write_unused_split(a, t, head, split);
     return;
   }
-  int begin, end;
-  split_range(length, a.block_n, nsplit, split, begin, end);
-  const int p_lo = max(t.sink_len + begin, 0), p_hi = t.sink_len + end;
+  int p_lo, p_hi;
+  history_positions(a, t, length, nsplit, split, p_lo, p_hi);
   const int lane = threadIdx.x & 63;
   const int wave = uniform(threadIdx.x >> 6);
   const int n = lane & 15, g = lane >> 4;
@@ -647,9 +646,8 @@ __device__ __forceinline__ void history_pair_body(const AttnArgs& a, const Finis
     if constexpr (!kFinish) write_unused_split(a, t, head, split);
     return;
   }
-  int begin, end;
-  split_range(length, a.block_n, nsplit, split, begin, end);
-  const int p_lo = max(t.sink_len + begin, 0), p_hi = t.sink_len + end;
+  int p_lo, p_hi;
+  history_positions(a, t, length, nsplit, split, p_lo, p_hi);
   const int lane = threadIdx.x & 63;
   const int wave = uniform(threadIdx.x >> 6);
   const int n = lane & 15, g = lane >> 4;

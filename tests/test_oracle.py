@@ -510,3 +510,23 @@ def test_cached_decode_reference_equals_hybrid_reference():
     np.testing.assert_allclose(lse, want_lse, atol=2e-4)
     rows = O.dequant_rows(history, [geo.slot_offset(geo.logical_slot(table[0], 50))])
     assert np.array_equal(rows[0], O.load_vec(history, geo.slot_offset(geo.logical_slot(table[0], 50))))
+
+
+@pytest.mark.parametrize("lo,length,nsplit,block_n", [(4, 32635, 16, 32), (4, 2000, 7, 32),
+                                                      (0, 1000, 5, 128), (3, 130, 40, 32),
+                                                      (4, 64, 3, 32)])
+def test_token_bounded_boundaries_sit_on_the_absolute_chunk_grid(lo, length, nsplit, block_n):
+    # The token-bounded split rule: the reference ranges (kernels.py:368-370) with each inner
+    # boundary moved down to a multiple of 64 in absolute positions (lo + history index).
+    tps = -(-(-(-length // block_n)) // nsplit)
+    cuts = []
+    for split in range(nsplit):
+        begin = split * tps * block_n
+        end = min((split + 1) * tps * block_n, length)
+        b, e = O.oscar_oracle._chunk_cut(begin, lo, length), O.oscar_oracle._chunk_cut(end, lo, length)
+        cuts.append((b, max(b, e)))
+        if 0 < begin < length:
+            assert (lo + b) % 64 == 0 or b == 0, (split, b)
+            assert 0 <= begin - b < 64
+    covered = [t for b, e in cuts for t in range(b, e)]
+    assert covered == list(range(length))  # contiguous, in order, each token once
