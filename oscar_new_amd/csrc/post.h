@@ -156,46 +156,56 @@ __device__ __forceinline__ void post_rows_map(const PostArgs& p, RowOf row_of, i
       [&](int, int64_t row, int col, uint16_t bits) { p.out[row * kHeadDim + col] = bits; });
 }
 
-// Rows [row0, min(row0 + R, p.rows)) (R <= 4, one per wavefront) for the 64 output columns
-// of `quarter`: wavefront w merges row w into LDS, then rotates the merged rows back for column
-// tile w of the quarter (16 columns) and merges them with the BF16 branch. The four quarter
-// workgroups of a row group each merge the same rows (the same bits) and read a quarter of
-// R_v, so that no workgroup streams all of R_v: a latency-bound workgroup's reads are limited
-// by its own outstanding requests, not by the memory system. Each output element takes the
-// arithmetic of rotate_merge (same operands, same MFMA k order, same path merge).
+// Rows [row0, min(row0 + R, p.rows)) (R <= 4, one per wavefront) for kQuarters quarters of
+// 64 output columns starting at `quarter`: wavefront w merges row w into LDS, then, per
+// quarter, rotates the merged rows back for column tile w of the quarter (16 columns) and
+// merges them with the BF16 branch. kQuarters 1 (few rows): the four quarter workgroups of a
+// row group each merge the same rows (the same bits) and read a quarter of R_v, so that no
+// workgroup streams all of R_v (a latency-bound workgroup's reads are limited by its own
+// outstanding requests). kQuarters 4 (many rows): one workgroup per row group merges once and
+// walks the four quarters, the next quarter's R_v columns and BF16 values requested before
+// the current quarter is computed. Each output element takes the arithmetic of rotate_merge
+// (same operands, same MFMA k order, same path merge).
 // kMode: the split merge of the launch (merge_mode): one round or a scan per wavefront-row,
 // or (R = 1) the four wavefronts merging the row together, as the other post paths do.
-template <int R, int kMode>
+template <int R, int kMode, int kQuarters = 1>
 __device__ __forceinline__ void post_rows_quarter(const PostArgs& p, int64_t row0, int quarter,
                                                   uint16_t (*s_h)[kHeadDim], float* s_l,
                                                   GroupMergeLds* group_lds) {
   static_assert(R >= 1 && R <= 4, "one merged row per wavefront");
   static_assert(kMode != kMergeScanGroup || R == 1, "a workgroup-row merge serves one row");
+  static_assert(kQuarters == 1 || kQuarters == 4, "one quarter or all four");
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int n = lane & 15, g = lane >> 4;
   const int64_t end = min(row0 + R, p.rows);
-  const int col = 64 * quarter + 16 * wave + n;
-  RotateOperands op;
-  rotate_load_b<true>(op, p.rv + static_cast<int64_t>(col) * kHeadDim, 1, g);
-  u32x4 rb[8];
-#pragma unroll
-  for (int m = 0; m < 8; ++m) rb[m] = op.b[m];
   const int active = p.counts[1];
-  // BF16-branch value and LSE of this lane's rows 4g + v at column `col`.
   int64_t row[4];
   bool valid[4];
-  float bv[4], lb[4];
 #pragma unroll
   for (int v = 0; v < 4; ++v) {
     const int r = 4 * g + v;
     row[v] = r < R && row0 + r < end ? row0 + r : -1;
-    const int64_t lrow = row[v] >= 0 ? row[v] : 0;
     valid[v] = row[v] >= 0 && row[v] / p.hq < active;
-    const float l = p.rl[lrow];
-    const float x = p.rp[lrow * kHeadDim + col];
-    lb[v] = valid[v] ? l : -INFINITY;
-    bv[v] = valid[v] ? x : 0.f;
   }
+  // R_v columns and BF16-branch values and LSEs of this lane's rows 4g + v at column `col`.
+  auto load_quarter = [&](int q, u32x4 (&rb)[8], float (&bv)[4], float (&lb)[4]) {
+    const int col = 64 * q + 16 * wave + n;
+    RotateOperands op;
+    rotate_load_b<true>(op, p.rv + static_cast<int64_t>(col) * kHeadDim, 1, g);
+#pragma unroll
+    for (int m = 0; m < 8; ++m) rb[m] = op.b[m];
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int64_t lrow = row[v] >= 0 ? row[v] : 0;
+      const float l = p.rl[lrow];
+      const float x = p.rp[lrow * kHeadDim + col];
+      lb[v] = valid[v] ? l : -INFINITY;
+      bv[v] = valid[v] ? x : 0.f;
+    }
+  };
+  u32x4 rb[8];
+  float bv[4], lb[4];
+  load_quarter(quarter, rb, bv, lb);
   if constexpr (kMode == kMergeScanGroup) {
     const bool in = row0 < end;
     const SplitMerge m = merge_splits_row_group(p.hp + (in ? row0 : 0) * p.splits * kHeadDim,
@@ -218,17 +228,35 @@ __device__ __forceinline__ void post_rows_quarter(const PostArgs& p, int64_t row
     if (lane == 0) s_l[wave] = merge_splits_lse(m);
   }
   __syncthreads();
+  RotateOperands op;
   rotate_load_a<true>(op, n < R ? &s_h[n][0] : nullptr, 1, g);
-  const f32x4 acc = rotate_mfma(op.a, rb);
+#pragma unroll 1
+  for (int qq = 0; qq < kQuarters; ++qq) {
+    const int q = quarter + qq;
+    const int col = 64 * q + 16 * wave + n;
+    u32x4 rb_next[8];
+    float bv_next[4], lb_next[4];
+    if (kQuarters > 1 && qq + 1 < kQuarters) load_quarter(q + 1, rb_next, bv_next, lb_next);
+    const f32x4 acc = rotate_mfma(op.a, rb);
 #pragma unroll
-  for (int v = 0; v < 4; ++v) {
-    const int r = 4 * g + v;
-    if (r >= R || row[v] < 0) continue;
-    const PathWeights w = path_weights(valid[v] ? s_l[r] : -INFINITY, lb[v]);
-    const float av = valid[v] ? bf16_to_float(float_to_bf16(acc[v])) : 0.f;
-    p.out[row[v] * kHeadDim + col] =
-        static_cast<uint16_t>(float_to_bf16(path_merge(w, av, bv[v])));
-    if (p.merged_lse && quarter == 0 && wave == 0 && n == 0) p.merged_lse[row[v]] = path_lse(w);
+    for (int v = 0; v < 4; ++v) {
+      const int r = 4 * g + v;
+      if (r >= R || row[v] < 0) continue;
+      const PathWeights w = path_weights(valid[v] ? s_l[r] : -INFINITY, lb[v]);
+      const float av = valid[v] ? bf16_to_float(float_to_bf16(acc[v])) : 0.f;
+      p.out[row[v] * kHeadDim + col] =
+          static_cast<uint16_t>(float_to_bf16(path_merge(w, av, bv[v])));
+      if (p.merged_lse && q == 0 && wave == 0 && n == 0) p.merged_lse[row[v]] = path_lse(w);
+    }
+    if (kQuarters > 1 && qq + 1 < kQuarters) {
+#pragma unroll
+      for (int m = 0; m < 8; ++m) rb[m] = rb_next[m];
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        bv[v] = bv_next[v];
+        lb[v] = lb_next[v];
+      }
+    }
   }
 }
 

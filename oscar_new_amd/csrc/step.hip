@@ -26,6 +26,8 @@ namespace oscar {
 namespace {
 
 constexpr int kPostQuarterRows = 2;  // rows per column-quarter post-attention workgroup
+constexpr int kPostWideRows = 4;     // rows per all-quarter workgroup (many rows)
+constexpr int64_t kPostWideFrom = 512;  // rows from which a workgroup walks all four quarters
 
 template <int RT>
 __global__ __launch_bounds__(kThreads) void pre_attention_kernel(const PreArgs p) {
@@ -54,18 +56,19 @@ __global__ __launch_bounds__(kThreads) void pre_attention_kernel(const PreArgs p
 // scanned split merge per wavefront-row; R = 1: the four wavefronts merge the row together).
 // The remaining workgroups store the window of one request each; both branches have read the
 // window before this launch, and the merges do not touch it.
-// Grid (merge_wgs + requests, 4): workgroup (x, y < 4) serves R rows (merge_mode's rule: R = 1
-// for a workgroup-row merge) for output columns [64 y, 64 y + 64); the window workgroups are
-// those of y = 0; both branches have read the window before this launch, and the merges do
-// not touch it.
-template <int R, int kMode>
+// Grid (merge_wgs + requests, kQuarters == 1 ? 4 : 1): workgroup (x, y) serves R rows
+// (merge_mode's rule: R = 1 for a workgroup-row merge) for output columns [64 y, 64 y + 64),
+// or for all 256 columns when kQuarters is 4 (many rows: one merge per row instead of four,
+// and a quarter of the workgroups); the window workgroups are those of y = 0; both branches
+// have read the window before this launch, and the merges do not touch it.
+template <int R, int kMode, int kQuarters = 1>
 __global__ __launch_bounds__(kThreads) void post_attention_kernel(const PostArgs p) {
   __shared__ __attribute__((aligned(16))) uint16_t s_h[R][kHeadDim];  // merged history rows
   __shared__ float s_l[R];
   __shared__ GroupMergeLds group_lds;
   if (static_cast<int>(blockIdx.x) < p.merge_wgs) {
-    post_rows_quarter<R, kMode>(p, static_cast<int64_t>(blockIdx.x) * R, blockIdx.y, s_h, s_l,
-                                &group_lds);
+    post_rows_quarter<R, kMode, kQuarters>(p, static_cast<int64_t>(blockIdx.x) * R,
+                                           blockIdx.y, s_h, s_l, &group_lds);
     return;
   }
   if (blockIdx.y != 0) return;
@@ -316,13 +319,20 @@ extern "C" int oscar_post_attention(
                                 table_stride, max_reqs, layout, &p);
   if (st != OSCAR_OK || n == 0) return st;
   const int mode = merge_mode(p.rows, splits);
-  const int rows_per_wg = mode == kMergeScanGroup ? 1 : kPostQuarterRows;
+  const bool wide = mode != kMergeScanGroup && p.rows >= kPostWideFrom;
+  const int rows_per_wg = mode == kMergeScanGroup ? 1 : wide ? kPostWideRows : kPostQuarterRows;
   const int64_t groups = (p.rows + rows_per_wg - 1) / rows_per_wg;
   if (groups + p.win_requests > 0x7fffffffll) return OSCAR_E_SHAPE;
   p.merge_wgs = static_cast<int32_t>(groups);
-  const dim3 grid(static_cast<unsigned>(groups + p.win_requests), 4);
+  const dim3 grid(static_cast<unsigned>(groups + p.win_requests), wide ? 1 : 4);
   hipStream_t s = as_stream(stream);
-  if (mode == kMergeOneRound)
+  if (wide && mode == kMergeOneRound)
+    hipLaunchKernelGGL((post_attention_kernel<kPostWideRows, kMergeOneRound, 4>), grid,
+                       dim3(kThreads), 0, s, p);
+  else if (wide)
+    hipLaunchKernelGGL((post_attention_kernel<kPostWideRows, kMergeScanWave, 4>), grid,
+                       dim3(kThreads), 0, s, p);
+  else if (mode == kMergeOneRound)
     hipLaunchKernelGGL((post_attention_kernel<kPostQuarterRows, kMergeOneRound>), grid,
                        dim3(kThreads), 0, s, p);
   else if (mode == kMergeScanWave)
