@@ -12,7 +12,7 @@ namespace {
 
 template <int RT>
 __global__ __launch_bounds__(kThreads) void raw_kernel(const AttnArgs a) {
-  __shared__ __attribute__((aligned(16))) uint8_t ring[kRawSlots * kRawSlotBytes];
+  __shared__ __attribute__((aligned(16))) uint8_t ring[kRawSlots * kRawLdsPerSlot];
   raw_block_staged<RT>(a, blockIdx.x, blockIdx.y, blockIdx.z, ring, kRawSlots);
 }
 

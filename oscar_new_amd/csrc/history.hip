@@ -622,7 +622,7 @@ __device__ __forceinline__ void history_pair_body(const AttnArgs& a, const Finis
     if (z < role_slices) {
       if (z == 0) {
         raw_block_staged<1>(pre->attn, blockIdx.x, blockIdx.y, 0, s_ring,
-                            kRingBytes / kRawSlotBytes);
+                            kRingBytes / kRawLdsPerSlot);
       } else {
         const int r = ((z - 1) * static_cast<int>(gridDim.x) + static_cast<int>(blockIdx.x)) *
                           static_cast<int>(gridDim.y) + static_cast<int>(blockIdx.y);

@@ -452,19 +452,24 @@ __device__ __forceinline__ void raw_block(const AttnArgs& a, int task, int head,
 // different bank quads; V row i at 16 KiB + 512 i, plain.
 constexpr int kRawHalfBytes = kBlock * kHeadDim * 2;
 constexpr int kRawSlotBytes = 2 * kRawHalfBytes;
+// After the slots: each slot's 32 row positions (INT_MAX for a row without a token).
+constexpr int kRawPosBytes = kBlock * 4;
+constexpr int kRawLdsPerSlot = kRawSlotBytes + kRawPosBytes;
 // Slots where the launch has the LDS to spare (4 x 32 KiB).
 constexpr int kRawSlots = 4;
 
 // DMA of block t0's K and V rows into `slot`: 2 x 16 KiB, 4 x 1 KiB per wavefront each.
 // Lane l resolves row l % 32 once (raw_row) and the DMA lanes fetch their rows' pointers
-// from it. Every lane issues (a row without a token copies the query row; its score and P
-// are masked and its V operand is replaced by zeros), so every wavefront counts 8 loads per
-// block.
+// from it; lanes 0..31 of wavefront 0 also store the rows' positions at `pos_table`. Every
+// lane issues (a row without a token copies the query row; its score and P are masked and
+// its V operand is replaced by zeros), so every wavefront counts 8 loads per block.
 __device__ __forceinline__ void raw_stage_block(const AttnArgs& a, const Task& t,
                                                 const RawTask& r, int head, int t0, int end,
-                                                int wave, int lane, uint32_t slot) {
+                                                int wave, int lane, uint32_t slot,
+                                                int* pos_table) {
   const uint16_t *kp, *vp;
-  raw_row(a, t, r, head, t0 + (lane & 31), end, kp, vp);
+  const int row_pos = raw_row(a, t, r, head, t0 + (lane & 31), end, kp, vp);
+  if (wave == 0 && lane < 32) pos_table[lane] = row_pos;
   kp = kp ? kp : a.query;
   vp = vp ? vp : a.query;
   // All eight sources first (the shuffles complete together), then the eight DMAs.
@@ -484,14 +489,15 @@ __device__ __forceinline__ void raw_stage_block(const AttnArgs& a, const Task& t
   }
 }
 
-// Wait until at most `ahead` blocks (8 loads each) of this wavefront are still in flight,
-// then meet the workgroup: every wavefront's share of the oldest block has landed.
+// Wait until at most `ahead` blocks (8 loads each) of this wavefront are still in flight
+// and its LDS stores (the position tables) are done, then meet the workgroup: every
+// wavefront's share of the oldest block has landed.
 __device__ __forceinline__ void raw_wait_blocks(int ahead) {
   switch (ahead) {
-    case 0: asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory"); break;
-    case 1: asm volatile("s_waitcnt vmcnt(8)\n\ts_barrier" ::: "memory"); break;
-    case 2: asm volatile("s_waitcnt vmcnt(16)\n\ts_barrier" ::: "memory"); break;
-    default: asm volatile("s_waitcnt vmcnt(24)\n\ts_barrier" ::: "memory"); break;
+    case 0: asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory"); break;
+    case 1: asm volatile("s_waitcnt vmcnt(8) lgkmcnt(0)\n\ts_barrier" ::: "memory"); break;
+    case 2: asm volatile("s_waitcnt vmcnt(16) lgkmcnt(0)\n\ts_barrier" ::: "memory"); break;
+    default: asm volatile("s_waitcnt vmcnt(24) lgkmcnt(0)\n\ts_barrier" ::: "memory"); break;
   }
 }
 
@@ -499,7 +505,7 @@ __device__ __forceinline__ void raw_wait_blocks(int ahead) {
 // slots by DMA, up to `slots` blocks in flight. The arithmetic is raw_block's, block for
 // block: the same bits. The block loop is not unrolled: a launch runs this code cold, so its
 // size, not its instruction count, sets the time of the first block. Every thread of the
-// workgroup calls this; `lds` holds slots x 32 KiB.
+// workgroup calls this; `lds` holds slots x kRawLdsPerSlot bytes.
 template <int RT, bool kDirect = false>
 __device__ __forceinline__ void raw_block_staged(const AttnArgs& a, int task, int head, int split,
                                                  uint8_t* lds, int slots) {
@@ -518,6 +524,7 @@ __device__ __forceinline__ void raw_block_staged(const AttnArgs& a, int task, in
   State<RT, 4> st;
   state_init(st);
   const uint32_t base = lds_addr(lds);
+  int* pos_tables = reinterpret_cast<int*>(lds + kRawSlotBytes * slots);
   const int nblk = s.begin < s.end ? cdiv(s.end - s.begin, kBlock) : 0;
   int issued = 0;
 #pragma unroll 1
@@ -526,7 +533,8 @@ __device__ __forceinline__ void raw_block_staged(const AttnArgs& a, int task, in
 #pragma unroll 1
     for (; issued < nblk && issued < b + slots; ++issued)
       raw_stage_block(a, s.t, s.r, head, s.begin + kBlock * issued, s.end, wave, lane,
-                      base + kRawSlotBytes * (issued % slots));
+                      base + kRawSlotBytes * (issued % slots),
+                      pos_tables + kBlock * (issued % slots));
     raw_wait_blocks(issued - b - 1);
     const int t0 = s.begin + kBlock * b;
     const uint8_t* slot = lds + kRawSlotBytes * (b % slots);
@@ -544,17 +552,18 @@ __device__ __forceinline__ void raw_block_staged(const AttnArgs& a, int task, in
 #pragma unroll
         for (int rt = 0; rt < RT; ++rt) sc[rt][tt] = mfma16x16x32(kd, s.qb[rt][m], sc[rt][tt]);
       }
-    // Positions of the block's rows (lane l: row l % 32); INT_MAX marks a row without a
-    // token, which fails every mask as raw_block's `live` does.
-    const uint16_t *kp_unused, *vp_unused;
-    const int row_pos = raw_row(a, s.t, s.r, head, t0 + (lane & 31), s.end, kp_unused, vp_unused);
-    int pos[8];
+    // Positions of the lane's eight tokens (4 g .. 4 g + 3 and 16 + 4 g .. 16 + 4 g + 3) from
+    // the slot's table; INT_MAX marks a row without a token, which fails every mask as
+    // raw_block's `live` does.
+    const int* table = pos_tables + kBlock * (b % slots);
+    const int4 p_lo = *reinterpret_cast<const int4*>(table + 4 * g);
+    const int4 p_hi = *reinterpret_cast<const int4*>(table + 16 + 4 * g);
+    const int pos[8] = {p_lo.x, p_lo.y, p_lo.z, p_lo.w, p_hi.x, p_hi.y, p_hi.z, p_hi.w};
     bool live[8];
     uint2 vq[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       const int tok = tau(g, e);
-      pos[e] = __shfl(row_pos, tok, kWave);
       live[e] = pos[e] != 0x7fffffff;
       const uint2 v = *reinterpret_cast<const uint2*>(slot + kRawHalfBytes + tok * 512 +
                                                       32 * n + 8 * wave);

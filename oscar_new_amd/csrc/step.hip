@@ -32,8 +32,8 @@ constexpr int64_t kPostWideFrom = 512;  // rows from which a workgroup walks all
 template <int RT>
 __global__ __launch_bounds__(kThreads) void pre_attention_kernel(const PreArgs p) {
   // K/V rotation tile of the store role, or the BF16 branch's K stages.
-  __shared__ __attribute__((aligned(16))) uint8_t smem[kRawSlots * kRawSlotBytes];
-  static_assert(16 * kHeadDim * 2 <= kRawSlots * kRawSlotBytes, "the store tile fits");
+  __shared__ __attribute__((aligned(16))) uint8_t smem[kRawSlots * kRawLdsPerSlot];
+  static_assert(16 * kHeadDim * 2 <= kRawSlots * kRawLdsPerSlot, "the store tile fits");
   const int bid = blockIdx.x;
   const AttnArgs& a = p.attn;
   if (bid < p.raw_wgs) {
