@@ -296,7 +296,27 @@ struct RawSetup {
   int qi_row[RT];
 };
 
+// The unrotated query rows of the workgroup's row tiles (lane (n, g): row n + 16 rt, dims
+// 64 g .. 64 g + 63), zeros for rows that are not live.
 template <int RT>
+__device__ __forceinline__ void raw_load_query(const AttnArgs& a, int head, int n, int g,
+                                               RawSetup<RT>& s) {
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt) {
+    const RowInfo ri = row_info(a, s.t, head, n + 16 * rt);
+    s.qi_row[rt] = ri.qi;
+#pragma unroll
+    for (int m = 0; m < 8; ++m) s.qb[rt][m] = u32x4{0u, 0u, 0u, 0u};
+    if (ri.valid) {
+      const uint16_t* qp = a.query + ri.token * a.qs0 + ri.qhead * a.qs1 + 64 * g;
+#pragma unroll
+      for (int m = 0; m < 8; ++m) s.qb[rt][m] = *reinterpret_cast<const u32x4*>(qp + 8 * m);
+    }
+  }
+}
+
+// kQuery false: the query rows are left to the caller (raw_load_query).
+template <int RT, bool kQuery = true>
 __device__ __forceinline__ bool raw_setup(const AttnArgs& a, int task, int head, int split,
                                           int n, int g, RawSetup<RT>& s) {
   if (!read_task(a, s.t, task)) return false;
@@ -312,18 +332,7 @@ __device__ __forceinline__ bool raw_setup(const AttnArgs& a, int task, int head,
     s.r.win = owner * (a.L.page_bytes / 2) + static_cast<int64_t>(head) * kHeadDim;
   }
   split_range(s.r.high + t.qlen, a.block_n, a.splits, split, s.begin, s.end);
-#pragma unroll
-  for (int rt = 0; rt < RT; ++rt) {
-    const RowInfo ri = row_info(a, t, head, n + 16 * rt);
-    s.qi_row[rt] = ri.qi;
-#pragma unroll
-    for (int m = 0; m < 8; ++m) s.qb[rt][m] = u32x4{0u, 0u, 0u, 0u};
-    if (ri.valid) {
-      const uint16_t* qp = a.query + ri.token * a.qs0 + ri.qhead * a.qs1 + 64 * g;
-#pragma unroll
-      for (int m = 0; m < 8; ++m) s.qb[rt][m] = *reinterpret_cast<const u32x4*>(qp + 8 * m);
-    }
-  }
+  if constexpr (kQuery) raw_load_query(a, head, n, g, s);
   return true;
 }
 
@@ -513,28 +522,34 @@ __device__ __forceinline__ void raw_block_staged(const AttnArgs& a, int task, in
   const int wave = uniform(threadIdx.x >> 6);
   const int n = lane & 15, g = lane >> 4;
   RawSetup<RT> s;
-  if (!raw_setup(a, task, head, split, n, g, s)) return;
-  // The query rows have landed before the ring's DMAs are issued: the compiler counts only
-  // its own loads, so a wait for them placed inside the block loop would also wait for the
-  // DMA of later blocks.
-#pragma unroll
-  for (int rt = 0; rt < RT; ++rt)
-#pragma unroll
-    for (int m = 0; m < 8; ++m) asm volatile("" ::"v"(s.qb[rt][m]));
+  if (!raw_setup<RT, false>(a, task, head, split, n, g, s)) return;
   State<RT, 4> st;
   state_init(st);
   const uint32_t base = lds_addr(lds);
   int* pos_tables = reinterpret_cast<int*>(lds + kRawSlotBytes * slots);
   const int nblk = s.begin < s.end ? cdiv(s.end - s.begin, kBlock) : 0;
   int issued = 0;
-#pragma unroll 1
-  for (int b = 0; b < nblk; ++b) {
-    // Top the ring up (all slots at the first block, then the slot block b - 1 freed).
+  // Top the ring up (all slots at the first block, then the slot block b - 1 freed).
+  auto top_up = [&](int b) {
 #pragma unroll 1
     for (; issued < nblk && issued < b + slots; ++issued)
       raw_stage_block(a, s.t, s.r, head, s.begin + kBlock * issued, s.end, wave, lane,
                       base + kRawSlotBytes * (issued % slots),
                       pos_tables + kBlock * (issued % slots));
+  };
+  top_up(0);
+  // The query rows are requested after the first blocks and consumed here, before the block
+  // loop: the compiler counts only its own loads, so a wait for them placed inside the loop
+  // would also wait for the DMA of later blocks; here it waits for the blocks in flight,
+  // which landed about when the rows did.
+  raw_load_query(a, head, n, g, s);
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+    for (int m = 0; m < 8; ++m) asm volatile("" ::"v"(s.qb[rt][m]));
+#pragma unroll 1
+  for (int b = 0; b < nblk; ++b) {
+    top_up(b);
     raw_wait_blocks(issued - b - 1);
     const int t0 = s.begin + kBlock * b;
     const uint8_t* slot = lds + kRawSlotBytes * (b % slots);
