@@ -135,9 +135,16 @@ int oscar_prepare_tasks(const int32_t* qstarts, const int32_t* counts, int32_t* 
  * Split boundaries follow kernels.py:368-370 with block_n tokens per tile.
  * split_tokens (history branch only; 0 = the reference rule above): a request with L history
  * tokens uses min(splits, max(1, ceil(L / split_tokens))) splits, its ranges following the
- * same rule with that count; the split slots above it get lse -inf and no partial row (no
+ * same rule with that count except that inner boundaries move down to the 64-token grid of
+ * absolute positions; the split slots above it get lse -inf and no partial row (no
  * reference counterpart: for ragged batches, whose long requests would otherwise hold the
  * whole launch). raw != 0 requires split_tokens == 0.
+ * queue_counters: NULL, or two int32 counters, zero before the first call, that a launch
+ * leaves zero again (no reference counterpart). With them, a history launch of 17-32 rows
+ * per task with split_tokens > 0 and programs <= 2048 runs as a work queue (one workgroup
+ * per CU taking the (task, split) units in use, instead of a grid of mostly empty
+ * workgroups); the outputs are the same bits. Launches that overlap on one device must not
+ * share counters.
  * max_query_len: host upper bound on query tokens per request (0 = unknown). Only
  * min(query_tile, max_query_len) * (hq / H) rows per task are computed, so a decode step
  * (max_query_len 1) does not pay for the query_tile padding; it must not undercount.
@@ -153,7 +160,7 @@ int oscar_attention_partials(const void* query, int64_t q_s0, int64_t q_s1, int6
                              int64_t hq, int64_t programs, int32_t splits, int32_t block_n,
                              int32_t query_tile, int32_t max_query_len, float scale, int32_t raw,
                              int32_t split_tokens, const oscar_layout* layout, float* partials,
-                             float* lse, void* stream);
+                             float* lse, int32_t* queue_counters, void* stream);
 
 /*
  * merge_splits -- replaces kernels.py:506-511 `merge_splits(partials, lse, counts)`.

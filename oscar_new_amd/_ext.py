@@ -67,7 +67,7 @@ SIGNATURES = {
         _P, _P, _P,  # counts, tasks, task_count
         _I64, _I64, _I64, _I32, _I32, _I32, _I32, _F, _I32,  # n hq programs splits bn qt mql scale raw
         _I32,  # split_tokens
-        POINTER(OscarLayout), _P, _P, _P,
+        POINTER(OscarLayout), _P, _P, _P, _P,  # layout, partials, lse, queue counters, stream
     ],
     "oscar_merge_splits": [_P, _P, _P, _I64, _I64, _I32, _I32, _P, _P, _P],
     "oscar_merge_paths": [_P, _P, _P, _P, _P, _I64, _I64, _I32, _P, _P, _P],

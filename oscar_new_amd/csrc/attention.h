@@ -143,7 +143,10 @@ __device__ __forceinline__ void write_unused_split(const AttnArgs& a, const Task
 }
 
 // INT2 history branch (history.hip); rows = query rows per task (<= 32).
-hipError_t launch_history(const AttnArgs& a, dim3 grid, int rows, hipStream_t stream);
+// `queue`: two zeroed int32 counters for the work-queue form of the 9-32-row kernel
+// (token-bounded splits), or nullptr for the grid form.
+hipError_t launch_history(const AttnArgs& a, dim3 grid, int rows, hipStream_t stream,
+                          int32_t* queue = nullptr);
 
 // The checks and fields of one attention_partials launch (attention.hip): OSCAR_OK with *out
 // filled and *qrows = query rows per task, or the entry point's error code. Nothing is

@@ -113,7 +113,7 @@ extern "C" int oscar_attention_partials(
     const int32_t* task_count, int64_t n, int64_t hq, int64_t programs, int32_t splits,
     int32_t block_n, int32_t query_tile, int32_t max_query_len, float scale, int32_t raw,
     int32_t split_tokens, const oscar_layout* layout, float* partials, float* lse,
-    void* stream) {
+    int32_t* queue_counters, void* stream) {
   using namespace oscar;
   AttnArgs a;
   int64_t qrows = 0;
@@ -127,7 +127,8 @@ extern "C" int oscar_attention_partials(
   const dim3 grid(static_cast<unsigned>(programs), static_cast<unsigned>(a.L.kv_heads),
                   static_cast<unsigned>(splits));
   hipStream_t s = as_stream(stream);
-  if (!raw) return static_cast<int>(launch_history(a, grid, static_cast<int>(qrows), s));
+  if (!raw)
+    return static_cast<int>(launch_history(a, grid, static_cast<int>(qrows), s, queue_counters));
   if (qrows <= 16)
     hipLaunchKernelGGL(raw_kernel<1>, grid, dim3(kThreads), 0, s, a);
   else

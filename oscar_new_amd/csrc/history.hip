@@ -141,18 +141,27 @@ __host__ __device__ constexpr int p_token(int g, int e) { return 16 * (e >> 2) +
 // to the first transposed read and p_token(2 (G&1) + 1, n) to the second. One E8M0 scale per
 // query row covers all four scale blocks: the scale of k block kb is read from lane group kb,
 // while an FP8 lane group G holds its bytes 0..15 in block G / 2 and 16..31 in block 2 + G / 2.
+// LDS of one general-kernel workgroup.
 template <int RT>
-__global__ __launch_bounds__(kThreads, 3 - RT) void history_kernel(const AttnArgs a) {
-  __shared__ __attribute__((aligned(16))) uint8_t s_ring[kRingBytes];
-  __shared__ uint32_t s_off[kTableCache];
-  __shared__ float s_red[3][4][RT * 16];  // per wavefront: row max, sum p, sum p z_v
+struct HistoryLds {
+  uint8_t ring[kRingBytes] __attribute__((aligned(16)));
+  uint32_t off[kTableCache];
+  float red[3][4][RT * 16];  // per wavefront: row max, sum p, sum p z_v
+};
+
+// One (task, kv head, split) unit of the general kernel; the whole workgroup calls it.
+template <int RT>
+__device__ __forceinline__ void history_unit(const AttnArgs& a, int task, int head, int split,
+                                             HistoryLds<RT>& lds) {
+  uint8_t* s_ring = lds.ring;
+  uint32_t* s_off = lds.off;
+  auto& s_red = lds.red;
   static_assert(RT * 16 * 512 <= 2 * kStageBytes, "query staging fits wavefront 3's stages");
   static_assert(2 * kQTerms * 64 * 32 <= 2 * kStageBytes, "query operands fit as well");
   static_assert(4 * 16 * 256 * 4 <= kRingBytes, "the epilogue merge fits the ring");
 
   Task t;
-  if (!read_task(a, t, blockIdx.x)) return;
-  const int head = blockIdx.y, split = blockIdx.z;
+  if (!read_task(a, t, task)) return;
   const int length = t.recent_begin - t.sink_len;
   const int nsplit = history_splits(a, length);
   if (split >= nsplit) {
@@ -546,6 +555,120 @@ __global__ __launch_bounds__(kThreads, 3 - RT) void history_kernel(const AttnArg
       if ((threadIdx.x & 15) == 0)
         a.lse[(ri.token * a.hq + ri.qhead) * a.splits + split] =
             den > 0.f ? (mx + log2f(den)) * kLn2 : -INFINITY;
+    }
+  }
+}
+
+template <int RT>
+__global__ __launch_bounds__(kThreads, 3 - RT) void history_kernel(const AttnArgs a) {
+  __shared__ HistoryLds<RT> lds;
+  history_unit<RT>(a, blockIdx.x, blockIdx.y, blockIdx.z, lds);
+}
+
+// The general kernel as a work queue (token-bounded splits, one workgroup per CU): a grid of
+// (task, kv head, split) workgroups is mostly empty when lengths are ragged (a request of L
+// history tokens uses ceil(L / split_tokens) of the split slots), and with one workgroup per
+// CU every empty workgroup holds a CU while it reads its task and exits. Here each
+// workgroup lists the units of every task (split counts from the task rows, an exclusive
+// scan in LDS), then takes units from a device counter until none are left: full splits
+// first, then each task's last (shorter) split. A unit is computed exactly as in the grid
+// form (the same bits). The split slots a task does not use get their -inf LSE from the
+// workgroups in task-stride order. The counters (next unit, finished workgroups) are zero at
+// launch; the last workgroup to finish sets them to zero again, so graph replays reuse them.
+// Launches that overlap on one device must not share counters.
+constexpr int kQueueTasks = 2048;  // task rows the workgroup lists in LDS
+
+template <int RT>
+__global__ __launch_bounds__(kThreads, 1) void history_queue_kernel(const AttnArgs a,
+                                                                     int32_t* counters,
+                                                                     int32_t programs) {
+  __shared__ HistoryLds<RT> lds;
+  __shared__ int32_t s_full[kQueueTasks + 1];  // full splits of the tasks before t
+  __shared__ int32_t s_nsplit[kQueueTasks];
+  __shared__ int16_t s_used[kQueueTasks];      // tasks in use, in order
+  __shared__ int32_t s_part[2][kThreads];      // per-thread sums, then their exclusive scan
+  __shared__ int32_t s_total[2];               // full splits, tasks in use
+  __shared__ int32_t s_claim;
+  const int heads = a.L.kv_heads;
+  // Split counts, then two exclusive scans (full splits, tasks in use) over thread chunks.
+  for (int task = threadIdx.x; task < programs; task += kThreads) {
+    Task t;
+    s_nsplit[task] = read_task(a, t, task) ? history_splits(a, t.recent_begin - t.sink_len) : 0;
+  }
+  __syncthreads();
+  const int per = (programs + kThreads - 1) / kThreads;
+  const int lo_t = min(static_cast<int>(threadIdx.x) * per, programs);
+  const int hi_t = min(lo_t + per, programs);
+  int fsum = 0, usum = 0;
+  for (int task = lo_t; task < hi_t; ++task) {
+    const int ns = s_nsplit[task];
+    fsum += max(ns - 1, 0);
+    usum += ns > 0;
+  }
+  s_part[0][threadIdx.x] = fsum;
+  s_part[1][threadIdx.x] = usum;
+  __syncthreads();
+  if (threadIdx.x < 2) {
+    int acc = 0;
+    for (int i = 0; i < kThreads; ++i) {
+      const int x = s_part[threadIdx.x][i];
+      s_part[threadIdx.x][i] = acc;
+      acc += x;
+    }
+    s_total[threadIdx.x] = acc;
+  }
+  __syncthreads();
+  int fbase = s_part[0][threadIdx.x], ubase = s_part[1][threadIdx.x];
+  for (int task = lo_t; task < hi_t; ++task) {
+    const int ns = s_nsplit[task];
+    s_full[task] = fbase;
+    fbase += max(ns - 1, 0);
+    if (ns > 0) s_used[ubase++] = static_cast<int16_t>(task);
+  }
+  if (threadIdx.x == 0) s_full[programs] = s_total[0];
+  __syncthreads();
+  const int full = s_total[0], used = s_total[1];
+  const int64_t units = (static_cast<int64_t>(full) + used) * heads;
+  for (;;) {
+    if (threadIdx.x == 0) s_claim = atomicAdd(&counters[0], 1);
+    __syncthreads();
+    const int64_t u = s_claim;
+    __syncthreads();  // every lane has read the claim (and the previous unit is done)
+    if (u >= units) break;
+    const int head = static_cast<int>(u % heads);
+    const int k = static_cast<int>(u / heads);
+    int task, split;
+    if (k < full) {
+      // The task that holds full split k: the last one whose first full split is <= k.
+      int lo = 0, hi = programs - 1;
+      while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (s_full[mid] <= k)
+          lo = mid;
+        else
+          hi = mid - 1;
+      }
+      task = lo;
+      split = k - s_full[task];
+    } else {
+      task = s_used[k - full];
+      split = s_nsplit[task] - 1;
+    }
+    history_unit<RT>(a, task, head, split, lds);
+  }
+  // Unused split slots: LSE -inf for the rows of every task in use.
+  for (int task = blockIdx.x; task < programs; task += gridDim.x) {
+    const int ns = s_nsplit[task];
+    if (ns <= 0) continue;
+    Task t;
+    if (!read_task(a, t, task)) continue;
+    for (int head = 0; head < heads; ++head)
+      for (int split = ns; split < a.splits; ++split) write_unused_split(a, t, head, split);
+  }
+  if (threadIdx.x == 0) {
+    if (atomicAdd(&counters[1], 1) == static_cast<int>(gridDim.x) - 1) {
+      atomicExch(&counters[0], 0);
+      atomicExch(&counters[1], 0);
     }
   }
 }
@@ -1141,13 +1264,27 @@ __global__ __launch_bounds__(kThreads, 2) void history_pre_kernel(const HistoryP
 
 }  // namespace
 
-hipError_t launch_history(const AttnArgs& a, dim3 grid, int rows, hipStream_t stream) {
-  if (rows <= 8)
+hipError_t launch_history(const AttnArgs& a, dim3 grid, int rows, hipStream_t stream,
+                          int32_t* queue) {
+  if (rows <= 8) {
     hipLaunchKernelGGL(history_pair_kernel, grid, dim3(kThreads), 0, stream, a);
-  else if (rows <= 16)
+  } else if (rows <= 16) {
     hipLaunchKernelGGL(history_kernel<1>, grid, dim3(kThreads), 0, stream, a);
-  else
+  } else if (queue != nullptr && a.split_tokens > 0 &&
+             static_cast<int64_t>(grid.x) <= kQueueTasks) {
+    int device = 0, cus = 0;
+    hipError_t e = hipGetDevice(&device);
+    if (e == hipSuccess)
+      e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device);
+    if (e != hipSuccess) return e;
+    const int64_t units = static_cast<int64_t>(grid.x) * grid.y * grid.z;
+    const int64_t cap = cus > 0 ? cus : 1;
+    const unsigned wgs = static_cast<unsigned>(units < cap ? units : cap);
+    hipLaunchKernelGGL(history_queue_kernel<2>, dim3(wgs), dim3(kThreads), 0, stream, a, queue,
+                       static_cast<int32_t>(grid.x));
+  } else {
     hipLaunchKernelGGL(history_kernel<2>, grid, dim3(kThreads), 0, stream, a);
+  }
   return hipGetLastError();
 }
 

@@ -201,7 +201,7 @@ def prepare_tasks(qstarts, counts, tasks, task_count, max_reqs, query_tile, num_
 
 
 def attention_partials(query, key, value, history, window, meta, layout, scale, splits, raw,
-                       split_tokens=0):
+                       split_tokens=0, use_queue=True):
     """Per-split partial attention and LSE of one branch (reference kernels.py:439-482).
 
     raw=False: INT2 history (``query`` must be the rotated query). raw=True: BF16 sink /
@@ -211,6 +211,9 @@ def attention_partials(query, key, value, history, window, meta, layout, scale, 
     ``split_tokens`` (history branch; no reference counterpart, 0 keeps kernels.py:368-370):
     a request with L history tokens uses min(splits, ceil(L / split_tokens)) splits and its
     remaining split slots get LSE -inf with no partial row, which the split merges skip.
+    ``use_queue`` (no reference counterpart): tasks of 17-32 rows with token-bounded splits
+    run as a work queue over the units in use (``queue_counters``); the same bits as the
+    grid form (``use_queue=False``).
     """
     if raw and split_tokens:
         raise ValueError("split_tokens applies to the history branch only")
@@ -249,7 +252,10 @@ def attention_partials(query, key, value, history, window, meta, layout, scale, 
             _ptr(_int32(meta.task_count, "task_count")),
             n, hq, programs, splits, cfg.block_n, cfg.queries_per_tile, max_query_len,
             float(scale), 1 if raw else 0, int(split_tokens), layout_struct(layout),
-            _ptr(partials), _ptr(lse), _stream(query),
+            _ptr(partials), _ptr(lse),
+            _ptr(queue_counters(meta, query.device))
+            if use_queue and not raw and split_tokens else None,
+            _stream(query),
         ),
         "attention_partials",
     )
@@ -432,6 +438,7 @@ def prefill_attention(query, key, value, window, meta, layout, scale, output, me
 
 
 _COUNTERS = {}
+_QUEUE_COUNTERS = {}
 DEFAULT_COUNTER_SLOTS = 1 << 16
 
 
@@ -451,6 +458,22 @@ def finish_counters(meta, device, slots):
     if buf.numel() < slots:
         raise ValueError(f"history_post needs {slots} completion counters; the buffer holds "
                          f"{buf.numel()}")
+    return buf
+
+
+def queue_counters(meta, device):
+    """The two int32 work-queue counters of a history launch: the metadata's own
+    (``meta.queue_counters``, allocated by the builder) or else one per-device buffer. Both
+    are zero at rest: every launch leaves them zero, and a captured graph keeps their address.
+    Launches that overlap on one device (two streams at once) must not share them."""
+    buf = getattr(meta, "queue_counters", None)
+    if buf is None:
+        buf = _QUEUE_COUNTERS.get(device)
+        if buf is None:
+            buf = torch.zeros(2, dtype=torch.int32, device=device)
+            _QUEUE_COUNTERS[device] = buf
+    if buf.numel() < 2 or buf.dtype != torch.int32:
+        raise ValueError("queue counters must be at least two int32 values")
     return buf
 
 

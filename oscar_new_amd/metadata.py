@@ -48,6 +48,7 @@ class OscarMetadata:
     total_seq_len: int | None = None  # host sum of seq_lens
     merged_lse: torch.Tensor | None = None  # optional [n, hq] output of the merged LSE
     finish_counters: torch.Tensor | None = None  # zeroed int32 slots of one-launch post
+    queue_counters: torch.Tensor | None = None  # two zeroed int32 work-queue counters
 
     @property
     def query_ends(self):
@@ -140,6 +141,9 @@ class OscarMetadataBuilder:
         # of the largest grid, allocated once (graphs keep the address), left zero by every
         # launch.
         self.finish_counters = torch.zeros(self.tasks.shape[0] * layout.kv_heads, **i32)
+        # Work-queue counters of the 17-32-row history launch (token-bounded splits), zero at
+        # rest like the completion counters.
+        self.queue_counters = torch.zeros(2, **i32)
 
     @classmethod
     def get_cudagraph_support(cls, vllm_config=None, kv_cache_spec=None):
@@ -210,7 +214,7 @@ class OscarMetadataBuilder:
             initial_prefill=initial, actual_seq_lengths_q=query_ends,
             causal=getattr(cm, "causal", True), is_dummy=dummy, tasks=self.tasks,
             task_count=self.task_count, max_seq_len=max_seq_len,
-            finish_counters=self.finish_counters,
+            finish_counters=self.finish_counters, queue_counters=self.queue_counters,
             total_seq_len=None if dummy or seq_cpu is None else int(seq_cpu[:nr].sum()),
         )
 

@@ -116,6 +116,56 @@ def test_token_bounded_splits_match_oracle_and_merge_to_one_split(splits, split_
     torch.testing.assert_close(ls, ls1, atol=1e-4, rtol=0)
 
 
+@pytest.mark.parametrize("splits,split_tokens", [(40, 128), (16, 512)])
+def test_work_queue_is_bitwise_the_grid_form(splits, split_tokens):
+    # MTP tasks of 4 query tokens x 6 heads (24 rows: the two-tile kernel) with token-bounded
+    # splits run as a work queue (one workgroup per CU over the units in use): the same LSEs
+    # and partial rows as the grid form, call after call (the counters reset themselves) and
+    # in graph replays with eager launches in between.
+    lengths = [2600, 900, 5000, 300, 40]
+    prefixes = [x - 4 for x in lengths]
+    layout, _, hist, window, meta, _, rk, rv, *_, q, k, v = _setup(lengths, prefixes)
+    kernels.prepare_tasks(meta.query_start_loc, meta.counts, meta.tasks, meta.task_count,
+                          meta.max_num_reqs, layout.config.queries_per_tile)
+    kernels.store_int2(kernels.rotate(k, rk), kernels.rotate(v, rv), hist, meta.slot_mapping,
+                       meta.counts, layout)
+    qr = kernels.rotate(q, rk)
+    assert kernels.history_rows(meta, layout, 6) == 24
+    print(f"[queue] splits {splits} split_tokens {split_tokens}", flush=True)
+
+    def run(use_queue):
+        return kernels.attention_partials(qr, k, v, hist, window, meta, layout, 1 / 16, splits,
+                                          False, split_tokens=split_tokens, use_queue=use_queue)
+
+    want_p, want_l = run(False)
+    fin = torch.isfinite(want_l)
+    assert fin.any() and torch.isneginf(want_l).any()  # used and unused split slots
+
+    def same(p, l, what):
+        assert torch.equal(l, want_l), what + ": LSE"
+        assert torch.equal(p[fin], want_p[fin]), what + ": partial rows"
+
+    for i in range(3):
+        same(*run(True), f"queue call {i}")
+    counters = kernels.queue_counters(meta, qr.device)
+    torch.cuda.synchronize()
+    assert int(counters.abs().sum()) == 0
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=side):
+        gp, gl = run(True)
+    torch.cuda.synchronize()
+    for i in range(3):
+        gp.fill_(float("nan"))
+        gl.fill_(float("nan"))
+        graph.replay()
+        torch.cuda.synchronize()
+        same(gp, gl, f"graph replay {i}")
+        same(*run(True), f"eager call after replay {i}")
+    assert int(counters.abs().sum()) == 0
+
+
 def _abi_partials(query, meta, layout, splits, raw, hist, window, k, v, partials, lse):
     """Direct C-ABI call with caller-provided (sentinel-filled) outputs."""
     cfg = layout.config
@@ -128,7 +178,7 @@ def _abi_partials(query, meta, layout, splits, raw, hist, window, k, v, partials
         meta.tasks.data_ptr(), meta.task_count.data_ptr(), n, hq,
         attention_programs(n, meta.max_num_reqs, cfg.queries_per_tile), splits, cfg.block_n,
         cfg.queries_per_tile, 0, 1 / 16, int(raw), 0, kernels.layout_struct(layout),
-        partials.data_ptr(), lse.data_ptr(), torch.cuda.current_stream().cuda_stream)
+        partials.data_ptr(), lse.data_ptr(), None, torch.cuda.current_stream().cuda_stream)
     _ext.check(status, "attention_partials")
 
 
