@@ -222,9 +222,11 @@ class OscarAttentionImpl:
             return choose_splits(meta.num_reqs, self.num_kv_heads, meta.max_query_len), 0
         tasks = meta.num_reqs if meta.max_query_len <= 1 else \
             -(-meta.num_actual_tokens // self.cfg.queries_per_tile)
+        rows = min(meta.max_query_len, self.cfg.queries_per_tile) * (
+            self.num_heads // self.num_kv_heads)
         return choose_history_partition(tasks, self.num_kv_heads, meta.max_query_len,
                                         getattr(meta, "max_seq_len", None),
-                                        getattr(meta, "total_seq_len", None))
+                                        getattr(meta, "total_seq_len", None), rows=rows)
 
     def _bind_cache(self, kv_cache, layout):
         identity = (kv_cache[0].data_ptr(), kv_cache[1].data_ptr(), layout)
