@@ -476,7 +476,7 @@ HIST_LAUNCHES = 20  # history launches per timed batch of the dominant-kernel me
 TRAFFIC_PROFILES = {  # rocprof PMC summaries (FETCH_SIZE / WRITE_SIZE runs) per (kernel, config)
     ("history_pair_kernel", "c3"): "history_kernel_c3_traffic.txt",
     ("history_pair_kernel", "c5"): "history_kernel_c5_traffic.txt",
-    ("history_kernel<2>", "c4"): "history_kernel_c4_traffic.txt",
+    ("history_queue_kernel<2>", "c4"): "history_queue_kernel_c4_traffic.txt",
 }
 
 
@@ -691,7 +691,7 @@ def main(argv=None):
         hist_alg += partial_bytes + rows * (1024 + 4) + rows * (512 + 4) + 256 * 256 * 2
         hist_alg += 2 * 2 * ntok * 512
     hist_kernel = ("history_pair_finish_kernel" if one_launch
-                   else kernels.history_kernel_name(w.meta, w.layout, 6))
+                   else kernels.history_kernel_name(w.meta, w.layout, 6, ntok, split_tokens))
     print(f"[bench] step {us_step:.1f} us, history kernel {hist_us:.1f} us", file=sys.stderr,
           flush=True)
 
