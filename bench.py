@@ -70,6 +70,9 @@ def parse_args(argv=None):
                         "launch instead of q rotation + history launch carrying the rest")
     p.add_argument("--layer-step", action="store_true",
                    help="the one-launch layer step (kernels.layer_step) instead of three launches")
+    p.add_argument("--separate-q-rotation", action="store_true",
+                   help="the q rotation as a launch of its own ahead of the history launch "
+                        "(default: the history workgroups rotate their query rows)")
     p.add_argument("--mode", default="step",
                    choices=("step", "history", "copy", "prefill", "store"),
                    help="step: full benchmark; history: only the history-attention launches "
@@ -562,7 +565,8 @@ def main(argv=None):
         impl = OscarAttentionImpl.standalone(6, 256, 1 / 16, 1, w.cfg, split_policy=cfg["splits"],
                                              one_launch_post=args.one_launch_post,
                                              overlap=not args.no_overlap,
-                                             layer_step=args.layer_step)
+                                             layer_step=args.layer_step,
+                                             rotate_in_history=not args.separate_q_rotation)
         impl.set_rotations(w.rk, w.rv)
         impls.append(impl)
     ntok = w.q.shape[0]
@@ -721,6 +725,7 @@ def main(argv=None):
             "one_launch_post": bool(args.one_launch_post),
             "overlap": not args.no_overlap,
             "layer_step": bool(args.layer_step),
+            "rotate_in_history": not args.separate_q_rotation,
         },
         "us_per_layer_step": us_step,
         "gpu_us_per_layer_step": gpu_ms / args.steps * 1e3,

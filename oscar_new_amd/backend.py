@@ -125,15 +125,17 @@ class OscarAttentionImpl:
     behind the INT2 stream's memory traffic) and
     ``one_launch_post`` (history branch and post-attention in one launch where it applies and
     the one-launch step does not; same bits as three launches) and ``overlap`` (default on:
-    where it applies, the three launches are the q rotation, the history launch carrying the
-    BF16 branch and the K/V INT2 store as extra workgroups, and post-attention; same bits).
+    where it applies, the step is the history launch carrying the BF16 branch and the K/V INT2
+    store as extra workgroups, and post-attention; same bits). ``rotate_in_history`` (default
+    on, with ``overlap``): the history workgroups rotate the query rows themselves; off, the q
+    rotation is a launch of its own ahead of the history launch; same bits.
     """
 
     def __init__(self, num_heads, head_size, scale, num_kv_heads, alibi_slopes=None,
                  sliding_window=None, kv_cache_dtype="auto", logits_soft_cap=None,
                  attn_type="decoder", kv_sharing_target_layer_name=None, *, vllm_config=None,
                  oscar_config=None, split_policy="reference", fused=True, one_launch_post=False,
-                 layer_step=False, overlap=True, **kwargs):
+                 layer_step=False, overlap=True, rotate_in_history=True, **kwargs):
         unsupported = (
             (alibi_slopes is not None, "ALiBi"),
             (sliding_window is not None, "sliding-window attention"),
@@ -172,6 +174,7 @@ class OscarAttentionImpl:
         self.one_launch_post = one_launch_post
         self.layer_step = layer_step
         self.overlap = overlap
+        self.rotate_in_history = rotate_in_history
         self.rk = self.rv = self.rk_cols = self.rv_cols = self.rk_t = self.rv_t = None
         self.history = self.window = None
         self.cache_identity = None
@@ -217,16 +220,26 @@ class OscarAttentionImpl:
     def partition_for(self, meta):
         """``(splits, split_tokens)`` of the history branch. "reference": config.py:84-89
         with the reference split rule; "mi355x": ``choose_history_partition`` (host-side
-        ``meta.max_seq_len`` and, when present, ``meta.total_seq_len``)."""
+        ``meta.max_seq_len`` and, when present, ``meta.total_seq_len``), leaving the slots of
+        the pre-attention role workgroups free when they share the history launch."""
         if self.split_policy == "reference":
             return choose_splits(meta.num_reqs, self.num_kv_heads, meta.max_query_len), 0
         tasks = meta.num_reqs if meta.max_query_len <= 1 else \
             -(-meta.num_actual_tokens // self.cfg.queries_per_tile)
         rows = min(meta.max_query_len, self.cfg.queries_per_tile) * (
             self.num_heads // self.num_kv_heads)
+        reserved = 0
+        layout = getattr(meta, "layout", None)
+        if (self.fused and self.overlap and not self.one_launch_post and not self.layer_step
+                and layout is not None
+                and kernels.history_pre_supported(meta, layout, self.num_heads)):
+            # BF16 branch: one workgroup per (task, kv head); K/V store: 8 per 16 rows.
+            kv_rows = meta.num_actual_tokens * self.num_kv_heads
+            reserved = tasks * self.num_kv_heads + 8 * -(-kv_rows // 16)
         return choose_history_partition(tasks, self.num_kv_heads, meta.max_query_len,
                                         getattr(meta, "max_seq_len", None),
-                                        getattr(meta, "total_seq_len", None), rows=rows)
+                                        getattr(meta, "total_seq_len", None), rows=rows,
+                                        reserved=reserved)
 
     def _bind_cache(self, kv_cache, layout):
         identity = (kv_cache[0].data_ptr(), kv_cache[1].data_ptr(), layout)
@@ -281,9 +294,11 @@ class OscarAttentionImpl:
         return output
 
     def _fused_step(self, q, k, v, meta, splits, split_tokens, rows, lse):
-        """The whole step in one launch (``layer_step``, where it applies), else pre-attention
-        (q rotation, K/V INT2 store, BF16 branch) -> history -> post (split merge, inverse V
-        rotation, path merge, windows), the last two in one launch with ``one_launch_post``."""
+        """The whole step in one launch (``layer_step``, where it applies); else, with
+        ``overlap``, the history launch carrying the pre-attention work (BF16 branch, K/V INT2
+        store and, with ``rotate_in_history``, the q rotation) -> post (split merge, inverse V
+        rotation, path merge, windows); else pre-attention -> history -> post, the last two in
+        one launch with ``one_launch_post``."""
         layout = meta.layout
         if self.layer_step and kernels.layer_step_supported(meta, layout, self.num_heads, splits,
                                                             q.shape[0]):
@@ -293,10 +308,11 @@ class OscarAttentionImpl:
             return
         if (self.overlap and not self.one_launch_post
                 and kernels.history_pre_supported(meta, layout, self.num_heads)):
-            # q rotation, then one launch holding the history branch and, dispatched ahead of
-            # it, the BF16 branch and the INT2 store (the history branch never reads the slots
-            # the store writes), then post-attention.
-            qrot = kernels.rotate(q, self.rk_cols)
+            # One launch holding the history branch (its workgroups rotate the query rows, or a
+            # q rotation launch goes first) and, dispatched ahead of it, the BF16 branch and
+            # the INT2 store (the history branch never reads the slots the store writes), then
+            # post-attention.
+            qrot = None if self.rotate_in_history else kernels.rotate(q, self.rk_cols)
             hp, hl, rp, rl = kernels.history_pre(qrot, q, k, v, self.history, self.window, meta,
                                                  layout, self.scale, splits, self.rk_t,
                                                  self.rv_t, split_tokens=split_tokens)

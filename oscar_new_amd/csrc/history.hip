@@ -714,6 +714,8 @@ static_assert(pair_slot(pair_slot(45)) == 45 && pair_slot(21) == 17, "pair_slot 
 // the finisher stores the windows; padded rows are cleared by split 0 of each program.
 // kMode 3: as 0, behind `role_slices` z slices of pre-attention roles (pre.h: the BF16 branch
 // and the K/V INT2 store of the step), which dispatch first and run beside the history stream.
+// kMode 4: as 3, and each workgroup rotates its task's query rows by R_k itself (a.query is
+// the unrotated query), with the operands and k order of the rotate entry point (same bits).
 template <int kMode>
 __device__ __forceinline__ void history_pair_body(const AttnArgs& a, const FinishArgs* fin,
                                                   const LayerArgs* lay,
@@ -740,7 +742,7 @@ __device__ __forceinline__ void history_pair_body(const AttnArgs& a, const Finis
   static_assert(16 * kStageRowBytes + 4 * 2 * 8 * 16 * 4 <= 2 * kStageBytes,
                 "the layer step's 16-row staging tile and operand images fit wavefront 3's stages");
   static_assert(16 * kHeadDim * 2 <= kRingBytes, "the K/V store role's tile fits the ring");
-  if constexpr (kMode == 3) {
+  if constexpr (kMode == 3 || kMode == 4) {
     const int z = blockIdx.z;
     if (z < role_slices) {
       if (z == 0) {
@@ -759,6 +761,7 @@ __device__ __forceinline__ void history_pair_body(const AttnArgs& a, const Finis
   // nothing), so that they arrive with the task metadata.
   u32x4 rb[4][8];
   if constexpr (kMode == 2) load_rt_tiles(lay->rk_t, rb);
+  if constexpr (kMode == 4) load_rt_tiles(pre->rk_t, rb);
 
   Task t;
   if (!read_task(a, t, blockIdx.x)) return;
@@ -875,6 +878,17 @@ __device__ __forceinline__ void history_pair_body(const AttnArgs& a, const Finis
       load_rt_tiles(lay->rv_t, rb);
       rotate_stage(aop, rb, q_lds, 12, 16);
     }
+    barrier_lds();
+  }
+  if constexpr (kMode == 4) {
+    // Rows 0..7 are staged; rows 8..15 of the tile are zero operands (never written back).
+    u32x4 aop[8];
+    load_stage_a(q_lds, aop);
+#pragma unroll
+    for (int m = 0; m < 8; ++m)
+      if (n >= 8) aop[m] = u32x4{0u, 0u, 0u, 0u};
+    barrier_lds();  // every operand is in registers; the rotated rows replace the staged ones
+    rotate_stage(aop, rb, q_lds, 0, 8);
     barrier_lds();
   }
 
@@ -1261,6 +1275,9 @@ struct HistoryPreArgs {
 __global__ __launch_bounds__(kThreads, 2) void history_pre_kernel(const HistoryPreArgs h) {
   history_pair_body<3>(h.a, nullptr, nullptr, &h.p, h.role_slices);
 }
+__global__ __launch_bounds__(kThreads, 2) void history_pre_rot_kernel(const HistoryPreArgs h) {
+  history_pair_body<4>(h.a, nullptr, nullptr, &h.p, h.role_slices);
+}
 
 }  // namespace
 
@@ -1289,9 +1306,12 @@ hipError_t launch_history(const AttnArgs& a, dim3 grid, int rows, hipStream_t st
 }
 
 hipError_t launch_history_pre(const AttnArgs& a, const PreArgs& p, int role_slices, dim3 grid,
-                              hipStream_t stream) {
+                              bool rotate_query, hipStream_t stream) {
   const HistoryPreArgs h{a, p, role_slices};
-  hipLaunchKernelGGL(history_pre_kernel, grid, dim3(kThreads), 0, stream, h);
+  if (rotate_query)
+    hipLaunchKernelGGL(history_pre_rot_kernel, grid, dim3(kThreads), 0, stream, h);
+  else
+    hipLaunchKernelGGL(history_pre_kernel, grid, dim3(kThreads), 0, stream, h);
   return hipGetLastError();
 }
 

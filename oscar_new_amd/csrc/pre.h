@@ -104,7 +104,8 @@ __device__ __forceinline__ void kv_store_role(const PreArgs& p, int r, uint8_t* 
 // The history launch with the pre-attention roles (history.hip): grid (programs, H,
 // role_slices + splits); z-slice 0 runs the BF16 branch of (task, kv head) (lean form, one
 // split), z-slices 1 .. role_slices - 1 the K/V store quads, the rest the history splits.
+// rotate_query: a.query is the unrotated query and each history workgroup rotates its rows.
 hipError_t launch_history_pre(const AttnArgs& a, const PreArgs& p, int role_slices, dim3 grid,
-                              hipStream_t stream);
+                              bool rotate_query, hipStream_t stream);
 
 }  // namespace oscar

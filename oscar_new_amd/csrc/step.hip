@@ -227,6 +227,15 @@ extern "C" int oscar_history_pre(
                          slots, clip, layout, raw_partials, raw_lse, nullptr, &p, &qrows);
   if (st != OSCAR_OK) return st;
   if (qrows > 8) return OSCAR_E_UNSUPPORTED;
+  // query_rot == nullptr: the history workgroups rotate the query rows themselves.
+  const bool rotate_query = query_rot == nullptr;
+  if (rotate_query) {
+    if (!rk_t) return OSCAR_E_NULL;
+    query_rot = query;
+    r_s0 = q_s0;
+    r_s1 = q_s1;
+    r_s2 = 1;
+  }
   AttnArgs a;
   int64_t hrows = 0;
   st = make_attn_args(query_rot, r_s0, r_s1, r_s2, nullptr, 0, 0, 1, nullptr, 0, 0, 1, history,
@@ -241,7 +250,8 @@ extern "C" int oscar_history_pre(
   const int role_slices = 1 + static_cast<int>((p.kv_wgs + per_slice - 1) / per_slice);
   const dim3 grid(static_cast<unsigned>(programs), static_cast<unsigned>(a.L.kv_heads),
                   static_cast<unsigned>(splits + role_slices));
-  return static_cast<int>(launch_history_pre(a, p, role_slices, grid, as_stream(stream)));
+  return static_cast<int>(
+      launch_history_pre(a, p, role_slices, grid, rotate_query, as_stream(stream)));
 }
 
 namespace oscar {

@@ -521,8 +521,9 @@ def history_pre(query_rot, query, key, value, history, window, meta, layout, sca
     splits (no reference counterpart as one call; it replaces ``attention_partials(qrot, ...,
     raw=False)`` plus ``pre_attention`` without its q rotation, with their bits).
 
-    ``query_rot``: the rotated query; ``query``/``key``/``value``: the step's unrotated rows.
-    Returns ``(partials [n, hq, splits, 256], lse [n, hq, splits], raw_partials
+    ``query_rot``: the rotated query, or None: then the history workgroups rotate the query
+    rows by R_k themselves (the bits of ``rotate(query, R_k)``; no launch of its own);
+    ``query``/``key``/``value``: the step's unrotated rows. Returns ``(partials [n, hq, splits, 256], lse [n, hq, splits], raw_partials
     [n, hq, 1, 256], raw_lse [n, hq, 1])``, all fp32.
     """
     _device_check(query_rot, query, key, value, history, window, rk_t, rv_t)
@@ -545,7 +546,8 @@ def history_pre(query_rot, query, key, value, history, window, meta, layout, sca
     for r in (rk_t, rv_t):
         if r.dtype != torch.bfloat16 or not r.is_contiguous() or tuple(r.shape) != (d, d):
             raise ValueError("rk_t / rv_t must be contiguous bf16 [256, 256] (R transposed)")
-    query_rot = _rows_contiguous(query_rot)
+    query_rot = _rows_contiguous(query_rot) if query_rot is not None else None
+    rot_strides = query_rot.stride() if query_rot is not None else (0, 0, 1)
     query, q0, q1 = _row_strides(query, "query")
     key, k0, k1 = _row_strides(key, "key")
     value, v0, v1 = _row_strides(value, "value")
@@ -556,7 +558,7 @@ def history_pre(query_rot, query, key, value, history, window, meta, layout, sca
     max_query_len = int(max_query_len) if isinstance(max_query_len, int) else 0
     _ext.check(
         _ext.library().oscar_history_pre(
-            _ptr(query_rot), *query_rot.stride(), _ptr(query), q0, q1, _ptr(key), k0, k1,
+            _ptr(query_rot), *rot_strides, _ptr(query), q0, q1, _ptr(key), k0, k1,
             _ptr(value), v0, v1, _ptr(history), history.numel() * history.element_size(),
             _ptr(window), window.numel(),
             _ptr(_int32(meta.query_start_loc, "query_start_loc")),

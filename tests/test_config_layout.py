@@ -134,6 +134,23 @@ def test_history_partition_mi355x():
     assert choose_history_partition(2, 1, 17, 8192, 9000) == (1, 0)
 
 
+def test_history_partition_leaves_the_role_slots_free():
+    # c3 (32 x 32635 history tokens) beside 48 role workgroups: at most 512 - 48 - 32 full
+    # shares, so 14 splits of 2432 tokens (448 history workgroups); c5 beside 12: 121 x 2176.
+    assert choose_history_partition(32, 1, 1, 32768, 32 * 32635, reserved=48) == (14, 2432)
+    assert choose_history_partition(4, 1, 1, 262144, 4 * 262011, reserved=12) == (121, 2176)
+    # For any lengths with that total, the splits in use fit the slots left.
+    rng = __import__("random").Random(5)
+    for _ in range(200):
+        tasks = rng.randint(1, 64)
+        lengths = [rng.randint(1, 70000) for _ in range(tasks)]
+        reserved = rng.randint(1, 200)
+        splits, tokens = choose_history_partition(tasks, 1, 1, max(lengths), sum(lengths),
+                                                  reserved=reserved, max_splits=10**6)
+        used = sum(-(-n // tokens) for n in lengths)
+        assert used <= max(512 - reserved, tasks) or tokens == 1024, (lengths, reserved)
+
+
 def test_bad_config_rejected():
     # Reference tests/test_layout.py:118-127.
     for kwargs in ({"group_size": 128}, {"head_dim": 128}, {"k_clip_ratio": 0.5},

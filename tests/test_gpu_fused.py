@@ -71,15 +71,17 @@ CASES = [
 
 def _forward(c, form, splits, raw=None):
     """One layer step in `form` ("single"; "fused": q rotation, history launch carrying the
-    BF16 branch and INT2 store, post-attention; "fused_serial": pre-attention, history,
-    post-attention; "fused1": history + post in one launch where it applies; "layer": the
-    one-launch step where it applies) on a copy of the cache."""
+    BF16 branch and INT2 store, post-attention; "fused_rot": as "fused" with the q rotation
+    done by the history workgroups; "fused_serial": pre-attention, history, post-attention;
+    "fused1": history + post in one launch where it applies; "layer": the one-launch step
+    where it applies) on a copy of the cache."""
     n = c.q.shape[0]
     raw = c.raw.clone() if raw is None else raw
     k_cache, v_cache = _views(raw, c.layout)
     impl = OscarAttentionImpl.standalone(6, 256, 1 / 16, 1, c.layout.config,
                                          fused=form != "single", one_launch_post=form == "fused1",
-                                         layer_step=form == "layer", overlap=form != "fused_serial")
+                                         layer_step=form == "layer", overlap=form != "fused_serial",
+                                         rotate_in_history=form == "fused_rot")
     impl.set_rotations(c.rk, c.rv)
     impl.partition_for = lambda meta, s=splits: (s, 0)
     c.meta.merged_lse = torch.full((n, 6), 7.0, device=DEV)
@@ -93,7 +95,8 @@ def _forward(c, form, splits, raw=None):
 def test_fused_step_is_bitwise_the_single_launch_step(lengths, prefixes, splits):
     c = _case(lengths, prefixes, seed=7)
     want = _forward(c, "single", splits)
-    for form in ("fused", "fused_serial", "fused1"):
+    for form in ("fused", "fused_rot", "fused_serial", "fused1"):
+        print(f"[fused] {lengths} splits {splits} form {form}", flush=True)
         got = _forward(c, form, splits)
         for a, b in zip(want, got):
             assert torch.equal(a, b), form
@@ -257,7 +260,12 @@ def test_pre_attention_matches_single_entry_points():
     ([69, 263, 1804, 40], [67, 261, 1802, 38], 0),  # two-token MTP (12 rows: > 8, refused)
     ([6000, 300, 4000], [5999, 299, 3999], 512),  # token-bounded splits
 ])
-def test_history_pre_matches_single_entry_points(lengths, prefixes, split_tokens):
+@pytest.mark.parametrize("rotate_in_history", [False, True])
+def test_history_pre_matches_single_entry_points(lengths, prefixes, split_tokens,
+                                                 rotate_in_history):
+    # rotate_in_history: query_rot None, each history workgroup rotates its task's query rows.
+    print(f"[history_pre] {lengths} split_tokens {split_tokens} rotate {rotate_in_history}",
+          flush=True)
     c = _case(lengths, prefixes, seed=4)
     meta, layout = c.meta, c.layout
     splits = 8
@@ -270,8 +278,9 @@ def test_history_pre_matches_single_entry_points(lengths, prefixes, split_tokens
             kernels.history_pre(qrot, c.q, c.k, c.v, hist_a, win_a, meta, layout, 1 / 16, splits,
                                 rk_t, rv_t)
         return
-    hp, hl, rp, rl = kernels.history_pre(qrot, c.q, c.k, c.v, hist_a, win_a, meta, layout, 1 / 16,
-                                         splits, rk_t, rv_t, split_tokens=split_tokens)
+    hp, hl, rp, rl = kernels.history_pre(None if rotate_in_history else qrot, c.q, c.k, c.v,
+                                         hist_a, win_a, meta, layout, 1 / 16, splits, rk_t, rv_t,
+                                         split_tokens=split_tokens)
     hp_ref, hl_ref = kernels.attention_partials(qrot, c.k, c.v, hist_b, win_b, meta, layout,
                                                 1 / 16, splits, False, split_tokens=split_tokens)
     _, rp_ref, rl_ref = kernels.pre_attention(c.q, c.k, c.v, hist_b, win_b, meta, layout, 1 / 16,
