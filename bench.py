@@ -35,7 +35,7 @@ PEAK_HBM_GBPS = 8000.0
 CONFIGS = {
     "c3": dict(batch=32, context=32768, qlen=1, ragged=False, splits="mi355x",
                desc="one TP rank of a Qwen3.5-27B-class layer: B32 x 32768 ctx, GQA 6:1, D256, "
-                    "INT2 history + 4 sink + 128 recent BF16, 16 splits of 2048 tokens"),
+                    "INT2 history + 4 sink + 128 recent BF16, MI355X split partition"),
     "c4": dict(batch=64, context=131072, qlen=4, ragged=True, splits="mi355x",
                desc="ragged MTP: B64, ctx log-uniform [256, 131072], 4 query tokens each"),
     "c5": dict(batch=4, context=262144, qlen=1, ragged=False, splits="mi355x",
