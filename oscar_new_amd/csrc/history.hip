@@ -565,6 +565,382 @@ __global__ __launch_bounds__(kThreads, 3 - RT) void history_kernel(const AttnArg
   history_unit<RT>(a, blockIdx.x, blockIdx.y, blockIdx.z, lds);
 }
 
+// ---------------------------------------------------------------- 17-32 rows: eight wavefronts
+
+// Tasks of 17-32 query rows (MTP: 4 query tokens x 6 query heads = 24 rows). Two row groups of
+// 16 rows share every chunk: wavefront w streams chunks (w % 4) + 4 j like the general
+// kernel's wavefront w % 4 and computes the rows 16 (w / 4) .. + 15 of them, so each chunk is
+// copied into LDS once (by the group-0 wavefront of its stream, three stages per stream) and
+// read by two wavefronts, and every SIMD holds two wavefronts (one workgroup of eight per CU;
+// a wavefront keeps one 16-row tile, 253 registers, instead of the two-tile kernel's 464,
+// whose single wavefront per SIMD left the VALU half idle). A workgroup barrier per chunk
+// publishes the chunk to the second wavefront of its stream and frees the stage of the chunk
+// before. A row's arithmetic is the general kernel's with one row tile; the lazy-max rescale
+// is decided per wavefront, so its bits depend on the 16-row grouping, not on the launch form
+// (grid or work queue).
+constexpr int kThreadsW8 = 512;
+constexpr int kStagesW8 = 3;
+constexpr int kRingBytesW8 = 4 * kStagesW8 * kStageBytes;
+
+struct HistoryLdsW8 {
+  uint8_t ring[kRingBytesW8] __attribute__((aligned(16)));
+  uint8_t qstage[32 * 512] __attribute__((aligned(16)));  // query rows, then operand images
+  uint32_t off[kTableCache];
+  float red[3][8][16];  // per wavefront: row max, sum p, sum p z_v of its 16 rows
+};
+static_assert(8 * 16 * 128 * 4 <= kRingBytesW8, "half the epilogue merge fits the ring");
+static_assert(2 * 2 * kQTerms * 64 * 32 <= 32 * 512, "both groups' operand images fit");
+
+__device__ __forceinline__ void history_unit_w8(const AttnArgs& a, int task, int head, int split,
+                                                HistoryLdsW8& lds) {
+  uint8_t* s_ring = lds.ring;
+  uint32_t* s_off = lds.off;
+  auto& s_red = lds.red;
+  Task t;
+  if (!read_task(a, t, task)) return;
+  const int length = t.recent_begin - t.sink_len;
+  const int nsplit = history_splits(a, length);
+  if (split >= nsplit) {
+    write_unused_split(a, t, head, split);
+    return;
+  }
+  int p_lo, p_hi;
+  history_positions(a, t, length, nsplit, split, p_lo, p_hi);
+  const int lane = threadIdx.x & 63;
+  const int wave = uniform(threadIdx.x >> 6);
+  const int stream = wave & 3, rg = wave >> 2;
+  const int n = lane & 15, g = lane >> 4;
+  const int first = p_lo >> 6;
+  const int nchunk = p_lo < p_hi ? ((p_hi - 1) >> 6) - first + 1 : 0;
+  const int nmine = nchunk > stream ? (nchunk - stream + 3) >> 2 : 0;  // chunks stream + 4 j
+  const int nmax = (nchunk + 3) >> 2;                                  // stream 0's count
+  const int kb_first = p_lo >> a.L.bk_shift;
+
+  // ---- DMA plan (as in the general kernel); the group-0 wavefront of a stream issues.
+  const uint32_t tok_bytes = static_cast<uint32_t>(a.L.kv_heads) * kSlot;
+  uint32_t voff[kDma];
+#pragma unroll
+  for (int i = 0; i < kDma; ++i) {
+    const int c = 64 * i + lane;
+    voff[i] = static_cast<uint32_t>(c / kPieces) * tok_bytes + 16 * (c % kPieces);
+  }
+  const uint32_t my_ring = lds_addr(s_ring) + stream * kStagesW8 * kStageBytes;
+  const uint32_t in_kb_mask = static_cast<uint32_t>(a.L.bk - 1);
+  // Offset (32-byte units) of the kernel block of this stream's chunk j, or kNoBlock.
+  auto block_of = [&](int j) {
+    const int t0 = (first + stream + 4 * j) << 6;
+    const int local = (t0 >> a.L.bk_shift) - kb_first;
+    uint32_t off32 = s_off[min(local, kTableCache - 1)];
+    if (local >= kTableCache) off32 = kernel_block_offset(a, t, head, t0 >> a.L.bk_shift);
+    return static_cast<uint32_t>(uniform(static_cast<int>(off32)));
+  };
+  auto issue = [&](int j, int s) {
+    const int t0 = (first + stream + 4 * j) << 6;
+    const uint32_t off32 = block_of(j);
+    const uint8_t* base = a.history;
+    if (off32 != kNoBlock)
+      base = a.history + (static_cast<uint64_t>(off32) << 5) +
+             (static_cast<uint32_t>(t0) & in_kb_mask) * tok_bytes;
+    const uint32_t l = my_ring + s * kStageBytes + kSkew;
+#pragma unroll
+    for (int i = 0; i < kDma; ++i) dma_x4(base, voff[i], l + 1024 * i);
+  };
+
+  // ---- query rows -> LDS: 32 rows, piece p of row r at r * 32 + (p ^ (r & 31)).
+  uint8_t* q_lds = lds.qstage;
+  {
+    const uint32_t q_base = lds_addr(q_lds);
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int slot = (wave * 2 + i) * 64 + lane;
+      const int row = slot >> 5, piece = (slot & 31) ^ (row & 31);
+      const RowInfo ri = row_info(a, t, head, row);
+      const uint16_t* src =
+          ri.valid ? a.query + ri.token * a.qs0 + ri.qhead * a.qs1 + 8 * piece : a.query;
+      dma_dwordx4(src, q_base + 1024 * (wave * 2 + i));
+    }
+  }
+  if (nchunk > 0) {
+    const int nkb = min(((p_hi - 1) >> a.L.bk_shift) - kb_first + 1, kTableCache);
+    for (int j = threadIdx.x; j < nkb; j += kThreadsW8)
+      s_off[j] = kernel_block_offset(a, t, head, kb_first + j);
+  }
+  OSCAR_WAIT_VM(0);
+  __syncthreads();
+  if (rg == 0) {
+    if (nmine > 0) issue(0, 0);
+    if (nmine > 1) issue(1, 1);
+  }
+
+  // ---- query -> FP8 B operands of this wavefront's 16 rows (row group rg), converted by the
+  // group's four wavefronts: wavefront stream s builds operand dwords 2s, 2s + 1 of every lane.
+  i32x8 qb[2][kQTerms];
+  float fq, qs2, qmult;
+  float qx[2][8];
+  {
+    const int row = 16 * rg + n;
+    const bool live = row_info(a, t, head, row).valid;
+    float mx = 0.f, qs = 0.f;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int piece = 16 * h + 8 * (stream >> 1) + 2 * g;
+      const u32x4 r0 = *reinterpret_cast<const u32x4*>(q_lds + row * 512 + 16 * (piece ^ (row & 31)));
+      const u32x4 r1 =
+          *reinterpret_cast<const u32x4*>(q_lds + row * 512 + 16 * ((piece + 1) ^ (row & 31)));
+      const uint32_t w[8] = {r0[0], r0[1], r0[2], r0[3], r1[0], r1[1], r1[2], r1[3]};
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const uint32_t bits = (stream & 1) ? (w[i] >> 16) : (w[i] & 0xffffu);
+        const float x = live ? bf16_to_float(bits) : 0.f;
+        qx[h][i] = x;
+        mx = fmaxf(mx, fabsf(x));
+        qs += x;
+      }
+    }
+    mx = fmaxf(mx, __shfl_xor(mx, 16, kWave));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
+    qs += __shfl_xor(qs, 16, kWave);
+    qs += __shfl_xor(qs, 32, kWave);
+    if (g == 0) {
+      s_red[0][wave][n] = mx;
+      s_red[1][wave][n] = qs;
+    }
+  }
+  barrier_lds();  // partial row max / sum published; the query rows are in registers
+  {
+    const int w0 = 4 * rg;
+    const float mx = fmaxf(fmaxf(s_red[0][w0][n], s_red[0][w0 + 1][n]),
+                           fmaxf(s_red[0][w0 + 2][n], s_red[0][w0 + 3][n]));
+    const float qs = (s_red[1][w0][n] + s_red[1][w0 + 1][n]) + (s_red[1][w0 + 2][n] + s_red[1][w0 + 3][n]);
+    const uint32_t eb = max((__float_as_uint(mx) >> 23) & 0xffu, 7u);
+    qmult = __uint_as_float((261u - eb) << 23);
+    fq = 2.0f * a.scale_log2 / qmult;  // FP4 holds c/2
+    qs2 = 0.5f * qs * qmult;
+  }
+  // Operand images [rg][h][term][lane][8 dwords] (alias the query rows, now in registers).
+  uint32_t* q_ops = reinterpret_cast<uint32_t*>(q_lds) + rg * (2 * kQTerms * 64 * 8);
+#pragma unroll
+  for (int h = 0; h < 2; ++h)
+#pragma unroll
+    for (int f = 0; f < 2; ++f) {
+      float v[4] = {qx[h][4 * f] * qmult, qx[h][4 * f + 1] * qmult, qx[h][4 * f + 2] * qmult,
+                    qx[h][4 * f + 3] * qmult};
+#pragma unroll
+      for (int term = 0; term < kQTerms; ++term)
+        q_ops[((h * kQTerms + term) * 64 + lane) * 8 + 2 * stream + f] = fp8x4_take(v);
+    }
+  barrier_lds();
+#pragma unroll
+  for (int h = 0; h < 2; ++h)
+#pragma unroll
+    for (int term = 0; term < kQTerms; ++term) {
+      const u32x4* src = reinterpret_cast<const u32x4*>(q_ops + ((h * kQTerms + term) * 64 + lane) * 8);
+      const u32x4 lo = src[0], hi = src[1];
+      qb[h][term] = i32x8{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3],
+                          (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
+    }
+
+  // ---- per-lane LDS offsets inside a stage (as in the general kernel)
+  const int k_off = kSkew + kRec * n + 8 * g;
+  const int sz_off = kSkew + kRec * 4 * g + 64;
+  const int v_off = kSkew + kRec * (16 * (n >> 2) + (n & 3)) + kRec * 8 * (g & 1) + kVector;
+
+  float m = -INFINITY, psum = 0.f, zsum = 0.f;
+  f32x4 o[16];  // o[2c + par]: rows 4g + v, dim 32c + 2n + par (units of c/2)
+#pragma unroll
+  for (int c = 0; c < 16; ++c) o[c] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  // One chunk from ring stage S (compile-time, so every LDS offset is an immediate).
+  auto process = [&](int j, auto stage_tag) {
+    constexpr int S = decltype(stage_tag)::value;
+    const uint8_t* st = s_ring + stream * kStagesW8 * kStageBytes + S * kStageBytes;
+    f32x4 acc[4];
+#pragma unroll
+    for (int tt = 0; tt < 4; ++tt) acc[tt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      i32x8 kf[4];
+#pragma unroll
+      for (int tt = 0; tt < 4; ++tt) {
+        const uint32_t* kp = reinterpret_cast<const uint32_t*>(st + k_off + 16 * kRec * tt + 32 * h);
+        const uint32_t w0 = kp[0], w1 = kp[1];
+        kf[tt] = i32x8{even_codes(w0), odd_codes(w0), even_codes(w1), odd_codes(w1), 0, 0, 0, 0};
+      }
+#pragma unroll
+      for (int term = 0; term < kQTerms; ++term)
+#pragma unroll
+        for (int tt = 0; tt < 4; ++tt) acc[tt] = mfma_qk(kf[tt], qb[h][term], acc[tt]);
+    }
+    uint32_t ksz[16], vsz[16];
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const int off = sz_off + kRec * (16 * (e >> 2) + (e & 3));
+      ksz[e] = *reinterpret_cast<const uint32_t*>(st + off);
+      vsz[e] = *reinterpret_cast<const uint32_t*>(st + off + kVector);
+    }
+    float r2[16];
+#pragma unroll
+    for (int e = 0; e < 16; ++e) r2[e] = fmaf(h16lo(ksz[e]), acc[e >> 2][e & 3], h16hi(ksz[e]) * qs2);
+    const int t0 = (first + stream + 4 * j) << 6;
+    const bool ok_block = block_of(j) != kNoBlock;
+    if (!(ok_block && t0 >= p_lo && t0 + kChunk <= p_hi)) {
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const bool ok = ok_block && static_cast<uint32_t>(t0 + p_token(g, e) - p_lo) <
+                                        static_cast<uint32_t>(p_hi - p_lo);
+        vsz[e] = ok ? vsz[e] : 0u;
+        r2[e] = ok ? r2[e] : -INFINITY;
+      }
+    }
+    float lm = r2[0];
+#pragma unroll
+    for (int e = 1; e < 16; ++e) lm = fmaxf(lm, r2[e]);
+    lm *= fq;
+    if (__any(lm > m + kTheta)) {
+      const float v = max_xor32(max_xor16(lm));
+      const float mn = fmaxf(m, v);
+      const float alpha = mn == -INFINITY ? 1.0f : exp2f(m - mn);
+      m = mn;
+      psum *= alpha;
+      zsum *= alpha;
+#pragma unroll
+      for (int v4 = 0; v4 < 4; ++v4) {
+        const float av = __shfl(alpha, 4 * g + v4, kWave);  // accumulator row 4g + v4
+#pragma unroll
+        for (int c = 0; c < 16; ++c) o[c][v4] *= av;
+      }
+    }
+    const float nm = m == -INFINITY ? 0.f : -m;
+    float av[16];
+    float amax = 0.f;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const float p = __builtin_amdgcn_exp2f(fmaf(r2[e], fq, nm));
+      psum += p;
+      zsum = fmaf(p, h16hi(vsz[e]), zsum);
+      av[e] = p * h16lo(vsz[e]);
+      amax = fmaxf(amax, av[e]);
+    }
+    amax = max_xor32(max_xor16(amax));
+    const uint32_t eb = max(__float_as_uint(amax) >> 23, 7u);
+    const float mult = __uint_as_float((260u - eb) << 23);
+    uint32_t hi[4], lo[4];
+#pragma unroll
+    for (int f = 0; f < 4; ++f) {
+      float x[4] = {av[4 * f] * mult, av[4 * f + 1] * mult, av[4 * f + 2] * mult,
+                    av[4 * f + 3] * mult};
+      hi[f] = fp8x4_take(x);
+      lo[f] = fp8x4(x[0], x[1], x[2], x[3]);
+    }
+    const i32x8 pa = i32x8{(int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3],
+                           (int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3]};
+    const int sa = static_cast<int>(eb) - 6;
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      const i32x2 r0 = __builtin_amdgcn_ds_read_tr4_b64_v2i32((lds_i32x2_ptr_t)(st + v_off + 8 * c));
+      const i32x2 r1 =
+          __builtin_amdgcn_ds_read_tr4_b64_v2i32((lds_i32x2_ptr_t)(st + v_off + 4 * kRec + 8 * c));
+      const i32x8 be = i32x8{even_codes(r0[0]), even_codes(r0[1]), even_codes(r1[0]),
+                             even_codes(r1[1]), 0, 0, 0, 0};
+      const i32x8 bo = i32x8{odd_codes(r0[0]), odd_codes(r0[1]), odd_codes(r1[0]),
+                             odd_codes(r1[1]), 0, 0, 0, 0};
+      o[2 * c] = mfma_pv(pa, be, o[2 * c], sa);
+      o[2 * c + 1] = mfma_pv(pa, bo, o[2 * c + 1], sa);
+    }
+  };
+
+  // ---- token loop: every wavefront takes the same number of barriers (nmax, stream 0's
+  // chunk count). Iteration j: the group-0 wavefront waits for its chunk j (chunk j + 1 may
+  // still be in flight), the barrier publishes it to both wavefronts of the stream and tells
+  // every wavefront that chunk j - 1 is consumed, so its stage takes chunk j + 2.
+  auto step = [&](int j, auto stage_tag) {
+    constexpr int S = decltype(stage_tag)::value;
+    if (rg == 0 && j < nmine) {
+      if (j + 1 < nmine)
+        OSCAR_WAIT_VM(kDma);
+      else
+        OSCAR_WAIT_VM(0);
+    }
+    barrier_lds();
+    if (rg == 0 && j + 2 < nmine) issue(j + 2, (S + 2) % kStagesW8);
+    if (j < nmine) process(j, stage_tag);
+  };
+  for (int j = 0; j < nmax; j += kStagesW8) {
+    step(j, std::integral_constant<int, 0>());
+    if (j + 1 < nmax) step(j + 1, std::integral_constant<int, 1>());
+    if (j + 2 < nmax) step(j + 2, std::integral_constant<int, 2>());
+  }
+
+  // ---- epilogue: merge the four stream wavefronts of each row group, 128 dims at a time.
+  psum = sum_xor32(sum_xor16(psum));
+  zsum = sum_xor32(sum_xor16(zsum));
+  barrier_lds();  // every chunk consumed; the ring is free for the merge
+  if (g == 0) {
+    s_red[0][wave][n] = m;
+    s_red[1][wave][n] = psum;
+    s_red[2][wave][n] = zsum;
+  }
+  barrier_lds();
+  float* s_o = reinterpret_cast<float*>(s_ring);  // [wave][row 0..15][128]
+  const int tid = threadIdx.x;
+  const int row32 = tid >> 4, d0 = 4 * (tid & 15);
+  const int rgx = row32 >> 4, r16 = row32 & 15;
+  const RowInfo ri = row_info(a, t, head, row32);
+  float mx = -INFINITY, den = 0.f, zs = 0.f;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) mx = fmaxf(mx, s_red[0][4 * rgx + w][r16]);
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    const float mw = s_red[0][4 * rgx + w][r16];
+    const float f = mw == -INFINITY ? 0.f : exp2f(mw - mx);
+    den = fmaf(f, s_red[1][4 * rgx + w][r16], den);
+    zs = fmaf(f, s_red[2][4 * rgx + w][r16], zs);
+  }
+  const float inv = 1.0f / fmaxf(den, 1.0e-30f);
+#pragma unroll
+  for (int hd = 0; hd < 2; ++hd) {
+    if (hd > 0) barrier_lds();  // the first half has been read
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int row = 4 * g + v;
+      const float mxr = fmaxf(fmaxf(s_red[0][4 * rg][row], s_red[0][4 * rg + 1][row]),
+                              fmaxf(s_red[0][4 * rg + 2][row], s_red[0][4 * rg + 3][row]));
+      const float mw = s_red[0][wave][row];
+      const float f = mw == -INFINITY ? 0.f : exp2f(mw - mxr);
+      float* dst = s_o + (wave * 16 + row) * 128 + 2 * n;
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+        *reinterpret_cast<float2*>(dst + 32 * c) =
+            make_float2(o[2 * (4 * hd + c)][v] * f, o[2 * (4 * hd + c) + 1][v] * f);
+    }
+    barrier_lds();
+    if (ri.valid) {
+      float* out = a.partials + ((ri.token * a.hq + ri.qhead) * a.splits + split) * kHeadDim +
+                   128 * hd + d0;
+      const float4* so = reinterpret_cast<const float4*>(s_o + ((4 * rgx) * 16 + r16) * 128 + d0);
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        const float4 x0 = so[16 * q], x1 = so[16 * 128 / 4 + 16 * q];
+        const float4 x2 = so[2 * 16 * 128 / 4 + 16 * q], x3 = so[3 * 16 * 128 / 4 + 16 * q];
+        const float4 r = make_float4((2.0f * ((x0.x + x1.x) + (x2.x + x3.x)) + zs) * inv,
+                                     (2.0f * ((x0.y + x1.y) + (x2.y + x3.y)) + zs) * inv,
+                                     (2.0f * ((x0.z + x1.z) + (x2.z + x3.z)) + zs) * inv,
+                                     (2.0f * ((x0.w + x1.w) + (x2.w + x3.w)) + zs) * inv);
+        *reinterpret_cast<float4*>(out + 64 * q) = r;
+      }
+      if (hd == 0 && (tid & 15) == 0)
+        a.lse[(ri.token * a.hq + ri.qhead) * a.splits + split] =
+            den > 0.f ? (mx + log2f(den)) * kLn2 : -INFINITY;
+    }
+  }
+  barrier_lds();  // the merge area is read before the next unit's DMA reuses the ring
+}
+
+__global__ __launch_bounds__(kThreadsW8, 1) void history_w8_kernel(const AttnArgs a) {
+  __shared__ HistoryLdsW8 lds;
+  history_unit_w8(a, blockIdx.x, blockIdx.y, blockIdx.z, lds);
+}
+
 // The general kernel as a work queue (token-bounded splits, one workgroup per CU): a grid of
 // (task, kv head, split) workgroups is mostly empty when lengths are ragged (a request of L
 // history tokens uses ceil(L / split_tokens) of the split slots), and with one workgroup per
@@ -578,25 +954,25 @@ __global__ __launch_bounds__(kThreads, 3 - RT) void history_kernel(const AttnArg
 // Launches that overlap on one device must not share counters.
 constexpr int kQueueTasks = 2048;  // task rows the workgroup lists in LDS
 
-template <int RT>
-__global__ __launch_bounds__(kThreads, 1) void history_queue_kernel(const AttnArgs a,
-                                                                     int32_t* counters,
-                                                                     int32_t programs) {
-  __shared__ HistoryLds<RT> lds;
+__global__ __launch_bounds__(kThreadsW8, 1) void history_queue_kernel(const AttnArgs a,
+                                                                       int32_t* counters,
+                                                                       int32_t programs) {
+  constexpr int kT = kThreadsW8;
+  __shared__ HistoryLdsW8 lds;
   __shared__ int32_t s_full[kQueueTasks + 1];  // full splits of the tasks before t
   __shared__ int32_t s_nsplit[kQueueTasks];
   __shared__ int16_t s_used[kQueueTasks];      // tasks in use, in order
-  __shared__ int32_t s_part[2][kThreads];      // per-thread sums, then their exclusive scan
+  __shared__ int32_t s_part[2][kT];            // per-thread sums, then their exclusive scan
   __shared__ int32_t s_total[2];               // full splits, tasks in use
   __shared__ int32_t s_claim;
   const int heads = a.L.kv_heads;
   // Split counts, then two exclusive scans (full splits, tasks in use) over thread chunks.
-  for (int task = threadIdx.x; task < programs; task += kThreads) {
+  for (int task = threadIdx.x; task < programs; task += kT) {
     Task t;
     s_nsplit[task] = read_task(a, t, task) ? history_splits(a, t.recent_begin - t.sink_len) : 0;
   }
   __syncthreads();
-  const int per = (programs + kThreads - 1) / kThreads;
+  const int per = (programs + kT - 1) / kT;
   const int lo_t = min(static_cast<int>(threadIdx.x) * per, programs);
   const int hi_t = min(lo_t + per, programs);
   int fsum = 0, usum = 0;
@@ -610,7 +986,7 @@ __global__ __launch_bounds__(kThreads, 1) void history_queue_kernel(const AttnAr
   __syncthreads();
   if (threadIdx.x < 2) {
     int acc = 0;
-    for (int i = 0; i < kThreads; ++i) {
+    for (int i = 0; i < kT; ++i) {
       const int x = s_part[threadIdx.x][i];
       s_part[threadIdx.x][i] = acc;
       acc += x;
@@ -654,7 +1030,7 @@ __global__ __launch_bounds__(kThreads, 1) void history_queue_kernel(const AttnAr
       task = s_used[k - full];
       split = s_nsplit[task] - 1;
     }
-    history_unit<RT>(a, task, head, split, lds);
+    history_unit_w8(a, task, head, split, lds);
   }
   // Unused split slots: LSE -inf for the rows of every task in use.
   for (int task = blockIdx.x; task < programs; task += gridDim.x) {
@@ -1297,10 +1673,10 @@ hipError_t launch_history(const AttnArgs& a, dim3 grid, int rows, hipStream_t st
     const int64_t units = static_cast<int64_t>(grid.x) * grid.y * grid.z;
     const int64_t cap = cus > 0 ? cus : 1;
     const unsigned wgs = static_cast<unsigned>(units < cap ? units : cap);
-    hipLaunchKernelGGL(history_queue_kernel<2>, dim3(wgs), dim3(kThreads), 0, stream, a, queue,
+    hipLaunchKernelGGL(history_queue_kernel, dim3(wgs), dim3(kThreadsW8), 0, stream, a, queue,
                        static_cast<int32_t>(grid.x));
   } else {
-    hipLaunchKernelGGL(history_kernel<2>, grid, dim3(kThreads), 0, stream, a);
+    hipLaunchKernelGGL(history_w8_kernel, grid, dim3(kThreadsW8), 0, stream, a);
   }
   return hipGetLastError();
 }

@@ -487,9 +487,9 @@ def history_rows(meta, layout, hq):
 
 def history_kernel_name(meta, layout, hq, tokens=0, split_tokens=0, use_queue=True):
     """The history-branch kernel ``attention_partials`` launches for ``tokens`` query rows:
-    the paired kernel up to 8 rows per task, then the one-tile and two-tile kernels; the
-    two-tile kernel's work-queue form with token-bounded splits (``use_queue``, a grid of at
-    most 2048 task rows)."""
+    the paired kernel up to 8 rows per task, the one-tile kernel up to 16, then the
+    eight-wavefront kernel, as a work queue with token-bounded splits (``use_queue``, a grid
+    of at most 2048 task rows)."""
     rows = history_rows(meta, layout, hq)
     if rows <= 8:
         return "history_pair_kernel"
@@ -497,8 +497,8 @@ def history_kernel_name(meta, layout, hq, tokens=0, split_tokens=0, use_queue=Tr
         return "history_kernel<1>"
     programs = attention_programs(tokens, meta.max_num_reqs, layout.config.queries_per_tile)
     if use_queue and split_tokens and programs <= 2048:
-        return "history_queue_kernel<2>"
-    return "history_kernel<2>"
+        return "history_queue_kernel"
+    return "history_w8_kernel"
 
 
 def history_post_supported(meta, layout, hq, splits, tokens=None):
