@@ -143,7 +143,7 @@ __device__ __forceinline__ void write_unused_split(const AttnArgs& a, const Task
 }
 
 // INT2 history branch (history.hip); rows = query rows per task (<= 32).
-// `queue`: two zeroed int32 counters for the work-queue form of the 9-32-row kernel
+// `queue`: two zeroed int32 counters for the work-queue form of the 17-32-row kernel
 // (token-bounded splits), or nullptr for the grid form.
 hipError_t launch_history(const AttnArgs& a, dim3 grid, int rows, hipStream_t stream,
                           int32_t* queue = nullptr);

@@ -572,7 +572,7 @@ __global__ __launch_bounds__(kThreads, 3 - RT) void history_kernel(const AttnArg
 // kernel's wavefront w % 4 and computes the rows 16 (w / 4) .. + 15 of them, so each chunk is
 // copied into LDS once (by the group-0 wavefront of its stream, three stages per stream) and
 // read by two wavefronts, and every SIMD holds two wavefronts (one workgroup of eight per CU;
-// a wavefront keeps one 16-row tile, 253 registers, instead of the two-tile kernel's 464,
+// a wavefront keeps one 16-row tile, about 210 registers, instead of 464 for two tiles,
 // whose single wavefront per SIMD left the VALU half idle). A workgroup barrier per chunk
 // publishes the chunk to the second wavefront of its stream and frees the stage of the chunk
 // before. A row's arithmetic is the general kernel's with one row tile; the lazy-max rescale
@@ -941,7 +941,7 @@ __global__ __launch_bounds__(kThreadsW8, 1) void history_w8_kernel(const AttnArg
   history_unit_w8(a, blockIdx.x, blockIdx.y, blockIdx.z, lds);
 }
 
-// The general kernel as a work queue (token-bounded splits, one workgroup per CU): a grid of
+// The 17-32-row kernel as a work queue (token-bounded splits, one workgroup per CU): a grid of
 // (task, kv head, split) workgroups is mostly empty when lengths are ragged (a request of L
 // history tokens uses ceil(L / split_tokens) of the split slots), and with one workgroup per
 // CU every empty workgroup holds a CU while it reads its task and exits. Here each
