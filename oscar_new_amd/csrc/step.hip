@@ -61,8 +61,11 @@ __global__ __launch_bounds__(kThreads) void pre_attention_kernel(const PreArgs p
 // or for all 256 columns when kQuarters is 4 (many rows: one merge per row instead of four,
 // and a quarter of the workgroups); the window workgroups are those of y = 0; both branches
 // have read the window before this launch, and the merges do not touch it.
+// At most 256 registers per wavefront (two workgroups per CU): the scanned merge's two
+// rounds of 16 partial rows in flight took the compiler to 260, one workgroup per CU, and
+// the c4 launch (448 workgroups) into two rounds on 256 CUs.
 template <int R, int kMode, int kQuarters = 1>
-__global__ __launch_bounds__(kThreads) void post_attention_kernel(const PostArgs p) {
+__global__ __launch_bounds__(kThreads, 2) void post_attention_kernel(const PostArgs p) {
   __shared__ __attribute__((aligned(16))) uint16_t s_h[R][kHeadDim];  // merged history rows
   __shared__ float s_l[R];
   __shared__ GroupMergeLds group_lds;
