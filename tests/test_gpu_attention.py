@@ -118,10 +118,10 @@ def test_token_bounded_splits_match_oracle_and_merge_to_one_split(splits, split_
 
 @pytest.mark.parametrize("splits,split_tokens", [(40, 128), (16, 512)])
 def test_work_queue_is_bitwise_the_grid_form(splits, split_tokens):
-    # MTP tasks of 4 query tokens x 6 heads (24 rows: the two-tile kernel) with token-bounded
-    # splits run as a work queue (one workgroup per CU over the units in use): the same LSEs
-    # and partial rows as the grid form, call after call (the counters reset themselves) and
-    # in graph replays with eager launches in between.
+    # MTP tasks of 4 query tokens x 6 heads (24 rows: the eight-wavefront kernel) with
+    # token-bounded splits run as a work queue (one workgroup per CU over the units in use): the
+    # same LSEs and partial rows as the grid form, call after call (the counters reset
+    # themselves) and in graph replays with eager launches in between.
     lengths = [2600, 900, 5000, 300, 40]
     prefixes = [x - 4 for x in lengths]
     layout, _, hist, window, meta, _, rk, rv, *_, q, k, v = _setup(lengths, prefixes)
