@@ -1186,15 +1186,18 @@ __device__ __forceinline__ void history_pair_body(const AttnArgs& a, const Finis
     for (int i = 0; i < kDma; ++i) dma_x4(base, voff[i], lds + 1024 * i);
   };
 
-  // ---- query rows -> LDS (wavefront 3's stages): piece p of row r at r * 32 + (p ^ r).
-  // Layer step: 16 staged rows, the query rows 0..7 and, in the workgroups that store them,
-  // the current key rows (8..11) and value rows (12..15) of the task's tokens.
-  uint8_t* q_lds = s_ring + 6 * kStageBytes;
-  // The FP8 operand images [b][term][r][h][d]: after the staged rows, or, in the layer step,
+  // ---- query rows -> LDS: piece p of row r at r * 32 + (p ^ r), in an area of their own
+  // (the FP8 operand images [b][term][r][h][d] replace them once every wavefront has read
+  // them), so that every wavefront requests its first chunks at once. Layer step: 16 staged
+  // rows in wavefront 3's stages, the query rows 0..7 and, in the workgroups that store them,
+  // the current key rows (8..11) and value rows (12..15) of the task's tokens, and the images
   // in the finisher's LDS (free until the end), so that they outlive wavefront 3's stages.
+  __shared__ __attribute__((aligned(16))) uint8_t s_q[kMode == 2 ? 16 : 8 * 512];
+  static_assert(4 * 2 * 8 * 16 * 4 <= 8 * 512, "the images fit the query rows' area");
+  uint8_t* q_lds = kMode == 2 ? s_ring + 6 * kStageBytes : s_q;
   __shared__ __attribute__((aligned(16))) uint8_t s_fin[kMode == 2 ? kLayerFinBytes : 16];
   static_assert(kMode != 2 || 4 * 2 * 8 * 16 * 4 <= kLayerFinBytes, "images fit s_fin");
-  uint32_t* q_img = reinterpret_cast<uint32_t*>(kMode == 2 ? s_fin : q_lds + 8 * 512);
+  uint32_t* q_img = reinterpret_cast<uint32_t*>(kMode == 2 ? s_fin : s_q);
   bool stores_k = false, stores_v = false;
   const int nraw = min(kRawSplits, nsplit);
   if constexpr (kMode == 2) {
@@ -1229,7 +1232,7 @@ __device__ __forceinline__ void history_pair_body(const AttnArgs& a, const Finis
   }
   OSCAR_WAIT_VM(0);
   __syncthreads();
-  if (wave < 3) {
+  if (kMode != 2 || wave < 3) {
     if (nmine > 0) issue(0, 0);
     if (nmine > 1) issue(1, 1);
   }
@@ -1259,10 +1262,11 @@ __device__ __forceinline__ void history_pair_body(const AttnArgs& a, const Finis
   if constexpr (kMode == 4) {
     // Rows 0..7 are staged; rows 8..15 of the tile are zero operands (never written back).
     u32x4 aop[8];
-    load_stage_a(q_lds, aop);
 #pragma unroll
     for (int m = 0; m < 8; ++m)
-      if (n >= 8) aop[m] = u32x4{0u, 0u, 0u, 0u};
+      aop[m] = n < 8 ? *reinterpret_cast<const u32x4*>(q_lds + n * kStageRowBytes +
+                                                       16 * ((4 * m + g) ^ n))
+                     : u32x4{0u, 0u, 0u, 0u};
     barrier_lds();  // every operand is in registers; the rotated rows replace the staged ones
     rotate_stage(aop, rb, q_lds, 0, 8);
     barrier_lds();
@@ -1305,14 +1309,22 @@ __device__ __forceinline__ void history_pair_body(const AttnArgs& a, const Finis
 
   // ---- operand images: wavefront w converts head-dim block b = w. Item (r, h, d) = dword d
   // of the live B operand of row r, k half h: FP8 terms of 4 dims, term 1 the residual.
+  u32x4 wq[2];
+#pragma unroll
+  for (int it = 0; it < 2; ++it) {
+    const int item = 64 * it + lane;
+    const int r = item >> 4, h = (item >> 3) & 1, d = item & 7;
+    const int piece = 8 * wave + 4 * (d >> 2) + 2 * h + (d & 1);
+    wq[it] = *reinterpret_cast<const u32x4*>(q_lds + r * 512 + 16 * (piece ^ r));
+  }
+  if constexpr (kMode != 2) barrier_lds();  // every wavefront has read the rows the images replace
 #pragma unroll
   for (int it = 0; it < 2; ++it) {
     const int item = 64 * it + lane;
     const int r = item >> 4, h = (item >> 3) & 1, d = item & 7;
     const float mult = __shfl(qmult_l, 8 * r, kWave);
     const bool live = row_info(a, t, head, r).valid;  // padding rows stage the wrong bytes
-    const int piece = 8 * wave + 4 * (d >> 2) + 2 * h + (d & 1);
-    const u32x4 w = *reinterpret_cast<const u32x4*>(q_lds + r * 512 + 16 * (piece ^ r));
+    const u32x4 w = wq[it];
     const bool odd = (d >> 1) & 1;
     float v[4];
 #pragma unroll
@@ -1351,10 +1363,12 @@ __device__ __forceinline__ void history_pair_body(const AttnArgs& a, const Finis
     if (do_k) stage_row_floats(q_lds, 8 + wave, kx);
     if (do_v) stage_row_floats(q_lds, 12 + wave, vx);
   }
-  barrier_lds();  // everyone is done with wavefront 3's stages
-  if (wave == 3) {
-    if (nmine > 0) issue(0, 0);
-    if (nmine > 1) issue(1, 1);
+  if constexpr (kMode == 2) {
+    barrier_lds();  // everyone is done with wavefront 3's stages
+    if (wave == 3) {
+      if (nmine > 0) issue(0, 0);
+      if (nmine > 1) issue(1, 1);
+    }
   }
   if constexpr (kMode == 2) {
     // INT2 store of the step's own key / value rows (store_int2 semantics), then this split's
