@@ -282,8 +282,8 @@ int oscar_prefill_attention(const void* query, int64_t q_s0, int64_t q_s1, const
  * attention_partials of backend.py:195-205. query_rot: the rotated query (as for
  * oscar_attention_partials), or NULL: then each history workgroup rotates its task's query rows
  * by R_k itself (the bits of oscar_rotate, so the q rotation of backend.py:195 needs no launch
- * of its own; r_s0..r_s2 are ignored); query/key/value/window/rk_t/rv_t/slots/clip/raw_partials/raw_lse:
- * as for oscar_pre_attention; partials/lse/splits/split_tokens: as for
+ * of its own; r_s0..r_s2 are ignored); query/key/value/window/rk_t/rv_t/slots/clip/
+ * raw_partials/raw_lse: as for oscar_pre_attention; partials/lse/splits/split_tokens: as for
  * oscar_attention_partials. All outputs have the bits of those two calls. Coverage: query rows
  * per task (min(query_tile, max_query_len) * hq / kv_heads) <= 8, else OSCAR_E_UNSUPPORTED.
  */

@@ -523,8 +523,8 @@ def history_pre(query_rot, query, key, value, history, window, meta, layout, sca
 
     ``query_rot``: the rotated query, or None: then the history workgroups rotate the query
     rows by R_k themselves (the bits of ``rotate(query, R_k)``; no launch of its own);
-    ``query``/``key``/``value``: the step's unrotated rows. Returns ``(partials [n, hq, splits, 256], lse [n, hq, splits], raw_partials
-    [n, hq, 1, 256], raw_lse [n, hq, 1])``, all fp32.
+    ``query``/``key``/``value``: the step's unrotated rows. Returns ``(partials [n, hq, splits,
+    256], lse [n, hq, splits], raw_partials [n, hq, 1, 256], raw_lse [n, hq, 1])``, all fp32.
     """
     _device_check(query_rot, query, key, value, history, window, rk_t, rv_t)
     n, hq, d = query.shape
