@@ -1,12 +1,13 @@
 // Initial prefill: causal attention of each request over its own tokens (no history), the
 // replacement of the reference's fused-infer call (oscar_ascend/backend.py:175-193).
 //
-// Flash layout for MI355X: a workgroup of 8 wavefronts serves 128 consecutive (query, head) rows
-// of one request and one KV head (wavefront w: rows 16 w .. 16 w + 15, all 256 output dims) and
-// streams the request's keys and values in 32-token blocks that its four wavefronts share:
-// each block is copied into LDS once by direct-to-LDS loads (three stages, one block in flight
-// while one is computed, one barrier per block), so the K/V bytes a workgroup reads serve all of
-// its 128 rows. The arithmetic of every row is the BF16 branch's (raw.h: the same MFMA
+// Flash layout for MI355X: a workgroup of 12 wavefronts (three per SIMD) serves 192 consecutive
+// (query, head) rows of one request and one KV head (wavefront w: rows 16 w .. 16 w + 15, all
+// 256 output dims) and streams the request's keys and values in 32-token blocks that its
+// wavefronts share: each block is copied into LDS once by direct-to-LDS loads (three stages,
+// one block in flight while one is computed, one barrier per block), so the K/V bytes a
+// workgroup reads from L2 serve all of its 192 rows (the copies, 32 KiB per block and
+// workgroup, are what bounds the kernel: 128-row workgroups took 16 % longer). The arithmetic of every row is the BF16 branch's (raw.h: the same MFMA
 // operands and k order, the same lazy max, p, sums and normalization), so the output, the LSE
 // and the bits are those of the decode path (attention_partials raw + merges) for a request
 // without history. Blocks past a workgroup's last query are not read (they are masked for
@@ -19,14 +20,15 @@
 namespace oscar {
 namespace {
 
-constexpr int kWavesP = 8;                           // wavefronts per workgroup
+constexpr int kWavesP = 12;                          // wavefronts per workgroup (3 per SIMD)
+constexpr int kCopyWavesP = 8;                       // the ones that copy blocks and pair V
 constexpr int kThreadsP = kWavesP * kWave;
 constexpr int kPrefillRT = 1;                        // row tiles per wavefront
-constexpr int kSpanRows = kWavesP * 16 * kPrefillRT;  // 128 rows per workgroup
+constexpr int kSpanRows = kWavesP * 16 * kPrefillRT;  // 192 rows per workgroup
 constexpr int kRowBytes = kHeadDim * 2;              // 512 bytes per K or V row
 constexpr int kBlockBytes = kBlock * kRowBytes;      // 16 KiB per K or V block
 constexpr int kStageBytesP = 2 * kBlockBytes;        // K then V
-constexpr int kDmaPerWave = kStageBytesP / 1024 / kWavesP;  // 1 KiB per DMA, 4 per wavefront
+constexpr int kDmaPerWave = kStageBytesP / 1024 / kCopyWavesP;  // 1 KiB per DMA, 4 per wavefront
 constexpr int kStagesP = 3;                          // K/V blocks in LDS
 constexpr int kAheadP = 1;                           // blocks in flight beyond the current one
 // Paired V (the P*V B operands, built once per block by the whole workgroup): row r(d) of dim
@@ -60,10 +62,10 @@ struct PrefillArgs {
   float* lse;
 };
 
-// Copies block b of (K, V) rows into `stage`: wavefront w issues DMAs 4 w .. 4 w + 3, DMA i
+// Copies block b of (K, V) rows into `stage`: wavefront w < 8 issues DMAs 4 w .. 4 w + 3, DMA i
 // covering K (i < 16) or V rows 2 (i mod 16), + 1. Lane l writes row t = 2 (i mod 16) + l / 32
 // at position l mod 32, fetching the chunk chunk_pos maps there. Every lane issues its copy
-// (the stage waits count 4 DMAs per wavefront): rows at or past the request's token count copy
+// (the stage waits count 4 DMAs per copying wavefront; the others have none): rows at or past the request's token count copy
 // its last row instead; they are masked for every query row, so their p is exactly 0 and their
 // products add exact zeros, as the decode path's zero rows do. `kb`/`vb`: the request's row 0
 // of this head's keys and values; `kstride`/`vstride`: bytes per token.
@@ -71,6 +73,7 @@ __device__ __forceinline__ void prefill_copy_block(const uint8_t* kb, const uint
                                                    uint32_t kstride, uint32_t vstride, int qlen,
                                                    int b, uint8_t* stage) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  if (wave >= kCopyWavesP) return;
   const int last = qlen - 1 - kBlock * b;  // rows past it copy the request's last row
   const int64_t block_row = static_cast<int64_t>(kBlock) * b;
   const uint8_t* kbase = kb + block_row * kstride;
@@ -150,7 +153,7 @@ __global__ __launch_bounds__(kThreadsP) void prefill_flash_kernel(const PrefillA
       const int t = 16 * tt + n;
       koff[tt][m] = t * kRowBytes + 16 * chunk_pos(t, 8 * g + m);
     }
-  // Pairing: lane l of wavefront w takes token pair q = l % 16 (tokens t0, t0 + 1 with
+  // Pairing (wavefronts w < 8): lane l of wavefront w takes token pair q = l % 16 (tokens t0, t0 + 1 with
   // t0 = tau(q / 4, 2 (q % 4))) and 8-dim chunk c = 8 (l / 16) + w of the block's V rows; dim
   // 8 c + j goes to row r = 16 ((8 c + j) % 16) + (8 c + j) / 16 = 128 (c % 2) + 16 j + c / 2.
   // (The two 16-lane halves of a write then fall on disjoint banks: their rows are 4 apart.)
@@ -245,7 +248,7 @@ __global__ __launch_bounds__(kThreadsP) void prefill_flash_kernel(const PrefillA
     update_max(st, s2, g);
     block_p(st, s2, ap_prev);
     // Pairs of block b (into the buffer block b - 2 used, read before the barrier above).
-    pair_block(stage, s_pair[b & 1]);
+    if (wave < kCopyWavesP) pair_block(stage, s_pair[b & 1]);
   }
   if (nblk > 0) {
     barrier_lds();  // the last block's pairs
