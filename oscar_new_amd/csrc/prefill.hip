@@ -290,11 +290,11 @@ __global__ __launch_bounds__(kThreadsP) void prefill_flash_kernel(const PrefillA
 // Rows of tokens at or past counts[1]: zero output, LSE -inf (the reference zeroes
 // output[num_actual_tokens:]).
 __global__ __launch_bounds__(kThreads) void prefill_clear_kernel(const PrefillArgs a) {
-  const int64_t active = a.counts[1];
+  // The rows of tokens [counts[1], n) only (all of them for a negative count, none past n).
+  const int64_t active = min(max(static_cast<int64_t>(a.counts[1]), int64_t{0}), a.n);
   const int64_t total = a.n * a.hq;
-  for (int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6); row < total;
-       row += static_cast<int64_t>(gridDim.x) * 4) {
-    if (row / a.hq < active) continue;
+  for (int64_t row = active * a.hq + static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+       row < total; row += static_cast<int64_t>(gridDim.x) * 4) {
     const int lane = threadIdx.x & 63;
     *reinterpret_cast<uint2*>(a.out + row * kHeadDim + 4 * lane) = make_uint2(0u, 0u);
     if (a.lse && lane == 0) a.lse[row] = -INFINITY;
