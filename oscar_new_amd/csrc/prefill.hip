@@ -4,10 +4,11 @@
 // Flash layout for MI355X: a workgroup of 12 wavefronts (three per SIMD) serves 192 consecutive
 // (query, head) rows of one request and one KV head (wavefront w: rows 16 w .. 16 w + 15, all
 // 256 output dims) and streams the request's keys and values in 32-token blocks that its
-// wavefronts share: each block is copied into LDS once by direct-to-LDS loads (three stages,
-// one block in flight while one is computed, one barrier per block), so the K/V bytes a
-// workgroup reads from L2 serve all of its 192 rows (the copies, 32 KiB per block and
-// workgroup, are what bounds the kernel: 128-row workgroups took 16 % longer). The arithmetic of every row is the BF16 branch's (raw.h: the same MFMA
+// wavefronts share: each block is copied into LDS once by direct-to-LDS loads (four stages,
+// two blocks in flight while one is computed, one barrier per block), so the K/V bytes a
+// workgroup reads from L2 serve all of its 192 rows. The copies, 32 KiB per block and
+// workgroup, are what bounds the kernel: 128-row workgroups took 16 % longer, and one block in
+// flight 11 % longer. The arithmetic of every row is the BF16 branch's (raw.h: the same MFMA
 // operands and k order, the same lazy max, p, sums and normalization), so the output, the LSE
 // and the bits are those of the decode path (attention_partials raw + merges) for a request
 // without history. Blocks past a workgroup's last query are not read (they are masked for
@@ -29,14 +30,18 @@ constexpr int kRowBytes = kHeadDim * 2;              // 512 bytes per K or V row
 constexpr int kBlockBytes = kBlock * kRowBytes;      // 16 KiB per K or V block
 constexpr int kStageBytesP = 2 * kBlockBytes;        // K then V
 constexpr int kDmaPerWave = kStageBytesP / 1024 / kCopyWavesP;  // 1 KiB per DMA, 4 per wavefront
-constexpr int kStagesP = 3;                          // K/V blocks in LDS
-constexpr int kAheadP = 1;                           // blocks in flight beyond the current one
+constexpr int kStagesP = 4;                          // K/V blocks in LDS
+constexpr int kAheadP = 2;                           // blocks in flight beyond the current one
 // Paired V (the P*V B operands, built once per block by the whole workgroup): row r(d) of dim
 // d holds 16 dwords, dword 4 g + f = (V[tau(g, 2 f + 1)][d] << 16) | V[tau(g, 2 f)][d]; rows
-// are 80 bytes apart and ordered r(16 n + j) = 16 j + n, so that the 8 lanes n = 0..7 of a
-// read (rows 16 n + j, one 16-byte column) hit 8 different bank quads.
-constexpr int kPairRowBytes = 80;
-constexpr int kPairBytes = kHeadDim * kPairRowBytes;  // 20 KiB per block
+// are 64 bytes apart and ordered r(16 n + j) = 16 j + n, and the 16-byte column g of row r
+// sits at column g ^ (r / 2 mod 4), so that the 8 lanes n = 0..7 of a read (rows 16 j + n, one
+// column) hit 8 different bank quads. Four K/V stages and two pair buffers fill the 160 KiB.
+constexpr int kPairRowBytes = 64;
+constexpr int kPairBytes = kHeadDim * kPairRowBytes;  // 16 KiB per block
+__device__ __forceinline__ uint32_t pair_pos(int r, int dword) {
+  return r * kPairRowBytes + 16 * ((dword >> 2) ^ ((r >> 1) & 3)) + 4 * (dword & 3);
+}
 
 // LDS position of 16-byte chunk c of block row t: the chunk's low three bits are XOR-swizzled by
 // the row's low three bits and the chunk's own bits 3-4, so that each group of 8 lanes the LDS
@@ -117,7 +122,7 @@ __global__ __launch_bounds__(kThreadsP) void prefill_flash_kernel(const PrefillA
   const uint8_t* kb = reinterpret_cast<const uint8_t*>(a.key + qstart * a.ks0 + head * a.ks1);
   const uint8_t* vb = reinterpret_cast<const uint8_t*>(a.value + qstart * a.vs0 + head * a.vs1);
   const uint32_t kstride = static_cast<uint32_t>(a.ks0 * 2), vstride = static_cast<uint32_t>(a.vs0 * 2);
-  for (int b = 0; b <= kAheadP && b < nblk; ++b)
+  for (int b = 0; b < kAheadP && b < nblk; ++b)  // block b + kAheadP: iteration b
     prefill_copy_block(kb, vb, kstride, vstride, qlen, b, s_kv[b]);
 
   // Query rows of this wavefront's tile: row16 = row0 + 16 w + n.
@@ -161,9 +166,11 @@ __global__ __launch_bounds__(kThreadsP) void prefill_flash_kernel(const PrefillA
   const int pt0 = tau(pq >> 2, 2 * (pq & 3));
   const uint32_t pair_src0 = kBlockBytes + pt0 * kRowBytes + 16 * chunk_pos(pt0, pc);
   const uint32_t pair_src1 = kBlockBytes + (pt0 + 1) * kRowBytes + 16 * chunk_pos(pt0 + 1, pc);
-  const uint32_t pair_dst = (128 * (pc & 1) + (pc >> 1)) * kPairRowBytes + 4 * pq;
+  // (Rows 16 j apart share the column swizzle, so the rows 16 j + r of one lane are a fixed
+  // stride apart.)
+  const uint32_t pair_dst = pair_pos(128 * (pc & 1) + (pc >> 1), pq);
   // P*V operand of lane (n, g), dim tile j: row 16 j + n, dwords 4 g .. 4 g + 3.
-  const uint32_t pv_off = n * kPairRowBytes + 16 * g;
+  const uint32_t pv_off = pair_pos(n, 4 * g);
   auto pair_block = [&](const uint8_t* stage, uint8_t* pairs) {
     const u32x4 x0 = *reinterpret_cast<const u32x4*>(stage + pair_src0);
     const u32x4 x1 = *reinterpret_cast<const u32x4*>(stage + pair_src1);
@@ -193,17 +200,20 @@ __global__ __launch_bounds__(kThreadsP) void prefill_flash_kernel(const PrefillA
 
   for (int b = 0; b < nblk; ++b) {
     const uint8_t* stage = s_kv[b % kStagesP];
-    // Block b + 1 goes to the stage of block b - 2: every wavefront finished with that block
+    // Block b + 2 goes to the stage of block b - 2: every wavefront finished with that block
     // (scores, pairing) before it reached the barrier of block b - 1, which this wavefront has
-    // passed. Then wait for block b (the block issued after it stays in flight) and the
+    // passed. Then wait for block b (the blocks issued after it stay in flight) and the
     // barrier that makes every wavefront's copies of it, and the pairs of block b - 1, visible;
     // it is the only barrier of a block.
     static_assert(kAheadP + 2 <= kStagesP, "the stage refilled is two blocks old");
     if (b + kAheadP < nblk)
       prefill_copy_block(kb, vb, kstride, vstride, qlen, b + kAheadP,
                          s_kv[(b + kAheadP) % kStagesP]);
+    static_assert(kAheadP == 2, "the waits below count two blocks at most");
     const int after = min(nblk - 1 - b, kAheadP);
-    if (after >= 1)
+    if (after >= 2)
+      OSCAR_WAIT_VM(2 * kDmaPerWave);
+    else if (after == 1)
       OSCAR_WAIT_VM(kDmaPerWave);
     else
       OSCAR_WAIT_VM(0);
