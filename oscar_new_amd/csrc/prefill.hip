@@ -5,7 +5,7 @@
 // (query, head) rows of one request and one KV head (wavefront w: rows 16 w .. 16 w + 15, all
 // 256 output dims) and streams the request's keys and values in 32-token blocks that its
 // wavefronts share: each block is copied into LDS once by direct-to-LDS loads (four stages,
-// two blocks in flight while one is computed, one barrier per block), so the K/V bytes a
+// three blocks in flight while one is computed, one barrier per block), so the K/V bytes a
 // workgroup reads from L2 serve all of its 192 rows. The copies, 32 KiB per block and
 // workgroup, are what bounds the kernel: 128-row workgroups took 16 % longer, and one block in
 // flight 11 % longer. The arithmetic of every row is the BF16 branch's (raw.h: the same MFMA
@@ -31,7 +31,7 @@ constexpr int kBlockBytes = kBlock * kRowBytes;      // 16 KiB per K or V block
 constexpr int kStageBytesP = 2 * kBlockBytes;        // K then V
 constexpr int kDmaPerWave = kStageBytesP / 1024 / kCopyWavesP;  // 1 KiB per DMA, 4 per wavefront
 constexpr int kStagesP = 4;                          // K/V blocks in LDS
-constexpr int kAheadP = 2;                           // blocks in flight beyond the current one
+constexpr int kAheadP = 3;                           // blocks in flight beyond the current one
 // Paired V (the P*V B operands, built once per block by the whole workgroup): row r(d) of dim
 // d holds 16 dwords, dword 4 g + f = (V[tau(g, 2 f + 1)][d] << 16) | V[tau(g, 2 f)][d]; rows
 // are 64 bytes apart and ordered r(16 n + j) = 16 j + n, and the 16-byte column g of row r
@@ -200,17 +200,12 @@ __global__ __launch_bounds__(kThreadsP) void prefill_flash_kernel(const PrefillA
 
   for (int b = 0; b < nblk; ++b) {
     const uint8_t* stage = s_kv[b % kStagesP];
-    // Block b + 2 goes to the stage of block b - 2: every wavefront finished with that block
-    // (scores, pairing) before it reached the barrier of block b - 1, which this wavefront has
-    // passed. Then wait for block b (the blocks issued after it stay in flight) and the
-    // barrier that makes every wavefront's copies of it, and the pairs of block b - 1, visible;
-    // it is the only barrier of a block.
-    static_assert(kAheadP + 2 <= kStagesP, "the stage refilled is two blocks old");
-    if (b + kAheadP < nblk)
-      prefill_copy_block(kb, vb, kstride, vstride, qlen, b + kAheadP,
-                         s_kv[(b + kAheadP) % kStagesP]);
-    static_assert(kAheadP == 2, "the waits below count two blocks at most");
-    const int after = min(nblk - 1 - b, kAheadP);
+    // Wait for block b (the blocks issued after it stay in flight) and the barrier that makes
+    // every wavefront's copies of it, and the pairs of block b - 1, visible; it is the only
+    // barrier of a block. After it, block b + 3 goes to the stage of block b - 1: every
+    // wavefront finished with that block (scores, pairing) before reaching the barrier.
+    static_assert(kAheadP + 1 <= kStagesP && kAheadP == 3, "the stage refilled is one block old");
+    const int after = min(nblk - 1 - b, kAheadP - 1);
     if (after >= 2)
       OSCAR_WAIT_VM(2 * kDmaPerWave);
     else if (after == 1)
@@ -218,6 +213,9 @@ __global__ __launch_bounds__(kThreadsP) void prefill_flash_kernel(const PrefillA
     else
       OSCAR_WAIT_VM(0);
     barrier_lds();  // block b landed, pairs of block b - 1 written
+    if (b + kAheadP < nblk)
+      prefill_copy_block(kb, vb, kstride, vstride, qlen, b + kAheadP,
+                         s_kv[(b + kAheadP) % kStagesP]);
     // P*V of block b - 1 (the accumulators take it before block b's lazy max may rescale
     // them, the order of the one-block-at-a-time stream) interleaved with block b's scores
     // S^T = K Q^T (A = K rows 16 tt + n, chunk 8 g + m): two P*V tiles per score k-step.
