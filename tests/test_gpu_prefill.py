@@ -8,7 +8,11 @@ kernels.prefill_attention, on MI355X.
   fp64 over bf16 inputs): the reference test's atol 0.035 / rtol 0.04
   (tests/test_npu_kernels.py:194), mean-abs <= 2e-3, LSE within 2e-2.
 * Padded rows past the token count: zero output, LSE -inf.
+* GQA 5:1 (two KV heads) and 7:1, where the 192-row spans start and end inside a query,
+  against causal attention in float64 over the same bf16 inputs.
 """
+
+from types import SimpleNamespace
 
 import numpy as np
 import pytest
@@ -17,6 +21,7 @@ import torch
 import oracle as O
 from oscar_new_amd.config import OscarConfig, task_capacity
 from oscar_new_amd import kernels
+from oscar_new_amd.layout import CacheLayout
 from tests._state import bits
 from tests.test_gpu_fused import _case, _forward
 
@@ -72,7 +77,7 @@ def test_prefill_matches_int2_path_and_dense_reference(lengths, pad):
     ([300, 5], False),  # max_query_len unknown: spans sized by the token count
 ])
 def test_long_prefill_is_bitwise_the_int2_path(lengths, max_query_len):
-    # The flash kernel's spans share K/V blocks across 128 rows; every row must still carry the
+    # The flash kernel's spans share K/V blocks across 192 rows; every row must still carry the
     # BF16 branch's bits (the general path runs that branch per 4-query task).
     c = _case(lengths, [0] * len(lengths), seed=43, cfg=OscarConfig(sink_tokens=4,
                                                                     recent_tokens=64))
@@ -86,3 +91,50 @@ def test_long_prefill_is_bitwise_the_int2_path(lengths, max_query_len):
     for a, b in zip(want, got):
         assert torch.equal(a, b)
     assert torch.isfinite(got[0].view(torch.bfloat16).float()).all()
+
+
+@pytest.mark.parametrize("g,kv_heads,lengths", [
+    (5, 2, [300, 77, 1]),  # 192-row spans end inside a query's 5 heads, two KV heads
+    (7, 1, [150, 40]),  # ... and inside a query's 7 heads
+])
+def test_prefill_spans_that_split_a_query(g, kv_heads, lengths):
+    # With 6 query heads per KV head a 192-row span holds 32 whole queries; with 5 or 7 a
+    # span starts and ends inside a query, whose heads then go to two workgroups (and two
+    # workgroups copy the same K/V blocks). Checked against causal attention in float64 over
+    # the same bf16 inputs: relative L2 <= 1e-2, |err| <= 2e-2 + 1e-2 |want|, LSE within 2e-2.
+    print(f"[prefill] g {g} kv_heads {kv_heads} lengths {lengths}", flush=True)
+    gen = torch.Generator().manual_seed(47)
+    n, hq = sum(lengths), g * kv_heads
+    q = torch.randn(n, hq, 256, generator=gen).bfloat16()
+    k = torch.randn(n, kv_heads, 256, generator=gen).bfloat16()
+    v = torch.randn(n, kv_heads, 256, generator=gen).bfloat16()
+    starts = [0]
+    for length in lengths:
+        starts.append(starts[-1] + length)
+    meta = SimpleNamespace(
+        query_start_loc=torch.tensor(starts, dtype=torch.int32, device=DEV),
+        seq_lens=torch.tensor(lengths, dtype=torch.int32, device=DEV),
+        counts=torch.tensor([len(lengths), n], dtype=torch.int32, device=DEV),
+        max_num_reqs=len(lengths), max_query_len=max(lengths))
+    layout = CacheLayout(768, kv_heads=kv_heads,
+                         config=OscarConfig(sink_tokens=4, recent_tokens=64))
+    scale = 256 ** -0.5
+    out = torch.full((n, hq * 256), float("nan"), dtype=torch.bfloat16, device=DEV)
+    lse = torch.full((n * hq,), float("nan"), dtype=torch.float32, device=DEV)
+    kernels.prefill_attention(q.to(DEV), k.to(DEV), v.to(DEV), None, meta, layout, scale, out,
+                              lse)
+    torch.cuda.synchronize()
+    got = out.cpu().float().view(n, hq, 256).double()
+    got_l = lse.cpu().view(n, hq).double()
+    qf, kf, vf = q.double(), k.double(), v.double()
+    for r, length in enumerate(lengths):
+        rows = slice(starts[r], starts[r + 1])
+        causal = torch.ones(length, length, dtype=torch.bool).tril()
+        for h in range(hq):
+            s = (qf[rows, h] @ kf[rows, h // g].T * scale).masked_fill(~causal, float("-inf"))
+            want = torch.softmax(s, dim=1) @ vf[rows, h // g]
+            o = got[rows, h]
+            assert torch.isfinite(o).all(), (r, h)
+            assert (o - want).norm() <= 1e-2 * want.norm(), (r, h)
+            assert ((o - want).abs() <= 2e-2 + 1e-2 * want.abs()).all(), (r, h)
+            assert (got_l[rows, h] - torch.logsumexp(s, dim=1)).abs().max() <= 2e-2, (r, h)
