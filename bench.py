@@ -33,12 +33,12 @@ METRIC = "INT2 decode-attn µs/layer-step + achieved HBM GB/s at 32k ctx; store 
 PEAK_HBM_GBPS = 8000.0
 
 CONFIGS = {
-    "c3": dict(batch=32, context=32768, qlen=1, ragged=False, splits="mi355x",
+    "c3": dict(batch=32, context=32768, qlen=1, ragged=False, splits="device",
                desc="one TP rank of a Qwen3.5-27B-class layer: B32 x 32768 ctx, GQA 6:1, D256, "
-                    "INT2 history + 4 sink + 128 recent BF16, MI355X split partition"),
-    "c4": dict(batch=64, context=131072, qlen=4, ragged=True, splits="mi355x",
+                    "INT2 history + 4 sink + 128 recent BF16, device split rule"),
+    "c4": dict(batch=64, context=131072, qlen=4, ragged=True, splits="device",
                desc="ragged MTP: B64, ctx log-uniform [256, 131072], 4 query tokens each"),
-    "c5": dict(batch=4, context=262144, qlen=1, ragged=False, splits="mi355x",
+    "c5": dict(batch=4, context=262144, qlen=1, ragged=False, splits="device",
                pool_blocks=300_000,
                desc="long context: B4 x 262144 ctx, adaptive splits, 128-token blocks scattered "
                     "over a 300k-block (50k-page, 39 GB) pool"),
@@ -81,6 +81,13 @@ def parse_args(argv=None):
                         "prefill config (--config p1); store: the c2 store forms, plain "
                         "launches (for rocprofv3 counters)")
     p.add_argument("--copy-mib", type=int, default=1024)
+    p.add_argument("--split-policy", default=None, choices=("device", "reference", "mi355x"),
+                   help="history split policy (default: the config's, the device rule)")
+    p.add_argument("--branch", action="store_true",
+                   help="--mode history: the history branch alone instead of the step's "
+                        "history launch")
+    p.add_argument("--no-sub-configs", action="store_true",
+                   help="c3: skip the c4 / c5 / p1 sub-records")
     return p.parse_args(argv)
 
 
@@ -215,15 +222,35 @@ def algorithmic_bytes(w):
                            q_out=q_out, table=4 * cols, total=136 * hist + 1024 * bf16 + q_out + 4 * cols)
 
 
+def history_lengths(w):
+    """History tokens of each request (positions [sink_len, recent_begin))."""
+    cfg = w.cfg
+    out = []
+    for prefix in w.prefixes:
+        sink = min(cfg.sink_tokens, prefix)
+        out.append(max(sink, prefix - cfg.recent_tokens) - sink)
+    return out
+
+
+def effective_split_tokens(w, split_tokens):
+    """The split length the kernels use: split_tokens, or under the device rule (negative)
+    the length the GPU derives from the step's lengths (config.device_split_tokens; one task
+    per request at these configs; a grid of unit slots up to 8 query rows per task)."""
+    from oscar_new_amd import config
+
+    if split_tokens >= 0:
+        return split_tokens
+    return config.device_split_tokens(sum(history_lengths(w)), len(w.seqs), 1, -split_tokens,
+                                      fit_grid=w.qlen * 6 <= 8)
+
+
 def split_partial_bytes(w, splits, split_tokens):
     """Bytes the history launch writes: a 1024-byte partial row + 4-byte LSE per live split
     of each query row; only the LSE for the split slots a request does not use."""
-    cfg = w.cfg
+    st = effective_split_tokens(w, split_tokens)
     total = 0
-    for s, prefix in zip(w.seqs, w.prefixes):
-        sink = min(cfg.sink_tokens, prefix)
-        hist = max(sink, prefix - cfg.recent_tokens) - sink
-        used = splits if not split_tokens else min(splits, max(1, -(-hist // split_tokens)))
+    for hist in history_lengths(w):
+        used = splits if not st else min(splits, max(1, -(-hist // st)))
         total += w.qlen * 6 * (used * (256 * 4 + 4) + (splits - used) * 4)
     return total
 
@@ -530,39 +557,123 @@ def prefill_measurement(args, w, device):
     return 0
 
 
-def main(argv=None):
-    args = parse_args(argv)
-    if args.gpus != 1:
-        print(f"bench.py: this build measures one MI355X; --gpus {args.gpus} is not supported "
-              "(no multi-GPU path exists; run with --gpus 1)", file=sys.stderr)
-        return 2
+def in_step_launch(impl, w, layers, splits, split_tokens):
+    """The launch the layer step makes for its history branch, as ``impl.forward`` makes it:
+    ``(kernel name, algorithmic bytes, fn(i))``, fn(i) launching it on layer i's cache.
+
+    With the pre-attention roles in the history launch (up to 8 query rows per task) that is
+    ``history_pre`` (its workgroups rotate the query rows, run the BF16 branch and the K/V
+    INT2 store beside the INT2 stream); otherwise the step runs the pre-attention launch first
+    and this is the history branch alone (``attention_partials``)."""
+    from oscar_new_amd import kernels
+
+    views = [w.layout.tensor_views(c) for c in layers]
+    meta, layout = w.meta, w.layout
+    ntok = w.q.shape[0]
+    alg = algorithmic_bytes(w)
+    hist = alg.int2 + ntok * 6 * 256 * 2 + alg.table + split_partial_bytes(w, splits,
+                                                                         split_tokens)
+    if impl._roles_share_history_launch(meta):
+        rows = ntok * 6
+        # + the BF16 branch (window and current K/V rows, its partial rows), the step's INT2
+        # slots and R_k / R_v.
+        extra = alg.bf16 + rows * 1028 + ntok * 136 + 2 * 256 * 256 * 2
+        name = "history_pre_rot_kernel" if impl.rotate_in_history else "history_pre_kernel"
+        qrot = None if impl.rotate_in_history else kernels.rotate(w.q, impl.rk_cols)
+
+        def fn(i):
+            h, win = views[i % len(views)]
+            kernels.history_pre(qrot, w.q, w.k, w.v, h, win, meta, layout, 1 / 16, splits,
+                                impl.rk_t, impl.rv_t, split_tokens=split_tokens)
+
+        return name, hist + extra, fn
+    qrot = kernels.rotate(w.q, impl.rk_cols)
+
+    def fn(i):
+        h, win = views[i % len(views)]
+        kernels.attention_partials(qrot, w.k, w.v, h, win, meta, layout, 1 / 16, splits, False,
+                                   split_tokens=split_tokens)
+
+    return kernels.history_kernel_name(meta, layout, 6, ntok, split_tokens), hist, fn
+
+
+def branch_launch(impl, w, layers, splits, split_tokens):
+    """The history branch alone (``attention_partials`` on a pre-rotated query, no role
+    workgroups), with the step's partition: ``(kernel name, algorithmic bytes, fn(i))``."""
+    from oscar_new_amd import kernels
+
+    from oscar_new_amd import config
+
+    views = [w.layout.tensor_views(c) for c in layers]
+    ntok = w.q.shape[0]
+    alg = algorithmic_bytes(w)
+    qrot = kernels.rotate(w.q, impl.rk_cols)
+    if split_tokens < 0:  # the branch alone has no role workgroups: the whole launch budget
+        split_tokens = -(config.HISTORY_SLOTS if kernels.history_rows(w.meta, w.layout, 6) <= 16
+                         else config.QUEUE_SLOTS)
+    hist = alg.int2 + ntok * 6 * 256 * 2 + alg.table + split_partial_bytes(w, splits,
+                                                                         split_tokens)
+
+    def fn(i):
+        h, win = views[i % len(views)]
+        kernels.attention_partials(qrot, w.k, w.v, h, win, w.meta, w.layout, 1 / 16, splits,
+                                   False, split_tokens=split_tokens)
+
+    return kernels.history_kernel_name(w.meta, w.layout, 6, ntok, split_tokens), hist, fn
+
+
+def time_launch(fn, nlayers, steps, use_graph, stream=None, pool=None):
+    """Mean device time of fn(i) per launch: HIST_LAUNCHES back-to-back launches (cycling the
+    layers' caches) captured in one graph, replays timed with HIP events on the launching
+    stream (torch's current stream when graphs are off)."""
+    import torch
+
+    for i in range(nlayers):
+        fn(i)
+    torch.cuda.synchronize()
+    reps = max(1, -(-steps // HIST_LAUNCHES))
+    if use_graph:
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=stream, pool=pool):
+            for i in range(HIST_LAUNCHES):
+                fn(i)
+        torch.cuda.synchronize()
+        g.replay()
+        run = g.replay
+    else:
+        def run():
+            for i in range(HIST_LAUNCHES):
+                fn(i)
+    torch.cuda.synchronize()
+    h0, h1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    h0.record()
+    for _ in range(reps):
+        run()
+    h1.record()
+    torch.cuda.synchronize()
+    return h0.elapsed_time(h1) * 1e3 / (reps * HIST_LAUNCHES)
+
+
+def measure_step(args, name, device, steps, warmup):
+    """Build config `name`, time `steps` layer steps (graph replays cycling the layers), the
+    step's history launch and the history branch alone. Returns a dict of figures and the
+    workload (for the CPU baseline)."""
     import torch
 
     from oscar_new_amd import kernels
     from oscar_new_amd.backend import OscarAttentionImpl
 
-    if not torch.cuda.is_available():
-        print("bench.py: no ROCm GPU visible", file=sys.stderr)
-        return 1
-    device = torch.device("cuda:0")
-    torch.cuda.set_device(device)
-    if args.mode == "copy":
-        return copy_calibration(args, device)
-    if args.mode == "store":
-        time_store(device, args, args.steps, eager=True)
-        print(json.dumps({"mode": "store", "calls_per_form": args.steps}))
-        return 0
-    cfg = CONFIGS[args.config]
-    print(f"[bench] building {args.config} workload", file=sys.stderr, flush=True)
+    cfg = CONFIGS[name]
+    print(f"[bench] building {name} workload", file=sys.stderr, flush=True)
     w = build_workload(args, cfg, device)
-    if args.layers is None:
-        args.layers = 2 if w.k_cache.numel() * 2 > 16 << 30 else 4
+    nlayers = args.layers or (2 if w.k_cache.numel() * 2 > 16 << 30 else 4)
     layers = [(w.k_cache, w.v_cache)]
-    for _ in range(args.layers - 1):
+    for _ in range(nlayers - 1):
         layers.append((w.k_cache.clone(), w.v_cache.clone()))
     impls = []
     for _ in layers:
-        impl = OscarAttentionImpl.standalone(6, 256, 1 / 16, 1, w.cfg, split_policy=cfg["splits"],
+        impl = OscarAttentionImpl.standalone(6, 256, 1 / 16, 1, w.cfg,
+                                             split_policy=args.split_policy or cfg["splits"],
                                              one_launch_post=args.one_launch_post,
                                              overlap=not args.no_overlap,
                                              layer_step=args.layer_step,
@@ -571,42 +682,34 @@ def main(argv=None):
         impls.append(impl)
     ntok = w.q.shape[0]
     outputs = [torch.empty(ntok, 6 * 256, dtype=torch.bfloat16, device=device) for _ in layers]
-    splits, split_tokens = impls[0].partition_for(w.meta)
+    splits, split_tokens = impls[0].partition_for(w.meta, ntok)
 
     def step(i):
         impls[i].forward(None, w.q, w.k, w.v, layers[i], w.meta, outputs[i])
-
-    if args.mode == "prefill":
-        return prefill_measurement(args, w, device)
-    if args.mode == "history":
-        qrot = kernels.rotate(w.q, w.rk)
-        views = [w.layout.tensor_views(c) for c in layers]
-        for i in range(args.warmup + args.steps):
-            h, win = views[i % len(layers)]
-            kernels.attention_partials(qrot, w.k, w.v, h, win, w.meta, w.layout, 1 / 16, splits,
-                                       False, split_tokens=split_tokens)
-        torch.cuda.synchronize()
-        alg = algorithmic_bytes(w)
-        print(json.dumps({"mode": "history", "launches": args.warmup + args.steps,
-                          "splits": splits, "split_tokens": split_tokens,
-                          "history_tokens": alg.history_tokens,
-                          "int2_bytes": alg.int2, "physical_record_bytes": 160 * alg.history_tokens}))
-        return 0
 
     for i in range(len(layers)):  # eager warm-up (also builds the tensor views)
         step(i)
     torch.cuda.synchronize()
     # The layer steps of consecutive layers are captured back to back in one HIP graph, as a
     # model's decode graph holds them; a step is one layer's forward. `full` replays all
-    # layers once, `tail` covers a remainder so that exactly --steps steps are timed.
+    # layers once, `tail` covers a remainder so that exactly `steps` steps are timed. Under the
+    # device split rule the graph is captured at a dummy batch's lengths (zero counts, as
+    # vLLM's capture build leaves them) and replayed at the workload's.
     nl = len(layers)
-    graphs = None
+    graphs = stream = pool = None
+    dummy_capture = not args.no_graph and split_tokens < 0
     if not args.no_graph:
         stream = torch.cuda.Stream()
         stream.wait_stream(torch.cuda.current_stream())
         graphs = {}
-        pool = None
-        for count in sorted({nl, args.steps % nl, args.warmup % nl} - {0}):
+        counts = w.meta.counts.clone()
+        if dummy_capture:
+            w.meta.counts.zero_()
+            kernels.prepare_tasks(w.meta.query_start_loc, w.meta.counts, w.meta.tasks,
+                                  w.meta.task_count, w.meta.max_num_reqs,
+                                  w.cfg.queries_per_tile)
+            torch.cuda.synchronize()
+        for count in sorted({nl, steps % nl, warmup % nl} - {0}):
             g = torch.cuda.CUDAGraph()
             with torch.cuda.graph(g, stream=stream, pool=pool):
                 for i in range(count):
@@ -614,6 +717,12 @@ def main(argv=None):
             pool = g.pool()
             graphs[count] = g
         torch.cuda.synchronize()
+        if dummy_capture:
+            w.meta.counts.copy_(counts)
+            kernels.prepare_tasks(w.meta.query_start_loc, w.meta.counts, w.meta.tasks,
+                                  w.meta.task_count, w.meta.max_num_reqs,
+                                  w.cfg.queries_per_tile)
+            torch.cuda.synchronize()
 
     def run_steps(count):
         """`count` layer steps, cycling layers 0, 1, ..., nl - 1, 0, ..."""
@@ -626,137 +735,201 @@ def main(argv=None):
         if count % nl:
             graphs[count % nl].replay()
 
-    print(f"[bench] warmup {args.warmup}, timed {args.steps}", file=sys.stderr, flush=True)
-    run_steps(args.warmup)
+    print(f"[bench] {name}: warmup {warmup}, timed {steps}", file=sys.stderr, flush=True)
+    run_steps(warmup)
     torch.cuda.synchronize()
     ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
     ev0.record()
-    run_steps(args.steps)
+    run_steps(steps)
     ev1.record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     gpu_ms = ev0.elapsed_time(ev1)
-    us_step = wall / args.steps * 1e6
-
-    # Dominant kernel alone, HIP events around each launch: the history launch of the step
-    # (history + split merge + path merge + window store when history_post covers the step,
-    # else the history branch alone).
-    hist_views = [w.layout.tensor_views(c) for c in layers]
-    one_launch = impls[0].one_launch_post and kernels.history_post_supported(
-        w.meta, w.layout, 6, splits, ntok)
-    qrot, rp, rl = kernels.pre_attention(w.q, w.k, w.v, hist_views[0][0], hist_views[0][1],
-                                         w.meta, w.layout, 1 / 16, impls[0].rk_t, impls[0].rv_t)
-    out = torch.empty(ntok, 6 * 256, dtype=torch.bfloat16, device=device)
-
-    def history_launch(i):
-        h, win = hist_views[i % len(layers)]
-        if one_launch:
-            kernels.history_post(qrot, h, w.meta, w.layout, 1 / 16, splits, rp, rl,
-                                 impls[0].rv, w.k, w.v, win, out, split_tokens=split_tokens)
-        else:
-            kernels.attention_partials(qrot, w.k, w.v, h, win, w.meta, w.layout, 1 / 16, splits,
-                                       False, split_tokens=split_tokens)
-
-    for i in range(len(layers)):
-        history_launch(i)
-    torch.cuda.synchronize()
-    # Back-to-back launches (cycling the layers' caches) between HIP events on the launching
-    # stream: a captured graph of HIST_LAUNCHES launches when graphs are on, so that host
-    # launch overhead does not show up as kernel time; the mean over all launches.
-    reps = max(1, -(-args.steps // HIST_LAUNCHES))
-    if graphs is not None:
-        hg = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(hg, stream=stream, pool=pool):
-            for i in range(HIST_LAUNCHES):
-                history_launch(i)
-        torch.cuda.synchronize()
-        hg.replay()
-        run_hist = hg.replay
-    else:
-        def run_hist():
-            for i in range(HIST_LAUNCHES):
-                history_launch(i)
-    torch.cuda.synchronize()
-    h0, h1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    h0.record()
-    for _ in range(reps):
-        run_hist()
-    h1.record()
-    torch.cuda.synchronize()
-    hist_us = h0.elapsed_time(h1) * 1e3 / (reps * HIST_LAUNCHES)
+    us_step = wall / steps * 1e6
     alg = algorithmic_bytes(w)
-    partial_bytes = split_partial_bytes(w, splits, split_tokens)
-    hist_alg = alg.int2 + ntok * 6 * 256 * 2 + alg.table + partial_bytes
-    if one_launch:
-        # + the partial rows and LSEs read back by the merges, the BF16-branch rows, the output
-        # and merged LSE, R_v once, and the window store's current K/V (read and written).
-        rows = ntok * 6
-        hist_alg += partial_bytes + rows * (1024 + 4) + rows * (512 + 4) + 256 * 256 * 2
-        hist_alg += 2 * 2 * ntok * 512
-    hist_kernel = ("history_pair_finish_kernel" if one_launch
-                   else kernels.history_kernel_name(w.meta, w.layout, 6, ntok, split_tokens))
-    print(f"[bench] step {us_step:.1f} us, history kernel {hist_us:.1f} us", file=sys.stderr,
-          flush=True)
 
+    use_graph = graphs is not None
+    kname, kbytes, kfn = in_step_launch(impls[0], w, layers, splits, split_tokens)
+    k_us = time_launch(kfn, nl, steps, use_graph, stream, pool)
+    bname, bbytes, bfn = branch_launch(impls[0], w, layers, splits, split_tokens)
+    b_us = time_launch(bfn, nl, steps, use_graph, stream, pool)
+    print(f"[bench] {name}: step {us_step:.1f} us, {kname} {k_us:.1f} us, history branch alone "
+          f"({bname}) {b_us:.1f} us", file=sys.stderr, flush=True)
+    t_dev = effective_split_tokens(w, split_tokens)
+    figures = {
+        "workload": f"{name}: {cfg['desc']}",
+        "us_per_layer_step": us_step,
+        "gpu_us_per_layer_step": gpu_ms / steps * 1e3,
+        "algorithmic_bytes_per_step": alg.total,
+        "GBps": alg.total / (us_step * 1e-6) / 1e9,
+        "splits": splits,
+        "split_tokens": t_dev,
+        "split_rule": ("device (budget %d workgroups)" % -split_tokens if split_tokens < 0
+                       else "token-bounded" if split_tokens else "reference"),
+        "graph_captured_at": ("dummy lengths" if dummy_capture else
+                              "workload lengths" if use_graph else None),
+        "dominant": {
+            "kernel": kname, "us": k_us, "algorithmic_bytes": kbytes,
+            "GBps": kbytes / (k_us * 1e-6) / 1e9,
+            "frac": kbytes / (k_us * 1e-6) / 1e9 / PEAK_HBM_GBPS,
+            "traffic": read_traffic(kname, name),
+        },
+        "history_branch": {
+            "kernel": bname, "us": b_us, "algorithmic_bytes": bbytes,
+            "history_tokens": alg.history_tokens,
+            "GBps": bbytes / (b_us * 1e-6) / 1e9,
+            "int2_GBps": alg.int2 / (b_us * 1e-6) / 1e9,
+            "frac": bbytes / (b_us * 1e-6) / 1e9 / PEAK_HBM_GBPS,
+            "traffic": read_traffic(bname, name),
+        },
+        "layers_cycled": nl,
+        "hip_graph": use_graph,
+    }
+    return figures, SimpleNamespace(w=w, layers=layers, outputs=outputs, step=step)
+
+
+def prefill_record(args, device, steps, warmup):
+    """Sub-record of the initial-prefill launch (config p1)."""
+    import torch
+
+    from oscar_new_amd import kernels
+
+    w = build_workload(args, CONFIGS["p1"], device)
+    ntok = w.q.shape[0]
+    w.meta.initial_prefill = True
+    _, win = w.layout.tensor_views((w.k_cache, w.v_cache))
+    out = torch.empty(ntok, 6 * 256, dtype=torch.bfloat16, device=device)
+    us = time_launch(lambda i: kernels.prefill_attention(w.q, w.k, w.v, win, w.meta, w.layout,
+                                                         1 / 16, out), 1, steps, False)
+    pairs = sum(s * (s + 1) // 2 for s in w.seqs)
+    tflops = 4.0 * pairs * 6 * 256 / (us * 1e-6) / 1e12
+    return {"workload": f"p1: {CONFIGS['p1']['desc']}", "kernel": "prefill_flash_kernel",
+            "us": us, "tflops": tflops, "peak_tflops": 2500.0, "frac": tflops / 2500.0,
+            "bound": "mfma (bf16)"}
+
+
+def main(argv=None):
+    args = parse_args(argv)
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one MI355X; --gpus {args.gpus} is not supported "
+              "(no multi-GPU path exists; run with --gpus 1)", file=sys.stderr)
+        return 2
+    import torch
+
+    from oscar_new_amd import kernels
+
+    if not torch.cuda.is_available():
+        print("bench.py: no ROCm GPU visible", file=sys.stderr)
+        return 1
+    device = torch.device("cuda:0")
+    torch.cuda.set_device(device)
+    if args.mode == "copy":
+        return copy_calibration(args, device)
+    if args.mode == "store":
+        time_store(device, args, args.steps, eager=True)
+        print(json.dumps({"mode": "store", "calls_per_form": args.steps}))
+        return 0
+    if args.mode == "prefill":
+        cfg = CONFIGS[args.config]
+        print(f"[bench] building {args.config} workload", file=sys.stderr, flush=True)
+        return prefill_measurement(args, build_workload(args, cfg, device), device)
+    if args.mode == "history":
+        from oscar_new_amd.backend import OscarAttentionImpl
+
+        cfg = CONFIGS[args.config]
+        w = build_workload(args, cfg, device)
+        impl = OscarAttentionImpl.standalone(6, 256, 1 / 16, 1, w.cfg,
+                                             split_policy=args.split_policy or cfg["splits"])
+        impl.set_rotations(w.rk, w.rv)
+        splits, split_tokens = impl.partition_for(w.meta, w.q.shape[0])
+        kname, _, fn = (branch_launch if args.branch else in_step_launch)(
+            impl, w, [(w.k_cache, w.v_cache)], splits, split_tokens)
+        for i in range(args.warmup + args.steps):
+            fn(i)
+        torch.cuda.synchronize()
+        alg = algorithmic_bytes(w)
+        print(json.dumps({"mode": "history", "kernel": kname,
+                          "launches": args.warmup + args.steps, "splits": splits,
+                          "split_tokens": split_tokens, "history_tokens": alg.history_tokens,
+                          "int2_bytes": alg.int2,
+                          "physical_record_bytes": 160 * alg.history_tokens}))
+        return 0
+
+    fig, run = measure_step(args, args.config, device, args.steps, args.warmup)
+    w = run.w
     store = time_store(device, args, max(20, args.steps // 2))
+    cfg = CONFIGS[args.config]
+    dom = fig["dominant"]
     result = {
         "metric": METRIC,
-        "value": alg.total / (us_step * 1e-6) / 1e9,
+        "value": fig["GBps"],
         "unit": "GB/s",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": us_step / 1e3,
+        "ms_per_step": fig["us_per_layer_step"] / 1e3,
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "bf16",
         "data": "synthetic",
         "config": {
-            "workload": f"{args.config}: {cfg['desc']}",
+            "workload": fig["workload"],
             "batch": len(w.seqs),
             "context": cfg["context"],
             "query_tokens_per_request": w.qlen,
             "q_heads": 6, "kv_heads": 1, "head_dim": 256,
             "page_tokens": 768, "kernel_block_tokens": 128,
-            "splits": splits, "split_tokens": split_tokens, "layers_cycled": len(layers),
-            "hip_graph": graphs is not None, "seed": args.seed,
+            "splits": fig["splits"], "split_tokens": fig["split_tokens"],
+            "split_rule": fig["split_rule"], "graph_captured_at": fig["graph_captured_at"],
+            "layers_cycled": fig["layers_cycled"],
+            "hip_graph": fig["hip_graph"], "seed": args.seed,
             "one_launch_post": bool(args.one_launch_post),
             "overlap": not args.no_overlap,
             "layer_step": bool(args.layer_step),
             "rotate_in_history": not args.separate_q_rotation,
         },
-        "us_per_layer_step": us_step,
-        "gpu_us_per_layer_step": gpu_ms / args.steps * 1e3,
-        "algorithmic_bytes_per_step": alg.total,
-        "history_kernel": {
-            "kernel": hist_kernel,
-            "us": hist_us,
-            "history_tokens": alg.history_tokens,
-            "algorithmic_bytes": hist_alg,
-            "GBps": hist_alg / (hist_us * 1e-6) / 1e9,
-            "int2_GBps": alg.int2 / (hist_us * 1e-6) / 1e9,
-        },
+        "us_per_layer_step": fig["us_per_layer_step"],
+        "gpu_us_per_layer_step": fig["gpu_us_per_layer_step"],
+        "algorithmic_bytes_per_step": fig["algorithmic_bytes_per_step"],
+        "dominant_kernel": dom,
+        "history_kernel": fig["history_branch"],
         "store": store,
         "roofline": {
             "bound": "hbm",
-            "achieved": hist_alg / (hist_us * 1e-6) / 1e9,
+            "kernel": dom["kernel"],
+            "achieved": dom["GBps"],
             "peak": PEAK_HBM_GBPS,
             "unit": "GB/s",
-            "frac": hist_alg / (hist_us * 1e-6) / 1e9 / PEAK_HBM_GBPS,
-            "traffic": read_traffic(hist_kernel, args.config),
+            "frac": dom["frac"],
+            "traffic": dom["traffic"],
         },
     }
     if not args.no_cpu_baseline:
         print("[bench] CPU oracle baseline", file=sys.stderr, flush=True)
-        step(0)
+        run.step(0)
         torch.cuda.synchronize()
-        cpu, parity = cpu_baseline(SimpleNamespace(**{**vars(w), "k_cache": layers[0][0],
-                                                      "v_cache": layers[0][1]}),
-                                   args, outputs[0])
+        cpu, parity = cpu_baseline(SimpleNamespace(**{**vars(w), "k_cache": run.layers[0][0],
+                                                      "v_cache": run.layers[0][1]}),
+                                   args, run.outputs[0])
         result["cpu_baseline"] = cpu
         result["parity_sample"] = parity
+    if args.config == "c3" and not args.no_sub_configs:
+        # The other BASELINE decode configs and the initial prefill, each on its own workload
+        # (built after the previous one is freed): step, dominant launch and its roofline.
+        del run, w
+        torch.cuda.empty_cache()
+        subs = {}
+        for name in ("c4", "c5"):
+            sub, srun = measure_step(args, name, device, max(10, args.steps), args.warmup)
+            subs[name] = sub
+            del srun
+            torch.cuda.empty_cache()
+        print("[bench] p1 prefill", file=sys.stderr, flush=True)
+        subs["p1"] = prefill_record(args, device, max(10, args.steps), args.warmup)
+        torch.cuda.empty_cache()
+        result["configs"] = subs
     print(json.dumps(result))
     return 0
 

@@ -24,7 +24,11 @@ import os
 import torch
 
 from . import kernels
-from .config import OscarConfig, choose_history_partition, choose_splits
+from .config import (OscarConfig, attention_programs, choose_device_partition,
+                     choose_history_partition, choose_splits)
+
+SPLIT_POLICIES = ("device", "reference", "mi355x")
+ENV_SPLIT_POLICY = "OSCAR_AMD_SPLIT_POLICY"
 
 
 class OscarAttentionBackend:
@@ -117,8 +121,11 @@ class OscarAttentionImpl:
     Constructed by vLLM with the standard implementation arguments. Options that are not
     vLLM's are keyword-only: ``vllm_config`` (default: the config vLLM is building under),
     ``oscar_config`` (default: from the environment, with the speculative token count of the
-    vLLM config), ``split_policy`` ("reference": config.py:84-89; "mi355x": fill the 256 CUs
-    with token-bounded splits), ``fused`` (three launches per step instead of the nine single
+    vLLM config), ``split_policy`` (default: ``OSCAR_AMD_SPLIT_POLICY``, else "device": fill
+    the 256 CUs with token-bounded splits whose length the GPU derives from the step's
+    lengths, so that a captured graph stays balanced at any context length; "reference":
+    config.py:84-89; "mi355x": token-bounded splits sized from the host-side lengths of the
+    step, which a captured graph would freeze), ``fused`` (three launches per step instead of the nine single
     launches; same bits), ``layer_step`` (opt-in: the whole step in one launch where it
     applies, the INT2 and window bytes of the other forms and the output within rounding of
     them; slower than three launches on MI355X today, because its latency-bound parts wait
@@ -134,7 +141,7 @@ class OscarAttentionImpl:
     def __init__(self, num_heads, head_size, scale, num_kv_heads, alibi_slopes=None,
                  sliding_window=None, kv_cache_dtype="auto", logits_soft_cap=None,
                  attn_type="decoder", kv_sharing_target_layer_name=None, *, vllm_config=None,
-                 oscar_config=None, split_policy="reference", fused=True, one_launch_post=False,
+                 oscar_config=None, split_policy=None, fused=True, one_launch_post=False,
                  layer_step=False, overlap=True, rotate_in_history=True, **kwargs):
         unsupported = (
             (alibi_slopes is not None, "ALiBi"),
@@ -150,8 +157,10 @@ class OscarAttentionImpl:
             raise ValueError("OSCAR serves FULL decoder attention with head size 256 only")
         if num_kv_heads <= 0 or num_heads % num_kv_heads:
             raise ValueError("the query head count must be a multiple of the KV head count")
-        if split_policy not in ("reference", "mi355x"):
-            raise ValueError("split_policy must be 'reference' or 'mi355x'")
+        if split_policy is None:
+            split_policy = os.getenv(ENV_SPLIT_POLICY, "device")
+        if split_policy not in SPLIT_POLICIES:
+            raise ValueError(f"split_policy must be one of {', '.join(SPLIT_POLICIES)}")
         if vllm_config is STANDALONE:
             vllm_config = None
         elif vllm_config is None:
@@ -217,23 +226,41 @@ class OscarAttentionImpl:
     def splits_for(self, meta):
         return self.partition_for(meta)[0]
 
-    def partition_for(self, meta):
-        """``(splits, split_tokens)`` of the history branch. "reference": config.py:84-89
-        with the reference split rule; "mi355x": ``choose_history_partition`` (host-side
-        ``meta.max_seq_len`` and, when present, ``meta.total_seq_len``), leaving the slots of
-        the pre-attention role workgroups free when they share the history launch."""
+    def _roles_share_history_launch(self, meta):
+        """Whether the step's history launch carries the pre-attention role workgroups."""
+        layout = getattr(meta, "layout", None)
+        return (self.fused and self.overlap and not self.one_launch_post and not self.layer_step
+                and layout is not None
+                and kernels.history_pre_supported(meta, layout, self.num_heads))
+
+    def partition_for(self, meta, tokens=None):
+        """``(splits, split_tokens)`` of the history branch for a step of ``tokens`` query
+        tokens (default ``meta.num_actual_tokens``). "device": ``choose_device_partition``
+        from values fixed when a graph is captured (grid capacity, token count, launch form);
+        the GPU derives the split length from the step's lengths. "reference": config.py:84-89
+        with the reference split rule. "mi355x": ``choose_history_partition`` (host-side
+        ``meta.max_seq_len`` and, when present, ``meta.total_seq_len``). Both token-bounded
+        policies leave the slots of the pre-attention role workgroups free when those share the
+        history launch. The one-launch forms (``one_launch_post``, ``layer_step``) count a grid
+        of split slots and take the "mi355x" partition under "device"."""
         if self.split_policy == "reference":
             return choose_splits(meta.num_reqs, self.num_kv_heads, meta.max_query_len), 0
+        roles = self._roles_share_history_launch(meta)
+        if self.split_policy == "device" and not (self.one_launch_post or self.layer_step):
+            n = int(meta.num_actual_tokens if tokens is None else tokens)
+            programs = attention_programs(n, meta.max_num_reqs, self.cfg.queries_per_tile)
+            # BF16 branch: one workgroup per (task, kv head); K/V store: 8 per 16 rows.
+            reserved = (programs * self.num_kv_heads + 8 * -(-n * self.num_kv_heads // 16)
+                        if roles else 0)
+            return choose_device_partition(programs, self.num_kv_heads, meta.max_query_len, n,
+                                           self.num_heads, self.cfg.queries_per_tile,
+                                           reserved=reserved)
         tasks = meta.num_reqs if meta.max_query_len <= 1 else \
             -(-meta.num_actual_tokens // self.cfg.queries_per_tile)
         rows = min(meta.max_query_len, self.cfg.queries_per_tile) * (
             self.num_heads // self.num_kv_heads)
         reserved = 0
-        layout = getattr(meta, "layout", None)
-        if (self.fused and self.overlap and not self.one_launch_post and not self.layer_step
-                and layout is not None
-                and kernels.history_pre_supported(meta, layout, self.num_heads)):
-            # BF16 branch: one workgroup per (task, kv head); K/V store: 8 per 16 rows.
+        if roles:
             kv_rows = meta.num_actual_tokens * self.num_kv_heads
             reserved = tasks * self.num_kv_heads + 8 * -(-kv_rows // 16)
         return choose_history_partition(tasks, self.num_kv_heads, meta.max_query_len,
@@ -286,7 +313,7 @@ class OscarAttentionImpl:
             kernels.prefill_attention(q, k, v, self.window, meta, layout, self.scale, rows, lse)
             kernels.store_windows(k, v, self.window, meta, layout)
             return output
-        splits, split_tokens = self.partition_for(meta)
+        splits, split_tokens = self.partition_for(meta, n)
         if self.fused:
             self._fused_step(q, k, v, meta, splits, split_tokens, rows, lse)
         else:

@@ -37,8 +37,7 @@ int make_attn_args(const void* query, int64_t q_s0, int64_t q_s1, int64_t q_s2, 
   if (st != OSCAR_OK) return st;
   const int64_t h = a.L.kv_heads;
   if (n < 0 || hq <= 0 || hq % h || programs < 1 || splits < 1 || splits > 65535 ||
-      block_n < 1 || query_tile < 1 || table_columns < 0 || programs > (1ll << 31) - 1 ||
-      split_tokens < 0)
+      block_n < 1 || query_tile < 1 || table_columns < 0 || programs > (1ll << 31) - 1)
     return OSCAR_E_SHAPE;
   if (raw && split_tokens) return OSCAR_E_UNSUPPORTED;  // the BF16 branch keeps one rule
   const int64_t g = hq / h;
@@ -124,8 +123,15 @@ extern "C" int oscar_attention_partials(
                                 max_query_len, scale, raw, split_tokens, layout, partials, lse, &a,
                                 &qrows);
   if (st != OSCAR_OK || n == 0) return st;
+  // The paired kernel (<= 8 rows) under the device rule: z slices of unit slots.
+  const int64_t z = !raw && qrows <= 8 && split_tokens < 0
+                        ? device_unit_slices(programs, a.L.kv_heads, split_tokens)
+                        : splits;
+  if (z > 65535) return OSCAR_E_SHAPE;
+  if (!raw && qrows <= 8 && split_tokens < 0 && programs > kDeviceUnitTasks)
+    return OSCAR_E_UNSUPPORTED;
   const dim3 grid(static_cast<unsigned>(programs), static_cast<unsigned>(a.L.kv_heads),
-                  static_cast<unsigned>(splits));
+                  static_cast<unsigned>(z));
   hipStream_t s = as_stream(stream);
   if (!raw)
     return static_cast<int>(launch_history(a, grid, static_cast<int>(qrows), s, queue_counters));

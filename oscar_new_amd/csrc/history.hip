@@ -150,9 +150,10 @@ struct HistoryLds {
 };
 
 // One (task, kv head, split) unit of the general kernel; the whole workgroup calls it.
+// `st`: the launch's split length (launch_split_tokens).
 template <int RT>
 __device__ __forceinline__ void history_unit(const AttnArgs& a, int task, int head, int split,
-                                             HistoryLds<RT>& lds) {
+                                             int st, HistoryLds<RT>& lds) {
   uint8_t* s_ring = lds.ring;
   uint32_t* s_off = lds.off;
   auto& s_red = lds.red;
@@ -163,13 +164,13 @@ __device__ __forceinline__ void history_unit(const AttnArgs& a, int task, int he
   Task t;
   if (!read_task(a, t, task)) return;
   const int length = t.recent_begin - t.sink_len;
-  const int nsplit = history_splits(a, length);
+  const int nsplit = history_splits(a, length, st);
   if (split >= nsplit) {
     write_unused_split(a, t, head, split);
     return;
   }
   int p_lo, p_hi;
-  history_positions(a, t, length, nsplit, split, p_lo, p_hi);
+  history_positions(a, t, length, nsplit, split, st, p_lo, p_hi);
   const int lane = threadIdx.x & 63;
   const int wave = uniform(threadIdx.x >> 6);
   const int n = lane & 15, g = lane >> 4;
@@ -562,7 +563,8 @@ __device__ __forceinline__ void history_unit(const AttnArgs& a, int task, int he
 template <int RT>
 __global__ __launch_bounds__(kThreads, 3 - RT) void history_kernel(const AttnArgs a) {
   __shared__ HistoryLds<RT> lds;
-  history_unit<RT>(a, blockIdx.x, blockIdx.y, blockIdx.z, lds);
+  const int st = launch_split_tokens<kThreads>(a, static_cast<int>(gridDim.x));
+  history_unit<RT>(a, blockIdx.x, blockIdx.y, blockIdx.z, st, lds);
 }
 
 // ---------------------------------------------------------------- 17-32 rows: eight wavefronts
@@ -591,21 +593,22 @@ struct HistoryLdsW8 {
 static_assert(8 * 16 * 128 * 4 <= kRingBytesW8, "half the epilogue merge fits the ring");
 static_assert(2 * 2 * kQTerms * 64 * 32 <= 32 * 512, "both groups' operand images fit");
 
+// `st`: the launch's split length (launch_split_tokens).
 __device__ __forceinline__ void history_unit_w8(const AttnArgs& a, int task, int head, int split,
-                                                HistoryLdsW8& lds) {
+                                                int st, HistoryLdsW8& lds) {
   uint8_t* s_ring = lds.ring;
   uint32_t* s_off = lds.off;
   auto& s_red = lds.red;
   Task t;
   if (!read_task(a, t, task)) return;
   const int length = t.recent_begin - t.sink_len;
-  const int nsplit = history_splits(a, length);
+  const int nsplit = history_splits(a, length, st);
   if (split >= nsplit) {
     write_unused_split(a, t, head, split);
     return;
   }
   int p_lo, p_hi;
-  history_positions(a, t, length, nsplit, split, p_lo, p_hi);
+  history_positions(a, t, length, nsplit, split, st, p_lo, p_hi);
   const int lane = threadIdx.x & 63;
   const int wave = uniform(threadIdx.x >> 6);
   const int stream = wave & 3, rg = wave >> 2;
@@ -938,7 +941,8 @@ __device__ __forceinline__ void history_unit_w8(const AttnArgs& a, int task, int
 
 __global__ __launch_bounds__(kThreadsW8, 1) void history_w8_kernel(const AttnArgs a) {
   __shared__ HistoryLdsW8 lds;
-  history_unit_w8(a, blockIdx.x, blockIdx.y, blockIdx.z, lds);
+  const int st = launch_split_tokens<kThreadsW8>(a, static_cast<int>(gridDim.x));
+  history_unit_w8(a, blockIdx.x, blockIdx.y, blockIdx.z, st, lds);
 }
 
 // The 17-32-row kernel as a work queue (token-bounded splits, one workgroup per CU): a grid of
@@ -966,10 +970,31 @@ __global__ __launch_bounds__(kThreadsW8, 1) void history_queue_kernel(const Attn
   __shared__ int32_t s_total[2];               // full splits, tasks in use
   __shared__ int32_t s_claim;
   const int heads = a.L.kv_heads;
-  // Split counts, then two exclusive scans (full splits, tasks in use) over thread chunks.
+  // Split counts (the launch's split length, or under the device rule the length derived from
+  // the task lengths read in the same pass), then two exclusive scans (full splits, tasks in
+  // use) over thread chunks.
+  __shared__ int64_t s_wave_total[kT / kWave];
+  int64_t hist = 0;
   for (int task = threadIdx.x; task < programs; task += kT) {
     Task t;
-    s_nsplit[task] = read_task(a, t, task) ? history_splits(a, t.recent_begin - t.sink_len) : 0;
+    const int len = read_task(a, t, task) ? max(t.recent_begin - t.sink_len, 0) : -1;
+    s_nsplit[task] = len;
+    hist += max(len, 0);
+  }
+  int st = a.split_tokens;
+  if (st < 0) {
+    hist = wave_sum_i64(hist);
+    if ((threadIdx.x & (kWave - 1)) == 0) s_wave_total[threadIdx.x / kWave] = hist;
+    __syncthreads();
+    int64_t total = 0;
+#pragma unroll
+    for (int w = 0; w < kT / kWave; ++w) total += s_wave_total[w];
+    const int count = max(min(a.task_count[0], programs), 0);
+    st = device_split_tokens(total, count, heads, -st, false);
+  }
+  for (int task = threadIdx.x; task < programs; task += kT) {
+    const int len = s_nsplit[task];
+    s_nsplit[task] = len >= 0 ? history_splits(a, len, st) : 0;
   }
   __syncthreads();
   const int per = (programs + kT - 1) / kT;
@@ -1030,7 +1055,7 @@ __global__ __launch_bounds__(kThreadsW8, 1) void history_queue_kernel(const Attn
       task = s_used[k - full];
       split = s_nsplit[task] - 1;
     }
-    history_unit_w8(a, task, head, split, lds);
+    history_unit_w8(a, task, head, split, st, lds);
   }
   // Unused split slots: LSE -inf for the rows of every task in use.
   for (int task = blockIdx.x; task < programs; task += gridDim.x) {
@@ -1038,8 +1063,7 @@ __global__ __launch_bounds__(kThreadsW8, 1) void history_queue_kernel(const Attn
     if (ns <= 0) continue;
     Task t;
     if (!read_task(a, t, task)) continue;
-    for (int head = 0; head < heads; ++head)
-      for (int split = ns; split < a.splits; ++split) write_unused_split(a, t, head, split);
+    for (int head = 0; head < heads; ++head) write_unused_splits<kT>(a, t, head, ns, a.splits);
   }
   if (threadIdx.x == 0) {
     if (atomicAdd(&counters[1], 1) == static_cast<int>(gridDim.x) - 1) {
@@ -1080,6 +1104,7 @@ __host__ __device__ constexpr int pair_token(int ga, int e) {
 // pair_slot(r) in slot r, so the copy itself is unchanged.
 __host__ __device__ constexpr int pair_slot(int t) { return t ^ (((t >> 4) & 3) << 2); }
 static_assert(pair_slot(pair_slot(45)) == 45 && pair_slot(21) == 17, "pair_slot is an involution");
+static_assert(kDeviceUnitTasks * 4 <= kRingBytes, "the unit resolver's task list fits the ring");
 
 // kMode 0: the history branch alone (attention_partials).
 // kMode 1: the two-launch step's history launch (finish.h): the grid has one more z slice
@@ -1140,16 +1165,34 @@ __device__ __forceinline__ void history_pair_body(const AttnArgs& a, const Finis
   if constexpr (kMode == 4) load_rt_tiles(pre->rk_t, rb);
 
   Task t;
-  if (!read_task(a, t, blockIdx.x)) return;
-  const int head = blockIdx.y, split = static_cast<int>(blockIdx.z) - role_slices;
-  const int length = t.recent_begin - t.sink_len;
-  const int nsplit = history_splits(a, length);
-  if (split >= nsplit) {
-    if constexpr (!kFinish) write_unused_split(a, t, head, split);
-    return;
+  const int head = blockIdx.y;
+  int split = static_cast<int>(blockIdx.z) - role_slices, nsplit, st = a.split_tokens;
+  if (!kFinish && a.split_tokens < 0) {
+    // Device rule: this workgroup slot computes unit u of the step's (task, split) units
+    // (task-major, the split length derived from the step's lengths); slots past the last
+    // unit compute nothing. The last split of a task marks the task's unused split slots
+    // (LSE -inf) for the split merges. The ring is free until the first DMA.
+    DeviceUnit du;
+    const int u = split * static_cast<int>(gridDim.x) + static_cast<int>(blockIdx.x);
+    if (!device_unit<kThreads>(a, static_cast<int>(gridDim.x), u,
+                               reinterpret_cast<int*>(s_ring), du))
+      return;
+    t = du.t;
+    split = du.split;
+    nsplit = du.nsplit;
+    st = du.split_tokens;
+    if (split == nsplit - 1) write_unused_splits<kThreads>(a, t, head, nsplit, a.splits);
+  } else {
+    if (!read_task(a, t, blockIdx.x)) return;
+    nsplit = history_splits(a, t.recent_begin - t.sink_len, st);
+    if (split >= nsplit) {
+      if constexpr (!kFinish) write_unused_split(a, t, head, split);
+      return;
+    }
   }
+  const int length = t.recent_begin - t.sink_len;
   int p_lo, p_hi;
-  history_positions(a, t, length, nsplit, split, p_lo, p_hi);
+  history_positions(a, t, length, nsplit, split, st, p_lo, p_hi);
   const int lane = threadIdx.x & 63;
   const int wave = uniform(threadIdx.x >> 6);
   const int n = lane & 15, g = lane >> 4;
@@ -1677,7 +1720,7 @@ hipError_t launch_history(const AttnArgs& a, dim3 grid, int rows, hipStream_t st
     hipLaunchKernelGGL(history_pair_kernel, grid, dim3(kThreads), 0, stream, a);
   } else if (rows <= 16) {
     hipLaunchKernelGGL(history_kernel<1>, grid, dim3(kThreads), 0, stream, a);
-  } else if (queue != nullptr && a.split_tokens > 0 &&
+  } else if (queue != nullptr && a.split_tokens != 0 &&
              static_cast<int64_t>(grid.x) <= kQueueTasks) {
     int device = 0, cus = 0;
     hipError_t e = hipGetDevice(&device);

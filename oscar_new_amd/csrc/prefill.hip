@@ -113,6 +113,21 @@ __global__ __launch_bounds__(kThreadsP) void prefill_flash_kernel(const PrefillA
   if (row0 >= rows_req) return;
   const int row_end = min(row0 + kSpanRows, rows_req);
   const bool history = a.seq_lens[req] != qlen;  // not an initial prefill: rows are NaN
+  // Rows past the grid's spans (a request with more query tokens than the caller's
+  // max_query_len) are written as NaN by the last span's workgroup, like the rows of a
+  // request with cached tokens, so that a wrong bound shows in the output.
+  if (span == static_cast<int>(gridDim.y) - 1) {
+    const int covered = static_cast<int>(gridDim.y) * kSpanRows;
+    for (int row = covered + static_cast<int>(threadIdx.x >> 5); row < rows_req;
+         row += kThreadsP / 32) {
+      const int qi = static_cast<int>(fastdiv(static_cast<uint32_t>(row), a.g_div));
+      const int qhead = head * a.g + (row - qi * a.g);
+      const int64_t orow = (qstart + qi) * a.hq + qhead;
+      *reinterpret_cast<u32x4*>(a.out + orow * kHeadDim + 8 * (threadIdx.x & 31)) =
+          u32x4{0x7fc07fc0u, 0x7fc07fc0u, 0x7fc07fc0u, 0x7fc07fc0u};
+      if (a.lse && (threadIdx.x & 31) == 0) a.lse[orow] = NAN;
+    }
+  }
   const int q_last = static_cast<int>(fastdiv(static_cast<uint32_t>(row_end - 1), a.g_div));
   const int nblk = history ? 0 : q_last / kBlock + 1;
   const int lane = threadIdx.x & 63;
@@ -356,8 +371,9 @@ extern "C" int oscar_prefill_attention(
   a.scale_log2 = scale * kLog2e;
   a.out = static_cast<uint16_t*>(output);
   a.lse = merged_lse;
-  // Spans per request: its rows (query tokens x g) in 128-row groups; a request never has more
-  // query tokens than max_query_len (when given) or n.
+  // Spans per request: its rows (query tokens x g) in kSpanRows-row groups (192); a request
+  // has at most max_query_len (when given) or n query tokens. Rows past the spans of a request
+  // that breaks the given bound are written as NaN.
   const int64_t qmax = max_query_len > 0 && max_query_len < n ? max_query_len : n;
   const int64_t spans = (qmax * g + kSpanRows - 1) / kSpanRows;
   if (spans > 65535) return OSCAR_E_SHAPE;  // grid y

@@ -248,11 +248,16 @@ extern "C" int oscar_history_pre(
                       partials, lse, &a, &hrows);
   if (st != OSCAR_OK || n == 0) return st;
   // Role slices in front of the history splits (dispatched first): slice 0 is the BF16
-  // branch of (task, kv head); the next ones hold the K/V store quads.
+  // branch of (task, kv head); the next ones hold the K/V store quads. Under the device rule
+  // the history slices hold unit slots.
   const int64_t per_slice = programs * a.L.kv_heads;
   const int role_slices = 1 + static_cast<int>((p.kv_wgs + per_slice - 1) / per_slice);
+  const int64_t hist_slices =
+      split_tokens < 0 ? device_unit_slices(programs, a.L.kv_heads, split_tokens) : splits;
+  if (hist_slices + role_slices > 65535) return OSCAR_E_SHAPE;
+  if (split_tokens < 0 && programs > kDeviceUnitTasks) return OSCAR_E_UNSUPPORTED;
   const dim3 grid(static_cast<unsigned>(programs), static_cast<unsigned>(a.L.kv_heads),
-                  static_cast<unsigned>(splits + role_slices));
+                  static_cast<unsigned>(hist_slices + role_slices));
   return static_cast<int>(
       launch_history_pre(a, p, role_slices, grid, rotate_query, as_stream(stream)));
 }
@@ -376,8 +381,10 @@ extern "C" int oscar_history_post(
                           block_n, query_tile, max_query_len, scale, 0, split_tokens, layout,
                           partials, lse, &a, &qrows);
   if (st != OSCAR_OK) return st;
-  // One-round split merge by the completing workgroup, paired-token history kernel.
-  if (qrows > 8 || splits > kWaveMergeSplits || splits + 1 > 65535) return OSCAR_E_UNSUPPORTED;
+  // One-round split merge by the completing workgroup, paired-token history kernel, a split
+  // rule fixed at launch (the completing workgroup counts a grid of (task, split) slots).
+  if (qrows > 8 || splits > kWaveMergeSplits || splits + 1 > 65535 || split_tokens < 0)
+    return OSCAR_E_UNSUPPORTED;
   FinishArgs f{};
   st = make_post_args(partials, lse, splits, raw_partials, raw_lse, counts, rv, n, hq, output,
                       merged_lse, key, k_s0, k_s1, value, v_s0, v_s1, window, window_elems,
@@ -416,7 +423,7 @@ extern "C" int oscar_layer_step(
   // One task per request (every request's tokens in one query tile), <= 8 query rows per task,
   // <= 16 splits (the one-round merges of the finisher).
   if (qrows > 8 || splits > kWaveMergeSplits || max_query_len < 1 || max_query_len > query_tile ||
-      query_tile > 4)
+      query_tile > 4 || split_tokens < 0)
     return OSCAR_E_UNSUPPORTED;
   if (!clip) return OSCAR_E_NULL;
   if (clip->mode < OSCAR_CLIP_PERCENTILE || clip->mode > OSCAR_CLIP_SEARCH) return OSCAR_E_SHAPE;

@@ -211,14 +211,15 @@ def attention_partials(query, key, value, history, window, meta, layout, scale, 
     ``split_tokens`` (history branch; no reference counterpart, 0 keeps kernels.py:368-370):
     a request with L history tokens uses min(splits, ceil(L / split_tokens)) splits and its
     remaining split slots get LSE -inf with no partial row, which the split merges skip.
+    A negative value is the device rule (``config.DEVICE_RULE``): the same token-bounded
+    splits with the split length derived on the GPU from the step's lengths for a budget of
+    ``-split_tokens`` workgroups, so that a captured launch stays balanced at any lengths.
     ``use_queue`` (no reference counterpart): tasks of 17-32 rows with token-bounded splits
     run as a work queue over the units in use (``queue_counters``); the same bits as the
     grid form (``use_queue=False``).
     """
     if raw and split_tokens:
         raise ValueError("split_tokens applies to the history branch only")
-    if split_tokens < 0:
-        raise ValueError("split_tokens must be >= 0")
     _device_check(query, key, value, history, window)
     n, hq, d = query.shape
     cfg = layout.config
@@ -531,8 +532,6 @@ def history_pre(query_rot, query, key, value, history, window, meta, layout, sca
     cfg = layout.config
     if not history_pre_supported(meta, layout, hq):
         raise ValueError("history_pre covers <= 8 query rows per task")
-    if split_tokens < 0:
-        raise ValueError("split_tokens must be >= 0")
     dev = query.device
     partials = torch.empty((n, hq, splits, d), dtype=torch.float32, device=dev)
     lse = torch.empty((n, hq, splits), dtype=torch.float32, device=dev)
@@ -594,6 +593,9 @@ def history_post(query, history, meta, layout, scale, splits, raw_partials, raw_
     if not history_post_supported(meta, layout, hq, splits, n):
         raise ValueError("history_post covers <= 8 query rows per task, <= 16 splits and "
                          "split rows below 4 GiB")
+    if split_tokens < 0:
+        raise ValueError("history_post counts a grid of split slots: the device split rule "
+                         "(split_tokens < 0) is not available")
     if rv.dtype != torch.bfloat16 or not rv.is_contiguous():
         raise ValueError("rv must be contiguous bf16 [256, 256]")
     cfg = layout.config
@@ -657,6 +659,9 @@ def layer_step(query, key, value, history, window, meta, layout, scale, splits, 
     n, hq, d = query.shape
     if not output.is_contiguous():
         raise ValueError("Attention output must be contiguous")
+    if split_tokens < 0:
+        raise ValueError("layer_step counts a grid of split slots: the device split rule "
+                         "(split_tokens < 0) is not available")
     if n == 0:
         return
     if not layer_step_supported(meta, layout, hq, splits, n):

@@ -10,19 +10,26 @@ Two hooks, both installed once and only when ``OSCAR_AMD_ENABLED=1``:
   (its cache and rotations are separate; plugin.py:106-114), and once a routed layer's
   weights are loaded its implementation loads the layer's rotations (plugin.py:116-125).
 
+vLLM caches backend selection per argument tuple, and draft and target layers ask with the
+same arguments, so the selector's answer must not depend on which layer asks. The draft layer
+therefore gets its backend class bound explicitly, as the reference binds
+``AscendAttentionBackend`` (plugin.py:110-113): the class the platform's own selector chose
+for the same arguments. The hooked selector records that native answer on every call; a draft
+layer built before any selection asks the platform's unhooked selector directly, through the
+selector configuration the layer would have built, without entering vLLM's cache.
+
 The platform and Attention classes are looked up lazily or passed in, so both hooks are
 tested against stand-ins without vLLM.
 """
 
 from __future__ import annotations
 
-import contextlib
 import functools
+import importlib
 import inspect
 import logging
 import os
 import sys
-import threading
 
 LOG = logging.getLogger(__name__)
 BACKEND = "oscar_new_amd.backend.OscarAttentionBackend"
@@ -33,7 +40,10 @@ UNSUPPORTED_OPTIONS = ("has_sink", "use_mm_prefix", "use_per_head_quant_scales",
 ATTENTION_MODULES = ("vllm.model_executor.layers.attention.attention", "vllm.attention.layer")
 
 _registered_on = set()
-_native = threading.local()  # set while an MTP draft layer is being constructed
+# Native backend class path the platform's selector gave, per attention type, and the
+# platform's unhooked selector (filled by ``register``).
+_native_paths = {}
+_native_selector = []
 
 
 def should_route(selector):
@@ -47,18 +57,49 @@ def is_draft_layer(prefix):
     return "mtp" in prefix.split(".")
 
 
-@contextlib.contextmanager
-def _native_selection():
-    depth = getattr(_native, "depth", 0)
-    _native.depth = depth + 1
+def _resolve(path):
+    """A backend class from its qualified name (vLLM's ``resolve_obj_by_qualname``)."""
+    if not isinstance(path, str):
+        return path
+    module, _, name = path.rpartition(".")
+    return getattr(importlib.import_module(module), name)
+
+
+def native_backend(attn_type="decoder", selector=None):
+    """The platform's native backend class for a draft layer: the answer its own selector
+    gave for these arguments (recorded by the hooked selector), or, before any selection,
+    the unhooked selector asked directly with ``selector``. None when neither is at hand."""
+    path = _native_paths.get(attn_type)
+    if path is None and selector is not None and _native_selector:
+        platform_cls, original = _native_selector[-1]
+        path = original(platform_cls, None, selector)
+        _native_paths[attn_type] = path
+    return None if path is None else _resolve(path)
+
+
+def _draft_selector(arguments):
+    """The selector configuration a draft layer would ask with, built as vLLM's Attention
+    builds it: head size and attention type from the constructor's arguments, dtype, KV cache
+    dtype and block size from the engine configuration being built."""
+    from types import SimpleNamespace
+
+    model = cache = None
     try:
-        yield
-    finally:
-        _native.depth = depth
+        from vllm.config import get_current_vllm_config
 
-
-def _selecting_native():
-    return getattr(_native, "depth", 0) > 0
+        config = get_current_vllm_config()
+        model = getattr(config, "model_config", None)
+        cache = getattr(config, "cache_config", None)
+    except Exception:  # vLLM absent or no configuration being built
+        pass
+    return SimpleNamespace(
+        attn_type=arguments.get("attn_type", "decoder") or "decoder",
+        head_size=arguments.get("head_size", 0),
+        dtype=getattr(model, "dtype", None),
+        kv_cache_dtype=getattr(cache, "cache_dtype", "auto"),
+        block_size=getattr(cache, "block_size", None),
+        use_mla=False, has_sink=False, use_sparse=False, use_non_causal=False,
+        use_mm_prefix=False, use_per_head_quant_scales=False, use_kv_connector=False)
 
 
 def backend_for(selector):
@@ -96,9 +137,11 @@ def install_attention_hooks(attention_cls=None):
         bound = signature.bind(layer, *args, **kwargs)
         prefix = bound.arguments.get("prefix", "") or ""
         if is_draft_layer(prefix) and bound.arguments.get("attn_backend") is None:
-            # The backend selector runs inside the constructor: answer it natively.
-            with _native_selection():
-                return init(*bound.args, **bound.kwargs)
+            # Bind the native class so that vLLM's (cached) selector is not consulted.
+            native = native_backend(bound.arguments.get("attn_type", "decoder") or "decoder",
+                                    _draft_selector(bound.arguments))
+            if native is not None:
+                bound.arguments["attn_backend"] = native
         return init(*bound.args, **bound.kwargs)
 
     after_load = attention_cls.process_weights_after_loading
@@ -136,11 +179,14 @@ def register(platform_cls=None, attention_cls=None):
     def select(cls, selected_backend, attn_selector_config, *args, **kwargs):
         # The Attention module is imported after the platform: hook it on first use.
         install_attention_hooks(attention_cls)
-        if should_route(attn_selector_config) and not _selecting_native():
+        native = original(cls, selected_backend, attn_selector_config, *args, **kwargs)
+        _native_paths[getattr(attn_selector_config, "attn_type", "decoder")] = native
+        if should_route(attn_selector_config):
             return backend_for(attn_selector_config)
-        return original(cls, selected_backend, attn_selector_config, *args, **kwargs)
+        return native
 
     platform_cls.get_attn_backend_cls = select
+    _native_selector.append((platform_cls, original))
     _registered_on.add(id(platform_cls))
     LOG.warning("OSCAR INT2 attention serves full decoder layers (prefix caching off; MTP "
                 "draft layers stay native)")

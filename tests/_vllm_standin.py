@@ -7,6 +7,7 @@ vLLM's positional arguments, an engine config, a ``vllm.config`` module with
 ``get_current_vllm_config`` and the KV cache spec the metadata builder reads.
 """
 
+import functools
 import importlib
 import sys
 import types
@@ -15,7 +16,7 @@ from types import SimpleNamespace
 
 import torch
 
-NATIVE_BACKEND = "standin.NativeBackend"
+NATIVE_BACKEND = "tests._vllm_standin.NativeBackend"
 
 
 class NativeImpl:
@@ -50,7 +51,16 @@ def _resolve(path):
 
 def make_attention(platform):
     """An Attention layer class that selects its backend like vLLM's: through the platform,
-    unless one is passed in, and builds the implementation with vLLM's positional order."""
+    unless one is passed in, and builds the implementation with vLLM's positional order.
+    Selection goes through a cache keyed by the selector arguments, as vLLM's
+    ``get_attn_backend`` does (``_cached_get_attn_backend``): draft and target layers ask with
+    the same arguments and share one answer."""
+
+    @functools.cache
+    def cached_backend(attn_type, head_size, num_heads):
+        selector = SimpleNamespace(attn_type=attn_type, use_mla=False, use_sparse=False,
+                                   use_non_causal=False, head_size=head_size)
+        return _resolve(platform.get_attn_backend_cls(None, selector, num_heads))
 
     class Attention(torch.nn.Module):
         def __init__(self, num_heads, head_size, scale, num_kv_heads=None, alibi_slopes=None,
@@ -62,9 +72,7 @@ def make_attention(platform):
             self.layer_name = prefix
             self.register_buffer("_k_scale", torch.ones(()))
             if attn_backend is None:
-                selector = SimpleNamespace(attn_type=attn_type, use_mla=False, use_sparse=False,
-                                           use_non_causal=False, head_size=head_size)
-                attn_backend = _resolve(platform.get_attn_backend_cls(None, selector, num_heads))
+                attn_backend = cached_backend(attn_type, head_size, num_heads)
             self.attn_backend = attn_backend
             self.impl = attn_backend.get_impl_cls()(
                 num_heads, head_size, scale, num_kv_heads, alibi_slopes,

@@ -2,6 +2,7 @@
 
 from dataclasses import replace
 
+import numpy as np
 import pytest
 import torch
 
@@ -9,8 +10,10 @@ from oscar_new_amd.config import (
     OscarConfig,
     attention_programs,
     choose_splits,
+    choose_device_partition,
     choose_history_partition,
     choose_splits_mi355x,
+    device_split_tokens,
     percentile_selection,
     task_capacity,
 )
@@ -178,3 +181,47 @@ def test_from_env(monkeypatch):
     monkeypatch.setenv("OSCAR_ASCEND_CLIP_MODE", "factor")
     cfg = OscarConfig.from_env(speculative_tokens=0)
     assert (cfg.sink_tokens, cfg.recent_tokens, cfg.ring_tokens, cfg.clip_mode) == (4, 128, 129, "factor")
+
+
+def test_device_partition_is_sized_from_capture_stable_values():
+    # Decode (6 rows per task, paired kernel): 512 slots less the roles of the launch (one
+    # BF16-branch workgroup per task, 8 K/V store workgroups per 16 rows); splits bound a
+    # request at twice the even share of a 32-request batch, never below 16.
+    assert choose_device_partition(32, 1, 1, 32, 6, reserved=32 + 16) == (16, -464)
+    assert choose_device_partition(4, 1, 1, 4, 6, reserved=4 + 8) == (128, -500)
+    assert choose_device_partition(8, 1, 1, 8, 6) == (64, -512)
+    assert choose_device_partition(512, 1, 1, 512, 6)[0] == 16
+    # MTP (24 rows per task, work queue): 448 slots, splits bounded by 128 MiB of scratch.
+    assert choose_device_partition(127, 1, 4, 256, 6) == (85, -448)
+    assert choose_device_partition(2048, 1, 4, 8192, 6) == (16, -448)
+    # Long prefill chunks keep one split (config.py:86-87).
+    assert choose_device_partition(4, 1, 17, 4096, 6) == (1, 0)
+
+
+def test_device_split_tokens_matches_the_host_partition_on_baseline_batches():
+    # c3: 32 x 32635 history tokens, budget 464 -> 2432-token splits, 14 per request, 448
+    # units (the measured host partition); c5: 4 x 262011, budget 500 -> 2176, 121 each.
+    t = device_split_tokens(32 * 32635, 32, 1, 464)
+    assert t == 2432 and -(-32635 // t) == 14
+    t = device_split_tokens(4 * 262011, 4, 1, 500)
+    assert t == 2176 and -(-262011 // t) == 121
+    # Never below 1024 tokens; one split per task once the budget is spent on tasks.
+    assert device_split_tokens(10, 2, 1, 512) == 1024
+    assert device_split_tokens(10 ** 6, 600, 1, 512) == 10 ** 6
+    # The work queue (no grid to fit): about `budget` units; c4 (seed 1234: 1,207,677 history
+    # tokens over 64 requests) -> 2752-token splits, 475 units, the host partition's.
+    assert device_split_tokens(1207677, 64, 1, 448, fit_grid=False) == 2752
+
+
+@pytest.mark.parametrize("seed", range(20))
+def test_device_rule_units_fit_the_budget(seed):
+    # Sum over tasks of ceil(L / T) stays within max(B / H, tasks + 1): the grid the host
+    # sizes (device_unit_slices) holds every unit of any batch.
+    rng = np.random.default_rng(seed)
+    tasks = int(rng.integers(1, 300))
+    heads = int(rng.integers(1, 3))
+    budget = int(rng.integers(16, 520))
+    lengths = rng.integers(0, 300000, tasks) * (rng.random(tasks) < 0.9)
+    t = device_split_tokens(int(lengths.sum()), tasks, heads, budget)
+    units = sum(max(1, -(-int(l) // t)) for l in lengths)
+    assert units <= max(-(-budget // heads), tasks + 1)

@@ -86,7 +86,7 @@ def test_vllm_constructed_step_matches_hand_built_metadata(monkeypatch, tmp_path
     n = c.q.shape[0]
     raw = c.raw.clone()
     kv_cache = _views(raw, c.layout)
-    layer.impl.partition_for = lambda m: (8, 0)
+    layer.impl.partition_for = lambda m, tokens=None: (8, 0)
     meta.merged_lse = torch.full((n, 6), 7.0, device=DEV)
     out = torch.full((n, 6 * 256), 3.0, device=DEV, dtype=torch.bfloat16)
     layer.impl.forward(layer, c.q.view(n, -1), c.k.view(n, -1), c.v.view(n, -1), kv_cache, meta,

@@ -69,8 +69,10 @@ def test_c1_decode_step_matches_oracle():
     cache = raw.clone()
     forms = {}
     for one_launch, layer in ((False, False), (True, False), (False, True)):
+        # The reference split rule: the fused forms carry the single launches' bits under the
+        # same partition.
         impl = OscarAttentionImpl.standalone(HQ, 256, 1 / 16, 1, cfg, one_launch_post=one_launch,
-                                             layer_step=layer)
+                                             layer_step=layer, split_policy="reference")
         impl.set_rotations(rk_d, rv_d)
         meta.merged_lse = torch.empty(1, HQ, device=DEV)
         out = torch.empty(1, HQ * 256, dtype=torch.bfloat16, device=DEV)

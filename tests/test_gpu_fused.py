@@ -83,7 +83,7 @@ def _forward(c, form, splits, raw=None):
                                          layer_step=form == "layer", overlap=form != "fused_serial",
                                          rotate_in_history=form == "fused_rot")
     impl.set_rotations(c.rk, c.rv)
-    impl.partition_for = lambda meta, s=splits: (s, 0)
+    impl.partition_for = lambda meta, tokens=None, s=splits: (s, 0)
     c.meta.merged_lse = torch.full((n, 6), 7.0, device=DEV)
     out = torch.full((n, 6 * 256), 3.0, device=DEV, dtype=torch.bfloat16)
     impl.forward(None, c.q, c.k, c.v, (k_cache, v_cache), c.meta, out)
@@ -139,7 +139,7 @@ def test_token_bounded_fused_step_against_dense_reference(lengths, prefixes, par
                                              split_policy="mi355x", fused=fused,
                                              one_launch_post=one, layer_step=False)
         impl.set_rotations(c.rk, c.rv)
-        impl.partition_for = lambda meta, pt=partition: pt
+        impl.partition_for = lambda meta, tokens=None, pt=partition: pt
         c.meta.merged_lse = torch.empty((n, 6), device=DEV)
         out = torch.empty((n, 6 * 256), device=DEV, dtype=torch.bfloat16)
         impl.forward(None, c.q, c.k, c.v, (k_cache, v_cache), c.meta, out)
@@ -179,7 +179,7 @@ def test_fused_step_replays_in_a_graph(lengths, prefixes, form):
     impl = OscarAttentionImpl.standalone(6, 256, 1 / 16, 1, c.layout.config, fused=True,
                                          layer_step=form == "layer")
     impl.set_rotations(c.rk, c.rv)
-    impl.partition_for = lambda meta: (8, 0)
+    impl.partition_for = lambda meta, tokens=None: (8, 0)
     lse = c.meta.merged_lse = torch.empty((n, 6), device=DEV)
     out = torch.empty((n, 6 * 256), device=DEV, dtype=torch.bfloat16)
     impl.forward(None, c.q, c.k, c.v, (kg, vg), c.meta, out)  # warm-up (views, library)
@@ -213,7 +213,7 @@ def test_fused_step_against_dense_reference(lengths, prefixes, splits):
     k_cache, v_cache = _views(c.raw, c.layout)
     impl = OscarAttentionImpl.standalone(6, 256, 1 / 16, 1, c.layout.config, fused=True)
     impl.set_rotations(c.rk, c.rv)
-    impl.partition_for = lambda meta, s=splits: (s, 0)
+    impl.partition_for = lambda meta, tokens=None, s=splits: (s, 0)
     c.meta.merged_lse = torch.empty((n, 6), device=DEV)
     out = torch.empty((n, 6 * 256), device=DEV, dtype=torch.bfloat16)
     before = c.raw.clone()  # the step's window store may overwrite ring slots it read

@@ -56,7 +56,7 @@ def _step(c, fused, one_launch, splits, layer=False):
     impl = OscarAttentionImpl.standalone(HQ, 256, 1 / 16, H, CFG, fused=fused,
                                          one_launch_post=one_launch, layer_step=layer)
     impl.set_rotations(rk, rv)
-    impl.partition_for = lambda meta: (splits, 0)
+    impl.partition_for = lambda meta, tokens=None: (splits, 0)
     n = q.shape[0]
     meta.merged_lse = torch.full((n, HQ), 7.0, device=DEV)
     out = torch.full((n, HQ * 256), 3.0, device=DEV, dtype=torch.bfloat16)

@@ -73,7 +73,7 @@ def test_prefill_matches_int2_path_and_dense_reference(lengths, pad):
 
 
 @pytest.mark.parametrize("lengths,max_query_len", [
-    ([2048, 1100, 9], True),  # many 32-token blocks and 128-row spans, a span crossing queries
+    ([2048, 1100, 9], True),  # many 32-token blocks and 192-row spans, a span crossing queries
     ([300, 5], False),  # max_query_len unknown: spans sized by the token count
 ])
 def test_long_prefill_is_bitwise_the_int2_path(lengths, max_query_len):
@@ -138,3 +138,40 @@ def test_prefill_spans_that_split_a_query(g, kv_heads, lengths):
             assert (o - want).norm() <= 1e-2 * want.norm(), (r, h)
             assert ((o - want).abs() <= 2e-2 + 1e-2 * want.abs()).all(), (r, h)
             assert (got_l[rows, h] - torch.logsumexp(s, dim=1)).abs().max() <= 2e-2, (r, h)
+
+
+def test_prefill_rows_past_a_broken_max_query_len_are_nan():
+    # A request with more query tokens than the caller's max_query_len: the grid holds
+    # ceil(max_query_len * g / 192) spans, the rows it covers are computed, and the rows past
+    # them are NaN (output and LSE), never stale memory.
+    lengths, g = [300, 40], 6
+    gen = torch.Generator().manual_seed(53)
+    n = sum(lengths)
+    q = torch.randn(n, g, 256, generator=gen).bfloat16()
+    k = torch.randn(n, 1, 256, generator=gen).bfloat16()
+    v = torch.randn(n, 1, 256, generator=gen).bfloat16()
+    meta = SimpleNamespace(
+        query_start_loc=torch.tensor([0, 300, 340], dtype=torch.int32, device=DEV),
+        seq_lens=torch.tensor(lengths, dtype=torch.int32, device=DEV),
+        counts=torch.tensor([2, n], dtype=torch.int32, device=DEV),
+        max_num_reqs=2, max_query_len=40)
+    layout = CacheLayout(768, config=OscarConfig(sink_tokens=4, recent_tokens=64))
+    scale = 256 ** -0.5
+    out = torch.zeros((n, g * 256), dtype=torch.bfloat16, device=DEV)
+    lse = torch.zeros((n * g,), dtype=torch.float32, device=DEV)
+    print("[prefill] broken max_query_len 40 for a 300-token request", flush=True)
+    kernels.prefill_attention(q.to(DEV), k.to(DEV), v.to(DEV), None, meta, layout, scale, out,
+                              lse)
+    torch.cuda.synchronize()
+    got = out.cpu().float().view(n, g, 256).double()
+    got_l = lse.cpu().view(n, g).double()
+    covered = (-(-40 * g // 192)) * 192 // g  # 64 whole queries of request 0
+    assert torch.isnan(got[covered:300]).all() and torch.isnan(got_l[covered:300]).all()
+    qf, kf, vf = q.double(), k.double(), v.double()
+    for rows, length in ((slice(0, covered), covered), (slice(300, 340), 40)):
+        causal = torch.ones(length, length, dtype=torch.bool).tril()
+        for h in range(g):
+            s = (qf[rows, h] @ kf[rows, 0].T * scale).masked_fill(~causal, float("-inf"))
+            want = torch.softmax(s, dim=1) @ vf[rows, 0]
+            o = got[rows, h]
+            assert (o - want).norm() <= 1e-2 * want.norm(), (rows, h)

@@ -1,6 +1,7 @@
-"""The inline-asm DMA of the history kernels (dma.h) against the GFX9 hazard "a VALU write of
-an SGPR, then a vector-memory instruction that reads it: 5 wait states", which the compiler
-checks for its own instructions but not inside asm. The kernels are compiled to ISA here
+"""The inline-asm DMA of every kernel that uses dma.h (history, prefill, fused step and BF16
+branch kernels) against the GFX9 hazard "a VALU write of an SGPR, then a vector-memory
+instruction that reads it: 5 wait states", which the compiler checks for its own
+instructions but not inside asm. The kernels are compiled to ISA here
 (hipcc, no GPU) and every direct-to-LDS load is traced back, in straight-line order, to the
 last writer of its SGPR operands (saddr base, M0): a VALU writer must be at least 5 wait
 states (an `s_nop N` counts N + 1) before it.
@@ -68,14 +69,20 @@ def test_scanner_flags_a_late_valu_base():
     assert not _late_sites(text.replace("v_readfirstlane_b32 s7, v3", "s_mov_b32 s7, 0"))
 
 
+# Every source whose kernels issue dma.h's direct-to-LDS loads, and a floor on how many
+# loads each holds (so that a build that lost them does not pass vacuously).
+DMA_SOURCES = {"history.hip": 100, "prefill.hip": 4, "step.hip": 4, "attention.hip": 4}
+
+
 @pytest.mark.skipif(not Path(HIPCC).exists(), reason="hipcc is not installed")
-def test_history_kernels_keep_five_wait_states_before_every_dma(tmp_path):
-    out = tmp_path / "history.s"
+@pytest.mark.parametrize("source", sorted(DMA_SOURCES))
+def test_kernels_keep_five_wait_states_before_every_dma(tmp_path, source):
+    out = tmp_path / (Path(source).stem + ".s")
     cmd = [HIPCC, "--offload-arch=gfx950", "-O3", "-std=c++17", "-fno-gpu-flush-denormals-to-zero",
            "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops", f"-I{ROOT / 'include'}",
-           "--cuda-device-only", "-S", str(ROOT / "oscar_new_amd" / "csrc" / "history.hip"), "-o",
+           "--cuda-device-only", "-S", str(ROOT / "oscar_new_amd" / "csrc" / source), "-o",
            str(out)]
     subprocess.run(cmd, check=True, capture_output=True, timeout=600)
     text = out.read_text()
-    assert text.count("global_load_lds_dwordx4") > 100
+    assert text.count("global_load_lds_dword") >= DMA_SOURCES[source]
     assert _late_sites(text) == []

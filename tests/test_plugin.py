@@ -11,11 +11,14 @@ backend.py:13-117, metadata.py:36-174), on stand-ins built as vLLM builds them:
   a dummy build.
 """
 
+import importlib
+from pathlib import Path
 from types import SimpleNamespace
 
 import pytest
 import torch
 
+import oscar_new_amd
 from oscar_new_amd import metadata, plugin, rotations
 from oscar_new_amd.backend import OscarAttentionBackend, OscarAttentionImpl, validate_vllm_config
 from oscar_new_amd.layout import CacheLayout
@@ -50,7 +53,10 @@ def test_register_is_gated_idempotent_and_routes(monkeypatch):
     assert platform.get_attn_backend_cls(None, _selector()) == plugin.BACKEND
     assert platform.get_attn_backend_cls(None, _selector(head_size=0)) == plugin.BACKEND
     assert platform.get_attn_backend_cls("x", _selector(use_mla=True)) == V.NATIVE_BACKEND
-    assert platform.calls == [None, "x"]  # native before registration, then the MLA layer
+    # The platform's own selector answers every call (its answer is kept for draft layers):
+    # before registration, the two routed layers, then the MLA layer.
+    assert platform.calls == [None, None, None, "x"]
+    assert plugin.native_backend() is V.NativeBackend
     with pytest.raises(ValueError, match="D256"):
         platform.get_attn_backend_cls(None, _selector(head_size=128))
     with pytest.raises(ValueError, match="has_sink"):
@@ -181,6 +187,32 @@ def test_attention_hooks_route_target_layers_keep_drafts_native_and_load_rotatio
         other.process_weights_after_loading(torch.bfloat16)
 
 
+@pytest.mark.parametrize("draft_first", [False, True])
+def test_draft_layers_stay_native_under_a_cached_selector(monkeypatch, draft_first):
+    """vLLM caches the selector's answer per argument tuple and draft and target layers ask
+    with the same arguments: whichever is built first must not decide the other's backend."""
+    monkeypatch.setenv(plugin.ENV_ENABLED, "1")
+    monkeypatch.setattr(plugin, "_native_paths", {})
+    platform = V.make_platform()
+    attention = V.make_attention(platform)
+    assert plugin.register(platform, attention)
+    layers = {}
+    order = ["draft", "target", "draft2"] if draft_first else ["target", "draft", "draft2"]
+    prefixes = {"draft": "model.mtp.layers.0.self_attn.attn",
+                "draft2": "model.mtp.layers.1.self_attn.attn",
+                "target": "model.layers.3.self_attn.attn"}
+    with V.current_vllm_config(V.make_vllm_config()):
+        for name in order:
+            layers[name] = attention(6, 256, 1 / 16, 1, prefix=prefixes[name])
+        late_target = attention(6, 256, 1 / 16, 1, prefix="model.layers.7.self_attn.attn")
+    for name in ("draft", "draft2"):
+        assert layers[name].attn_backend is V.NativeBackend
+        assert isinstance(layers[name].impl, V.NativeImpl)
+    for layer in (layers["target"], late_target):
+        assert layer.attn_backend is OscarAttentionBackend
+        assert isinstance(layer.impl, OscarAttentionImpl)
+
+
 def _builder(config=None, layers=("model.layers.3.self_attn.attn",)):
     config = config or V.make_vllm_config()
     with V.current_vllm_config(config):
@@ -246,3 +278,16 @@ def test_builder_build_and_capture_build(monkeypatch):
         builder.build(0, _common(causal=False))
     with pytest.raises(ValueError, match="exceeds"):
         builder.build(0, _common(num_actual_tokens=10_000))
+
+
+def test_plugin_entry_point_resolves_to_register():
+    """vLLM finds general plugins through the ``vllm.general_plugins`` entry-point group
+    (reference pyproject.toml:15-16); the package declares ``register`` there."""
+    import tomli
+
+    project = tomli.loads((Path(__file__).resolve().parents[1] / "pyproject.toml").read_text())
+    entry = project["project"]["entry-points"]["vllm.general_plugins"]["oscar_new_amd"]
+    module, _, attr = entry.partition(":")
+    target = getattr(importlib.import_module(module), attr)
+    assert target is plugin.register
+    assert project["project"]["version"] == oscar_new_amd.__version__
