@@ -70,9 +70,9 @@ def parse_args(argv=None):
                         "launch instead of q rotation + history launch carrying the rest")
     p.add_argument("--layer-step", action="store_true",
                    help="the one-launch layer step (kernels.layer_step) instead of three launches")
-    p.add_argument("--separate-q-rotation", action="store_true",
-                   help="the q rotation as a launch of its own ahead of the history launch "
-                        "(default: the history workgroups rotate their query rows)")
+    p.add_argument("--rotate-in-history", action="store_true",
+                   help="the history workgroups rotate their query rows (default: the q "
+                        "rotation is a launch of its own ahead of the history launch)")
     p.add_argument("--mode", default="step",
                    choices=("step", "history", "copy", "prefill", "store"),
                    help="step: full benchmark; history: only the history-attention launches "
@@ -677,7 +677,7 @@ def measure_step(args, name, device, steps, warmup):
                                              one_launch_post=args.one_launch_post,
                                              overlap=not args.no_overlap,
                                              layer_step=args.layer_step,
-                                             rotate_in_history=not args.separate_q_rotation)
+                                             rotate_in_history=args.rotate_in_history)
         impl.set_rotations(w.rk, w.rv)
         impls.append(impl)
     ntok = w.q.shape[0]
@@ -888,7 +888,7 @@ def main(argv=None):
             "one_launch_post": bool(args.one_launch_post),
             "overlap": not args.no_overlap,
             "layer_step": bool(args.layer_step),
-            "rotate_in_history": not args.separate_q_rotation,
+            "rotate_in_history": bool(args.rotate_in_history),
         },
         "us_per_layer_step": fig["us_per_layer_step"],
         "gpu_us_per_layer_step": fig["gpu_us_per_layer_step"],

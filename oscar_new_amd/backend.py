@@ -134,15 +134,17 @@ class OscarAttentionImpl:
     the one-launch step does not; same bits as three launches) and ``overlap`` (default on:
     where it applies, the step is the history launch carrying the BF16 branch and the K/V INT2
     store as extra workgroups, and post-attention; same bits). ``rotate_in_history`` (default
-    on, with ``overlap``): the history workgroups rotate the query rows themselves; off, the q
-    rotation is a launch of its own ahead of the history launch; same bits.
+    off; with ``overlap``): the history workgroups rotate the query rows themselves instead of
+    a q rotation launch of its own ahead of the history launch; same bits. Every history
+    workgroup then reads all of R_k (57 MB of L2 reads at c3), which costs more than the
+    extra launch (c3 step 53.1 against 52.3 us, c5 53.2 against 51.9 us, one process).
     """
 
     def __init__(self, num_heads, head_size, scale, num_kv_heads, alibi_slopes=None,
                  sliding_window=None, kv_cache_dtype="auto", logits_soft_cap=None,
                  attn_type="decoder", kv_sharing_target_layer_name=None, *, vllm_config=None,
                  oscar_config=None, split_policy=None, fused=True, one_launch_post=False,
-                 layer_step=False, overlap=True, rotate_in_history=True, **kwargs):
+                 layer_step=False, overlap=True, rotate_in_history=False, **kwargs):
         unsupported = (
             (alibi_slopes is not None, "ALiBi"),
             (sliding_window is not None, "sliding-window attention"),

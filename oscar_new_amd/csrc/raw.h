@@ -551,7 +551,6 @@ __device__ __forceinline__ void raw_block_staged(const AttnArgs& a, int task, in
   for (int b = 0; b < nblk; ++b) {
     top_up(b);
     raw_wait_blocks(issued - b - 1);
-    const int t0 = s.begin + kBlock * b;
     const uint8_t* slot = lds + kRawSlotBytes * (b % slots);
     f32x4 sc[RT][2];
 #pragma unroll

@@ -61,7 +61,6 @@ __global__ __launch_bounds__(kWavesPerBlock * kWave) void rotate_kernel(const Ro
 // order of rotate_kernel (bit-identical results), and the block's output goes through LDS
 // so that every lane stores 16 bytes.
 constexpr int kTiledRt = kHeadDim * kHeadDim * 2;  // R^T image, 128 KiB
-constexpr int kTiledOut = 16 * kHeadDim * 2;        // one 16-row output block, 8 KiB
 constexpr int64_t kTiledMinRows = 1024;             // below this, rotate_kernel
 
 __device__ __forceinline__ int rt_piece_offset(int col, int piece) {

@@ -259,6 +259,7 @@ def test_pre_attention_matches_single_entry_points():
     ([1804, 2601], [1803, 2600], 0),  # decode: one query row group per task
     ([69, 263, 1804, 40], [67, 261, 1802, 38], 0),  # two-token MTP (12 rows: > 8, refused)
     ([6000, 300, 4000], [5999, 299, 3999], 512),  # token-bounded splits
+    ([6000, 300, 4000], [5999, 299, 3999], -40),  # the device rule, a 40-workgroup budget
 ])
 @pytest.mark.parametrize("rotate_in_history", [False, True])
 def test_history_pre_matches_single_entry_points(lengths, prefixes, split_tokens,
