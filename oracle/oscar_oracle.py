@@ -22,6 +22,10 @@ Pinning (what checks each function independently of its own formula):
   * ``fma_f32``: exact rational arithmetic (fractions.Fraction) on random triples.
   * ``search`` clip mode: BASELINE extension with no reference counterpart; pinned by a
     brute-force argmin over the 8 factors computed with Python floats.
+  * ``cached_decode_variants``: "exact" against ``dense_attention`` on the float64 dequant
+    (and against "oracle" within bf16 dequant rounding); "reference_kernel" against the
+    blocked online softmax reducing to the dense softmax when no rounding is applied, and
+    the split merge's invariance to the split count.
 """
 
 from __future__ import annotations
@@ -53,6 +57,7 @@ __all__ = [
     "unpack",
     "dequant_rows",
     "cached_decode_reference",
+    "cached_decode_variants",
 ]
 
 NEG_INF = np.float32(-np.inf)
@@ -734,3 +739,141 @@ def cached_decode_reference(history, window, table_row, seq, q_bits, k_bits, v_b
     out = (p / den) @ values.astype(np.float64)
     lse = (m + np.log(den))[:, 0]
     return out.reshape(t, hq, d).astype(np.float32), lse.reshape(t, hq).astype(np.float32)
+
+
+def _dequant_exact(history, offsets, d=256):
+    """Dequantized vectors without the bf16 rounding of ``load_vec``: code * scale + zero in
+    float64 (fp16 scale and zero are exact in float64), [N, d]."""
+    offsets = np.asarray(offsets, np.int64)
+    data = history[offsets[:, None] + np.arange(d // 4)[None, :]].astype(np.int32)
+    codes = ((data[:, :, None] >> (2 * np.arange(4))[None, None, :]) & 3).reshape(len(offsets), d)
+    sz = history[offsets[:, None] + d // 4 + np.arange(4)[None, :]]
+    scale = np.ascontiguousarray(sz[:, :2]).view(np.float16)[:, 0].astype(np.float64)
+    zero = np.ascontiguousarray(sz[:, 2:]).view(np.float16)[:, 0].astype(np.float64)
+    return codes.astype(np.float64) * scale[:, None] + zero[:, None]
+
+
+def _blocked_softmax(q, keys, values, pos, limit, scale, block_n, round_p):
+    """One split of the reference kernel's online softmax (kernels.py:421-436) for rows q
+    [R, D] over keys/values [L, D] (float64 holding bf16 values) in blocks of ``block_n``:
+    fp32 scores, running max with the -inf guard, ``p.to(bf16)`` in the P V product
+    (``round_p``), fp32 state. ``limit`` [R]: a row sees positions <= limit. Returns
+    (normalized [R, D] float32, lse [R] float32); an empty split gives 0 / -inf."""
+    r = q.shape[0]
+    f32 = np.float32
+    m = np.full(r, -np.inf, f32)
+    den = np.zeros(r, f32)
+    acc = np.zeros((r, q.shape[1]), f32)
+    for b0 in range(0, max(len(pos), 1), block_n):
+        sl = slice(b0, b0 + block_n)
+        if b0 >= len(pos):
+            break
+        score = ((q @ keys[sl].T).astype(f32) * f32(scale)).astype(f32)
+        score = np.where(pos[sl][None, :] <= limit[:, None], score, -np.inf).astype(f32)
+        new_m = np.maximum(m, score.max(1))
+        safe = np.where(new_m == -np.inf, f32(0), new_m).astype(f32)
+        alpha = np.exp((m - safe).astype(np.float64)).astype(f32)
+        pr = np.exp((score - safe[:, None]).astype(np.float64)).astype(f32)
+        pv = bf16_to_f32(f32_to_bf16(pr)) if round_p else pr
+        acc = (acc * alpha[:, None] + (pv.astype(np.float64) @ values[sl]).astype(f32)).astype(f32)
+        den = (den * alpha + pr.sum(1, dtype=np.float64).astype(f32)).astype(f32)
+        m = new_m
+    out = (acc / np.maximum(den, f32(1e-30))[:, None]).astype(f32)
+    lse = np.where(den > 0, m + np.log(np.maximum(den, f32(1e-30))), -np.inf).astype(f32)
+    return out, lse
+
+
+def cached_decode_variants(history, window, table_row, seq, q_bits, k_bits, v_bits, rk_bits,
+                           rv_bits, geometry: Geometry, scale=None, head=0, splits=16,
+                           block_n=32):
+    """Three references for one request's decode step, read back from one quantized cache.
+
+    * "oracle": ``cached_decode_reference`` (tests/oracle.py:55-65: the dequantized history
+      rounded to bf16, inverse-rotated in float, dense attention).
+    * "exact": the same attention with the history dequantized exactly (code * scale + zero,
+      no bf16 rounding), inverse-rotated and attended in float64: the value every
+      implementation of this cache format approximates.
+    * "reference_kernel": the rounding points of the reference's own kernels in
+      backend.py:195-226 order: q rotated by R_k and rounded to bf16 (rotate); history keys
+      and values dequantized to bf16 (_load_vec, kernels.py:205-219); each of ``splits``
+      splits (kernels.py:368-370) a blocked online softmax with fp32 state and ``p.to(bf16)``
+      (kernels.py:421-431); the LSE merge of the splits rounded to bf16 (merge_splits); the
+      inverse V rotation rounded to bf16 (rotate(hrot, Rv.T)); the BF16 branch the same
+      blocked softmax over the window and current rows (one split); the path merge to bf16.
+
+    Returns {name: (out float32 [T, Hq, D], lse float32 [T, Hq])}; "reference_kernel" holds
+    bf16 values and the merged LSE of merge_paths.
+    """
+    t, hq, d = q_bits.shape
+    scale = d ** -0.5 if scale is None else float(scale)
+    prefix = seq - t
+    s_tok, recent = geometry.sink_tokens, geometry.recent_tokens
+    sink_len = min(s_tok, prefix)
+    recent_begin = max(sink_len, prefix - recent)
+    bk = geometry.kernel_block_tokens
+    pos = np.arange(sink_len, recent_begin)
+    slots = np.asarray(table_row, np.int64)[pos // bk] * bk + pos % bk
+    pages, within = np.divmod(slots, geometry.physical_block_tokens)
+    offs = pages * geometry.stripe_page_bytes + (within * geometry.kv_heads + head) * geometry.slot_bytes
+    rk = bf16_to_f32(rk_bits).astype(np.float64)
+    rv = bf16_to_f32(rv_bits).astype(np.float64)
+    first = int(table_row[0])
+    window_pos = list(range(0, sink_len)) + list(range(recent_begin, prefix))
+    wk = np.array([bf16_to_f32(window[geometry.window_element(first, p, 0, head):][:d])
+                   for p in window_pos], np.float64).reshape(-1, d)
+    wv = np.array([bf16_to_f32(window[geometry.window_element(first, p, 1, head):][:d])
+                   for p in window_pos], np.float64).reshape(-1, d)
+    ck = bf16_to_f32(k_bits[:, head]).astype(np.float64)
+    cv = bf16_to_f32(v_bits[:, head]).astype(np.float64)
+    q = bf16_to_f32(q_bits).astype(np.float64).reshape(t * hq, d)
+    qi = np.repeat(np.arange(t), hq) + prefix  # position limit of each row
+
+    def dense(keys, values):
+        sc = (q @ keys.T) * scale
+        sc = np.where(np.arange(seq)[None, :] > qi[:, None], -np.inf, sc)
+        m = sc.max(-1, keepdims=True)
+        p = np.exp(sc - m)
+        den = p.sum(-1, keepdims=True)
+        out = (p / den) @ values
+        lse = (m + np.log(den))[:, 0]
+        return out.reshape(t, hq, d).astype(np.float32), lse.reshape(t, hq).astype(np.float32)
+
+    def assemble(hk, hv):
+        keys = np.empty((seq, d), np.float64)
+        values = np.empty((seq, d), np.float64)
+        keys[sink_len:recent_begin], values[sink_len:recent_begin] = hk, hv
+        keys[window_pos], values[window_pos] = wk, wv
+        keys[prefix:], values[prefix:] = ck, cv
+        return keys, values
+
+    out = {"oracle": cached_decode_reference(history, window, table_row, seq, q_bits, k_bits,
+                                             v_bits, rk_bits, rv_bits, geometry, scale, head)}
+    out["exact"] = dense(*assemble(_dequant_exact(history, offs, d) @ rk.T,
+                                   _dequant_exact(history, offs + geometry.vector_bytes, d) @ rv.T))
+
+    # The reference kernels' rounding points, in the rotated space for the history branch.
+    q_rot = bf16_to_f32(rotate(q_bits.reshape(t * hq, d), rk_bits)).astype(np.float64)
+    hk = bf16_to_f32(dequant_rows(history, offs, d)).astype(np.float64)
+    hv = bf16_to_f32(dequant_rows(history, offs + geometry.vector_bytes, d)).astype(np.float64)
+    length = recent_begin - sink_len
+    tps = -(-(-(-length // block_n)) // splits)
+    parts = np.zeros((t * hq, splits, d), np.float32)
+    lses = np.full((t * hq, splits), -np.inf, np.float32)
+    for split in range(splits):
+        b, e = split * tps * block_n, min((split + 1) * tps * block_n, length)
+        if e > b:
+            parts[:, split], lses[:, split] = _blocked_softmax(
+                q_rot, hk[b:e], hv[b:e], pos[b:e], qi, scale, block_n, True)
+        else:
+            parts[:, split] = 0.0
+    counts = np.array([1, t * hq])
+    hrot, hl = merge_splits(parts[:, None], lses[:, None], counts)
+    hout = rotate(hrot[:, 0], rv_bits.T)
+    raw_pos = np.array(window_pos + list(range(prefix, seq)), np.int64)
+    raw_k = np.concatenate([wk, ck])
+    raw_v = np.concatenate([wv, cv])
+    rp, rl = _blocked_softmax(q, raw_k, raw_v, raw_pos, qi, scale, block_n, True)
+    merged, mlse = merge_paths(hout.reshape(t * hq, 1, d), hl.reshape(t * hq, 1), rp,
+                               rl.reshape(t * hq, 1), np.array([1, t * hq]))
+    out["reference_kernel"] = (bf16_to_f32(merged).reshape(t, hq, d), mlse.reshape(t, hq))
+    return out

@@ -15,6 +15,7 @@ import pytest
 import torch
 
 import oracle as O
+from oracle import oscar_oracle as OO
 
 # ------------------------------------------------------------------ number formats
 
@@ -530,3 +531,76 @@ def test_token_bounded_boundaries_sit_on_the_absolute_chunk_grid(lo, length, nsp
             assert 0 <= begin - b < 64
     covered = [t for b, e in cuts for t in range(b, e)]
     assert covered == list(range(length))  # contiguous, in order, each token once
+
+
+def test_blocked_online_softmax_reduces_to_the_dense_softmax():
+    # The reference kernel's blocked online softmax (kernels.py:421-436) without the bf16
+    # rounding of p is the dense softmax up to fp32 state; with it, each p carries one bf16
+    # rounding (relative 2^-8 at most), so the output moves by at most that fraction of the
+    # values' magnitude. Masked positions (pos > limit) take no weight.
+    rng = np.random.default_rng(21)
+    q = rng.standard_normal((6, 256))
+    keys = O.bf16_to_f32(O.f32_to_bf16(rng.standard_normal((300, 256)).astype(np.float32)))
+    values = O.bf16_to_f32(O.f32_to_bf16(rng.standard_normal((300, 256)).astype(np.float32)))
+    pos = np.arange(300)
+    limit = np.array([299, 299, 150, 150, 37, 0])
+    keys64, values64 = keys.astype(np.float64), values.astype(np.float64)
+    for r in range(6):
+        sc = (keys64[: limit[r] + 1] @ q[r]) / 16
+        want, want_l = OO._row_softmax(sc, values64[: limit[r] + 1])
+        out, lse = OO._blocked_softmax(q[r:r + 1], keys64, values64, pos, limit[r:r + 1], 1 / 16,
+                                      32, False)
+        np.testing.assert_allclose(out[0], want, atol=2e-6)
+        np.testing.assert_allclose(lse[0], want_l, atol=2e-6)
+        rounded, _ = OO._blocked_softmax(q[r:r + 1], keys64, values64, pos, limit[r:r + 1],
+                                        1 / 16, 32, True)
+        assert np.abs(rounded[0] - want).max() <= 2.0 ** -8 * np.abs(values).max()
+    out, lse = OO._blocked_softmax(q[:1], keys64[:0], values64[:0], pos[:0], limit[:1], 1 / 16,
+                                  32, True)
+    assert not out.any() and np.isneginf(lse).all()
+
+
+def test_decode_variants_agree_within_their_rounding():
+    # One cache, three references: "exact" (float64 dequant) is dense attention over the
+    # exactly dequantized history; "oracle" rounds the dequantized values to bf16 and
+    # "reference_kernel" adds the reference kernels' bf16 roundings (q_rot, p, merged
+    # history, inverse rotation, output), so both stay within a few bf16 steps of "exact"
+    # in relative L2 (a bf16 rounding is 2^-9 relative at most). The reference kernel's
+    # result does not depend on its split count beyond rounding.
+    geo = O.Geometry(768, sink_tokens=4, recent_tokens=16, speculative_tokens=3)
+    history, window, table, ks, vs, rk, rv = _paged_state([700], [696], geo, seed=11)
+    q = O.f32_to_bf16(np.random.default_rng(2).standard_normal((4, 6, 256)).astype(np.float32))
+    args = (history, window, table[0], 700, q, ks[0][696:], vs[0][696:], rk, rv, geo)
+    v = O.cached_decode_variants(*args, scale=1 / 16, splits=4)
+    exact, exact_l = v["exact"]
+
+    def rel(a):
+        return np.linalg.norm(a - exact) / np.linalg.norm(exact)
+
+    assert rel(v["oracle"][0]) < 1e-2 and rel(v["reference_kernel"][0]) < 1.5e-2
+    np.testing.assert_allclose(v["oracle"][1], exact_l, atol=2e-3)
+    np.testing.assert_allclose(v["reference_kernel"][1], exact_l, atol=2e-2)
+    # "exact" is dense attention over the float64 dequantized history (recomputed here).
+    d = 256
+    bk = geo.kernel_block_tokens
+    pos = np.arange(4, 696 - 16)
+    slots = table[0][pos // bk].astype(np.int64) * bk + pos % bk
+    offs = np.array([geo.slot_offset(s) for s in slots])
+    keys = np.zeros((700, d))
+    values = np.zeros((700, d))
+    rkf, rvf = O.bf16_to_f32(rk).astype(np.float64), O.bf16_to_f32(rv).astype(np.float64)
+    keys[4:680] = OO._dequant_exact(history, offs) @ rkf.T
+    values[4:680] = OO._dequant_exact(history, offs + geo.vector_bytes) @ rvf.T
+    for p in list(range(4)) + list(range(680, 696)):
+        keys[p] = O.bf16_to_f32(window[geo.window_element(table[0][0], p, 0):][:d])
+        values[p] = O.bf16_to_f32(window[geo.window_element(table[0][0], p, 1):][:d])
+    keys[696:] = O.bf16_to_f32(ks[0][696:, 0])
+    values[696:] = O.bf16_to_f32(vs[0][696:, 0])
+    want, want_l = O.dense_attention(O.bf16_to_f32(q), keys[:, None], values[:, None], 696)
+    np.testing.assert_allclose(exact, want, atol=1e-6)
+    np.testing.assert_allclose(exact_l, want_l, atol=1e-5)
+    # The exact dequant differs from load_vec's only by the bf16 rounding.
+    diff = OO._dequant_exact(history, offs[:8]) - O.bf16_to_f32(O.dequant_rows(history, offs[:8]))
+    assert np.abs(diff).max() <= 2.0 ** -8 * np.abs(OO._dequant_exact(history, offs[:8])).max()
+    one = O.cached_decode_variants(*args, scale=1 / 16, splits=1)["reference_kernel"][0]
+    assert np.linalg.norm(one - v["reference_kernel"][0]) <= 1e-2 * np.linalg.norm(exact)
