@@ -504,6 +504,8 @@ def cpu_baseline(w, args, outputs):
 
 HIST_LAUNCHES = 20  # history launches per timed batch of the dominant-kernel measurement
 TRAFFIC_PROFILES = {  # rocprof PMC summaries (FETCH_SIZE / WRITE_SIZE runs) per (kernel, config)
+    ("history_pre_kernel", "c3"): "history_pre_kernel_c3_traffic.txt",
+    ("history_pre_kernel", "c5"): "history_pre_kernel_c5_traffic.txt",
     ("history_pair_kernel", "c3"): "history_kernel_c3_traffic.txt",
     ("history_pair_kernel", "c5"): "history_kernel_c5_traffic.txt",
     ("history_queue_kernel", "c4"): "history_queue_kernel_c4_traffic.txt",
