@@ -73,6 +73,9 @@ def parse_args(argv=None):
     p.add_argument("--rotate-in-history", action="store_true",
                    help="the history workgroups rotate their query rows (default: the q "
                         "rotation is a launch of its own ahead of the history launch)")
+    p.add_argument("--q-roles", action="store_true",
+                   help="the q rotation as role workgroups of the history launch instead of a "
+                        "launch of its own")
     p.add_argument("--mode", default="step",
                    choices=("step", "history", "copy", "prefill", "store"),
                    help="step: full benchmark; history: only the history-attention launches "
@@ -580,13 +583,23 @@ def in_step_launch(impl, w, layers, splits, split_tokens):
         # + the BF16 branch (window and current K/V rows, its partial rows), the step's INT2
         # slots and R_k / R_v.
         extra = alg.bf16 + rows * 1028 + ntok * 136 + 2 * 256 * 256 * 2
-        name = "history_pre_rot_kernel" if impl.rotate_in_history else "history_pre_kernel"
-        qrot = None if impl.rotate_in_history else kernels.rotate(w.q, impl.rk_cols)
+        q_sync = None
+        if impl._q_roles():
+            # + the rotation roles' rotated rows (written, then read by the history rows).
+            name = "history_pre_q_kernel"
+            extra += ntok * 6 * 256 * 2
+            qrot = w.q.new_empty(w.q.shape)
+            q_sync = impl.q_sync
+        elif impl.rotate_in_history:
+            name, qrot = "history_pre_rot_kernel", None
+        else:
+            name, qrot = "history_pre_kernel", kernels.rotate(w.q, impl.rk_cols)
 
         def fn(i):
             h, win = views[i % len(views)]
             kernels.history_pre(qrot, w.q, w.k, w.v, h, win, meta, layout, 1 / 16, splits,
-                                impl.rk_t, impl.rv_t, split_tokens=split_tokens)
+                                impl.rk_t, impl.rv_t, split_tokens=split_tokens,
+                                q_sync=q_sync)
 
         return name, hist + extra, fn
     qrot = kernels.rotate(w.q, impl.rk_cols)
@@ -679,7 +692,8 @@ def measure_step(args, name, device, steps, warmup):
                                              one_launch_post=args.one_launch_post,
                                              overlap=not args.no_overlap,
                                              layer_step=args.layer_step,
-                                             rotate_in_history=args.rotate_in_history)
+                                             rotate_in_history=args.rotate_in_history,
+                                             q_roles=args.q_roles)
         impl.set_rotations(w.rk, w.rv)
         impls.append(impl)
     ntok = w.q.shape[0]
@@ -891,6 +905,7 @@ def main(argv=None):
             "overlap": not args.no_overlap,
             "layer_step": bool(args.layer_step),
             "rotate_in_history": bool(args.rotate_in_history),
+            "q_roles": bool(args.q_roles),
         },
         "us_per_layer_step": fig["us_per_layer_step"],
         "gpu_us_per_layer_step": fig["gpu_us_per_layer_step"],

@@ -302,6 +302,31 @@ int oscar_history_pre(const void* query_rot, int64_t r_s0, int64_t r_s1, int64_t
                       void* stream);
 
 /*
+ * history_pre_q -- oscar_history_pre with the q rotation of backend.py:195 as role workgroups
+ * of the same launch (no reference counterpart as one call; it replaces oscar_rotate(query,
+ * R_k) followed by oscar_history_pre, with their bits). qrot: bf16 [n, hq, 256] contiguous,
+ * receives rotate(query, R_k); the history workgroups read it once the rotation roles are
+ * done. qsync: int32 [4], all zero before the first call; each launch leaves it zero (the
+ * workgroup that completes the grid resets it). After the launch qsync[2] != 0 means that a
+ * history workgroup stopped waiting for the rotation roles (about a millisecond) and its rows
+ * are wrong; it never happens when the launch has the device to itself. Calls that overlap on
+ * one device with the same qsync race. Other arguments and coverage: as oscar_history_pre.
+ */
+int oscar_history_pre_q(void* qrot, int32_t* qsync, const void* query, int64_t q_s0,
+                        int64_t q_s1, const void* key, int64_t k_s0, int64_t k_s1,
+                        const void* value, int64_t v_s0, int64_t v_s1, void* history,
+                        int64_t history_bytes, const void* window, int64_t window_elems,
+                        const int32_t* qstarts, const int32_t* seq_lens,
+                        const int32_t* block_tables, int64_t table_stride, int64_t table_columns,
+                        const int32_t* counts, const int32_t* tasks, const int32_t* task_count,
+                        int64_t n, int64_t hq, int64_t programs, int32_t splits, int32_t block_n,
+                        int32_t query_tile, int32_t max_query_len, float scale,
+                        int32_t split_tokens, const void* rk_t, const void* rv_t,
+                        const int64_t* slots, const oscar_clip* clip, const oscar_layout* layout,
+                        float* partials, float* lse, float* raw_partials, float* raw_lse,
+                        void* stream);
+
+/*
  * history_post -- the history branch and post_attention in ONE launch (no reference
  * counterpart: it replaces oscar_attention_partials(raw = 0) followed by
  * oscar_post_attention, with the same output and merged_lse bits). The arguments are those of

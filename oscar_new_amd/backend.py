@@ -134,17 +134,23 @@ class OscarAttentionImpl:
     the one-launch step does not; same bits as three launches) and ``overlap`` (default on:
     where it applies, the step is the history launch carrying the BF16 branch and the K/V INT2
     store as extra workgroups, and post-attention; same bits). ``rotate_in_history`` (default
-    off; with ``overlap``): the history workgroups rotate the query rows themselves instead of
-    a q rotation launch of its own ahead of the history launch; same bits. Every history
-    workgroup then reads all of R_k (57 MB of L2 reads at c3), which costs more than the
-    extra launch (c3 step 53.1 against 52.3 us, c5 53.2 against 51.9 us, one process).
+    off; with ``overlap``): the history workgroups rotate the query rows themselves; every
+    history workgroup then reads all of R_k (57 MB of L2 reads at c3). ``q_roles`` (default
+    off; with ``overlap``, unless ``rotate_in_history``): the q rotation runs as role workgroups
+    of the history launch, whose history workgroups wait for the rotated rows after their
+    first chunk requests; same bits. Under the history stream's load the roles' chain of
+    memory round trips (load, write-through, count, poll, copy) ends after the first chunks
+    arrive: c5 step 53.0-53.4 against 53.8-54.5 us, c3 55.3-57.2 against 53.7-54.8 us (A/B
+    on one box). With neither, the q rotation is a launch of its own ahead of the history
+    launch (the default).
     """
 
     def __init__(self, num_heads, head_size, scale, num_kv_heads, alibi_slopes=None,
                  sliding_window=None, kv_cache_dtype="auto", logits_soft_cap=None,
                  attn_type="decoder", kv_sharing_target_layer_name=None, *, vllm_config=None,
                  oscar_config=None, split_policy=None, fused=True, one_launch_post=False,
-                 layer_step=False, overlap=True, rotate_in_history=False, **kwargs):
+                 layer_step=False, overlap=True, rotate_in_history=False, q_roles=False,
+                 **kwargs):
         unsupported = (
             (alibi_slopes is not None, "ALiBi"),
             (sliding_window is not None, "sliding-window attention"),
@@ -186,6 +192,8 @@ class OscarAttentionImpl:
         self.layer_step = layer_step
         self.overlap = overlap
         self.rotate_in_history = rotate_in_history
+        self.q_roles = q_roles
+        self.q_sync = None  # int32 [4] of the q rotation roles (zero between launches)
         self.rk = self.rv = self.rk_cols = self.rv_cols = self.rk_t = self.rv_t = None
         self.history = self.window = None
         self.cache_identity = None
@@ -224,9 +232,15 @@ class OscarAttentionImpl:
         self.rv_t = self.rv.T.contiguous()
         self.rk_cols = self.rk_t.T
         self.rv_cols = self.rv_t.T
+        # Allocated here, outside any graph capture; the launches keep it zero.
+        self.q_sync = torch.zeros(4, dtype=torch.int32, device=self.rk.device)
 
     def splits_for(self, meta):
         return self.partition_for(meta)[0]
+
+    def _q_roles(self):
+        """Whether the q rotation runs as role workgroups of the history launch."""
+        return self.q_roles and not self.rotate_in_history
 
     def _roles_share_history_launch(self, meta):
         """Whether the step's history launch carries the pre-attention role workgroups."""
@@ -253,6 +267,7 @@ class OscarAttentionImpl:
             programs = attention_programs(n, meta.max_num_reqs, self.cfg.queries_per_tile)
             # BF16 branch: one workgroup per (task, kv head); K/V store: 8 per 16 rows.
             reserved = (programs * self.num_kv_heads + 8 * -(-n * self.num_kv_heads // 16)
+                        + (-(-n * self.num_heads // 16) if self._q_roles() else 0)
                         if roles else 0)
             return choose_device_partition(programs, self.num_kv_heads, meta.max_query_len, n,
                                            self.num_heads, self.cfg.queries_per_tile,
@@ -265,6 +280,8 @@ class OscarAttentionImpl:
         if roles:
             kv_rows = meta.num_actual_tokens * self.num_kv_heads
             reserved = tasks * self.num_kv_heads + 8 * -(-kv_rows // 16)
+            if self._q_roles():
+                reserved += -(-meta.num_actual_tokens * self.num_heads // 16)
         return choose_history_partition(tasks, self.num_kv_heads, meta.max_query_len,
                                         getattr(meta, "max_seq_len", None),
                                         getattr(meta, "total_seq_len", None), rows=rows,
@@ -341,10 +358,16 @@ class OscarAttentionImpl:
             # q rotation launch goes first) and, dispatched ahead of it, the BF16 branch and
             # the INT2 store (the history branch never reads the slots the store writes), then
             # post-attention.
-            qrot = None if self.rotate_in_history else kernels.rotate(q, self.rk_cols)
+            q_sync = None
+            if self._q_roles():
+                qrot = torch.empty(q.shape, dtype=torch.bfloat16, device=q.device)
+                q_sync = self.q_sync
+            else:
+                qrot = None if self.rotate_in_history else kernels.rotate(q, self.rk_cols)
             hp, hl, rp, rl = kernels.history_pre(qrot, q, k, v, self.history, self.window, meta,
                                                  layout, self.scale, splits, self.rk_t,
-                                                 self.rv_t, split_tokens=split_tokens)
+                                                 self.rv_t, split_tokens=split_tokens,
+                                                 q_sync=q_sync)
             kernels.post_attention(hp, hl, rp, rl, self.rv, k, v, self.window, meta, layout,
                                    rows, lse)
             return

@@ -32,6 +32,12 @@ __device__ __forceinline__ void dma_dwordx4(const void* src, uint32_t lds) {
   asm volatile("s_nop 4\n\tglobal_load_lds_dwordx4 %1, off" : : "{m0}"(lds), "v"(src)
                : "memory");
 }
+// The same with the device-coherent cache policy (sc1): rows that another workgroup of the
+// launch wrote with device-coherent stores (the L2 of each XCD is not coherent with the others').
+__device__ __forceinline__ void dma_dwordx4_coherent(const void* src, uint32_t lds) {
+  asm volatile("s_nop 4\n\tglobal_load_lds_dwordx4 %1, off sc1" : : "{m0}"(lds), "v"(src)
+               : "memory");
+}
 #define OSCAR_WAIT_VM(n) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(n) : "memory")
 #define OSCAR_WAIT_LGKM() asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory")
 

@@ -1117,6 +1117,9 @@ static_assert(kDeviceUnitTasks * 4 <= kRingBytes, "the unit resolver's task list
 // and the K/V INT2 store of the step), which dispatch first and run beside the history stream.
 // kMode 4: as 3, and each workgroup rotates its task's query rows by R_k itself (a.query is
 // the unrotated query), with the operands and k order of the rotate entry point (same bits).
+// kMode 5: as 3, and q rotation roles of the same launch (pre.h q_rotate_role) write the
+// rotated query into a.query: every wavefront requests its first chunks, then wavefront 3
+// waits for the roles' tile count and copies the task's rotated rows.
 template <int kMode>
 __device__ __forceinline__ void history_pair_body(const AttnArgs& a, const FinishArgs* fin,
                                                   const LayerArgs* lay,
@@ -1143,15 +1146,22 @@ __device__ __forceinline__ void history_pair_body(const AttnArgs& a, const Finis
   static_assert(16 * kStageRowBytes + 4 * 2 * 8 * 16 * 4 <= 2 * kStageBytes,
                 "the layer step's 16-row staging tile and operand images fit wavefront 3's stages");
   static_assert(16 * kHeadDim * 2 <= kRingBytes, "the K/V store role's tile fits the ring");
-  if constexpr (kMode == 3 || kMode == 4) {
+  if constexpr (kMode == 3 || kMode == 4 || kMode == 5) {
     const int z = blockIdx.z;
     if (z < role_slices) {
       if (z == 0) {
         raw_block_staged<1>(pre->attn, blockIdx.x, blockIdx.y, 0, s_ring,
                             kRingBytes / kRawLdsPerSlot);
       } else {
-        const int r = ((z - 1) * static_cast<int>(gridDim.x) + static_cast<int>(blockIdx.x)) *
-                          static_cast<int>(gridDim.y) + static_cast<int>(blockIdx.y);
+        int r = ((z - 1) * static_cast<int>(gridDim.x) + static_cast<int>(blockIdx.x)) *
+                    static_cast<int>(gridDim.y) + static_cast<int>(blockIdx.y);
+        if constexpr (kMode == 5) {
+          if (r < pre->q_wgs) {
+            q_rotate_role(*pre, r, s_ring);
+            return;
+          }
+          r -= pre->q_wgs;
+        }
         if (r < pre->kv_wgs) kv_store_role(*pre, r, s_ring);
       }
       return;
@@ -1247,7 +1257,7 @@ __device__ __forceinline__ void history_pair_body(const AttnArgs& a, const Finis
     stores_k = split == 4 % nsplit;
     stores_v = split == 5 % nsplit;
   }
-  {
+  if constexpr (kMode != 5) {
     const int slot = wave * 64 + lane;
     const int row = slot >> 5, piece = (slot & 31) ^ row;
     const RowInfo ri = row_info(a, t, head, row);
@@ -1275,7 +1285,35 @@ __device__ __forceinline__ void history_pair_body(const AttnArgs& a, const Finis
   }
   OSCAR_WAIT_VM(0);
   __syncthreads();
-  if (kMode != 2 || wave < 3) {
+  if constexpr (kMode == 5) {
+    // Every wavefront requests its first chunks, then wavefront 3 waits for the rotated rows
+    // and copies them (its wait for the copy also covers its first chunks).
+    if (nmine > 0) issue(0, 0);
+    if (nmine > 1) issue(1, 1);
+    if (wave == 3) {
+      for (int poll = 0;; ++poll) {
+        const int done = __builtin_amdgcn_readfirstlane(
+            __hip_atomic_load(pre->qsync, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+        if (done >= pre->q_wgs) break;
+        if (poll == kQSyncPolls) {
+          __hip_atomic_store(pre->qsync + 2, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          break;
+        }
+        __builtin_amdgcn_s_sleep(8);
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int slot = i * 64 + lane;
+        const int row = slot >> 5, piece = (slot & 31) ^ row;
+        const RowInfo ri = row_info(a, t, head, row);
+        const uint16_t* src =
+            ri.valid ? a.query + ri.token * a.qs0 + ri.qhead * a.qs1 + 8 * piece : a.query;
+        dma_dwordx4_coherent(src, lds_addr(q_lds) + 1024 * i);
+      }
+      OSCAR_WAIT_VM(0);
+    }
+    barrier_lds();  // the rotated rows are in LDS
+  } else if (kMode != 2 || wave < 3) {
     if (nmine > 0) issue(0, 0);
     if (nmine > 1) issue(1, 1);
   }
@@ -1711,6 +1749,11 @@ __global__ __launch_bounds__(kThreads, 2) void history_pre_kernel(const HistoryP
 __global__ __launch_bounds__(kThreads, 2) void history_pre_rot_kernel(const HistoryPreArgs h) {
   history_pair_body<4>(h.a, nullptr, nullptr, &h.p, h.role_slices);
 }
+__global__ __launch_bounds__(kThreads, 2) void history_pre_q_kernel(const HistoryPreArgs h) {
+  history_pair_body<5>(h.a, nullptr, nullptr, &h.p, h.role_slices);
+  if (threadIdx.x == 0)
+    q_sync_leave(h.p.qsync, static_cast<int>(gridDim.x * gridDim.y * gridDim.z));
+}
 
 }  // namespace
 
@@ -1741,7 +1784,9 @@ hipError_t launch_history(const AttnArgs& a, dim3 grid, int rows, hipStream_t st
 hipError_t launch_history_pre(const AttnArgs& a, const PreArgs& p, int role_slices, dim3 grid,
                               bool rotate_query, hipStream_t stream) {
   const HistoryPreArgs h{a, p, role_slices};
-  if (rotate_query)
+  if (p.qsync)
+    hipLaunchKernelGGL(history_pre_q_kernel, grid, dim3(kThreads), 0, stream, h);
+  else if (rotate_query)
     hipLaunchKernelGGL(history_pre_rot_kernel, grid, dim3(kThreads), 0, stream, h);
   else
     hipLaunchKernelGGL(history_pre_kernel, grid, dim3(kThreads), 0, stream, h);

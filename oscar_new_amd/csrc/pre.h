@@ -23,6 +23,11 @@ struct PreArgs {
   float k_ratio, v_ratio, k_factor, v_factor;
   FastDiv h_div, hq_div;    // division by H and by hq
   int32_t raw_wgs, kv_wgs;  // role boundaries in blockIdx.x
+  // History launch with q rotation roles (qsync set): q_wgs 16-row tiles rotated into qrot
+  // by role workgroups of the same launch; qsync[0] counts finished tiles, qsync[1] finished
+  // workgroups, qsync[2] is set when a history workgroup gave up waiting (see q_rotate_role).
+  int32_t* qsync;
+  int32_t q_wgs;
 };
 
 // Rotation of rows [16 tile, +16) by R (given as R^T rows) into a [16][256] bf16 LDS tile
@@ -100,6 +105,52 @@ __device__ __forceinline__ void kv_store_role(const PreArgs& p, int r, uint8_t* 
   quantize_store(x, p.mode, is_v ? p.v_ratio : p.k_ratio, is_v ? p.v_factor : p.k_factor,
                  p.history + base + is_v * a.L.vector_bytes);
 }
+
+// q rotation role of the history launch (its history workgroups read the rotated rows):
+// rotates 16-row tile `tile` into a bf16 LDS tile (the bits of rotate_rows16 and the rotate
+// entry point), writes the live rows to qrot with device-coherent stores, waits for them, and
+// then adds 1 to qsync[0]. Protocol (qsync zero between launches): a history workgroup waits
+// until qsync[0] == q_wgs before it reads qrot with device-coherent loads; every workgroup of
+// the launch adds 1 to qsync[1] as it ends (q_sync_leave), and the one that completes the
+// grid resets both counters, when no workgroup of the launch reads them any more. The q roles
+// sit in the leading z-slices, so they are dispatched before any history workgroup, and a
+// waiting workgroup never holds a slot that a q role still needs. `smem`: 8 KiB of LDS.
+__device__ __forceinline__ void q_rotate_role(const PreArgs& p, int64_t tile, uint8_t* smem) {
+  const AttnArgs& a = p.attn;
+  uint16_t* tile_lds = reinterpret_cast<uint16_t*>(smem);
+  rotate_rows16(a.query, a.qs0, a.qs1, p.hq_div, a.hq, p.q_rows, tile, p.rk_t, tile_lds,
+                nullptr);
+  __syncthreads();
+  const uint32_t* src = reinterpret_cast<const uint32_t*>(tile_lds);
+  uint32_t* dst = reinterpret_cast<uint32_t*>(p.qrot + tile * 16 * kHeadDim);
+  const int64_t live_words = (p.q_rows - tile * 16) * (kHeadDim / 2);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int w = static_cast<int>(threadIdx.x) + kThreads * i;  // 16 rows x 128 words
+    if (w < live_words) __hip_atomic_store(dst + w, src[w], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this thread's rows are at the device
+  __syncthreads();
+  if (threadIdx.x == 0) __hip_atomic_fetch_add(p.qsync, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// End of a workgroup of the launch (thread 0, after every wait of its workgroup): the
+// workgroup that completes the grid resets the q counters for the next launch. The wait
+// orders this workgroup's tile count (q roles) before its arrival here.
+__device__ __forceinline__ void q_sync_leave(int32_t* qsync, int total) {
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  const int done =
+      __hip_atomic_fetch_add(qsync + 1, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (done == total - 1) {
+    __hip_atomic_store(qsync, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(qsync + 1, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
+// Polls of qsync[0] before a history workgroup gives up (about a millisecond; the roles take
+// a few microseconds). Giving up sets qsync[2] and the workgroup's rows are then wrong, never
+// a hang.
+constexpr int kQSyncPolls = 4096;
 
 // The history launch with the pre-attention roles (history.hip): grid (programs, H,
 // role_slices + splits); z-slice 0 runs the BF16 branch of (task, kv head) (lean form, one

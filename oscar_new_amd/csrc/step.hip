@@ -209,7 +209,11 @@ extern "C" int oscar_pre_attention(
   return static_cast<int>(hipGetLastError());
 }
 
-extern "C" int oscar_history_pre(
+namespace oscar {
+namespace {
+
+// oscar_history_pre and oscar_history_pre_q: `qrot_out` / `qsync` set (the latter) or NULL.
+int history_pre_common(
     const void* query_rot, int64_t r_s0, int64_t r_s1, int64_t r_s2, const void* query,
     int64_t q_s0, int64_t q_s1, const void* key, int64_t k_s0, int64_t k_s1, const void* value,
     int64_t v_s0, int64_t v_s1, void* history, int64_t history_bytes, const void* window,
@@ -219,20 +223,31 @@ extern "C" int oscar_history_pre(
     int64_t hq, int64_t programs, int32_t splits, int32_t block_n, int32_t query_tile,
     int32_t max_query_len, float scale, int32_t split_tokens, const void* rk_t,
     const void* rv_t, const int64_t* slots, const oscar_clip* clip, const oscar_layout* layout,
-    float* partials, float* lse, float* raw_partials, float* raw_lse, void* stream) {
-  using namespace oscar;
+    float* partials, float* lse, float* raw_partials, float* raw_lse, void* qrot_out,
+    int32_t* qsync, void* stream) {
   PreArgs p;
   int64_t qrows = 0;
   int st = make_pre_args(query, q_s0, q_s1, key, k_s0, k_s1, value, v_s0, v_s1, window,
                          window_elems, qstarts, seq_lens, block_tables, table_stride,
                          table_columns, counts, tasks, task_count, n, hq, programs, block_n,
                          query_tile, max_query_len, scale, rk_t, rv_t, history, history_bytes,
-                         slots, clip, layout, raw_partials, raw_lse, nullptr, &p, &qrows);
+                         slots, clip, layout, raw_partials, raw_lse, qrot_out, &p, &qrows);
   if (st != OSCAR_OK) return st;
   if (qrows > 8) return OSCAR_E_UNSUPPORTED;
   // query_rot == nullptr: the history workgroups rotate the query rows themselves.
-  const bool rotate_query = query_rot == nullptr;
-  if (rotate_query) {
+  const bool q_roles = qsync != nullptr;
+  const bool rotate_query = !q_roles && query_rot == nullptr;
+  if (q_roles) {
+    // q rotation roles write qrot_out ([n, hq, 256] contiguous), the history reads it.
+    if (!rk_t || !qrot_out) return OSCAR_E_NULL;
+    if (!aligned16(qrot_out) || reinterpret_cast<uintptr_t>(qsync) % 4) return OSCAR_E_ALIGN;
+    query_rot = qrot_out;
+    r_s0 = hq * kHeadDim;
+    r_s1 = kHeadDim;
+    r_s2 = 1;
+    p.qsync = qsync;
+    p.q_wgs = static_cast<int32_t>((p.q_rows + 15) / 16);
+  } else if (rotate_query) {
     if (!rk_t) return OSCAR_E_NULL;
     query_rot = query;
     r_s0 = q_s0;
@@ -248,18 +263,62 @@ extern "C" int oscar_history_pre(
                       partials, lse, &a, &hrows);
   if (st != OSCAR_OK || n == 0) return st;
   // Role slices in front of the history splits (dispatched first): slice 0 is the BF16
-  // branch of (task, kv head); the next ones hold the K/V store quads. Under the device rule
-  // the history slices hold unit slots.
+  // branch of (task, kv head); the next ones hold the q rotation tiles (q roles) and then the
+  // K/V store quads. Under the device rule the history slices hold unit slots.
   const int64_t per_slice = programs * a.L.kv_heads;
-  const int role_slices = 1 + static_cast<int>((p.kv_wgs + per_slice - 1) / per_slice);
+  const int role_slices =
+      1 + static_cast<int>((p.kv_wgs + p.q_wgs + per_slice - 1) / per_slice);
   const int64_t hist_slices =
       split_tokens < 0 ? device_unit_slices(programs, a.L.kv_heads, split_tokens) : splits;
   if (hist_slices + role_slices > 65535) return OSCAR_E_SHAPE;
+  if (q_roles && per_slice * (hist_slices + role_slices) > 0x7fffffffll) return OSCAR_E_SHAPE;
   if (split_tokens < 0 && programs > kDeviceUnitTasks) return OSCAR_E_UNSUPPORTED;
   const dim3 grid(static_cast<unsigned>(programs), static_cast<unsigned>(a.L.kv_heads),
                   static_cast<unsigned>(hist_slices + role_slices));
   return static_cast<int>(
       launch_history_pre(a, p, role_slices, grid, rotate_query, as_stream(stream)));
+}
+
+}  // namespace
+}  // namespace oscar
+
+extern "C" int oscar_history_pre(
+    const void* query_rot, int64_t r_s0, int64_t r_s1, int64_t r_s2, const void* query,
+    int64_t q_s0, int64_t q_s1, const void* key, int64_t k_s0, int64_t k_s1, const void* value,
+    int64_t v_s0, int64_t v_s1, void* history, int64_t history_bytes, const void* window,
+    int64_t window_elems, const int32_t* qstarts, const int32_t* seq_lens,
+    const int32_t* block_tables, int64_t table_stride, int64_t table_columns,
+    const int32_t* counts, const int32_t* tasks, const int32_t* task_count, int64_t n,
+    int64_t hq, int64_t programs, int32_t splits, int32_t block_n, int32_t query_tile,
+    int32_t max_query_len, float scale, int32_t split_tokens, const void* rk_t,
+    const void* rv_t, const int64_t* slots, const oscar_clip* clip, const oscar_layout* layout,
+    float* partials, float* lse, float* raw_partials, float* raw_lse, void* stream) {
+  return oscar::history_pre_common(
+      query_rot, r_s0, r_s1, r_s2, query, q_s0, q_s1, key, k_s0, k_s1, value, v_s0, v_s1,
+      history, history_bytes, window, window_elems, qstarts, seq_lens, block_tables,
+      table_stride, table_columns, counts, tasks, task_count, n, hq, programs, splits, block_n,
+      query_tile, max_query_len, scale, split_tokens, rk_t, rv_t, slots, clip, layout, partials,
+      lse, raw_partials, raw_lse, nullptr, nullptr, stream);
+}
+
+extern "C" int oscar_history_pre_q(
+    void* qrot, int32_t* qsync, const void* query, int64_t q_s0, int64_t q_s1, const void* key,
+    int64_t k_s0, int64_t k_s1, const void* value, int64_t v_s0, int64_t v_s1, void* history,
+    int64_t history_bytes, const void* window, int64_t window_elems, const int32_t* qstarts,
+    const int32_t* seq_lens, const int32_t* block_tables, int64_t table_stride,
+    int64_t table_columns, const int32_t* counts, const int32_t* tasks,
+    const int32_t* task_count, int64_t n, int64_t hq, int64_t programs, int32_t splits,
+    int32_t block_n, int32_t query_tile, int32_t max_query_len, float scale,
+    int32_t split_tokens, const void* rk_t, const void* rv_t, const int64_t* slots,
+    const oscar_clip* clip, const oscar_layout* layout, float* partials, float* lse,
+    float* raw_partials, float* raw_lse, void* stream) {
+  if (!qsync) return OSCAR_E_NULL;
+  return oscar::history_pre_common(
+      nullptr, 0, 0, 1, query, q_s0, q_s1, key, k_s0, k_s1, value, v_s0, v_s1, history,
+      history_bytes, window, window_elems, qstarts, seq_lens, block_tables, table_stride,
+      table_columns, counts, tasks, task_count, n, hq, programs, splits, block_n, query_tile,
+      max_query_len, scale, split_tokens, rk_t, rv_t, slots, clip, layout, partials, lse,
+      raw_partials, raw_lse, qrot, qsync, stream);
 }
 
 namespace oscar {

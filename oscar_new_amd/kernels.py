@@ -516,14 +516,18 @@ def history_pre_supported(meta, layout, hq):
 
 
 def history_pre(query_rot, query, key, value, history, window, meta, layout, scale, splits,
-                rk_t, rv_t, split_tokens=0):
+                rk_t, rv_t, split_tokens=0, q_sync=None):
     """The history branch and the pre-attention work other than the q rotation (BF16 branch,
     K/V INT2 store) in one launch, the latter as workgroups dispatched ahead of the history
     splits (no reference counterpart as one call; it replaces ``attention_partials(qrot, ...,
     raw=False)`` plus ``pre_attention`` without its q rotation, with their bits).
 
     ``query_rot``: the rotated query, or None: then the history workgroups rotate the query
-    rows by R_k themselves (the bits of ``rotate(query, R_k)``; no launch of its own);
+    rows by R_k themselves (the bits of ``rotate(query, R_k)``; no launch of its own).
+    ``q_sync`` (int32 [4] on the device, zero before the first call, left zero by every call):
+    the q rotation runs as role workgroups of the same launch and ``query_rot`` is its output
+    buffer (bf16 [n, hq, 256], contiguous), which the history workgroups read once the roles
+    are done; ``q_sync[2]`` is non-zero after a launch in which a workgroup gave up waiting.
     ``query``/``key``/``value``: the step's unrotated rows. Returns ``(partials [n, hq, splits,
     256], lse [n, hq, splits], raw_partials [n, hq, 1, 256], raw_lse [n, hq, 1])``, all fp32.
     """
@@ -545,7 +549,14 @@ def history_pre(query_rot, query, key, value, history, window, meta, layout, sca
     for r in (rk_t, rv_t):
         if r.dtype != torch.bfloat16 or not r.is_contiguous() or tuple(r.shape) != (d, d):
             raise ValueError("rk_t / rv_t must be contiguous bf16 [256, 256] (R transposed)")
-    query_rot = _rows_contiguous(query_rot) if query_rot is not None else None
+    if q_sync is not None:
+        if (query_rot is None or query_rot.dtype != torch.bfloat16 or not query_rot.is_contiguous()
+                or tuple(query_rot.shape) != (n, hq, d)):
+            raise ValueError("with q_sync, query_rot must be a contiguous bf16 [n, hq, 256] buffer")
+        if q_sync.dtype != torch.int32 or q_sync.numel() < 4 or q_sync.device != dev:
+            raise ValueError("q_sync must be an int32 device tensor of at least 4 elements")
+    else:
+        query_rot = _rows_contiguous(query_rot) if query_rot is not None else None
     rot_strides = query_rot.stride() if query_rot is not None else (0, 0, 1)
     query, q0, q1 = _row_strides(query, "query")
     key, k0, k1 = _row_strides(key, "key")
@@ -555,9 +566,13 @@ def history_pre(query_rot, query, key, value, history, window, meta, layout, sca
     table = _int32(meta.block_tables, "block_tables")
     max_query_len = getattr(meta, "max_query_len", None)
     max_query_len = int(max_query_len) if isinstance(max_query_len, int) else 0
+    if q_sync is not None:
+        entry, lead = _ext.library().oscar_history_pre_q, (_ptr(query_rot), _ptr(q_sync))
+    else:
+        entry, lead = _ext.library().oscar_history_pre, (_ptr(query_rot), *rot_strides)
     _ext.check(
-        _ext.library().oscar_history_pre(
-            _ptr(query_rot), *rot_strides, _ptr(query), q0, q1, _ptr(key), k0, k1,
+        entry(
+            *lead, _ptr(query), q0, q1, _ptr(key), k0, k1,
             _ptr(value), v0, v1, _ptr(history), history.numel() * history.element_size(),
             _ptr(window), window.numel(),
             _ptr(_int32(meta.query_start_loc, "query_start_loc")),

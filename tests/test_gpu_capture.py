@@ -168,6 +168,16 @@ def test_graph_captured_at_dummy_lengths_replays_full_size_steps(qlen, max_reqs,
     with torch.cuda.graph(graph, stream=stream):
         impl.forward(None, q, k, v, cache, meta, out)
     torch.cuda.synchronize()
+    # The q rotation as role workgroups of the history launch (opt-in): its own graph.
+    qr = OscarAttentionImpl.standalone(6, 256, 1 / 16, 1, cfg, q_roles=True)
+    qr.set_rotations(rk, rv)
+    qr_out = torch.zeros_like(out)
+    qr.forward(None, q, k, v, cache, meta, qr_out)
+    torch.cuda.synchronize()
+    qr_graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(qr_graph, stream=stream):
+        qr.forward(None, q, k, v, cache, meta, qr_out)
+    torch.cuda.synchronize()
 
     for name, lengths in scenarios.items():
         lengths = lengths or _c4_lengths()
@@ -188,6 +198,19 @@ def test_graph_captured_at_dummy_lengths_replays_full_size_steps(qlen, max_reqs,
         torch.cuda.synchronize()
         assert torch.equal(eager, got), name
         assert torch.equal(buf.merged_lse, got_lse), name
+        if kernels.history_pre_supported(meta, meta.layout, 6):
+            for _ in range(2):
+                qr_out.zero_()
+                qr_graph.replay()
+                torch.cuda.synchronize()
+                qr_got = qr_out.clone()
+                qr.forward(None, q, k, v, cache, meta, qr_out)
+                torch.cuda.synchronize()
+                assert torch.equal(qr_out, qr_got), name
+                assert qr.q_sync.tolist() == [0, 0, 0, 0], name
+            assert_scaled_close(qr_got[:len(lengths) * qlen].float().cpu().numpy(),
+                                got[:len(lengths) * qlen].float().cpu().numpy(),
+                                f"{name} q roles", rel=5e-3)
         nt = len(lengths) * qlen
         live = got[:nt].float().view(nt, 6, 256)
         assert torch.isfinite(live).all() and torch.isfinite(got_lse[:nt]).all()

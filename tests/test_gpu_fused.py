@@ -261,12 +261,11 @@ def test_pre_attention_matches_single_entry_points():
     ([6000, 300, 4000], [5999, 299, 3999], 512),  # token-bounded splits
     ([6000, 300, 4000], [5999, 299, 3999], -40),  # the device rule, a 40-workgroup budget
 ])
-@pytest.mark.parametrize("rotate_in_history", [False, True])
-def test_history_pre_matches_single_entry_points(lengths, prefixes, split_tokens,
-                                                 rotate_in_history):
-    # rotate_in_history: query_rot None, each history workgroup rotates its task's query rows.
-    print(f"[history_pre] {lengths} split_tokens {split_tokens} rotate {rotate_in_history}",
-          flush=True)
+@pytest.mark.parametrize("q_form", ["launch", "in_history", "roles"])
+def test_history_pre_matches_single_entry_points(lengths, prefixes, split_tokens, q_form):
+    # in_history: query_rot None, each history workgroup rotates its task's query rows;
+    # roles: q rotation role workgroups of the same launch write the rotated rows (q_sync).
+    print(f"[history_pre] {lengths} split_tokens {split_tokens} q {q_form}", flush=True)
     c = _case(lengths, prefixes, seed=4)
     meta, layout = c.meta, c.layout
     splits = 8
@@ -279,9 +278,20 @@ def test_history_pre_matches_single_entry_points(lengths, prefixes, split_tokens
             kernels.history_pre(qrot, c.q, c.k, c.v, hist_a, win_a, meta, layout, 1 / 16, splits,
                                 rk_t, rv_t)
         return
-    hp, hl, rp, rl = kernels.history_pre(None if rotate_in_history else qrot, c.q, c.k, c.v,
-                                         hist_a, win_a, meta, layout, 1 / 16, splits, rk_t, rv_t,
-                                         split_tokens=split_tokens)
+    q_sync = torch.zeros(4, dtype=torch.int32, device=DEV) if q_form == "roles" else None
+    q_arg = {"launch": qrot, "in_history": None, "roles": None}[q_form]
+    calls = 2 if q_form == "roles" else 1  # the second call sees the counters the first left
+    for _ in range(calls):
+        hist_a.copy_(hist_b)
+        if q_form == "roles":
+            q_arg = torch.full_like(c.q, float("nan"))
+        hp, hl, rp, rl = kernels.history_pre(q_arg, c.q, c.k, c.v, hist_a, win_a, meta, layout,
+                                             1 / 16, splits, rk_t, rv_t,
+                                             split_tokens=split_tokens, q_sync=q_sync)
+    if q_form == "roles":
+        torch.cuda.synchronize()
+        assert q_sync.tolist() == [0, 0, 0, 0]
+        assert torch.equal(q_arg.view(torch.int16), qrot.view(torch.int16))
     hp_ref, hl_ref = kernels.attention_partials(qrot, c.k, c.v, hist_b, win_b, meta, layout,
                                                 1 / 16, splits, False, split_tokens=split_tokens)
     _, rp_ref, rl_ref = kernels.pre_attention(c.q, c.k, c.v, hist_b, win_b, meta, layout, 1 / 16,
