@@ -28,6 +28,13 @@ __device__ __forceinline__ void dma_x4(const uint8_t* base, uint32_t voff, uint3
   asm volatile("s_nop 4\n\tglobal_load_lds_dwordx4 %1, %2" : : "{m0}"(lds), "v"(voff), "s"(base)
                : "memory");
 }
+// The same with the non-temporal hint: records read once per step, which should not displace
+// the step's reused data (rotations, query rows, split partials) from the caches.
+__device__ __forceinline__ void dma_x4_stream(const uint8_t* base, uint32_t voff, uint32_t lds) {
+  base = uniform_ptr(base);
+  asm volatile("s_nop 4\n\tglobal_load_lds_dwordx4 %1, %2 nt" : : "{m0}"(lds), "v"(voff), "s"(base)
+               : "memory");
+}
 __device__ __forceinline__ void dma_dwordx4(const void* src, uint32_t lds) {
   asm volatile("s_nop 4\n\tglobal_load_lds_dwordx4 %1, off" : : "{m0}"(lds), "v"(src)
                : "memory");

@@ -206,7 +206,7 @@ __device__ __forceinline__ void history_unit(const AttnArgs& a, int task, int he
     valid_bits = ok ? (valid_bits | (1u << s)) : (valid_bits & ~(1u << s));
     const uint32_t lds = my_ring + s * kStageBytes + kSkew;
 #pragma unroll
-    for (int i = 0; i < kDma; ++i) dma_x4(base, voff[i], lds + 1024 * i);
+    for (int i = 0; i < kDma; ++i) dma_x4_stream(base, voff[i], lds + 1024 * i);
   };
 
   // ---- query rows -> LDS (wavefront 3's stages, whose first chunks are issued once the
@@ -646,7 +646,7 @@ __device__ __forceinline__ void history_unit_w8(const AttnArgs& a, int task, int
              (static_cast<uint32_t>(t0) & in_kb_mask) * tok_bytes;
     const uint32_t l = my_ring + s * kStageBytes + kSkew;
 #pragma unroll
-    for (int i = 0; i < kDma; ++i) dma_x4(base, voff[i], l + 1024 * i);
+    for (int i = 0; i < kDma; ++i) dma_x4_stream(base, voff[i], l + 1024 * i);
   };
 
   // ---- query rows -> LDS: 32 rows, piece p of row r at r * 32 + (p ^ (r & 31)).
@@ -1236,7 +1236,7 @@ __device__ __forceinline__ void history_pair_body(const AttnArgs& a, const Finis
     valid_bits = ok ? (valid_bits | (1u << s)) : (valid_bits & ~(1u << s));
     const uint32_t lds = my_ring + s * kStageBytes + kSkew;
 #pragma unroll
-    for (int i = 0; i < kDma; ++i) dma_x4(base, voff[i], lds + 1024 * i);
+    for (int i = 0; i < kDma; ++i) dma_x4_stream(base, voff[i], lds + 1024 * i);
   };
 
   // ---- query rows -> LDS: piece p of row r at r * 32 + (p ^ r), in an area of their own
