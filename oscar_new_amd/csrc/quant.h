@@ -85,16 +85,9 @@ struct Quantized {
 // [0.5, 3.5] it differs from the correctly rounded quotient by less than 1.2e-6, so a value of
 // y = q + 0.5 further than 2^-16 from 1, 2 and 3 truncates to the same code. If any lane has a
 // value that close, the wavefront redoes its quotients with IEEE division.
-__device__ __forceinline__ Quantized quantize_clipped(const float xc[4], float mn, float mx) {
+// The codes of quantize_clipped for q.zf, q.sf and r = 1 / q.sf (correctly rounded).
+__device__ __forceinline__ void quantize_codes(const float xc[4], float r, Quantized& q) {
 #pragma clang fp contract(off)
-  Quantized q;
-  float spread = (mx - mn) / 3.0f;
-  spread = spread < 6.103515625e-05f ? 6.103515625e-05f : spread;
-  q.zero = float_to_f16_bits(mn);
-  q.scale = float_to_f16_bits(spread);
-  q.zf = f16_bits_to_float(q.zero);
-  q.sf = f16_bits_to_float(q.scale);
-  const float r = 1.0f / q.sf;
   float y[4];
   bool near = false;
 #pragma unroll
@@ -114,6 +107,18 @@ __device__ __forceinline__ Quantized quantize_clipped(const float xc[4], float m
     q.code[i] = c;
     q.byte |= static_cast<uint32_t>(c) << (2 * i);
   }
+}
+
+__device__ __forceinline__ Quantized quantize_clipped(const float xc[4], float mn, float mx) {
+#pragma clang fp contract(off)
+  Quantized q;
+  float spread = (mx - mn) / 3.0f;
+  spread = spread < 6.103515625e-05f ? 6.103515625e-05f : spread;
+  q.zero = float_to_f16_bits(mn);
+  q.scale = float_to_f16_bits(spread);
+  q.zf = f16_bits_to_float(q.zero);
+  q.sf = f16_bits_to_float(q.scale);
+  quantize_codes(xc, 1.0f / q.sf, q);
   return q;
 }
 
@@ -123,6 +128,129 @@ __device__ __forceinline__ void clamp4(const float x[4], float thr, float out[4]
   for (int i = 0; i < 4; ++i) out[i] = fminf(fmaxf(x[i], -thr), thr);
 }
 __device__ __forceinline__ float clamp1(float x, float thr) { return fminf(fmaxf(x, -thr), thr); }
+
+// Squared error of candidate i (lane i holds its threshold t, zero z, scale s and 1 / s) over
+// this lane's four values, summed in pairs as the oracle's tree does. `exact`: codes from the
+// IEEE quotient wherever the reciprocal product lies within 2^-16 of a code boundary (the
+// codes of quantize_clipped); otherwise from the reciprocal product alone.
+template <bool kExact>
+__device__ __forceinline__ float candidate_sq(const float x[4], float tc, float zc, float sc,
+                                              float rc, int i) {
+#pragma clang fp contract(off)
+  const float zf = lane_value(zc, i), sf = lane_value(sc, i), r = lane_value(rc, i);
+  if constexpr (!kExact) {
+    // Fast pass (within search_best's margin of the exact value): no clip (a clipped value's
+    // code is 0 or 3 either way, since z ~ -t or t - z ~ 3 s), and err = (x - z) - c s (c s is
+    // exact: c < 4 and s is an fp16 value) instead of x - fl(c s + z).
+    float sq[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float d = x[e] - zf;
+      const float c = __builtin_amdgcn_fmed3f(truncf(__builtin_fmaf(d, r, 0.5f)), 0.0f, 3.0f);
+      const float err = __builtin_fmaf(-c, sf, d);
+      sq[e] = err * err;
+    }
+    return (sq[0] + sq[1]) + (sq[2] + sq[3]);
+  }
+  const float t = lane_value(tc, i);
+  float xi[4], y[4];
+  // Clip (one median-of-three per element: the same value as the min/max pair for the
+  // finite inputs here).
+#pragma unroll
+  for (int e = 0; e < 4; ++e) xi[e] = __builtin_amdgcn_fmed3f(x[e], -t, t);
+#pragma unroll
+  for (int e = 0; e < 4; ++e) y[e] = __builtin_fmaf(xi[e] - zf, r, 0.5f);
+  if constexpr (kExact) {
+    // A wider test than quantize_clipped's (any y within 2^-16 of an integer): an estimate
+    // that far from 1, 2 and 3 truncates to the code of the exact quotient, and codes can only
+    // be redone exactly more often, never less.
+    bool near = false;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) near |= fabsf(y[e] - rintf(y[e])) < 1.52587890625e-05f;
+    if (__any(near)) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) y[e] = (xi[e] - zf) / sf + 0.5f;
+    }
+  }
+  float sq[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    // The code as a float: truncation toward zero clamped to [0, 3], the value of the
+    // integer code (a -0 here decodes to the same sum: -0 * sf + zf == 0 * sf + zf).
+    const float c = __builtin_amdgcn_fmed3f(truncf(y[e]), 0.0f, 3.0f);
+    const float dec = c * sf + zf;
+    const float err = x[e] - dec;
+    sq[e] = err * err;
+  }
+  return (sq[0] + sq[1]) + (sq[2] + sq[3]);
+}
+
+// The clip search's argmin (tests/oracle.py extension: the first of the 8 factors with the
+// least float32 MSE, summed as a pairwise tree over the 256 values). Fast pass: every
+// candidate's MSE from reciprocal-product codes, the 8 sums reduced together (each tree level
+// halves the candidates a lane keeps until lane l holds candidate (l&1)*4 + (l&2) + (l>>2&1)).
+// A reciprocal-product code differs from the exact one only for a value within about 2^-16 s
+// of a code boundary, i.e. of the midpoint of two decoded values, where the two squared errors
+// differ by at most s (2^-14 s + 2^-21 |z|); the fast error's different rounding moves each
+// squared error by at most 2^-20 m (2 m + 3 s) (m = max |x|); over 256 values and the tree's
+// rounding that bounds each fast MSE within
+// M = 2^-5 s^2 + 2^-12 s |z| + 2^-18 MSE + 2^-10 m (m + s) of the exact one (twice the bound). If no other candidate's interval reaches the fast minimum's, that minimum is
+// the exact one; otherwise the exact pass decides. Same result as the exact pass alone.
+__device__ __forceinline__ int search_best(const float x[4], float tc, float zc, float sc,
+                                           float rc, float maxabs, int lane) {
+#pragma clang fp contract(off)
+  float part[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) part[i] = candidate_sq<false>(x, tc, zc, sc, rc, i);
+  // Levels 3-5 of the tree (lane pairs 1, 2 and 4 apart), keeping half the candidates each.
+  const bool b0 = lane & 1, b1 = lane & 2, b2 = lane & 4;
+  float q4[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const float keep = b0 ? part[k + 4] : part[k], give = b0 ? part[k] : part[k + 4];
+    q4[k] = keep + dpp<kDppQuadXor1>(give);
+  }
+  float q2[2];
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    const float keep = b1 ? q4[k + 2] : q4[k], give = b1 ? q4[k] : q4[k + 2];
+    q2[k] = keep + dpp<kDppQuadXor2>(give);
+  }
+  const float keep = b2 ? q2[1] : q2[0], give = b2 ? q2[0] : q2[1];
+  float v = keep + __shfl_xor(give, 4, kWave);
+  // Levels 6-8: lanes 8, 16 and 32 apart.
+  v = v + dpp<kDppRowRor8>(v);
+  v = sum_xor16(v);
+  v = sum_xor32(v);
+  // Lane c (< 8) takes candidate c's sum, its margin and the decision.
+  const int c = lane & 7;
+  const float fv = __shfl(v, ((c >> 2) & 1) | (c & 2) | ((c & 1) << 2), kWave);
+  const float margin = 0.03125f * sc * sc + 2.44140625e-04f * sc * fabsf(zc) +
+                       3.814697265625e-06f * fv + 9.765625e-04f * maxabs * (maxabs + sc);
+  float m8 = fv;
+  m8 = fminf(m8, dpp<kDppQuadXor1>(m8));
+  m8 = fminf(m8, dpp<kDppQuadXor2>(m8));
+  m8 = fminf(m8, dpp<kDppRowHalfMirror>(m8));
+  const float fmin = lane_value(m8, 0);
+  const uint64_t at_min = __ballot(lane < 8 && fv == fmin);
+  const int best = __ffsll(static_cast<long long>(at_min)) - 1;
+  if (best >= 0) {
+    const float reach = lane_value(fv + margin, best);
+    if (!__any(lane < 8 && lane != best && fv - margin <= reach)) return best;
+  }
+  // A near tie: the exact pass over the 8 candidates, in order.
+  float best_err = 0.f;
+  int exact = 0;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const float err = wave_tree_sum_dpp(candidate_sq<true>(x, tc, zc, sc, rc, i));
+    if (i == 0 || err < best_err) {
+      best_err = err;
+      exact = i;
+    }
+  }
+  return exact;
+}
 
 // Quantize one vector and write codes + scale + zero (68 bytes) at `dst`. Clipping is
 // monotone, so the extremes of the clipped vector are the clipped extremes of the vector: one
@@ -152,48 +280,21 @@ __device__ __forceinline__ void quantize_store(const float x[4], int mode, float
     const float zc = f16_bits_to_float(float_to_f16_bits(lo));
     const float sc = f16_bits_to_float(float_to_f16_bits(spread));
     const float rc = 1.0f / sc;
-    float best_err = 0.f;
-    int best = 0;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const float t = lane_value(tc, i), zf = lane_value(zc, i), sf = lane_value(sc, i);
-      const float r = lane_value(rc, i);
-      float xi[4], y[4];
-      // Clip (one median-of-three per element: the same value as the min/max pair for the
-      // finite inputs here).
-#pragma unroll
-      for (int e = 0; e < 4; ++e) xi[e] = __builtin_amdgcn_fmed3f(x[e], -t, t);
-      // As quantize_clipped, with the reciprocal product fused into its + 0.5 and a wider
-      // test for the IEEE fallback (any y within 2^-16 of an integer): an estimate that far
-      // from 1, 2 and 3 truncates to the code of the exact quotient, and codes can only be
-      // redone exactly more often, never less.
-      bool near = false;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        y[e] = __builtin_fmaf(xi[e] - zf, r, 0.5f);
-        near |= fabsf(y[e] - rintf(y[e])) < 1.52587890625e-05f;
-      }
-      if (__any(near)) {
-#pragma unroll
-        for (int e = 0; e < 4; ++e) y[e] = (xi[e] - zf) / sf + 0.5f;
-      }
-      float sq[4];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        // The code as a float: truncation toward zero clamped to [0, 3], the value of the
-        // integer code (a -0 here decodes to the same sum: -0 * sf + zf == 0 * sf + zf).
-        const float c = __builtin_amdgcn_fmed3f(truncf(y[e]), 0.0f, 3.0f);
-        const float dec = c * sf + zf;
-        const float err = x[e] - dec;
-        sq[e] = err * err;
-      }
-      const float err = wave_tree_sum_dpp((sq[0] + sq[1]) + (sq[2] + sq[3]));
-      if (i == 0 || err < best_err) {
-        best_err = err;
-        best = i;
-      }
-    }
-    thr = maxabs * search_factor(best);
+    const int best = search_best(x, tc, zc, sc, rc, maxabs, lane);
+    // The winner's threshold, zero and scale are the values its lane computed above (those of
+    // quantize_clipped on the clipped extremes), so only its codes are left to compute.
+    const float t = lane_value(tc, best), zf = lane_value(zc, best), sf = lane_value(sc, best);
+    Quantized q;
+    q.zero = float_to_f16_bits(zf);
+    q.scale = float_to_f16_bits(sf);
+    q.zf = zf;
+    q.sf = sf;
+    float xc[4];
+    clamp4(x, t, xc);
+    quantize_codes(xc, lane_value(rc, best), q);
+    dst[lane] = static_cast<uint8_t>(q.byte);
+    if (lane == 0) *reinterpret_cast<uint32_t*>(dst + 64) = q.scale | (q.zero << 16);
+    return;
   } else if (ratio != 0.0f) {
     thr = percentile_threshold(x, ratio);
   }
