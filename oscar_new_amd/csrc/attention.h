@@ -41,8 +41,6 @@ struct AttnArgs {
   // about split_tokens tokens; < 0 = the device rule (token-bounded splits whose length the
   // kernel derives from the step's lengths, for a budget of -split_tokens workgroups).
   int32_t split_tokens;
-  // Device rule, paired kernel: unit slots u < fast_slots take longer units (0: one length).
-  int32_t fast_slots;
   FastDiv g_div;  // division by g (query heads per kv head)
   float scale_log2;
   // BF16 branch written as the layer output (initial prefill, no history): bf16 rows
@@ -160,153 +158,12 @@ __device__ __forceinline__ int launch_split_tokens(const AttnArgs& a, int progra
 struct DeviceUnit {
   Task t;
   int task, split, nsplit, split_tokens;
-  // Two-length form (fast_slots > 0): the task's first `fast` units (fast slots) split
-  // `fast_span` history tokens evenly, the others the rest; fast < 0: one length.
-  int fast, fast_span;
 };
-
-// Two unit lengths (no reference counterpart). The paired kernel runs two workgroups per CU,
-// and the workgroup dispatched first on a CU (unit slots u < fast_slots, one per CU) streams
-// its records ahead of the one dispatched second: its first chunks arrive about 3 us earlier
-// (the memory system serves the launch's first requests in order) and it then takes the
-// larger share of issue cycles, about 12 % more chunks per microsecond (per-workgroup
-// timestamps, c3). With equal units the second workgroup of every CU ends about 6 us after
-// the first. Fast slots therefore take units kFastUnit64 / 64 times as long:
-//   T_slow = max(1024, 64 * ceil(ceil(H * total / W) / 64)),  W = r * F + (room - F),
-//   T_fast = 64 * ceil(r * T_slow / 64),  F = min(fast_slots, room),  room as one length.
-// Units stay task-major: tasks whose units all fall below fast_slots split their history
-// into ceil(L / T_fast) even units, later ones into ceil(L / T_slow), and the task that
-// straddles the boundary gives its fast units T_fast tokens each and splits the rest evenly.
-// Each task takes at most `splits` units. Every slot's unit follows from the lengths alone, so
-// the result does not depend on which workgroup runs first.
-constexpr int kFastUnit64 = 86;  // r = 1.34
-
-__device__ __forceinline__ int units_of(int length, int t, int cap) {
-  return min(cap, max(1, cdiv(max(length, 0), t)));
-}
-
-// Every thread of the NT-thread workgroup calls it, with its own task row (programs <= NT):
-// `len` its history length, `mine` / `mine_task` its row (mine_task -1 if inactive).
-// 1: `out` filled, 0: no unit for slot u, -1: the units would not fit `slots` (the caller
-// takes the one-length rule).
-template <int NT>
-__device__ int device_unit_two(const AttnArgs& a, int u, int slots, int count, int64_t total,
-                               int len, const Task& mine, DeviceUnit& out) {
-  constexpr int kWaves = NT / kWave;
-  __shared__ int s_sum[2][kWaves];
-  __shared__ int s_star[kWaves];
-  __shared__ int s_info[4];  // straddling task, its base, its units, slow base after it
-  __shared__ int s_out[11];
-  const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
-  const int i = threadIdx.x;
-  const int heads = a.L.kv_heads;
-  const int64_t room =
-      max(static_cast<int64_t>(1), static_cast<int64_t>(-a.split_tokens) - int64_t{heads} * count);
-  const int64_t fast = min(static_cast<int64_t>(a.fast_slots), room);
-  const int64_t weight = (kFastUnit64 * fast + 63) / 64 + (room - fast);
-  const int64_t per = (int64_t{heads} * total + weight - 1) / weight;
-  const int t_slow = static_cast<int>(min(max((per + 63) / 64 * 64, int64_t{kDeviceMinSplit}),
-                                          int64_t{1} << 29));
-  const int t_fast = static_cast<int>((int64_t{t_slow} * kFastUnit64 / 64 + 63) / 64 * 64);
-  const bool live = i < count;
-  const int nf = live ? units_of(len, t_fast, a.splits) : 0;
-  const int ns = live ? units_of(len, t_slow, a.splits) : 0;
-  // Exclusive scans of nf and ns over the task rows.
-  int incl_f = nf, incl_s = ns;
-#pragma unroll
-  for (int d = 1; d < kWave; d <<= 1) {
-    const int yf = __shfl_up(incl_f, d, kWave), ys = __shfl_up(incl_s, d, kWave);
-    incl_f += lane >= d ? yf : 0;
-    incl_s += lane >= d ? ys : 0;
-  }
-  if (lane == kWave - 1) {
-    s_sum[0][wave] = incl_f;
-    s_sum[1][wave] = incl_s;
-  }
-  __syncthreads();
-  int pf = incl_f - nf, ps = incl_s - ns;
-  for (int w = 0; w < wave; ++w) {
-    pf += s_sum[0][w];
-    ps += s_sum[1][w];
-  }
-  // The straddling task: the first live row whose fast units would pass the fast slots.
-  const bool cross = live && pf + nf > fast;
-  const uint64_t ball = __ballot(cross);
-  if (lane == 0) s_star[wave] = ball ? wave * kWave + __ffsll(static_cast<long long>(ball)) - 1
-                                     : 0x7fffffff;
-  __syncthreads();
-  int star = 0x7fffffff;
-#pragma unroll
-  for (int w = 0; w < kWaves; ++w) star = min(star, s_star[w]);
-  if (i == star) {
-    // k fast units of t_fast tokens, then the rest evenly over slow units.
-    const int k = static_cast<int>(fast) - pf;
-    const int rest = max(len - k * t_fast, 0);
-    const int n = min(a.splits, k + (rest > 0 ? cdiv(rest, t_slow) : 0));
-    s_info[0] = i;
-    s_info[1] = pf;
-    s_info[2] = max(n, 1);
-    s_info[3] = ps + ns;  // slow-unit prefix of the rows after the straddling one
-  }
-  if (i == 0) s_out[0] = -1;
-  __syncthreads();
-  if (live) {
-    int base, n, kf;
-    if (i < star) {
-      base = pf;
-      n = nf;
-      kf = nf;
-    } else if (i == star) {
-      base = s_info[1];
-      n = s_info[2];
-      kf = min(static_cast<int>(fast) - base, n);
-    } else {
-      base = s_info[1] + s_info[2] + (ps - s_info[3]);
-      n = ns;
-      kf = 0;
-    }
-    if (i == count - 1) s_out[10] = base + n;  // units in all
-    if (u >= base && u < base + n) {
-      s_out[0] = i;
-      s_out[1] = u - base;
-      s_out[2] = n;
-      s_out[3] = kf;
-      s_out[4] = mine.req;
-      s_out[5] = mine.qoff;
-      s_out[6] = mine.qstart;
-      s_out[7] = mine.qlen;
-      s_out[8] = mine.prefix;
-      s_out[9] = mine.sink_len;
-    }
-  }
-  __syncthreads();
-  if (count > 0 && s_out[10] > slots) return -1;
-  const int task = s_out[0];
-  if (task < 0) return 0;
-  out.task = task;
-  out.split = s_out[1];
-  out.nsplit = s_out[2];
-  out.split_tokens = t_slow;
-  const int kf = s_out[3];
-  out.fast = kf;
-  out.t.req = s_out[4];
-  out.t.qoff = s_out[5];
-  out.t.qstart = s_out[6];
-  out.t.qlen = s_out[7];
-  out.t.prefix = s_out[8];
-  out.t.sink_len = s_out[9];
-  out.t.recent_begin = max(out.t.sink_len, out.t.prefix - a.L.recent);
-  const int length = max(out.t.recent_begin - out.t.sink_len, 0);
-  // A task entirely on fast slots splits evenly over its units; the straddling one gives its
-  // fast units t_fast tokens each.
-  out.fast_span = kf >= out.nsplit ? length : min(length, kf * t_fast);
-  return 1;
-}
 
 // Every thread of the NT-thread workgroup calls it. `scratch`: LDS for programs + 16 ints,
 // free until the call returns. False for a slot past the last unit.
 template <int NT>
-__device__ bool device_unit(const AttnArgs& a, int programs, int u, int slots, int* scratch,
+__device__ bool device_unit(const AttnArgs& a, int programs, int u, int* scratch,
                             DeviceUnit& out) {
   constexpr int kWaves = NT / kWave;
   int* nsplit = scratch;  // per task row: history length, then split count
@@ -315,18 +172,10 @@ __device__ bool device_unit(const AttnArgs& a, int programs, int u, int slots, i
   __shared__ int s_found[9];
   const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
   int64_t s = 0;
-  // The row of this thread's last task stays in registers: with at most NT task rows, the
-  // thread that finds the unit's task has its row already (no second round of loads).
-  Task mine{};
-  int mine_task = -1;
   for (int i = threadIdx.x; i < programs; i += NT) {
-    Task t;
-    const bool live = read_task(a, t, i);
-    const int len = live ? max(t.recent_begin - t.sink_len, 0) : 0;
+    const int len = task_history(a, i);
     nsplit[i] = len;
     s += len;
-    mine = t;
-    mine_task = live ? i : -1;
   }
   s = wave_sum_i64(s);
   if (lane == 0) s_total[wave] = s;
@@ -336,13 +185,7 @@ __device__ bool device_unit(const AttnArgs& a, int programs, int u, int slots, i
 #pragma unroll
   for (int w = 0; w < kWaves; ++w) total += s_total[w];
   const int count = max(min(a.task_count[0], programs), 0);
-  if (a.fast_slots > 0 && programs <= NT) {
-    const int len = static_cast<int>(threadIdx.x) < programs ? nsplit[threadIdx.x] : 0;
-    const int r = device_unit_two<NT>(a, u, slots, count, total, len, mine, out);
-    if (r >= 0) return r > 0;
-  }
   const int st = device_split_tokens(total, count, a.L.kv_heads, -a.split_tokens, true);
-  out.fast = -1;
   // Exclusive scan of the split counts, NT task rows at a time (inactive rows: 0 units).
   int carry = 0;
   for (int c0 = 0; c0 < programs; c0 += NT) {
@@ -366,22 +209,12 @@ __device__ bool device_unit(const AttnArgs& a, int programs, int u, int slots, i
       s_found[0] = i;
       s_found[1] = u - base;
       s_found[2] = ns;
-      if (i == mine_task) {
-        s_found[3] = mine.req;
-        s_found[4] = mine.qoff;
-        s_found[5] = mine.qstart;
-        s_found[6] = mine.qlen;
-        s_found[7] = mine.prefix;
-        s_found[8] = mine.sink_len;
-      } else {
-        s_found[3] = -1;  // the row is read again below
-      }
     }
     carry += chunk;
     __syncthreads();  // s_carry is read before the next chunk writes it
   }
   const int task = s_found[0];
-  if (task >= 0 && s_found[3] < 0 && static_cast<int>(threadIdx.x) == 0) {
+  if (task >= 0 && static_cast<int>(threadIdx.x) == 0) {
     Task t;
     read_task(a, t, task);  // the owner's row, again (the loads hit the L2)
     s_found[3] = t.req;
@@ -435,31 +268,6 @@ __device__ __forceinline__ void history_positions(const AttnArgs& a, const Task&
   p_hi = cut(end);
 }
 
-// Positions [p_lo, p_hi) of unit `du.split` of the two-length device rule: units below
-// du.fast split the first du.fast_span history tokens evenly, the others the rest; inner
-// boundaries move down to the 64-token chunk grid of absolute positions (as
-// history_positions' token-bounded rule).
-__device__ __forceinline__ void unit_positions(const AttnArgs& a, const Task& t, int length,
-                                               const DeviceUnit& du, int& p_lo, int& p_hi) {
-  const int lo = t.sink_len, hi = t.sink_len + max(length, 0);
-  auto cut = [&](int h) {
-    if (h <= 0) return lo;
-    if (h >= length) return hi;
-    return max(lo, (lo + h) & ~63);
-  };
-  auto start = [&](int k) {
-    if (k <= 0) return 0;
-    if (k >= du.nsplit) return length;
-    if (k <= du.fast)  // even over the fast span
-      return static_cast<int>(static_cast<int64_t>(du.fast_span) * k / max(du.fast, 1));
-    const int slow = du.nsplit - du.fast;
-    return du.fast_span + static_cast<int>(static_cast<int64_t>(length - du.fast_span) *
-                                           (k - du.fast) / slow);
-  };
-  p_lo = cut(start(du.split));
-  p_hi = cut(start(du.split + 1));
-}
-
 struct RowInfo {
   bool valid;
   int qi, qhead;
@@ -510,10 +318,6 @@ __device__ __forceinline__ void write_unused_splits(const AttnArgs& a, const Tas
     if (ri.valid) a.lse[(ri.token * a.hq + ri.qhead) * a.splits + split] = -INFINITY;
   }
 }
-
-// Fast unit slots per kv head of the paired kernel's two-length device rule: the device's
-// CU count over the kv heads (0 if it cannot be read: one length).
-int32_t device_fast_slots(int heads);
 
 // INT2 history branch (history.hip); rows = query rows per task (<= 32).
 // `queue`: two zeroed int32 counters for the work-queue form of the 17-32-row kernel

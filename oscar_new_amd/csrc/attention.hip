@@ -101,14 +101,6 @@ int make_attn_args(const void* query, int64_t q_s0, int64_t q_s1, int64_t q_s2, 
   return OSCAR_OK;
 }
 
-int32_t device_fast_slots(int heads) {
-  int device = 0, cus = 0;
-  if (hipGetDevice(&device) != hipSuccess ||
-      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess)
-    return 0;  // one unit length
-  return heads > 0 ? cus / heads : 0;
-}
-
 }  // namespace oscar
 
 extern "C" int oscar_attention_partials(
@@ -141,7 +133,6 @@ extern "C" int oscar_attention_partials(
   const dim3 grid(static_cast<unsigned>(programs), static_cast<unsigned>(a.L.kv_heads),
                   static_cast<unsigned>(z));
   hipStream_t s = as_stream(stream);
-  if (!raw && qrows <= 8 && split_tokens < 0) a.fast_slots = device_fast_slots(a.L.kv_heads);
   if (!raw)
     return static_cast<int>(launch_history(a, grid, static_cast<int>(qrows), s, queue_counters));
   if (qrows <= 16)

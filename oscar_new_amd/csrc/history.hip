@@ -1177,7 +1177,6 @@ __device__ __forceinline__ void history_pair_body(const AttnArgs& a, const Finis
   Task t;
   const int head = blockIdx.y;
   int split = static_cast<int>(blockIdx.z) - role_slices, nsplit, st = a.split_tokens;
-  int unit_fast = -1, unit_fast_span = 0;  // two-length device rule (unit_positions)
   if (!kFinish && a.split_tokens < 0) {
     // Device rule: this workgroup slot computes unit u of the step's (task, split) units
     // (task-major, the split length derived from the step's lengths); slots past the last
@@ -1185,16 +1184,13 @@ __device__ __forceinline__ void history_pair_body(const AttnArgs& a, const Finis
     // (LSE -inf) for the split merges. The ring is free until the first DMA.
     DeviceUnit du;
     const int u = split * static_cast<int>(gridDim.x) + static_cast<int>(blockIdx.x);
-    const int slots = static_cast<int>(gridDim.x) * (static_cast<int>(gridDim.z) - role_slices);
-    if (!device_unit<kThreads>(a, static_cast<int>(gridDim.x), u, slots,
+    if (!device_unit<kThreads>(a, static_cast<int>(gridDim.x), u,
                                reinterpret_cast<int*>(s_ring), du))
       return;
     t = du.t;
     split = du.split;
     nsplit = du.nsplit;
     st = du.split_tokens;
-    unit_fast = du.fast;
-    unit_fast_span = du.fast_span;
     if (split == nsplit - 1) write_unused_splits<kThreads>(a, t, head, nsplit, a.splits);
   } else {
     if (!read_task(a, t, blockIdx.x)) return;
@@ -1206,16 +1202,7 @@ __device__ __forceinline__ void history_pair_body(const AttnArgs& a, const Finis
   }
   const int length = t.recent_begin - t.sink_len;
   int p_lo, p_hi;
-  if (unit_fast >= 0) {
-    DeviceUnit du;
-    du.split = split;
-    du.nsplit = nsplit;
-    du.fast = unit_fast;
-    du.fast_span = unit_fast_span;
-    unit_positions(a, t, length, du, p_lo, p_hi);
-  } else {
-    history_positions(a, t, length, nsplit, split, st, p_lo, p_hi);
-  }
+  history_positions(a, t, length, nsplit, split, st, p_lo, p_hi);
   const int lane = threadIdx.x & 63;
   const int wave = uniform(threadIdx.x >> 6);
   const int n = lane & 15, g = lane >> 4;

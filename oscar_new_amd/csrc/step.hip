@@ -275,7 +275,6 @@ int history_pre_common(
   if (split_tokens < 0 && programs > kDeviceUnitTasks) return OSCAR_E_UNSUPPORTED;
   const dim3 grid(static_cast<unsigned>(programs), static_cast<unsigned>(a.L.kv_heads),
                   static_cast<unsigned>(hist_slices + role_slices));
-  if (split_tokens < 0) a.fast_slots = device_fast_slots(a.L.kv_heads);
   return static_cast<int>(
       launch_history_pre(a, p, role_slices, grid, rotate_query, as_stream(stream)));
 }

@@ -225,37 +225,3 @@ def test_device_rule_units_fit_the_budget(seed):
     t = device_split_tokens(int(lengths.sum()), tasks, heads, budget)
     units = sum(max(1, -(-int(l) // t)) for l in lengths)
     assert units <= max(-(-budget // heads), tasks + 1)
-
-
-@pytest.mark.parametrize("lengths,budget,fast,splits,slots", [
-    ([32636] * 32, 464, 256, 16, 480),           # c3: fast tasks, one straddling, slow tasks
-    ([262012] * 4, 500, 256, 128, 512),          # c5: the slow tasks capped at `splits`
-    ([5, 0, 900, 70000, 31000, 1200] * 7, 300, 128, 32, 320),  # ragged, empty rows
-    ([4000] * 3, 512, 256, 16, 516),             # every task on fast slots
-])
-def test_two_length_device_units_cover_every_token_once(lengths, budget, fast, splits, slots):
-    from oscar_new_amd.config import device_units_two
-
-    units = device_units_two(lengths, 1, budget, fast, splits, slots)
-    assert units is not None
-    nxt = 0
-    for length, (base, ranges) in zip(lengths, units):
-        assert base == nxt and 1 <= len(ranges) <= splits
-        nxt = base + len(ranges)
-        pos = 0
-        for lo, hi in ranges:
-            assert lo == pos and lo <= hi
-            pos = hi
-        assert pos == max(length, 0)
-    assert nxt <= slots
-    # Units on fast slots are about FAST_UNIT_64 / 64 times as long as the others.
-    fast_len = [hi - lo for base, rs in units for k, (lo, hi) in enumerate(rs) if base + k < fast]
-    slow_len = [hi - lo for base, rs in units for k, (lo, hi) in enumerate(rs) if base + k >= fast]
-    if lengths[0] == 32636:
-        assert 1.25 < (sum(fast_len) / len(fast_len)) / (sum(slow_len) / len(slow_len)) < 1.45
-
-
-def test_two_length_device_units_refuse_an_overfull_grid():
-    from oscar_new_amd.config import device_units_two
-
-    assert device_units_two([32636] * 32, 1, 464, 256, 16, 400) is None
