@@ -172,10 +172,18 @@ __device__ bool device_unit(const AttnArgs& a, int programs, int u, int* scratch
   __shared__ int s_found[9];
   const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
   int64_t s = 0;
+  // The row of this thread's last task stays in registers: with at most NT task rows, the
+  // thread that finds the unit's task has its row already (no second round of loads).
+  Task mine{};
+  int mine_task = -1;
   for (int i = threadIdx.x; i < programs; i += NT) {
-    const int len = task_history(a, i);
+    Task t;
+    const bool live = read_task(a, t, i);
+    const int len = live ? max(t.recent_begin - t.sink_len, 0) : 0;
     nsplit[i] = len;
     s += len;
+    mine = t;
+    mine_task = live ? i : -1;
   }
   s = wave_sum_i64(s);
   if (lane == 0) s_total[wave] = s;
@@ -209,12 +217,22 @@ __device__ bool device_unit(const AttnArgs& a, int programs, int u, int* scratch
       s_found[0] = i;
       s_found[1] = u - base;
       s_found[2] = ns;
+      if (i == mine_task) {
+        s_found[3] = mine.req;
+        s_found[4] = mine.qoff;
+        s_found[5] = mine.qstart;
+        s_found[6] = mine.qlen;
+        s_found[7] = mine.prefix;
+        s_found[8] = mine.sink_len;
+      } else {
+        s_found[3] = -1;  // the row is read again below
+      }
     }
     carry += chunk;
     __syncthreads();  // s_carry is read before the next chunk writes it
   }
   const int task = s_found[0];
-  if (task >= 0 && static_cast<int>(threadIdx.x) == 0) {
+  if (task >= 0 && s_found[3] < 0 && static_cast<int>(threadIdx.x) == 0) {
     Task t;
     read_task(a, t, task);  // the owner's row, again (the loads hit the L2)
     s_found[3] = t.req;
