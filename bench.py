@@ -45,6 +45,11 @@ CONFIGS = {
     # --mode prefill only (initial prefill, no cached tokens): every token is a query token.
     "p1": dict(batch=4, context=4096, qlen=4096, ragged=False, splits="reference",
                desc="initial prefill: B4 x 4096 tokens, GQA 6:1, D256, causal"),
+    # --mode prefill: a continuation chunk over a cached prefix (one history split, the long
+    # chunk rule of config.py:86-87); the history branch is MFMA-bound.
+    "p2": dict(batch=1, context=32768 + 2048, qlen=2048, ragged=False, splits="device",
+               desc="continuation chunk: 2048 query tokens over 32768 cached tokens, GQA 6:1, "
+                    "D256, one history split"),
 }
 
 
@@ -536,7 +541,8 @@ def prefill_measurement(args, w, device):
 
     ntok = w.q.shape[0]
     if any(p != 0 for p in w.prefixes):
-        raise SystemExit("bench.py --mode prefill needs a config whose requests have no prefix")
+        print(json.dumps(continuation_measurement(args, w, device)))
+        return 0
     w.meta.initial_prefill = True
     _, win = w.layout.tensor_views((w.k_cache, w.v_cache))
     out = torch.empty(ntok, 6 * 256, dtype=torch.bfloat16, device=device)
@@ -560,6 +566,61 @@ def prefill_measurement(args, w, device):
                       "mfma_bf16_peak_tflops": 2500.0,
                       "frac": flops / (us * 1e-6) / 1e12 / 2500.0}))
     return 0
+
+
+def continuation_flops(w):
+    """MFMA work of a continuation step: per request, the history branch (every query row
+    against the request's INT2 history tokens) and the BF16 branch (the sink and recent
+    window, then the chunk's own tokens causally). Useful flops count 4 per (query row, key,
+    dim): QK and PV products. The history kernel issues 6: its QK runs the query as two FP8
+    terms (hi + lo) against the FP4 codes."""
+    cfg = w.cfg
+    hist_pairs = bf16_pairs = 0
+    for prefix, hist in zip(w.prefixes, history_lengths(w)):
+        sink = min(cfg.sink_tokens, prefix)
+        window = sink + (prefix - max(sink, prefix - cfg.recent_tokens))
+        hist_pairs += w.qlen * hist
+        bf16_pairs += w.qlen * window + w.qlen * (w.qlen + 1) // 2
+    per_pair = 6 * 256  # query heads x head dim
+    return SimpleNamespace(history_useful=4.0 * hist_pairs * per_pair,
+                           history_issued=6.0 * hist_pairs * per_pair,
+                           bf16=4.0 * bf16_pairs * per_pair)
+
+
+def continuation_measurement(args, w, device):
+    """A continuation chunk (config p2): the layer step as ``impl.forward`` runs it (eager
+    launches: a 2048-token step is far above launch overheads), and its history branch alone,
+    timed with HIP events. The history branch is MFMA-bound: its issued FP8 x FP4 work over
+    the launch time against the FP8 dense peak (5.0 PFLOP/s, the rate of
+    v_mfma_scale_f32_16x16x128_f8f6f4 with an FP8 operand)."""
+    import torch
+
+    from oscar_new_amd.backend import OscarAttentionImpl
+
+    cfg = CONFIGS[args.config]
+    impl = OscarAttentionImpl.standalone(6, 256, 1 / 16, 1, w.cfg,
+                                         split_policy=args.split_policy or cfg["splits"])
+    impl.set_rotations(w.rk, w.rv)
+    ntok = w.q.shape[0]
+    layers = [(w.k_cache, w.v_cache)]
+    out = torch.empty(ntok, 6 * 256, dtype=torch.bfloat16, device=device)
+    splits, split_tokens = impl.partition_for(w.meta, ntok)
+    step_us = time_launch(lambda i: impl.forward(None, w.q, w.k, w.v, layers[0], w.meta, out),
+                          1, args.steps, False)
+    bname, _, bfn = branch_launch(impl, w, layers, splits, split_tokens)
+    b_us = time_launch(bfn, 1, args.steps, False)
+    fl = continuation_flops(w)
+    hist_tf = fl.history_issued / (b_us * 1e-6) / 1e12
+    return {"mode": "prefill", "config": args.config, "workload": f"{args.config}: {cfg['desc']}",
+            "tokens": ntok, "cached_tokens": sum(w.prefixes), "splits": splits,
+            "split_tokens": split_tokens, "us_per_layer_step": step_us,
+            "step_useful_tflops": (fl.history_useful + fl.bf16) / (step_us * 1e-6) / 1e12,
+            "history_branch": {
+                "kernel": bname, "us": b_us, "issued_flops": fl.history_issued,
+                "useful_flops": fl.history_useful, "tflops_issued": hist_tf,
+                "tflops_useful": fl.history_useful / (b_us * 1e-6) / 1e12,
+                "peak_tflops": 5000.0, "frac": hist_tf / 5000.0, "bound": "mfma (fp8 x fp4)"},
+            "bf16_branch_flops": fl.bf16}
 
 
 def in_step_launch(impl, w, layers, splits, split_tokens):

@@ -219,7 +219,9 @@ int oscar_unpack(const void* history, int64_t history_bytes, const int64_t* slot
  * aligned (row strides in elements, multiples of 8). qrot == NULL leaves the q rotation out
  * (the caller rotates q itself, e.g. with oscar_rotate on another stream, so that the history
  * launch can start while this one runs: the history branch never reads the slots written
- * here).
+ * here). raw_partials and raw_lse both NULL leaves the BF16 branch out (the caller runs it
+ * with oscar_chunk_raw_attention, as for long continuation chunks); one of them NULL is
+ * OSCAR_E_NULL.
  */
 int oscar_pre_attention(const void* query, int64_t q_s0, int64_t q_s1, const void* key,
                         int64_t k_s0, int64_t k_s1, const void* value, int64_t v_s0, int64_t v_s1,
@@ -256,7 +258,7 @@ int oscar_post_attention(const float* history_partials, const float* history_lse
  * prefill_attention -- initial prefill (every request's history empty): replaces the
  * reference's fused-infer call (oscar_ascend/backend.py:175-193: causal attention of each
  * request over its own current tokens, output rows past num_actual_tokens zeroed). A flash
- * kernel: 128 (query, head) rows per workgroup share each 32-token K/V block through LDS. Each
+ * kernel: 192 (query, head) rows per workgroup share each 32-token K/V block through LDS. Each
  * row has the bits the BF16 branch of oscar_attention_partials (raw, one split) followed by
  * merge_splits + rotate + merge_paths gives a row whose history branch is empty; output: bf16
  * [n, hq*256] (16-byte aligned), merged_lse (optional): fp32 [n, hq]. query: bf16 [n][hq][256],
@@ -272,6 +274,30 @@ int oscar_prefill_attention(const void* query, int64_t q_s0, int64_t q_s1, const
                             const int32_t* counts, int64_t n, int64_t hq, int64_t max_reqs,
                             int32_t max_query_len, float scale, const oscar_layout* layout,
                             void* output, float* merged_lse, void* stream);
+
+/*
+ * chunk_raw_attention -- the BF16 branch of kernels.py:439-482 (`attention_partials(..., 1,
+ * raw=True)`, oscar_ascend/kernels.py: each query row over the sink and recent rows of the
+ * request's window page, then its chunk's current tokens causally) as the flash kernel of
+ * oscar_prefill_attention, for continuation chunks of many query tokens: the rows of 32
+ * consecutive query tokens of a request share each 32-key block through LDS. Writes
+ * raw_partials fp32 [n, hq, 1, 256] (16-byte aligned) and raw_lse [n, hq, 1] with the bits of
+ * oscar_attention_partials (raw != 0, one split); rows of tokens at or past counts[1] are not
+ * written. Arguments as for oscar_pre_attention (window, block table and layout locate each
+ * request's window page; max_query_len: host bound on query tokens per request, 0 = n). A
+ * request with fewer tokens than query tokens gets NaN rows. A window page that does not lie
+ * wholly inside the window buffer contributes no rows (the decode path drops such rows one by
+ * one; the two agree whenever the buffer holds whole pages).
+ */
+int oscar_chunk_raw_attention(const void* query, int64_t q_s0, int64_t q_s1, const void* key,
+                              int64_t k_s0, int64_t k_s1, const void* value, int64_t v_s0,
+                              int64_t v_s1, const void* window, int64_t window_elems,
+                              const int32_t* qstarts, const int32_t* seq_lens,
+                              const int32_t* block_tables, int64_t table_stride,
+                              int64_t table_columns, const int32_t* counts, int64_t n, int64_t hq,
+                              int64_t max_reqs, int32_t max_query_len, float scale,
+                              const oscar_layout* layout, float* raw_partials, float* raw_lse,
+                              void* stream);
 
 /*
  * history_pre -- the history branch (oscar_attention_partials with raw = 0) and the BF16 branch

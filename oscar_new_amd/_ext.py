@@ -97,6 +97,13 @@ SIGNATURES = {
         _I64, _I64, _I64, _I32, _F,  # n, hq, max_reqs, max_query_len, scale
         POINTER(OscarLayout), _P, _P, _P,  # layout, output, merged_lse, stream
     ],
+    "oscar_chunk_raw_attention": [
+        _P, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64,  # query, key, value (+ row strides)
+        _P, _I64,  # window, elements
+        _P, _P, _P, _I64, _I64, _P,  # qstarts, seq_lens, block_tables, stride, columns, counts
+        _I64, _I64, _I64, _I32, _F,  # n, hq, max_reqs, max_query_len, scale
+        POINTER(OscarLayout), _P, _P, _P,  # layout, raw_partials, raw_lse, stream
+    ],
     "oscar_history_post": [
         _P, _I64, _I64, _I64,  # query (rotated)
         _P, _I64,  # history, bytes

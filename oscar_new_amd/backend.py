@@ -371,8 +371,10 @@ class OscarAttentionImpl:
             kernels.post_attention(hp, hl, rp, rl, self.rv, k, v, self.window, meta, layout,
                                    rows, lse)
             return
+        # A long chunk's BF16 branch runs as the chunk flash launch (same bits).
         qrot, rp, rl = kernels.pre_attention(q, k, v, self.history, self.window, meta, layout,
-                                             self.scale, self.rk_t, self.rv_t)
+                                             self.scale, self.rk_t, self.rv_t,
+                                             raw=not kernels.chunk_raw_preferred(meta))
         if self.one_launch_post and kernels.history_post_supported(
                 meta, layout, self.num_heads, splits, q.shape[0]):
             kernels.history_post(qrot, self.history, meta, layout, self.scale, splits, rp, rl,

@@ -65,7 +65,61 @@ struct PrefillArgs {
   float scale_log2;
   uint16_t* out;
   float* lse;
+  // Continuation chunks (the chunk form): each request's sink and recent rows come from its
+  // window page (block-table column 0's page), and the rows are written as fp32 partials.
+  Layout L;
+  const uint16_t* window;
+  int64_t window_elems;
+  const int32_t* table;
+  int64_t table_stride, table_columns;
+  float* partials;  // [n][hq][256]
+  float* plse;      // [n][hq]
 };
+
+// The BF16 branch's raw index sequence of one request and KV head in the chunk form
+// (raw.h raw_row): indices [0, sink_len) are the sink positions, [sink_len, high) the recent
+// positions recent_begin.., then the current tokens prefix... `win`: element offset of the
+// head's K row at window index 0 in the owner page, or -1 when the page does not lie wholly in
+// the window buffer (the window rows are then masked; the decode path masks row by row, and
+// the two agree whenever the buffer holds whole pages, as the layout's views do).
+struct ChunkRows {
+  int prefix, sink_len, recent_begin, high;
+  int64_t win;
+};
+
+__device__ __forceinline__ ChunkRows chunk_rows(const PrefillArgs& a, int req, int seq, int qlen,
+                                                int head) {
+  ChunkRows c;
+  c.prefix = seq - qlen;
+  c.sink_len = min(a.L.sink, c.prefix);
+  c.recent_begin = max(c.sink_len, c.prefix - a.L.recent);
+  c.high = c.sink_len + c.prefix - c.recent_begin;
+  c.win = -1;
+  const int first = a.table_columns > 0 ? a.table[static_cast<int64_t>(req) * a.table_stride] : -1;
+  if (first >= 0) {
+    const int64_t owner = fastdiv(static_cast<uint32_t>(first), a.L.bpp_div);
+    const int64_t win = owner * (a.L.page_bytes / 2) + static_cast<int64_t>(head) * kHeadDim;
+    // Last row read: V of window index sink + ring - 1.
+    const int64_t last = win + (static_cast<int64_t>(a.L.sink + a.L.ring - 1) * 2 + 1) *
+                                   a.L.kv_heads * kHeadDim + kHeadDim;
+    if (last <= a.window_elems) c.win = win;
+  }
+  return c;
+}
+
+// K (kv 0) or V row of raw index ns (0 <= ns < high + qlen): a window row or a current token;
+// a masked window row (no window page) reads the request's first current token instead.
+__device__ __forceinline__ const uint16_t* chunk_row(const PrefillArgs& a, const ChunkRows& c,
+                                                     int64_t qstart, int head, int ns, int kv) {
+  if (ns >= c.high || c.win < 0) {
+    const int64_t ci = qstart + max(ns - c.high, 0);
+    return kv ? a.value + ci * a.vs0 + head * a.vs1 : a.key + ci * a.ks0 + head * a.ks1;
+  }
+  const int pos = ns < c.sink_len ? ns : c.recent_begin + ns - c.sink_len;
+  const int lap = static_cast<int>(fastdiv(static_cast<uint32_t>(pos), a.L.ring_div));
+  const int wi = pos < a.L.sink ? pos : a.L.sink + pos - lap * a.L.ring;
+  return a.window + c.win + (static_cast<int64_t>(wi) * 2 + kv) * a.L.kv_heads * kHeadDim;
+}
 
 // Copies block b of (K, V) rows into `stage`: wavefront w < 8 issues DMAs 4 w .. 4 w + 3, DMA i
 // covering K (i < 16) or V rows 2 (i mod 16), + 1. Lane l writes row t = 2 (i mod 16) + l / 32
@@ -97,6 +151,30 @@ __device__ __forceinline__ void prefill_copy_block(const uint8_t* kb, const uint
   }
 }
 
+// The chunk form of prefill_copy_block: block b of the raw index sequence (rows at or past
+// `end` copy raw index end - 1, a current token; they are masked for every query row), each
+// lane's row from its own address (window page or current tokens).
+__device__ __forceinline__ void chunk_copy_block(const PrefillArgs& a, const ChunkRows& c,
+                                                 int64_t qstart, int head, int end, int b,
+                                                 uint8_t* stage) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  if (wave >= kCopyWavesP) return;
+#pragma unroll
+  for (int k = 0; k < kDmaPerWave; ++k) {
+    const int i = kDmaPerWave * wave + k;  // is_v = i >> 4 is wave-uniform
+    const int t = 2 * (i & 15) + (lane >> 5);
+    const int ns = min(kBlock * b + t, end - 1);
+    const uint8_t* row = reinterpret_cast<const uint8_t*>(chunk_row(a, c, qstart, head, ns, i >> 4));
+    const uint32_t lds = lds_addr(stage + (i >> 4) * kBlockBytes + (i & 15) * 1024);
+    dma_dwordx4(row + 16u * chunk_pos(t, lane & 31), lds);
+  }
+}
+
+// kChunk false: initial prefill (bf16 output rows and LSE; requests with cached tokens get
+// NaN rows). kChunk true: the BF16 branch of continuation chunks (sink, recent and causal
+// current keys; fp32 partial rows and LSE, as attention_partials raw with one split), with
+// the same row arithmetic.
+template <bool kChunk>
 __global__ __launch_bounds__(kThreadsP) void prefill_flash_kernel(const PrefillArgs a) {
   __shared__ __attribute__((aligned(16))) uint8_t s_kv[kStagesP][kStageBytesP];
   __shared__ __attribute__((aligned(16))) uint8_t s_pair[2][kPairBytes];
@@ -112,7 +190,18 @@ __global__ __launch_bounds__(kThreadsP) void prefill_flash_kernel(const PrefillA
   const int row0 = span * kSpanRows;
   if (row0 >= rows_req) return;
   const int row_end = min(row0 + kSpanRows, rows_req);
-  const bool history = a.seq_lens[req] != qlen;  // not an initial prefill: rows are NaN
+  const int seq = a.seq_lens[req];
+  // Initial prefill: a request with cached tokens is not one; chunk form: a request with
+  // fewer tokens than query tokens is malformed. Their rows are NaN.
+  const bool history = kChunk ? seq < qlen : seq != qlen;
+  ChunkRows c{};
+  if constexpr (kChunk) {
+    if (!history) c = chunk_rows(a, req, seq, qlen, head);
+  }
+  const int high = kChunk ? c.high : 0;  // raw index of the first current token
+  const int end = high + qlen;           // raw indices of the request
+  // Raw indices below this are window rows without a window page (masked).
+  const int masked_below = kChunk && c.win < 0 ? high : 0;
   // Rows past the grid's spans (a request with more query tokens than the caller's
   // max_query_len) are written as NaN by the last span's workgroup, like the rows of a
   // request with cached tokens, so that a wrong bound shows in the output.
@@ -123,13 +212,20 @@ __global__ __launch_bounds__(kThreadsP) void prefill_flash_kernel(const PrefillA
       const int qi = static_cast<int>(fastdiv(static_cast<uint32_t>(row), a.g_div));
       const int qhead = head * a.g + (row - qi * a.g);
       const int64_t orow = (qstart + qi) * a.hq + qhead;
-      *reinterpret_cast<u32x4*>(a.out + orow * kHeadDim + 8 * (threadIdx.x & 31)) =
-          u32x4{0x7fc07fc0u, 0x7fc07fc0u, 0x7fc07fc0u, 0x7fc07fc0u};
-      if (a.lse && (threadIdx.x & 31) == 0) a.lse[orow] = NAN;
+      if constexpr (kChunk) {
+        float* dst = a.partials + orow * kHeadDim + 8 * (threadIdx.x & 31);
+        *reinterpret_cast<float4*>(dst) = make_float4(NAN, NAN, NAN, NAN);
+        *reinterpret_cast<float4*>(dst + 4) = make_float4(NAN, NAN, NAN, NAN);
+        if ((threadIdx.x & 31) == 0) a.plse[orow] = NAN;
+      } else {
+        *reinterpret_cast<u32x4*>(a.out + orow * kHeadDim + 8 * (threadIdx.x & 31)) =
+            u32x4{0x7fc07fc0u, 0x7fc07fc0u, 0x7fc07fc0u, 0x7fc07fc0u};
+        if (a.lse && (threadIdx.x & 31) == 0) a.lse[orow] = NAN;
+      }
     }
   }
   const int q_last = static_cast<int>(fastdiv(static_cast<uint32_t>(row_end - 1), a.g_div));
-  const int nblk = history ? 0 : q_last / kBlock + 1;
+  const int nblk = history ? 0 : (q_last + high) / kBlock + 1;
   const int lane = threadIdx.x & 63;
   const int wave = uniform(threadIdx.x >> 6);
   const int n = lane & 15, g = lane >> 4;
@@ -137,8 +233,14 @@ __global__ __launch_bounds__(kThreadsP) void prefill_flash_kernel(const PrefillA
   const uint8_t* kb = reinterpret_cast<const uint8_t*>(a.key + qstart * a.ks0 + head * a.ks1);
   const uint8_t* vb = reinterpret_cast<const uint8_t*>(a.value + qstart * a.vs0 + head * a.vs1);
   const uint32_t kstride = static_cast<uint32_t>(a.ks0 * 2), vstride = static_cast<uint32_t>(a.vs0 * 2);
+  auto copy_block = [&](int b, uint8_t* stage) {
+    if constexpr (kChunk)
+      chunk_copy_block(a, c, qstart, head, end, b, stage);
+    else
+      prefill_copy_block(kb, vb, kstride, vstride, qlen, b, stage);
+  };
   for (int b = 0; b < kAheadP && b < nblk; ++b)  // block b + kAheadP: iteration b
-    prefill_copy_block(kb, vb, kstride, vstride, qlen, b, s_kv[b]);
+    copy_block(b, s_kv[b]);
 
   // Query rows of this wavefront's tile: row16 = row0 + 16 w + n.
   u32x4 qb[kPrefillRT][8];
@@ -159,11 +261,14 @@ __global__ __launch_bounds__(kThreadsP) void prefill_flash_kernel(const PrefillA
   }
   State<kPrefillRT, 16> st;
   state_init(st);
-  // Blocks whose every key is below this wavefront's first query and the request's end need
-  // no mask.
+  // Blocks whose every key (raw index) is at or below this wavefront's first query's last
+  // key and the request's end, and at or above masked_below, need no mask.
   const int qi_first = static_cast<int>(
       fastdiv(static_cast<uint32_t>(row0 + 16 * kPrefillRT * wave), a.g_div));
-  const int full_below = min(qi_first, qlen - 1);  // last key every row of the wave sees
+  const int full_below = min(qi_first + high, end - 1);  // last key every row of the wave sees
+  int key_lim[kPrefillRT];  // last raw index row rt sees (-1: a row past the span's end)
+#pragma unroll
+  for (int rt = 0; rt < kPrefillRT; ++rt) key_lim[rt] = qi_row[rt] < 0 ? -1 : qi_row[rt] + high;
   // Per-lane LDS offsets of the K operands within a stage: rows 16 tt + n, chunk 8 g + m.
   uint32_t koff[2][8];
 #pragma unroll
@@ -228,9 +333,7 @@ __global__ __launch_bounds__(kThreadsP) void prefill_flash_kernel(const PrefillA
     else
       OSCAR_WAIT_VM(0);
     barrier_lds();  // block b landed, pairs of block b - 1 written
-    if (b + kAheadP < nblk)
-      prefill_copy_block(kb, vb, kstride, vstride, qlen, b + kAheadP,
-                         s_kv[(b + kAheadP) % kStagesP]);
+    if (b + kAheadP < nblk) copy_block(b + kAheadP, s_kv[(b + kAheadP) % kStagesP]);
     // P*V of block b - 1 (the accumulators take it before block b's lazy max may rescale
     // them, the order of the one-block-at-a-time stream) interleaved with block b's scores
     // S^T = K Q^T (A = K rows 16 tt + n, chunk 8 g + m): two P*V tiles per score k-step.
@@ -255,7 +358,7 @@ __global__ __launch_bounds__(kThreadsP) void prefill_flash_kernel(const PrefillA
       }
     }
     float s2[kPrefillRT][8];
-    if (kBlock * b + kBlock - 1 <= full_below) {
+    if (kBlock * b >= masked_below && kBlock * b + kBlock - 1 <= full_below) {
       block_scores_full(sc, a.scale_log2, s2);
     } else {
       bool ok[kPrefillRT][8];
@@ -264,7 +367,7 @@ __global__ __launch_bounds__(kThreadsP) void prefill_flash_kernel(const PrefillA
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
           const int key = kBlock * b + tau(g, e);
-          ok[rt][e] = key < qlen && key <= qi_row[rt];
+          ok[rt][e] = key < end && key <= key_lim[rt] && key >= masked_below;
         }
       block_scores(sc, ok, a.scale_log2, s2);
     }
@@ -290,6 +393,19 @@ __global__ __launch_bounds__(kThreadsP) void prefill_flash_kernel(const PrefillA
       if (row >= row_end) continue;
       const int qi = static_cast<int>(fastdiv(static_cast<uint32_t>(row), a.g_div));
       const int qhead = head * a.g + (row - qi * a.g);
+      if constexpr (kChunk) {
+        float* dst = a.partials + ((qstart + qi) * a.hq + qhead) * kHeadDim + 16 * n;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const float4 x = history ? make_float4(NAN, NAN, NAN, NAN)
+                                   : make_float4(st.o[rt][4 * k][v] / den,
+                                                 st.o[rt][4 * k + 1][v] / den,
+                                                 st.o[rt][4 * k + 2][v] / den,
+                                                 st.o[rt][4 * k + 3][v] / den);
+          *reinterpret_cast<float4*>(dst + 4 * k) = x;
+        }
+        continue;
+      }
       uint32_t w[8];
 #pragma unroll
       for (int k = 0; k < 8; ++k)
@@ -299,12 +415,13 @@ __global__ __launch_bounds__(kThreadsP) void prefill_flash_kernel(const PrefillA
       *reinterpret_cast<u32x4*>(dst) = u32x4{w[0], w[1], w[2], w[3]};
       *reinterpret_cast<u32x4*>(dst + 8) = u32x4{w[4], w[5], w[6], w[7]};
     }
-    if (g == 0 && a.lse) {
+    float* lse_out = kChunk ? a.plse : a.lse;
+    if (g == 0 && lse_out) {
       const int row = tile_row + n;
       if (row < row_end) {
         const int qi = static_cast<int>(fastdiv(static_cast<uint32_t>(row), a.g_div));
         const int qhead = head * a.g + (row - qi * a.g);
-        a.lse[(qstart + qi) * a.hq + qhead] = history ? NAN : row_lse(st.m[rt], den_n);
+        lse_out[(qstart + qi) * a.hq + qhead] = history ? NAN : row_lse(st.m[rt], den_n);
       }
     }
   }
@@ -381,7 +498,7 @@ extern "C" int oscar_prefill_attention(
   // Requests vary fastest: the workgroups of the longest spans of every request dispatch
   // first (a longest-first order of the whole batch), and consecutive workgroups, which the
   // dispatcher spreads over the XCDs, keep each XCD on few requests (their K/V stay in its L2).
-  hipLaunchKernelGGL(prefill_flash_kernel,
+  hipLaunchKernelGGL(prefill_flash_kernel<false>,
                      dim3(static_cast<unsigned>(max_reqs), static_cast<unsigned>(spans),
                           static_cast<unsigned>(h)),
                      dim3(kThreadsP), 0, s, a);
@@ -389,5 +506,65 @@ extern "C" int oscar_prefill_attention(
   hipLaunchKernelGGL(prefill_clear_kernel,
                      dim3(static_cast<unsigned>(clear < 1024 ? clear : 1024)), dim3(kThreads), 0,
                      s, a);
+  return static_cast<int>(hipGetLastError());
+}
+
+extern "C" int oscar_chunk_raw_attention(
+    const void* query, int64_t q_s0, int64_t q_s1, const void* key, int64_t k_s0, int64_t k_s1,
+    const void* value, int64_t v_s0, int64_t v_s1, const void* window, int64_t window_elems,
+    const int32_t* qstarts, const int32_t* seq_lens, const int32_t* block_tables,
+    int64_t table_stride, int64_t table_columns, const int32_t* counts, int64_t n, int64_t hq,
+    int64_t max_reqs, int32_t max_query_len, float scale, const oscar_layout* layout,
+    float* raw_partials, float* raw_lse, void* stream) {
+  using namespace oscar;
+  PrefillArgs a{};
+  const int st = make_layout(layout, &a.L);
+  if (st != OSCAR_OK) return st;
+  const int64_t h = a.L.kv_heads;
+  if (n < 0 || hq <= 0 || hq % h || max_reqs < 1 || max_reqs > 65535 || max_query_len < 0 ||
+      table_columns < 0 || window_elems < 0 || n * hq > 0x7fffffffll)
+    return OSCAR_E_SHAPE;
+  if (!(scale > 0.f) || !(scale < INFINITY)) return OSCAR_E_UNSUPPORTED;
+  if (n == 0) return OSCAR_OK;
+  if (!query || !key || !value || !window || !qstarts || !seq_lens || !block_tables || !counts ||
+      !raw_partials || !raw_lse)
+    return OSCAR_E_NULL;
+  if (q_s0 % 8 || q_s1 % 8 || k_s0 % 8 || k_s1 % 8 || v_s0 % 8 || v_s1 % 8 || !aligned16(query) ||
+      !aligned16(key) || !aligned16(value) || !aligned16(window) || !aligned16(raw_partials) ||
+      a.L.page_bytes % 16)
+    return OSCAR_E_ALIGN;
+  const int64_t g = hq / h;
+  a.query = static_cast<const uint16_t*>(query);
+  a.qs0 = q_s0;
+  a.qs1 = q_s1;
+  a.key = static_cast<const uint16_t*>(key);
+  a.ks0 = k_s0;
+  a.ks1 = k_s1;
+  a.value = static_cast<const uint16_t*>(value);
+  a.vs0 = v_s0;
+  a.vs1 = v_s1;
+  a.qstarts = qstarts;
+  a.seq_lens = seq_lens;
+  a.counts = counts;
+  a.n = n;
+  a.g = static_cast<int32_t>(g);
+  a.hq = static_cast<int32_t>(hq);
+  a.kv_heads = static_cast<int32_t>(h);
+  a.g_div = make_fastdiv(static_cast<uint32_t>(g));
+  a.scale_log2 = scale * kLog2e;
+  a.window = static_cast<const uint16_t*>(window);
+  a.window_elems = window_elems;
+  a.table = block_tables;
+  a.table_stride = table_stride;
+  a.table_columns = table_columns;
+  a.partials = raw_partials;
+  a.plse = raw_lse;
+  const int64_t qmax = max_query_len > 0 && max_query_len < n ? max_query_len : n;
+  const int64_t spans = (qmax * g + kSpanRows - 1) / kSpanRows;
+  if (spans > 65535) return OSCAR_E_SHAPE;  // grid y
+  hipLaunchKernelGGL(prefill_flash_kernel<true>,
+                     dim3(static_cast<unsigned>(max_reqs), static_cast<unsigned>(spans),
+                          static_cast<unsigned>(h)),
+                     dim3(kThreadsP), 0, as_stream(stream), a);
   return static_cast<int>(hipGetLastError());
 }

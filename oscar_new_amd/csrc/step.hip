@@ -28,6 +28,7 @@ namespace {
 constexpr int kPostQuarterRows = 2;  // rows per column-quarter post-attention workgroup
 constexpr int kPostWideRows = 4;     // rows per all-quarter workgroup (many rows)
 constexpr int64_t kPostWideFrom = 512;  // rows from which a workgroup walks all four quarters
+constexpr int64_t kPostTileFrom = 4096;  // rows from which a workgroup serves 16 rows
 
 template <int RT>
 __global__ __launch_bounds__(kThreads) void pre_attention_kernel(const PreArgs p) {
@@ -79,6 +80,29 @@ __global__ __launch_bounds__(kThreads, 2) void post_attention_kernel(const PostA
   for (int head = 0; head < p.win.L.kv_heads; ++head) store_window_request(p.win, req, head);
 }
 
+// Many rows (a long chunk: thousands of (token, query head) rows, one split): 16 rows per
+// workgroup, a full MFMA tile. Wavefront w merges rows w, w + 4, ... into LDS, then rotates
+// the 16 rows back for its 64 output columns and merges them with the BF16 branch
+// (post_rows_map: the row arithmetic of the other forms, the same bits). A workgroup reads
+// R_v once per 16 rows instead of once per 4, and the launch needs a quarter of the
+// workgroups of the 4-row form, whose rounds of latency set its time at these row counts.
+template <int kMode>
+__global__ __launch_bounds__(kThreads, 2) void post_attention_tile_kernel(const PostArgs p) {
+  __shared__ __attribute__((aligned(16))) uint16_t s_h[16][kHeadDim];
+  __shared__ float s_l[16];
+  __shared__ GroupMergeLds group_lds;
+  if (static_cast<int>(blockIdx.x) < p.merge_wgs) {
+    const int64_t row0 = static_cast<int64_t>(blockIdx.x) * 16;
+    const int64_t rows = p.rows;
+    post_rows_map<16, kMode>(
+        p, [row0, rows](int r) -> int64_t { return row0 + r < rows ? row0 + r : -1; },
+        p.splits, s_h, s_l, &group_lds);
+    return;
+  }
+  const int req = static_cast<int>(blockIdx.x) - p.merge_wgs;
+  for (int head = 0; head < p.win.L.kv_heads; ++head) store_window_request(p.win, req, head);
+}
+
 }  // namespace
 }  // namespace oscar
 
@@ -90,8 +114,9 @@ namespace oscar {
 namespace {
 
 // The checks and fields of one pre-attention launch (all roles; grid sizes in raw_wgs and
-// kv_wgs, the q tiles follow when qrot is set). OSCAR_OK with *p filled and *qrows = query rows
-// per task, or the entry point's error code (OSCAR_OK with nothing filled when n == 0).
+// kv_wgs, the q tiles follow when qrot is set). raw_partials and raw_lse both NULL: no BF16
+// branch role (raw_wgs 0). OSCAR_OK with *p filled and *qrows = query rows per task, or the
+// entry point's error code (OSCAR_OK with nothing filled when n == 0).
 int make_pre_args(const void* query, int64_t q_s0, int64_t q_s1, const void* key, int64_t k_s0,
                   int64_t k_s1, const void* value, int64_t v_s0, int64_t v_s1, const void* window,
                   int64_t window_elems, const int32_t* qstarts, const int32_t* seq_lens,
@@ -119,13 +144,14 @@ int make_pre_args(const void* query, int64_t q_s0, int64_t q_s1, const void* key
   if (qrows > 32) return OSCAR_E_UNSUPPORTED;
   *qrows_out = qrows;
   if (n == 0) return OSCAR_OK;
+  const bool raw = raw_partials || raw_lse;
   if (!query || !key || !value || !window || !qstarts || !seq_lens || !block_tables || !counts ||
-      !tasks || !task_count || !rk_t || !rv_t || !history || !slots || !raw_partials ||
-      !raw_lse)
+      !tasks || !task_count || !rk_t || !rv_t || !history || !slots ||
+      (raw && (!raw_partials || !raw_lse)))
     return OSCAR_E_NULL;
   if (q_s0 % 8 || q_s1 % 8 || k_s0 % 8 || k_s1 % 8 || v_s0 % 8 || v_s1 % 8 || !aligned16(query) ||
       !aligned16(key) || !aligned16(value) || !aligned16(window) || !aligned16(rk_t) ||
-      !aligned16(rv_t) || !aligned16(raw_partials) || (qrot && !aligned16(qrot)) ||
+      !aligned16(rv_t) || (raw && !aligned16(raw_partials)) || (qrot && !aligned16(qrot)) ||
       reinterpret_cast<uintptr_t>(history) % 4)
     return OSCAR_E_ALIGN;
   a.query = static_cast<const uint16_t*>(query);
@@ -172,7 +198,7 @@ int make_pre_args(const void* query, int64_t q_s0, int64_t q_s1, const void* key
   p.v_factor = clip->v_factor;
   p.h_div = make_fastdiv(static_cast<uint32_t>(h));
   p.hq_div = make_fastdiv(static_cast<uint32_t>(hq));
-  p.raw_wgs = static_cast<int32_t>(programs * h);
+  p.raw_wgs = raw ? static_cast<int32_t>(programs * h) : 0;
   p.kv_wgs = static_cast<int32_t>(2 * 4 * ((p.kv_rows + 15) / 16));
   return OSCAR_OK;
 }
@@ -200,6 +226,7 @@ extern "C" int oscar_pre_attention(
                                &p, &qrows);
   if (st != OSCAR_OK || n == 0) return st;
   const int64_t q_wgs = qrot ? (p.q_rows + 15) / 16 : 0;  // NULL qrot: no q rotation role
+  if (p.raw_wgs + p.kv_wgs + q_wgs > 0x7fffffffll) return OSCAR_E_SHAPE;
   const dim3 grid(static_cast<unsigned>(p.raw_wgs + p.kv_wgs + q_wgs));
   hipStream_t s = as_stream(stream);
   if (qrows <= 16)
@@ -225,6 +252,7 @@ int history_pre_common(
     const void* rv_t, const int64_t* slots, const oscar_clip* clip, const oscar_layout* layout,
     float* partials, float* lse, float* raw_partials, float* raw_lse, void* qrot_out,
     int32_t* qsync, void* stream) {
+  if (n > 0 && (!raw_partials || !raw_lse)) return OSCAR_E_NULL;  // slice 0 is the BF16 branch
   PreArgs p;
   int64_t qrows = 0;
   int st = make_pre_args(query, q_s0, q_s1, key, k_s0, k_s1, value, v_s0, v_s1, window,
@@ -396,13 +424,24 @@ extern "C" int oscar_post_attention(
                                 table_stride, max_reqs, layout, &p);
   if (st != OSCAR_OK || n == 0) return st;
   const int mode = merge_mode(p.rows, splits);
+  hipStream_t s = as_stream(stream);
+  if (mode != kMergeScanGroup && p.rows >= kPostTileFrom) {
+    const int64_t tiles = (p.rows + 15) / 16;
+    if (tiles + p.win_requests > 0x7fffffffll) return OSCAR_E_SHAPE;
+    p.merge_wgs = static_cast<int32_t>(tiles);
+    const dim3 grid(static_cast<unsigned>(tiles + p.win_requests));
+    if (mode == kMergeOneRound)
+      hipLaunchKernelGGL(post_attention_tile_kernel<kMergeOneRound>, grid, dim3(kThreads), 0, s, p);
+    else
+      hipLaunchKernelGGL(post_attention_tile_kernel<kMergeScanWave>, grid, dim3(kThreads), 0, s, p);
+    return static_cast<int>(hipGetLastError());
+  }
   const bool wide = mode != kMergeScanGroup && p.rows >= kPostWideFrom;
   const int rows_per_wg = mode == kMergeScanGroup ? 1 : wide ? kPostWideRows : kPostQuarterRows;
   const int64_t groups = (p.rows + rows_per_wg - 1) / rows_per_wg;
   if (groups + p.win_requests > 0x7fffffffll) return OSCAR_E_SHAPE;
   p.merge_wgs = static_cast<int32_t>(groups);
   const dim3 grid(static_cast<unsigned>(groups + p.win_requests), wide ? 1 : 4);
-  hipStream_t s = as_stream(stream);
   if (wide && mode == kMergeOneRound)
     hipLaunchKernelGGL((post_attention_kernel<kPostWideRows, kMergeOneRound, 4>), grid,
                        dim3(kThreads), 0, s, p);

@@ -34,8 +34,12 @@ struct WindowArgs {
 // (prefix <= pos < seq) are written, never a ring write of a position below S. Stated per
 // current token, that is the same set of writes: token pos writes index pos if pos < S, else
 // index S + pos % C if no later token of the request has the same residue (pos + C >= seq).
-// Each index therefore has at most one writer; wavefront w handles tokens prefix + w, + 4, ...
+// Each index therefore has at most one writer. The writers are the sink tokens
+// [prefix, min(S, seq)) and the ring tokens [max(prefix, S, seq - C), seq): at most S + C of
+// them however long the chunk, taken kBatch at a time per wavefront (writer j by wavefront
+// (j / kBatch) mod 4), each batch's rows all requested before any is stored.
 __device__ __forceinline__ void store_window_request(const WindowArgs& a, int req, int head) {
+  constexpr int kBatch = 8;
   if (req >= a.counts[0]) return;
   const int qstart = a.qstarts[req];
   const int qend = min(a.qstarts[req + 1], a.counts[1]);
@@ -47,28 +51,47 @@ __device__ __forceinline__ void store_window_request(const WindowArgs& a, int re
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int h = a.L.kv_heads, sink = a.L.sink, ring = a.L.ring;
   const int64_t page_elems = a.L.page_bytes / 2;
-  for (int pos = max(prefix, 0) + wave; pos < seq; pos += kThreads / kWave) {
-    int index;
-    if (pos < sink) {
-      index = pos;
-    } else {
-      if (pos + ring < seq) continue;  // a later current token owns this ring index
-      const uint32_t lap = fastdiv(static_cast<uint32_t>(pos), a.L.ring_div);
-      index = sink + pos - static_cast<int>(lap) * ring;
-    }
-    const int64_t current = static_cast<int64_t>(qstart) + pos - prefix;
-    if (current < 0 || current >= a.n) continue;
-    const int64_t dst = owner * page_elems + (static_cast<int64_t>(index) * 2 * h + head) * kHeadDim;
-    if (dst + static_cast<int64_t>(h) * kHeadDim + kHeadDim > a.window_elems) continue;
-    const uint16_t* ks = a.k + current * a.ks0 + head * a.ks1;
-    const uint16_t* vs = a.v + current * a.vs0 + head * a.vs1;
-    uint16_t* kd = a.window + dst;
-    uint16_t* vd = a.window + dst + static_cast<int64_t>(h) * kHeadDim;
+  const int s0 = max(prefix, 0), s1 = max(s0, min(sink, seq));  // sink writers
+  const int r0 = max(max(prefix, sink), seq - ring), r1 = max(r0, seq);  // ring writers
+  const int nsink = s1 - s0, total = nsink + (r1 - r0);
+  for (int base = wave * kBatch; base < total; base += (kThreads / kWave) * kBatch) {
+    uint16_t kx[kBatch][4], vx[kBatch][4];
+    int64_t dst[kBatch];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int d = lane * 4 + i;
-      kd[d] = ks[d * a.ks2];
-      vd[d] = vs[d * a.vs2];
+    for (int b = 0; b < kBatch; ++b) {
+      const int j = base + b;
+      dst[b] = -1;
+      if (j >= total) continue;
+      const int pos = j < nsink ? s0 + j : r0 + (j - nsink);
+      int index = pos;
+      if (pos >= sink) {
+        const uint32_t lap = fastdiv(static_cast<uint32_t>(pos), a.L.ring_div);
+        index = sink + pos - static_cast<int>(lap) * ring;
+      }
+      const int64_t current = static_cast<int64_t>(qstart) + pos - prefix;
+      if (current < 0 || current >= a.n) continue;
+      const int64_t d = owner * page_elems + (static_cast<int64_t>(index) * 2 * h + head) * kHeadDim;
+      if (d + static_cast<int64_t>(h) * kHeadDim + kHeadDim > a.window_elems) continue;
+      dst[b] = d;
+      const uint16_t* ks = a.k + current * a.ks0 + head * a.ks1;
+      const uint16_t* vs = a.v + current * a.vs0 + head * a.vs1;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int e = lane * 4 + i;
+        kx[b][i] = ks[e * a.ks2];
+        vx[b][i] = vs[e * a.vs2];
+      }
+    }
+#pragma unroll
+    for (int b = 0; b < kBatch; ++b) {
+      if (dst[b] < 0) continue;
+      uint16_t* kd = a.window + dst[b];
+      uint16_t* vd = kd + static_cast<int64_t>(h) * kHeadDim;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        kd[lane * 4 + i] = kx[b][i];
+        vd[lane * 4 + i] = vx[b][i];
+      }
     }
   }
 }

@@ -359,13 +359,16 @@ def _row_strides(t, name):
     return t, s0, s1
 
 
-def pre_attention(query, key, value, history, window, meta, layout, scale, rk_t, rv_t):
+def pre_attention(query, key, value, history, window, meta, layout, scale, rk_t, rv_t,
+                  raw=True):
     """BF16-branch partials, q rotation and the K/V INT2 store of one step, in one launch.
 
     Replaces ``rotate(key, Rk)``, ``rotate(value, Rv)``, ``store_int2``, ``rotate(query, Rk)``
     and ``attention_partials(..., 1, raw=True)`` of the reference layer step
     (backend.py:171-173, 195, 211-222). ``rk_t``/``rv_t`` are R^T as contiguous bf16 [256, 256].
     Returns ``(qrot bf16 [n, hq, 256], raw_partials fp32 [n, hq, 1, 256], raw_lse [n, hq, 1])``.
+    ``raw=False``: the launch leaves the BF16 branch out and the partials come from
+    ``chunk_raw_attention`` (a launch of its own, for long chunks), with the same bits.
     """
     _device_check(query, key, value, history, window, rk_t, rv_t)
     n, hq, d = query.shape
@@ -399,12 +402,68 @@ def pre_attention(query, key, value, history, window, meta, layout, scale, rk_t,
             _ptr(_int32(meta.task_count, "task_count")),
             n, hq, programs, cfg.block_n, cfg.queries_per_tile, max_query_len, float(scale),
             _ptr(rk_t), _ptr(rv_t), _ptr(history), history.numel() * history.element_size(),
-            _ptr(meta.slot_mapping), clip_struct(cfg), layout_struct(layout), _ptr(partials),
-            _ptr(lse), _ptr(qrot), _stream(query),
+            _ptr(meta.slot_mapping), clip_struct(cfg), layout_struct(layout),
+            _ptr(partials) if raw else None, _ptr(lse) if raw else None, _ptr(qrot),
+            _stream(query),
         ),
         "pre_attention",
     )
+    if not raw:
+        chunk_raw_attention(query, key, value, window, meta, layout, scale, partials, lse)
     return qrot, partials, lse
+
+
+# Query tokens per request from which a step's BF16 branch runs as the chunk flash launch
+# (chunk_raw_attention) instead of decode-shaped roles of the pre-attention launch.
+CHUNK_RAW_FROM = 64
+
+
+def chunk_raw_preferred(meta):
+    """Whether a step's BF16 branch runs as ``chunk_raw_attention``: a host bound of at least
+    CHUNK_RAW_FROM query tokens per request (a continuation chunk)."""
+    mql = getattr(meta, "max_query_len", None)
+    return isinstance(mql, int) and mql >= CHUNK_RAW_FROM
+
+
+def chunk_raw_attention(query, key, value, window, meta, layout, scale, partials=None, lse=None):
+    """The BF16 branch (reference kernels.py:439-482: ``attention_partials(..., 1, raw=True)``,
+    sink + recent window rows, then the chunk's current tokens causally) as a flash launch in
+    which the rows of 32 consecutive query tokens share each 32-key block; the bits of
+    ``attention_partials(..., 1, raw=True)``. Returns ``(partials fp32 [n, hq, 1, 256], lse
+    fp32 [n, hq, 1])`` (into the given buffers when passed); rows of tokens at or past
+    ``counts[1]`` are not written."""
+    _device_check(query, key, value, window, partials, lse)
+    n, hq, d = query.shape
+    if partials is None:
+        partials = torch.empty((n, hq, 1, d), dtype=torch.float32, device=query.device)
+    if lse is None:
+        lse = torch.empty((n, hq, 1), dtype=torch.float32, device=query.device)
+    if (partials.dtype != torch.float32 or not partials.is_contiguous()
+            or tuple(partials.shape) != (n, hq, 1, d)):
+        raise ValueError("partials must be contiguous fp32 [n, hq, 1, 256]")
+    if lse.dtype != torch.float32 or not lse.is_contiguous() or lse.numel() != n * hq:
+        raise ValueError("lse must be contiguous fp32 [n, hq, 1]")
+    if n == 0:
+        return partials, lse
+    query, q0, q1 = _row_strides(query, "query")
+    key, k0, k1 = _row_strides(key, "key")
+    value, v0, v1 = _row_strides(value, "value")
+    table = _int32(meta.block_tables, "block_tables")
+    max_query_len = getattr(meta, "max_query_len", None)
+    max_query_len = int(max_query_len) if isinstance(max_query_len, int) else 0
+    _ext.check(
+        _ext.library().oscar_chunk_raw_attention(
+            _ptr(query), q0, q1, _ptr(key), k0, k1, _ptr(value), v0, v1,
+            _ptr(window), window.numel(),
+            _ptr(_int32(meta.query_start_loc, "query_start_loc")),
+            _ptr(_int32(meta.seq_lens, "seq_lens")), _ptr(table), table.stride(0), table.shape[1],
+            _ptr(_int32(meta.counts, "counts")),
+            n, hq, int(meta.max_num_reqs), max_query_len, float(scale), layout_struct(layout),
+            _ptr(partials), _ptr(lse), _stream(query),
+        ),
+        "chunk_raw_attention",
+    )
+    return partials, lse
 
 
 def prefill_attention(query, key, value, window, meta, layout, scale, output, merged_lse=None):
