@@ -46,6 +46,12 @@ __device__ __forceinline__ void dma_dwordx4_coherent(const void* src, uint32_t l
                : "memory");
 }
 #define OSCAR_WAIT_VM(n) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(n) : "memory")
+// vmcnt(0) as the compiler's own wait instruction (gfx9 encoding: expcnt and lgkmcnt left
+// open). The compiler's wait insertion does not see the DMAs of the inline assembly above,
+// nor waits written in inline assembly: a register loaded by an ordinary load before a loop
+// of DMAs gets a wait for it placed inside the loop, where at run time it also waits for
+// every DMA in flight. After this wait the compiler counts such loads as landed.
+#define OSCAR_WAIT_VM0_SEEN() __builtin_amdgcn_s_waitcnt(0xF70)
 #define OSCAR_WAIT_LGKM() asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory")
 
 // Workgroup barrier that waits for this wavefront's LDS traffic but not for its DMA

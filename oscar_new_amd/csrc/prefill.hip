@@ -259,6 +259,9 @@ __global__ __launch_bounds__(kThreadsP) void prefill_flash_kernel(const PrefillA
       for (int m = 0; m < 8; ++m) qb[rt][m] = *reinterpret_cast<const u32x4*>(qp + 8 * m);
     }
   }
+  // The query rows land here (with the first blocks' copies): no wait for them in the loop,
+  // where it would also wait for the blocks in flight.
+  OSCAR_WAIT_VM0_SEEN();
   State<kPrefillRT, 16> st;
   state_init(st);
   // Blocks whose every key (raw index) is at or below this wavefront's first query's last
