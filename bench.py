@@ -85,8 +85,9 @@ def parse_args(argv=None):
                    choices=("step", "history", "copy", "prefill", "store"),
                    help="step: full benchmark; history: only the history-attention launches "
                         "(for rocprofv3 counters); copy: a plain device copy of --copy-mib MiB "
-                        "(counter calibration); prefill: the initial-prefill launch on a "
-                        "prefill config (--config p1); store: the c2 store forms, plain "
+                        "(counter calibration); prefill: the initial-prefill launch (--config "
+                        "p1) or the continuation-chunk step (--config p2); store: the c2 store "
+                        "forms, plain "
                         "launches (for rocprofv3 counters)")
     p.add_argument("--copy-mib", type=int, default=1024)
     p.add_argument("--split-policy", default=None, choices=("device", "reference", "mi355x"),
@@ -95,7 +96,7 @@ def parse_args(argv=None):
                    help="--mode history: the history branch alone instead of the step's "
                         "history launch")
     p.add_argument("--no-sub-configs", action="store_true",
-                   help="c3: skip the c4 / c5 / p1 sub-records")
+                   help="c3: skip the c4 / c5 / p1 / p2 sub-records")
     return p.parse_args(argv)
 
 
@@ -541,7 +542,7 @@ def prefill_measurement(args, w, device):
 
     ntok = w.q.shape[0]
     if any(p != 0 for p in w.prefixes):
-        print(json.dumps(continuation_measurement(args, w, device)))
+        print(json.dumps(continuation_measurement(args, w, device, args.config, args.steps)))
         return 0
     w.meta.initial_prefill = True
     _, win = w.layout.tensor_views((w.k_cache, w.v_cache))
@@ -587,7 +588,7 @@ def continuation_flops(w):
                            bf16=4.0 * bf16_pairs * per_pair)
 
 
-def continuation_measurement(args, w, device):
+def continuation_measurement(args, w, device, name, steps):
     """A continuation chunk (config p2): the layer step as ``impl.forward`` runs it (eager
     launches: a 2048-token step is far above launch overheads), and its history branch alone,
     timed with HIP events. The history branch is MFMA-bound: its issued FP8 x FP4 work over
@@ -597,7 +598,7 @@ def continuation_measurement(args, w, device):
 
     from oscar_new_amd.backend import OscarAttentionImpl
 
-    cfg = CONFIGS[args.config]
+    cfg = CONFIGS[name]
     impl = OscarAttentionImpl.standalone(6, 256, 1 / 16, 1, w.cfg,
                                          split_policy=args.split_policy or cfg["splits"])
     impl.set_rotations(w.rk, w.rv)
@@ -606,12 +607,12 @@ def continuation_measurement(args, w, device):
     out = torch.empty(ntok, 6 * 256, dtype=torch.bfloat16, device=device)
     splits, split_tokens = impl.partition_for(w.meta, ntok)
     step_us = time_launch(lambda i: impl.forward(None, w.q, w.k, w.v, layers[0], w.meta, out),
-                          1, args.steps, False)
+                          1, steps, False)
     bname, _, bfn = branch_launch(impl, w, layers, splits, split_tokens)
-    b_us = time_launch(bfn, 1, args.steps, False)
+    b_us = time_launch(bfn, 1, steps, False)
     fl = continuation_flops(w)
     hist_tf = fl.history_issued / (b_us * 1e-6) / 1e12
-    return {"mode": "prefill", "config": args.config, "workload": f"{args.config}: {cfg['desc']}",
+    return {"mode": "prefill", "config": name, "workload": f"{name}: {cfg['desc']}",
             "tokens": ntok, "cached_tokens": sum(w.prefixes), "splits": splits,
             "split_tokens": split_tokens, "us_per_layer_step": step_us,
             "step_useful_tflops": (fl.history_useful + fl.bf16) / (step_us * 1e-6) / 1e12,
@@ -1006,6 +1007,11 @@ def main(argv=None):
             torch.cuda.empty_cache()
         print("[bench] p1 prefill", file=sys.stderr, flush=True)
         subs["p1"] = prefill_record(args, device, max(10, args.steps), args.warmup)
+        torch.cuda.empty_cache()
+        print("[bench] p2 continuation chunk", file=sys.stderr, flush=True)
+        w2 = build_workload(args, CONFIGS["p2"], device)
+        subs["p2"] = continuation_measurement(args, w2, device, "p2", min(max(10, args.steps), 50))
+        del w2
         torch.cuda.empty_cache()
         result["configs"] = subs
     print(json.dumps(result))
