@@ -25,7 +25,7 @@ constexpr int kWavesP = 12;                          // wavefronts per workgroup
 constexpr int kCopyWavesP = 8;                       // the ones that copy blocks and pair V
 constexpr int kThreadsP = kWavesP * kWave;
 constexpr int kPrefillRT = 1;                        // row tiles per wavefront
-constexpr int kSpanRows = kWavesP * 16 * kPrefillRT;  // 192 rows per workgroup
+constexpr int kSpanRows = kWavesP * 16 * kPrefillRT;  // 192 rows per workgroup (at most)
 constexpr int kRowBytes = kHeadDim * 2;              // 512 bytes per K or V row
 constexpr int kBlockBytes = kBlock * kRowBytes;      // 16 KiB per K or V block
 constexpr int kStageBytesP = 2 * kBlockBytes;        // K then V
@@ -61,6 +61,9 @@ struct PrefillArgs {
   const int32_t* counts;
   int64_t n;
   int32_t g, hq, kv_heads;
+  // Rows per workgroup: kSpanRows, or 96 or 48 when a launch would have fewer workgroups
+  // than CUs (one long request); the wavefronts past them only copy and pair blocks.
+  int32_t span_rows;
   FastDiv g_div;
   float scale_log2;
   uint16_t* out;
@@ -187,9 +190,9 @@ __global__ __launch_bounds__(kThreadsP) void prefill_flash_kernel(const PrefillA
   const int qlen = static_cast<int>(qend - qstart);
   if (qlen <= 0) return;
   const int rows_req = qlen * a.g;
-  const int row0 = span * kSpanRows;
+  const int row0 = span * a.span_rows;
   if (row0 >= rows_req) return;
-  const int row_end = min(row0 + kSpanRows, rows_req);
+  const int row_end = min(row0 + a.span_rows, rows_req);
   const int seq = a.seq_lens[req];
   // Initial prefill: a request with cached tokens is not one; chunk form: a request with
   // fewer tokens than query tokens is malformed. Their rows are NaN.
@@ -206,7 +209,7 @@ __global__ __launch_bounds__(kThreadsP) void prefill_flash_kernel(const PrefillA
   // max_query_len) are written as NaN by the last span's workgroup, like the rows of a
   // request with cached tokens, so that a wrong bound shows in the output.
   if (span == static_cast<int>(gridDim.y) - 1) {
-    const int covered = static_cast<int>(gridDim.y) * kSpanRows;
+    const int covered = static_cast<int>(gridDim.y) * a.span_rows;
     for (int row = covered + static_cast<int>(threadIdx.x >> 5); row < rows_req;
          row += kThreadsP / 32) {
       const int qi = static_cast<int>(fastdiv(static_cast<uint32_t>(row), a.g_div));
@@ -229,6 +232,7 @@ __global__ __launch_bounds__(kThreadsP) void prefill_flash_kernel(const PrefillA
   const int lane = threadIdx.x & 63;
   const int wave = uniform(threadIdx.x >> 6);
   const int n = lane & 15, g = lane >> 4;
+  const bool has_rows = 16 * kPrefillRT * wave < a.span_rows;  // wavefront-uniform
 
   const uint8_t* kb = reinterpret_cast<const uint8_t*>(a.key + qstart * a.ks0 + head * a.ks1);
   const uint8_t* vb = reinterpret_cast<const uint8_t*>(a.value + qstart * a.vs0 + head * a.vs1);
@@ -341,6 +345,7 @@ __global__ __launch_bounds__(kThreadsP) void prefill_flash_kernel(const PrefillA
     // them, the order of the one-block-at-a-time stream) interleaved with block b's scores
     // S^T = K Q^T (A = K rows 16 tt + n, chunk 8 g + m): two P*V tiles per score k-step.
     const uint8_t* pairs = s_pair[(b + 1) & 1];  // block b - 1's
+    if (has_rows) {
     f32x4 sc[kPrefillRT][2];
 #pragma unroll
     for (int rt = 0; rt < kPrefillRT; ++rt)
@@ -376,13 +381,15 @@ __global__ __launch_bounds__(kThreadsP) void prefill_flash_kernel(const PrefillA
     }
     update_max(st, s2, g);
     block_p(st, s2, ap_prev);
+    }
     // Pairs of block b (into the buffer block b - 2 used, read before the barrier above).
     if (wave < kCopyWavesP) pair_block(stage, s_pair[b & 1]);
   }
   if (nblk > 0) {
     barrier_lds();  // the last block's pairs
-    pv_block(s_pair[(nblk - 1) & 1], ap_prev);
+    if (has_rows) pv_block(s_pair[(nblk - 1) & 1], ap_prev);
   }
+  if (!has_rows) return;
 
   // Normalize and store: lane (n, g) holds rows 4 g + v of each tile, dims 16 n + j.
 #pragma unroll
@@ -446,6 +453,17 @@ __global__ __launch_bounds__(kThreads) void prefill_clear_kernel(const PrefillAr
 
 bool aligned16(const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; }
 
+// Rows per workgroup of a launch over `rows` rows per (request, KV head): kSpanRows, unless
+// the launch would then have fewer workgroups than the chip's 256 CUs (one long request);
+// then 96 or 48 rows: more workgroups over the same blocks, each copying every block of its
+// rows. A row's arithmetic does not depend on the rows beside it, so neither do its bits.
+int span_rows_for(int64_t rows, int64_t reqs, int64_t heads) {
+  constexpr int64_t kChipCUs = 256;
+  for (const int r : {kSpanRows, kSpanRows / 2})
+    if (reqs * heads * ((rows + r - 1) / r) >= kChipCUs) return r;
+  return kSpanRows / 4;
+}
+
 }  // namespace
 }  // namespace oscar
 
@@ -491,11 +509,12 @@ extern "C" int oscar_prefill_attention(
   a.scale_log2 = scale * kLog2e;
   a.out = static_cast<uint16_t*>(output);
   a.lse = merged_lse;
-  // Spans per request: its rows (query tokens x g) in kSpanRows-row groups (192); a request
-  // has at most max_query_len (when given) or n query tokens. Rows past the spans of a request
-  // that breaks the given bound are written as NaN.
+  // Spans per request: its rows (query tokens x g) in span_rows-row groups; a request has at
+  // most max_query_len (when given) or n query tokens. Rows past the spans of a request that
+  // breaks the given bound are written as NaN.
   const int64_t qmax = max_query_len > 0 && max_query_len < n ? max_query_len : n;
-  const int64_t spans = (qmax * g + kSpanRows - 1) / kSpanRows;
+  a.span_rows = span_rows_for(qmax * g, max_reqs, h);
+  const int64_t spans = (qmax * g + a.span_rows - 1) / a.span_rows;
   if (spans > 65535) return OSCAR_E_SHAPE;  // grid y
   hipStream_t s = as_stream(stream);
   // Requests vary fastest: the workgroups of the longest spans of every request dispatch
@@ -563,7 +582,8 @@ extern "C" int oscar_chunk_raw_attention(
   a.partials = raw_partials;
   a.plse = raw_lse;
   const int64_t qmax = max_query_len > 0 && max_query_len < n ? max_query_len : n;
-  const int64_t spans = (qmax * g + kSpanRows - 1) / kSpanRows;
+  a.span_rows = span_rows_for(qmax * g, max_reqs, h);
+  const int64_t spans = (qmax * g + a.span_rows - 1) / a.span_rows;
   if (spans > 65535) return OSCAR_E_SHAPE;  // grid y
   hipLaunchKernelGGL(prefill_flash_kernel<true>,
                      dim3(static_cast<unsigned>(max_reqs), static_cast<unsigned>(spans),
