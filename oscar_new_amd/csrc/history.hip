@@ -567,35 +567,43 @@ __global__ __launch_bounds__(kThreads, 3 - RT) void history_kernel(const AttnArg
   history_unit<RT>(a, blockIdx.x, blockIdx.y, blockIdx.z, st, lds);
 }
 
-// ---------------------------------------------------------------- 17-32 rows: eight wavefronts
+// ---------------------------------------------------------------- 17-32 rows: two row groups
 
 // Tasks of 17-32 query rows (MTP: 4 query tokens x 6 query heads = 24 rows). Two row groups of
-// 16 rows share every chunk: wavefront w streams chunks (w % 4) + 4 j like the general
-// kernel's wavefront w % 4 and computes the rows 16 (w / 4) .. + 15 of them, so each chunk is
-// copied into LDS once (by the group-0 wavefront of its stream, three stages per stream) and
-// read by two wavefronts, and every SIMD holds two wavefronts (one workgroup of eight per CU;
-// a wavefront keeps one 16-row tile, about 210 registers, instead of 464 for two tiles,
-// whose single wavefront per SIMD left the VALU half idle). A workgroup barrier per chunk
-// publishes the chunk to the second wavefront of its stream and frees the stage of the chunk
-// before. A row's arithmetic is the general kernel's with one row tile; the lazy-max rescale
-// is decided per wavefront, so its bits depend on the 16-row grouping, not on the launch form
-// (grid or work queue).
+// 16 rows share every chunk: with S streams (S = 4: eight wavefronts, one workgroup per CU;
+// S = 2: four wavefronts, two workgroups per CU), wavefront w streams chunks (w % S) + S j and
+// computes the rows 16 (w / S) .. + 15 of them, so each chunk is copied into LDS once (by the
+// group-0 wavefront of its stream, three stages per stream) and read by two wavefronts, and
+// every SIMD holds two wavefronts (a wavefront keeps one 16-row tile, about 210 registers,
+// instead of 464 for two tiles, whose single wavefront per SIMD left the VALU half idle). A
+// workgroup barrier per chunk publishes the chunk to the second wavefront of its stream and
+// frees the stage of the chunk before; with two workgroups per CU those barriers are
+// independent, so one workgroup's MFMAs meet the other's softmax. A row's arithmetic is the
+// general kernel's with one row tile; the lazy-max rescale is decided per wavefront, so its
+// bits depend on the 16-row grouping and the stream count, not on the launch form (grid or
+// work queue, which take the same stream count for the same task count).
 constexpr int kThreadsW8 = 512;
 constexpr int kStagesW8 = 3;
-constexpr int kRingBytesW8 = 4 * kStagesW8 * kStageBytes;
 
+// kWaves 8: four streams x two row groups; kWaves 4: two streams x two row groups, in under
+// 80 KB of LDS with the work queue's task lists (two workgroups per CU).
+template <int kWaves>
 struct HistoryLdsW8 {
-  uint8_t ring[kRingBytesW8] __attribute__((aligned(16)));
+  uint8_t ring[(kWaves / 2) * kStagesW8 * kStageBytes] __attribute__((aligned(16)));
   uint8_t qstage[32 * 512] __attribute__((aligned(16)));  // query rows, then operand images
   uint32_t off[kTableCache];
-  float red[3][8][16];  // per wavefront: row max, sum p, sum p z_v of its 16 rows
+  float red[3][8][16];  // per wavefront (or query stream): row max, sum p, sum p z_v of 16 rows
 };
-static_assert(8 * 16 * 128 * 4 <= kRingBytesW8, "half the epilogue merge fits the ring");
+static_assert(8 * 16 * 128 * 4 <= sizeof(HistoryLdsW8<8>::ring), "half the merge fits the ring");
+static_assert(4 * 16 * 128 * 4 <= sizeof(HistoryLdsW8<4>::ring), "half the merge fits the ring");
 static_assert(2 * 2 * kQTerms * 64 * 32 <= 32 * 512, "both groups' operand images fit");
 
 // `st`: the launch's split length (launch_split_tokens).
+template <int kWaves>
 __device__ __forceinline__ void history_unit_w8(const AttnArgs& a, int task, int head, int split,
-                                                int st, HistoryLdsW8& lds) {
+                                                int st, HistoryLdsW8<kWaves>& lds) {
+  constexpr int kStreams = kWaves / 2;
+  constexpr int kT = kWaves * kWave;
   uint8_t* s_ring = lds.ring;
   uint32_t* s_off = lds.off;
   auto& s_red = lds.red;
@@ -611,12 +619,13 @@ __device__ __forceinline__ void history_unit_w8(const AttnArgs& a, int task, int
   history_positions(a, t, length, nsplit, split, st, p_lo, p_hi);
   const int lane = threadIdx.x & 63;
   const int wave = uniform(threadIdx.x >> 6);
-  const int stream = wave & 3, rg = wave >> 2;
+  const int stream = wave % kStreams, rg = wave / kStreams;
   const int n = lane & 15, g = lane >> 4;
   const int first = p_lo >> 6;
   const int nchunk = p_lo < p_hi ? ((p_hi - 1) >> 6) - first + 1 : 0;
-  const int nmine = nchunk > stream ? (nchunk - stream + 3) >> 2 : 0;  // chunks stream + 4 j
-  const int nmax = (nchunk + 3) >> 2;                                  // stream 0's count
+  // chunks stream + kStreams j
+  const int nmine = nchunk > stream ? (nchunk - stream + kStreams - 1) / kStreams : 0;
+  const int nmax = (nchunk + kStreams - 1) / kStreams;  // stream 0's count
   const int kb_first = p_lo >> a.L.bk_shift;
 
   // ---- DMA plan (as in the general kernel); the group-0 wavefront of a stream issues.
@@ -631,14 +640,14 @@ __device__ __forceinline__ void history_unit_w8(const AttnArgs& a, int task, int
   const uint32_t in_kb_mask = static_cast<uint32_t>(a.L.bk - 1);
   // Offset (32-byte units) of the kernel block of this stream's chunk j, or kNoBlock.
   auto block_of = [&](int j) {
-    const int t0 = (first + stream + 4 * j) << 6;
+    const int t0 = (first + stream + kStreams * j) << 6;
     const int local = (t0 >> a.L.bk_shift) - kb_first;
     uint32_t off32 = s_off[min(local, kTableCache - 1)];
     if (local >= kTableCache) off32 = kernel_block_offset(a, t, head, t0 >> a.L.bk_shift);
     return static_cast<uint32_t>(uniform(static_cast<int>(off32)));
   };
   auto issue = [&](int j, int s) {
-    const int t0 = (first + stream + 4 * j) << 6;
+    const int t0 = (first + stream + kStreams * j) << 6;
     const uint32_t off32 = block_of(j);
     const uint8_t* base = a.history;
     if (off32 != kNoBlock)
@@ -652,20 +661,21 @@ __device__ __forceinline__ void history_unit_w8(const AttnArgs& a, int task, int
   // ---- query rows -> LDS: 32 rows, piece p of row r at r * 32 + (p ^ (r & 31)).
   uint8_t* q_lds = lds.qstage;
   {
+    constexpr int kQPer = 16 / kWaves;  // 1 KiB DMAs per wavefront
     const uint32_t q_base = lds_addr(q_lds);
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int slot = (wave * 2 + i) * 64 + lane;
+    for (int i = 0; i < kQPer; ++i) {
+      const int slot = (wave * kQPer + i) * 64 + lane;
       const int row = slot >> 5, piece = (slot & 31) ^ (row & 31);
       const RowInfo ri = row_info(a, t, head, row);
       const uint16_t* src =
           ri.valid ? a.query + ri.token * a.qs0 + ri.qhead * a.qs1 + 8 * piece : a.query;
-      dma_dwordx4(src, q_base + 1024 * (wave * 2 + i));
+      dma_dwordx4(src, q_base + 1024 * (wave * kQPer + i));
     }
   }
   if (nchunk > 0) {
     const int nkb = min(((p_hi - 1) >> a.L.bk_shift) - kb_first + 1, kTableCache);
-    for (int j = threadIdx.x; j < nkb; j += kThreadsW8)
+    for (int j = threadIdx.x; j < nkb; j += kT)
       s_off[j] = kernel_block_offset(a, t, head, kb_first + j);
   }
   OSCAR_WAIT_VM(0);
@@ -676,37 +686,43 @@ __device__ __forceinline__ void history_unit_w8(const AttnArgs& a, int task, int
   }
 
   // ---- query -> FP8 B operands of this wavefront's 16 rows (row group rg), converted by the
-  // group's four wavefronts: wavefront stream s builds operand dwords 2s, 2s + 1 of every lane.
+  // group's wavefronts in four query streams: stream qs builds operand dwords 2 qs, 2 qs + 1
+  // of every lane (four wavefronts: one stream each; two: streams w and w + 2).
   i32x8 qb[2][kQTerms];
   float fq, qs2, qmult;
-  float qx[2][8];
+  constexpr int kQStreams = 4 / kStreams;
+  float qx[kQStreams][2][8];
   {
     const int row = 16 * rg + n;
     const bool live = row_info(a, t, head, row).valid;
-    float mx = 0.f, qs = 0.f;
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const int piece = 16 * h + 8 * (stream >> 1) + 2 * g;
-      const u32x4 r0 = *reinterpret_cast<const u32x4*>(q_lds + row * 512 + 16 * (piece ^ (row & 31)));
-      const u32x4 r1 =
-          *reinterpret_cast<const u32x4*>(q_lds + row * 512 + 16 * ((piece + 1) ^ (row & 31)));
-      const uint32_t w[8] = {r0[0], r0[1], r0[2], r0[3], r1[0], r1[1], r1[2], r1[3]};
+    for (int k = 0; k < kQStreams; ++k) {
+      const int qsid = stream + kStreams * k;
+      float mx = 0.f, qsum = 0.f;
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const uint32_t bits = (stream & 1) ? (w[i] >> 16) : (w[i] & 0xffffu);
-        const float x = live ? bf16_to_float(bits) : 0.f;
-        qx[h][i] = x;
-        mx = fmaxf(mx, fabsf(x));
-        qs += x;
+      for (int h = 0; h < 2; ++h) {
+        const int piece = 16 * h + 8 * (qsid >> 1) + 2 * g;
+        const u32x4 r0 = *reinterpret_cast<const u32x4*>(q_lds + row * 512 + 16 * (piece ^ (row & 31)));
+        const u32x4 r1 =
+            *reinterpret_cast<const u32x4*>(q_lds + row * 512 + 16 * ((piece + 1) ^ (row & 31)));
+        const uint32_t w[8] = {r0[0], r0[1], r0[2], r0[3], r1[0], r1[1], r1[2], r1[3]};
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const uint32_t bits = (qsid & 1) ? (w[i] >> 16) : (w[i] & 0xffffu);
+          const float x = live ? bf16_to_float(bits) : 0.f;
+          qx[k][h][i] = x;
+          mx = fmaxf(mx, fabsf(x));
+          qsum += x;
+        }
       }
-    }
-    mx = fmaxf(mx, __shfl_xor(mx, 16, kWave));
-    mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
-    qs += __shfl_xor(qs, 16, kWave);
-    qs += __shfl_xor(qs, 32, kWave);
-    if (g == 0) {
-      s_red[0][wave][n] = mx;
-      s_red[1][wave][n] = qs;
+      mx = fmaxf(mx, __shfl_xor(mx, 16, kWave));
+      mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
+      qsum += __shfl_xor(qsum, 16, kWave);
+      qsum += __shfl_xor(qsum, 32, kWave);
+      if (g == 0) {
+        s_red[0][4 * rg + qsid][n] = mx;
+        s_red[1][4 * rg + qsid][n] = qsum;
+      }
     }
   }
   barrier_lds();  // partial row max / sum published; the query rows are in registers
@@ -714,24 +730,28 @@ __device__ __forceinline__ void history_unit_w8(const AttnArgs& a, int task, int
     const int w0 = 4 * rg;
     const float mx = fmaxf(fmaxf(s_red[0][w0][n], s_red[0][w0 + 1][n]),
                            fmaxf(s_red[0][w0 + 2][n], s_red[0][w0 + 3][n]));
-    const float qs = (s_red[1][w0][n] + s_red[1][w0 + 1][n]) + (s_red[1][w0 + 2][n] + s_red[1][w0 + 3][n]);
+    const float qsum = (s_red[1][w0][n] + s_red[1][w0 + 1][n]) + (s_red[1][w0 + 2][n] + s_red[1][w0 + 3][n]);
     const uint32_t eb = max((__float_as_uint(mx) >> 23) & 0xffu, 7u);
     qmult = __uint_as_float((261u - eb) << 23);
     fq = 2.0f * a.scale_log2 / qmult;  // FP4 holds c/2
-    qs2 = 0.5f * qs * qmult;
+    qs2 = 0.5f * qsum * qmult;
   }
   // Operand images [rg][h][term][lane][8 dwords] (alias the query rows, now in registers).
   uint32_t* q_ops = reinterpret_cast<uint32_t*>(q_lds) + rg * (2 * kQTerms * 64 * 8);
 #pragma unroll
-  for (int h = 0; h < 2; ++h)
+  for (int k = 0; k < kQStreams; ++k) {
+    const int qsid = stream + kStreams * k;
 #pragma unroll
-    for (int f = 0; f < 2; ++f) {
-      float v[4] = {qx[h][4 * f] * qmult, qx[h][4 * f + 1] * qmult, qx[h][4 * f + 2] * qmult,
-                    qx[h][4 * f + 3] * qmult};
+    for (int h = 0; h < 2; ++h)
 #pragma unroll
-      for (int term = 0; term < kQTerms; ++term)
-        q_ops[((h * kQTerms + term) * 64 + lane) * 8 + 2 * stream + f] = fp8x4_take(v);
-    }
+      for (int f = 0; f < 2; ++f) {
+        float v[4] = {qx[k][h][4 * f] * qmult, qx[k][h][4 * f + 1] * qmult,
+                      qx[k][h][4 * f + 2] * qmult, qx[k][h][4 * f + 3] * qmult};
+#pragma unroll
+        for (int term = 0; term < kQTerms; ++term)
+          q_ops[((h * kQTerms + term) * 64 + lane) * 8 + 2 * qsid + f] = fp8x4_take(v);
+      }
+  }
   barrier_lds();
 #pragma unroll
   for (int h = 0; h < 2; ++h)
@@ -784,7 +804,7 @@ __device__ __forceinline__ void history_unit_w8(const AttnArgs& a, int task, int
     float r2[16];
 #pragma unroll
     for (int e = 0; e < 16; ++e) r2[e] = fmaf(h16lo(ksz[e]), acc[e >> 2][e & 3], h16hi(ksz[e]) * qs2);
-    const int t0 = (first + stream + 4 * j) << 6;
+    const int t0 = (first + stream + kStreams * j) << 6;
     const bool ok_block = block_of(j) != kNoBlock;
     if (!(ok_block && t0 >= p_lo && t0 + kChunk <= p_hi)) {
 #pragma unroll
@@ -886,28 +906,38 @@ __device__ __forceinline__ void history_unit_w8(const AttnArgs& a, int task, int
   barrier_lds();
   float* s_o = reinterpret_cast<float*>(s_ring);  // [wave][row 0..15][128]
   const int tid = threadIdx.x;
-  const int row32 = tid >> 4, d0 = 4 * (tid & 15);
-  const int rgx = row32 >> 4, r16 = row32 & 15;
-  const RowInfo ri = row_info(a, t, head, row32);
-  float mx = -INFINITY, den = 0.f, zs = 0.f;
+  constexpr int kPasses = 512 / kT;  // 32 rows x 16 threads
+  RowInfo ri[kPasses];
+  float mx[kPasses], den[kPasses], zs[kPasses], inv[kPasses];
 #pragma unroll
-  for (int w = 0; w < 4; ++w) mx = fmaxf(mx, s_red[0][4 * rgx + w][r16]);
+  for (int pass = 0; pass < kPasses; ++pass) {
+    const int row32 = (tid >> 4) + pass * (kT >> 4);
+    const int rgx = row32 >> 4, r16 = row32 & 15;
+    ri[pass] = row_info(a, t, head, row32);
+    mx[pass] = -INFINITY;
+    den[pass] = 0.f;
+    zs[pass] = 0.f;
 #pragma unroll
-  for (int w = 0; w < 4; ++w) {
-    const float mw = s_red[0][4 * rgx + w][r16];
-    const float f = mw == -INFINITY ? 0.f : exp2f(mw - mx);
-    den = fmaf(f, s_red[1][4 * rgx + w][r16], den);
-    zs = fmaf(f, s_red[2][4 * rgx + w][r16], zs);
+    for (int w = 0; w < kStreams; ++w) mx[pass] = fmaxf(mx[pass], s_red[0][kStreams * rgx + w][r16]);
+#pragma unroll
+    for (int w = 0; w < kStreams; ++w) {
+      const float mw = s_red[0][kStreams * rgx + w][r16];
+      const float f = mw == -INFINITY ? 0.f : exp2f(mw - mx[pass]);
+      den[pass] = fmaf(f, s_red[1][kStreams * rgx + w][r16], den[pass]);
+      zs[pass] = fmaf(f, s_red[2][kStreams * rgx + w][r16], zs[pass]);
+    }
+    inv[pass] = 1.0f / fmaxf(den[pass], 1.0e-30f);
   }
-  const float inv = 1.0f / fmaxf(den, 1.0e-30f);
+  const int d0 = 4 * (tid & 15);
 #pragma unroll
   for (int hd = 0; hd < 2; ++hd) {
     if (hd > 0) barrier_lds();  // the first half has been read
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
       const int row = 4 * g + v;
-      const float mxr = fmaxf(fmaxf(s_red[0][4 * rg][row], s_red[0][4 * rg + 1][row]),
-                              fmaxf(s_red[0][4 * rg + 2][row], s_red[0][4 * rg + 3][row]));
+      float mxr = s_red[0][kStreams * rg][row];
+#pragma unroll
+      for (int w = 1; w < kStreams; ++w) mxr = fmaxf(mxr, s_red[0][kStreams * rg + w][row]);
       const float mw = s_red[0][wave][row];
       const float f = mw == -INFINITY ? 0.f : exp2f(mw - mxr);
       float* dst = s_o + (wave * 16 + row) * 128 + 2 * n;
@@ -917,32 +947,47 @@ __device__ __forceinline__ void history_unit_w8(const AttnArgs& a, int task, int
             make_float2(o[2 * (4 * hd + c)][v] * f, o[2 * (4 * hd + c) + 1][v] * f);
     }
     barrier_lds();
-    if (ri.valid) {
-      float* out = a.partials + ((ri.token * a.hq + ri.qhead) * a.splits + split) * kHeadDim +
+#pragma unroll
+    for (int pass = 0; pass < kPasses; ++pass) {
+      if (!ri[pass].valid) continue;
+      const int row32 = (tid >> 4) + pass * (kT >> 4);
+      const int rgx = row32 >> 4, r16 = row32 & 15;
+      float* out = a.partials +
+                   ((ri[pass].token * a.hq + ri[pass].qhead) * a.splits + split) * kHeadDim +
                    128 * hd + d0;
-      const float4* so = reinterpret_cast<const float4*>(s_o + ((4 * rgx) * 16 + r16) * 128 + d0);
+      const float4* so =
+          reinterpret_cast<const float4*>(s_o + ((kStreams * rgx) * 16 + r16) * 128 + d0);
 #pragma unroll
       for (int q = 0; q < 2; ++q) {
-        const float4 x0 = so[16 * q], x1 = so[16 * 128 / 4 + 16 * q];
-        const float4 x2 = so[2 * 16 * 128 / 4 + 16 * q], x3 = so[3 * 16 * 128 / 4 + 16 * q];
-        const float4 r = make_float4((2.0f * ((x0.x + x1.x) + (x2.x + x3.x)) + zs) * inv,
-                                     (2.0f * ((x0.y + x1.y) + (x2.y + x3.y)) + zs) * inv,
-                                     (2.0f * ((x0.z + x1.z) + (x2.z + x3.z)) + zs) * inv,
-                                     (2.0f * ((x0.w + x1.w) + (x2.w + x3.w)) + zs) * inv);
+        float4 x[kStreams];
+#pragma unroll
+        for (int w = 0; w < kStreams; ++w) x[w] = so[w * 16 * 128 / 4 + 16 * q];
+        float4 acc;
+        if constexpr (kStreams == 4) {
+          acc = make_float4((x[0].x + x[1].x) + (x[2].x + x[3].x), (x[0].y + x[1].y) + (x[2].y + x[3].y),
+                            (x[0].z + x[1].z) + (x[2].z + x[3].z), (x[0].w + x[1].w) + (x[2].w + x[3].w));
+        } else {
+          acc = make_float4(x[0].x + x[1].x, x[0].y + x[1].y, x[0].z + x[1].z, x[0].w + x[1].w);
+        }
+        const float4 r = make_float4((2.0f * acc.x + zs[pass]) * inv[pass],
+                                     (2.0f * acc.y + zs[pass]) * inv[pass],
+                                     (2.0f * acc.z + zs[pass]) * inv[pass],
+                                     (2.0f * acc.w + zs[pass]) * inv[pass]);
         *reinterpret_cast<float4*>(out + 64 * q) = r;
       }
       if (hd == 0 && (tid & 15) == 0)
-        a.lse[(ri.token * a.hq + ri.qhead) * a.splits + split] =
-            den > 0.f ? (mx + log2f(den)) * kLn2 : -INFINITY;
+        a.lse[(ri[pass].token * a.hq + ri[pass].qhead) * a.splits + split] =
+            den[pass] > 0.f ? (mx[pass] + log2f(den[pass])) * kLn2 : -INFINITY;
     }
   }
   barrier_lds();  // the merge area is read before the next unit's DMA reuses the ring
 }
 
-__global__ __launch_bounds__(kThreadsW8, 1) void history_w8_kernel(const AttnArgs a) {
-  __shared__ HistoryLdsW8 lds;
-  const int st = launch_split_tokens<kThreadsW8>(a, static_cast<int>(gridDim.x));
-  history_unit_w8(a, blockIdx.x, blockIdx.y, blockIdx.z, st, lds);
+template <int kWaves>
+__global__ __launch_bounds__(kWaves * kWave, 8 / kWaves) void history_w8_kernel(const AttnArgs a) {
+  __shared__ HistoryLdsW8<kWaves> lds;
+  const int st = launch_split_tokens<kWaves * kWave>(a, static_cast<int>(gridDim.x));
+  history_unit_w8<kWaves>(a, blockIdx.x, blockIdx.y, blockIdx.z, st, lds);
 }
 
 // The 17-32-row kernel as a work queue (token-bounded splits, one workgroup per CU): a grid of
@@ -956,16 +1001,17 @@ __global__ __launch_bounds__(kThreadsW8, 1) void history_w8_kernel(const AttnArg
 // workgroups in task-stride order. The counters (next unit, finished workgroups) are zero at
 // launch; the last workgroup to finish sets them to zero again, so graph replays reuse them.
 // Launches that overlap on one device must not share counters.
-constexpr int kQueueTasks = 2048;  // task rows the workgroup lists in LDS
+constexpr int kQueueTasks = 2048;  // task rows the workgroup lists in LDS (eight wavefronts)
+constexpr int kQueueTasks4 = 512;  // the same with four wavefronts (80 KB of LDS)
 
-__global__ __launch_bounds__(kThreadsW8, 1) void history_queue_kernel(const AttnArgs a,
-                                                                       int32_t* counters,
-                                                                       int32_t programs) {
-  constexpr int kT = kThreadsW8;
-  __shared__ HistoryLdsW8 lds;
-  __shared__ int32_t s_full[kQueueTasks + 1];  // full splits of the tasks before t
-  __shared__ int32_t s_nsplit[kQueueTasks];
-  __shared__ int16_t s_used[kQueueTasks];      // tasks in use, in order
+template <int kWaves, int kTasks>
+__global__ __launch_bounds__(kWaves * kWave, 8 / kWaves) void history_queue_kernel(
+    const AttnArgs a, int32_t* counters, int32_t programs) {
+  constexpr int kT = kWaves * kWave;
+  __shared__ HistoryLdsW8<kWaves> lds;
+  __shared__ int32_t s_full[kTasks + 1];  // full splits of the tasks before t
+  __shared__ int32_t s_nsplit[kTasks];
+  __shared__ int16_t s_used[kTasks];      // tasks in use, in order
   __shared__ int32_t s_part[2][kT];            // per-thread sums, then their exclusive scan
   __shared__ int32_t s_total[2];               // full splits, tasks in use
   __shared__ int32_t s_claim;
@@ -1055,7 +1101,7 @@ __global__ __launch_bounds__(kThreadsW8, 1) void history_queue_kernel(const Attn
       task = s_used[k - full];
       split = s_nsplit[task] - 1;
     }
-    history_unit_w8(a, task, head, split, st, lds);
+    history_unit_w8<kWaves>(a, task, head, split, st, lds);
   }
   // Unused split slots: LSE -inf for the rows of every task in use.
   for (int task = blockIdx.x; task < programs; task += gridDim.x) {
@@ -1763,20 +1809,31 @@ hipError_t launch_history(const AttnArgs& a, dim3 grid, int rows, hipStream_t st
     hipLaunchKernelGGL(history_pair_kernel, grid, dim3(kThreads), 0, stream, a);
   } else if (rows <= 16) {
     hipLaunchKernelGGL(history_kernel<1>, grid, dim3(kThreads), 0, stream, a);
-  } else if (queue != nullptr && a.split_tokens != 0 &&
-             static_cast<int64_t>(grid.x) <= kQueueTasks) {
-    int device = 0, cus = 0;
-    hipError_t e = hipGetDevice(&device);
-    if (e == hipSuccess)
-      e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device);
-    if (e != hipSuccess) return e;
-    const int64_t units = static_cast<int64_t>(grid.x) * grid.y * grid.z;
-    const int64_t cap = cus > 0 ? cus : 1;
-    const unsigned wgs = static_cast<unsigned>(units < cap ? units : cap);
-    hipLaunchKernelGGL(history_queue_kernel, dim3(wgs), dim3(kThreadsW8), 0, stream, a, queue,
-                       static_cast<int32_t>(grid.x));
   } else {
-    hipLaunchKernelGGL(history_w8_kernel, grid, dim3(kThreadsW8), 0, stream, a);
+    // Four-wavefront workgroups (two per CU) up to kQueueTasks4 task rows, eight-wavefront
+    // ones above; the grid and queue forms take the same size, so they give the same bits.
+    const bool four = static_cast<int64_t>(grid.x) <= kQueueTasks4;
+    if (queue != nullptr && a.split_tokens != 0 &&
+        static_cast<int64_t>(grid.x) <= kQueueTasks) {
+      int device = 0, cus = 0;
+      hipError_t e = hipGetDevice(&device);
+      if (e == hipSuccess)
+        e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device);
+      if (e != hipSuccess) return e;
+      const int64_t units = static_cast<int64_t>(grid.x) * grid.y * grid.z;
+      const int64_t cap = (cus > 0 ? cus : 1) * (four ? 2 : 1);
+      const unsigned wgs = static_cast<unsigned>(units < cap ? units : cap);
+      if (four)
+        hipLaunchKernelGGL((history_queue_kernel<4, kQueueTasks4>), dim3(wgs), dim3(4 * kWave), 0,
+                           stream, a, queue, static_cast<int32_t>(grid.x));
+      else
+        hipLaunchKernelGGL((history_queue_kernel<8, kQueueTasks>), dim3(wgs), dim3(kThreadsW8), 0,
+                           stream, a, queue, static_cast<int32_t>(grid.x));
+    } else if (four) {
+      hipLaunchKernelGGL(history_w8_kernel<4>, grid, dim3(4 * kWave), 0, stream, a);
+    } else {
+      hipLaunchKernelGGL(history_w8_kernel<8>, grid, dim3(kThreadsW8), 0, stream, a);
+    }
   }
   return hipGetLastError();
 }

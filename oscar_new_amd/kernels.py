@@ -548,8 +548,9 @@ def history_rows(meta, layout, hq):
 def history_kernel_name(meta, layout, hq, tokens=0, split_tokens=0, use_queue=True):
     """The history-branch kernel ``attention_partials`` launches for ``tokens`` query rows:
     the paired kernel up to 8 rows per task, the one-tile kernel up to 16, then the
-    eight-wavefront kernel, as a work queue with token-bounded splits (``use_queue``, a grid
-    of at most 2048 task rows)."""
+    two-row-group kernel (four wavefronts per workgroup up to 512 task rows, eight above), as
+    a work queue with token-bounded splits (``use_queue``, a grid of at most 2048 task
+    rows)."""
     rows = history_rows(meta, layout, hq)
     if rows <= 8:
         return "history_pair_kernel"
