@@ -628,10 +628,11 @@ def in_step_launch(impl, w, layers, splits, split_tokens):
     """The launch the layer step makes for its history branch, as ``impl.forward`` makes it:
     ``(kernel name, algorithmic bytes, fn(i))``, fn(i) launching it on layer i's cache.
 
-    With the pre-attention roles in the history launch (up to 8 query rows per task) that is
-    ``history_pre`` (its workgroups rotate the query rows, run the BF16 branch and the K/V
-    INT2 store beside the INT2 stream); otherwise the step runs the pre-attention launch first
-    and this is the history branch alone (``attention_partials``)."""
+    With the pre-attention roles in the history launch (up to 8 query rows per task, or the
+    17-32-row work queue with token-bounded splits) that is ``history_pre`` (its workgroups
+    run the BF16 branch and the K/V INT2 store beside the INT2 stream); otherwise the step
+    runs the pre-attention launch first and this is the history branch alone
+    (``attention_partials``)."""
     from oscar_new_amd import kernels
 
     views = [w.layout.tensor_views(c) for c in layers]
@@ -640,13 +641,17 @@ def in_step_launch(impl, w, layers, splits, split_tokens):
     alg = algorithmic_bytes(w)
     hist = alg.int2 + ntok * 6 * 256 * 2 + alg.table + split_partial_bytes(w, splits,
                                                                          split_tokens)
-    if impl._roles_share_history_launch(meta):
+    queue = impl._queue_roles(meta, split_tokens, ntok)
+    if impl._roles_share_history_launch(meta) or queue:
         rows = ntok * 6
         # + the BF16 branch (window and current K/V rows, its partial rows), the step's INT2
         # slots and R_k / R_v.
         extra = alg.bf16 + rows * 1028 + ntok * 136 + 2 * 256 * 256 * 2
         q_sync = None
-        if impl._q_roles():
+        if queue:
+            # The 17-32-row work queue with the roles as units of its own.
+            name, qrot = "history_queue_pre_kernel", kernels.rotate(w.q, impl.rk_cols)
+        elif impl._q_roles():
             # + the rotation roles' rotated rows (written, then read by the history rows).
             name = "history_pre_q_kernel"
             extra += ntok * 6 * 256 * 2

@@ -328,6 +328,35 @@ int oscar_history_pre(const void* query_rot, int64_t r_s0, int64_t r_s1, int64_t
                       void* stream);
 
 /*
+ * history_pre_queue -- oscar_history_pre for 17-32 query rows per task (MTP verification:
+ * query_tile x hq / kv_heads rows): the history branch as the work queue of token-bounded
+ * (task, split) units (split_tokens != 0; at most 512 task rows, `programs`) with the BF16
+ * branch of each (task, kv head) and the K/V store as units of the queue. No reference
+ * counterpart as one call: it replaces backend.py:171-173 and 211-222 beside the history
+ * attention_partials of backend.py:195-205 for these steps, with the bits of
+ * oscar_pre_attention (without its q rotation) and oscar_attention_partials (raw = 0, with the
+ * same queue counters). query_rot: the rotated query (required). queue_counters: int32 [2],
+ * zero at rest and left zero, as for oscar_attention_partials. Other rows per task, or
+ * split_tokens == 0, or more task rows: OSCAR_E_UNSUPPORTED. Calls that overlap on one
+ * device must not share the counters.
+ */
+int oscar_history_pre_queue(const void* query_rot, int64_t r_s0, int64_t r_s1, int64_t r_s2,
+                            const void* query, int64_t q_s0, int64_t q_s1, const void* key,
+                            int64_t k_s0, int64_t k_s1, const void* value, int64_t v_s0,
+                            int64_t v_s1, void* history, int64_t history_bytes,
+                            const void* window, int64_t window_elems, const int32_t* qstarts,
+                            const int32_t* seq_lens, const int32_t* block_tables,
+                            int64_t table_stride, int64_t table_columns, const int32_t* counts,
+                            const int32_t* tasks, const int32_t* task_count, int64_t n,
+                            int64_t hq, int64_t programs, int32_t splits, int32_t block_n,
+                            int32_t query_tile, int32_t max_query_len, float scale,
+                            int32_t split_tokens, const void* rk_t, const void* rv_t,
+                            const int64_t* slots, const oscar_clip* clip,
+                            const oscar_layout* layout, float* partials, float* lse,
+                            float* raw_partials, float* raw_lse, int32_t* queue_counters,
+                            void* stream);
+
+/*
  * history_pre_q -- oscar_history_pre with the q rotation of backend.py:195 as role workgroups
  * of the same launch (no reference counterpart as one call; it replaces oscar_rotate(query,
  * R_k) followed by oscar_history_pre, with their bits). qrot: bf16 [n, hq, 256] contiguous,

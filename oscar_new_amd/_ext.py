@@ -147,6 +147,16 @@ SIGNATURES = {
         _P, _P, _P, POINTER(OscarClip), POINTER(OscarLayout),  # rk_t, rv_t, slots, clip, layout
         _P, _P, _P, _P, _P,  # partials, lse, raw partials, raw lse, stream
     ],
+    "oscar_history_pre_queue": [
+        _P, _I64, _I64, _I64,  # query (rotated)
+        _P, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64,  # query, key, value (+ row strides)
+        _P, _I64, _P, _I64,  # history, bytes, window, elems
+        _P, _P, _P, _I64, _I64,  # qstarts, seq_lens, block_tables, stride, columns
+        _P, _P, _P,  # counts, tasks, task_count
+        _I64, _I64, _I64, _I32, _I32, _I32, _I32, _F, _I32,  # n hq programs splits bn qt mql scale st
+        _P, _P, _P, POINTER(OscarClip), POINTER(OscarLayout),  # rk_t, rv_t, slots, clip, layout
+        _P, _P, _P, _P, _P, _P,  # partials, lse, raw partials, raw lse, queue counters, stream
+    ],
     "oscar_history_pre_q": [
         _P, _P,  # qrot (out), qsync
         _P, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64,  # query, key, value (+ row strides)

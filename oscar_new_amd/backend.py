@@ -249,6 +249,17 @@ class OscarAttentionImpl:
                 and layout is not None
                 and kernels.history_pre_supported(meta, layout, self.num_heads))
 
+    def _queue_roles(self, meta, split_tokens, tokens):
+        """Whether the step's history launch is the 17-32-row work queue carrying the BF16
+        branch and the K/V store as units of its own (MTP steps with token-bounded splits; the
+        q rotation stays a launch of its own)."""
+        layout = getattr(meta, "layout", None)
+        return (self.fused and self.overlap and not self.one_launch_post and not self.layer_step
+                and layout is not None and not self.rotate_in_history and not self.q_roles
+                and kernels.history_rows(meta, layout, self.num_heads) > 8
+                and kernels.history_pre_supported(meta, layout, self.num_heads, split_tokens,
+                                                  tokens))
+
     def partition_for(self, meta, tokens=None):
         """``(splits, split_tokens)`` of the history branch for a step of ``tokens`` query
         tokens (default ``meta.num_actual_tokens``). "device": ``choose_device_partition``
@@ -352,18 +363,20 @@ class OscarAttentionImpl:
                                splits, self.rk_t, self.rv_t, self.rv, rows, lse,
                                split_tokens=split_tokens)
             return
-        if (self.overlap and not self.one_launch_post
-                and kernels.history_pre_supported(meta, layout, self.num_heads)):
+        queue = self._queue_roles(meta, split_tokens, q.shape[0])
+        if queue or (self.overlap and not self.one_launch_post
+                     and kernels.history_pre_supported(meta, layout, self.num_heads)):
             # One launch holding the history branch (its workgroups rotate the query rows, or a
             # q rotation launch goes first) and, dispatched ahead of it, the BF16 branch and
             # the INT2 store (the history branch never reads the slots the store writes), then
             # post-attention.
             q_sync = None
-            if self._q_roles():
+            if self._q_roles() and not queue:
                 qrot = torch.empty(q.shape, dtype=torch.bfloat16, device=q.device)
                 q_sync = self.q_sync
             else:
-                qrot = None if self.rotate_in_history else kernels.rotate(q, self.rk_cols)
+                qrot = (None if self.rotate_in_history and not queue
+                        else kernels.rotate(q, self.rk_cols))
             hp, hl, rp, rl = kernels.history_pre(qrot, q, k, v, self.history, self.window, meta,
                                                  layout, self.scale, splits, self.rk_t,
                                                  self.rv_t, split_tokens=split_tokens,

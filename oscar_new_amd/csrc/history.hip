@@ -1002,11 +1002,16 @@ __global__ __launch_bounds__(kWaves * kWave, 8 / kWaves) void history_w8_kernel(
 // launch; the last workgroup to finish sets them to zero again, so graph replays reuse them.
 // Launches that overlap on one device must not share counters.
 constexpr int kQueueTasks = 2048;  // task rows the workgroup lists in LDS (eight wavefronts)
-constexpr int kQueueTasks4 = 512;  // the same with four wavefronts (80 KB of LDS)
 
-template <int kWaves, int kTasks>
-__global__ __launch_bounds__(kWaves * kWave, 8 / kWaves) void history_queue_kernel(
-    const AttnArgs a, int32_t* counters, int32_t programs) {
+// kRoles (four wavefronts): the step's pre-attention roles `pre` run as units of the queue,
+// each with the role code of the other launches (the same bits): the BF16 branch of each
+// (task, kv head), in two units of 16 rows, is claimed before any history unit (it is the
+// longest unit); the K/V store quads, short, are claimed after the last history unit, where
+// they fill the queue's tail (first: 2.3 us slower per c4 step). A role borrows the unit's LDS
+// (the ring and the query stage) and ends with a barrier.
+template <int kWaves, int kTasks, bool kRoles>
+__device__ __forceinline__ void history_queue_body(const AttnArgs& a, int32_t* counters,
+                                                   int32_t programs, const PreArgs* pre) {
   constexpr int kT = kWaves * kWave;
   __shared__ HistoryLdsW8<kWaves> lds;
   __shared__ int32_t s_full[kTasks + 1];  // full splits of the tasks before t
@@ -1075,13 +1080,32 @@ __global__ __launch_bounds__(kWaves * kWave, 8 / kWaves) void history_queue_kern
   if (threadIdx.x == 0) s_full[programs] = s_total[0];
   __syncthreads();
   const int full = s_total[0], used = s_total[1];
-  const int64_t units = (static_cast<int64_t>(full) + used) * heads;
+  // Roles: the BF16 branch of each (task, kv head) in two 16-row halves, then the K/V quads.
+  const int64_t roles = kRoles ? 2 * static_cast<int64_t>(pre->raw_wgs) + pre->kv_wgs : 0;
+  const int64_t units = (static_cast<int64_t>(full) + used) * heads + roles;
   for (;;) {
     if (threadIdx.x == 0) s_claim = atomicAdd(&counters[0], 1);
     __syncthreads();
-    const int64_t u = s_claim;
+    int64_t u = s_claim;
     __syncthreads();  // every lane has read the claim (and the previous unit is done)
     if (u >= units) break;
+    if constexpr (kRoles) {
+      const int64_t bf = 2 * static_cast<int64_t>(pre->raw_wgs);
+      const int64_t hist_units = units - roles;
+      if (u < bf || u >= bf + hist_units) {
+        uint8_t* role_lds = reinterpret_cast<uint8_t*>(&lds);
+        if (u < bf) {
+          const int r = static_cast<int>(u);
+          const int th = r >> 1;  // (task, kv head) as in the pre-attention launch
+          raw_block_staged<1>(pre->attn, th / heads, th % heads, 0, role_lds, 2, 16 * (r & 1));
+        } else {
+          kv_store_role(*pre, static_cast<int>(u - bf - hist_units), role_lds);
+        }
+        __syncthreads();  // the role's LDS is free for the next unit
+        continue;
+      }
+      u -= bf;
+    }
     const int head = static_cast<int>(u % heads);
     const int k = static_cast<int>(u / heads);
     int task, split;
@@ -1117,6 +1141,24 @@ __global__ __launch_bounds__(kWaves * kWave, 8 / kWaves) void history_queue_kern
       atomicExch(&counters[1], 0);
     }
   }
+}
+
+template <int kWaves, int kTasks>
+__global__ __launch_bounds__(kWaves * kWave, 8 / kWaves) void history_queue_kernel(
+    const AttnArgs a, int32_t* counters, int32_t programs) {
+  history_queue_body<kWaves, kTasks, false>(a, counters, programs, nullptr);
+}
+
+// The MTP step's history launch: the work queue with the pre-attention roles as its first
+// units (the counterpart of history_pre_kernel for 17-32 query rows per task).
+static_assert(2 * kRawLdsPerSlot <= sizeof(HistoryLdsW8<4>::ring) + sizeof(HistoryLdsW8<4>::qstage),
+              "a BF16 role's two ring slots fit the unit's ring and query stage");
+static_assert(16 * kHeadDim * 2 <= sizeof(HistoryLdsW8<4>::ring), "the K/V store role's tile fits");
+__global__ __launch_bounds__(4 * kWave, 2) void history_queue_pre_kernel(const AttnArgs a,
+                                                                         const PreArgs p,
+                                                                         int32_t* counters,
+                                                                         int32_t programs) {
+  history_queue_body<4, kQueueTasks4, true>(a, counters, programs, &p);
 }
 
 // ---------------------------------------------------------------- paired-token kernel
@@ -1835,6 +1877,19 @@ hipError_t launch_history(const AttnArgs& a, dim3 grid, int rows, hipStream_t st
       hipLaunchKernelGGL(history_w8_kernel<8>, grid, dim3(kThreadsW8), 0, stream, a);
     }
   }
+  return hipGetLastError();
+}
+
+hipError_t launch_history_queue_pre(const AttnArgs& a, const PreArgs& p, int32_t* queue,
+                                    int32_t programs, hipStream_t stream) {
+  int device = 0, cus = 0;
+  hipError_t e = hipGetDevice(&device);
+  if (e == hipSuccess)
+    e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device);
+  if (e != hipSuccess) return e;
+  const unsigned wgs = static_cast<unsigned>(2 * (cus > 0 ? cus : 1));  // two per CU
+  hipLaunchKernelGGL(history_queue_pre_kernel, dim3(wgs), dim3(4 * kWave), 0, stream, a, p,
+                     queue, programs);
   return hipGetLastError();
 }
 

@@ -159,4 +159,15 @@ constexpr int kQSyncPolls = 4096;
 hipError_t launch_history_pre(const AttnArgs& a, const PreArgs& p, int role_slices, dim3 grid,
                               bool rotate_query, hipStream_t stream);
 
+// Task rows of a four-wavefront history work queue (its task lists fit 80 KB of LDS with the
+// unit's ring, two workgroups per CU).
+constexpr int kQueueTasks4 = 512;
+
+// The history launch of a step with 17-32 query rows per task (history.hip): the work queue of
+// token-bounded history units (at most kQueueTasks4 task rows; `queue`: its two counters,
+// zero at rest) with the BF16 branch (p.raw_wgs units of (task, kv head)) and the K/V store
+// quads (p.kv_wgs) as units of the queue (the BF16 branch first, the K/V store last).
+hipError_t launch_history_queue_pre(const AttnArgs& a, const PreArgs& p, int32_t* queue,
+                                    int32_t programs, hipStream_t stream);
+
 }  // namespace oscar

@@ -294,6 +294,7 @@ struct RawSetup {
   int begin, end;
   u32x4 qb[RT][8];  // unrotated query as B operand of S^T = K Q^T: k-step m, d = 64 g + 8 m ..
   int qi_row[RT];
+  int row0 = 0;  // the task's first row of this workgroup's row tiles
 };
 
 // The unrotated query rows of the workgroup's row tiles (lane (n, g): row n + 16 rt, dims
@@ -303,7 +304,7 @@ __device__ __forceinline__ void raw_load_query(const AttnArgs& a, int head, int 
                                                RawSetup<RT>& s) {
 #pragma unroll
   for (int rt = 0; rt < RT; ++rt) {
-    const RowInfo ri = row_info(a, s.t, head, n + 16 * rt);
+    const RowInfo ri = row_info(a, s.t, head, s.row0 + n + 16 * rt);
     s.qi_row[rt] = ri.qi;
 #pragma unroll
     for (int m = 0; m < 8; ++m) s.qb[rt][m] = u32x4{0u, 0u, 0u, 0u};
@@ -372,7 +373,7 @@ __device__ __forceinline__ void raw_finish(const AttnArgs& a, const RawSetup<RT>
     const float den_n = row_sum(st.psum[rt]);
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
-      const int row = 16 * rt + 4 * g + v;
+      const int row = s.row0 + 16 * rt + 4 * g + v;
       const float den = fmaxf(__shfl(den_n, 4 * g + v, kWave), 1.0e-30f);
       const RowInfo ri = row_info(a, s.t, head, row);
       if (!ri.valid) continue;
@@ -390,7 +391,7 @@ __device__ __forceinline__ void raw_finish(const AttnArgs& a, const RawSetup<RT>
     }
     // LSE of row n (wavefront 0, lane group 0).
     if (wave == 0 && g == 0) {
-      const RowInfo ri = row_info(a, s.t, head, n + 16 * rt);
+      const RowInfo ri = row_info(a, s.t, head, s.row0 + n + 16 * rt);
       const float lse = row_lse(st.m[rt], den_n);
       if constexpr (kDirect) {
         if (ri.valid && a.direct_lse) a.direct_lse[ri.token * a.hq + ri.qhead] = lse;
@@ -514,15 +515,18 @@ __device__ __forceinline__ void raw_wait_blocks(int ahead) {
 // slots by DMA, up to `slots` blocks in flight. The arithmetic is raw_block's, block for
 // block: the same bits. The block loop is not unrolled: a launch runs this code cold, so its
 // size, not its instruction count, sets the time of the first block. Every thread of the
-// workgroup calls this; `lds` holds slots x kRawLdsPerSlot bytes.
+// workgroup calls this; `lds` holds slots x kRawLdsPerSlot bytes. `row0`: the task's first row
+// of the workgroup's RT row tiles (a task of more rows can be served 16 rows at a time: a row's
+// bits do not depend on the rows beside it).
 template <int RT, bool kDirect = false>
 __device__ __forceinline__ void raw_block_staged(const AttnArgs& a, int task, int head, int split,
-                                                 uint8_t* lds, int slots) {
+                                                 uint8_t* lds, int slots, int row0 = 0) {
   const int lane = threadIdx.x & 63;
   const int wave = uniform(threadIdx.x >> 6);
   const int n = lane & 15, g = lane >> 4;
   RawSetup<RT> s;
   if (!raw_setup<RT, false>(a, task, head, split, n, g, s)) return;
+  s.row0 = row0;
   State<RT, 4> st;
   state_init(st);
   const uint32_t base = lds_addr(lds);

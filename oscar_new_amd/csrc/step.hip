@@ -86,8 +86,10 @@ __global__ __launch_bounds__(kThreads, 2) void post_attention_kernel(const PostA
 // (post_rows_map: the row arithmetic of the other forms, the same bits). A workgroup reads
 // R_v once per 16 rows instead of once per 4, and the launch needs a quarter of the
 // workgroups of the 4-row form, whose rounds of latency set its time at these row counts.
+// One workgroup per CU is allowed its registers: the scanned merge of 16 rows with their
+// rotation operands needs more than 256 (two workgroups per CU spilled).
 template <int kMode>
-__global__ __launch_bounds__(kThreads, 2) void post_attention_tile_kernel(const PostArgs p) {
+__global__ __launch_bounds__(kThreads, 1) void post_attention_tile_kernel(const PostArgs p) {
   __shared__ __attribute__((aligned(16))) uint16_t s_h[16][kHeadDim];
   __shared__ float s_l[16];
   __shared__ GroupMergeLds group_lds;
@@ -239,7 +241,8 @@ extern "C" int oscar_pre_attention(
 namespace oscar {
 namespace {
 
-// oscar_history_pre and oscar_history_pre_q: `qrot_out` / `qsync` set (the latter) or NULL.
+// oscar_history_pre, oscar_history_pre_q and oscar_history_pre_queue: `qrot_out` / `qsync` set
+// (the second) or NULL; `queue` set (the third: 17-32 query rows per task) or NULL.
 int history_pre_common(
     const void* query_rot, int64_t r_s0, int64_t r_s1, int64_t r_s2, const void* query,
     int64_t q_s0, int64_t q_s1, const void* key, int64_t k_s0, int64_t k_s1, const void* value,
@@ -251,7 +254,7 @@ int history_pre_common(
     int32_t max_query_len, float scale, int32_t split_tokens, const void* rk_t,
     const void* rv_t, const int64_t* slots, const oscar_clip* clip, const oscar_layout* layout,
     float* partials, float* lse, float* raw_partials, float* raw_lse, void* qrot_out,
-    int32_t* qsync, void* stream) {
+    int32_t* qsync, int32_t* queue, void* stream) {
   if (n > 0 && (!raw_partials || !raw_lse)) return OSCAR_E_NULL;  // slice 0 is the BF16 branch
   PreArgs p;
   int64_t qrows = 0;
@@ -261,6 +264,24 @@ int history_pre_common(
                          query_tile, max_query_len, scale, rk_t, rv_t, history, history_bytes,
                          slots, clip, layout, raw_partials, raw_lse, qrot_out, &p, &qrows);
   if (st != OSCAR_OK) return st;
+  if (queue) {
+    // 17-32 rows per task: the work queue with the roles as units of its own; the rotated
+    // query is given, the split length token-bounded, the task rows within the queue's lists.
+    if (qrows <= 16 || qrows > 32 || qsync || split_tokens == 0 || programs > kQueueTasks4)
+      return OSCAR_E_UNSUPPORTED;
+    if (!query_rot) return OSCAR_E_NULL;
+    if (reinterpret_cast<uintptr_t>(queue) % 4) return OSCAR_E_ALIGN;
+    AttnArgs a;
+    int64_t hrows = 0;
+    st = make_attn_args(query_rot, r_s0, r_s1, r_s2, nullptr, 0, 0, 1, nullptr, 0, 0, 1, history,
+                        history_bytes, window, window_elems, qstarts, seq_lens, block_tables,
+                        table_stride, table_columns, counts, tasks, task_count, n, hq, programs,
+                        splits, block_n, query_tile, max_query_len, scale, 0, split_tokens,
+                        layout, partials, lse, &a, &hrows);
+    if (st != OSCAR_OK || n == 0) return st;
+    return static_cast<int>(launch_history_queue_pre(a, p, queue, static_cast<int32_t>(programs),
+                                                     as_stream(stream)));
+  }
   if (qrows > 8) return OSCAR_E_UNSUPPORTED;
   // query_rot == nullptr: the history workgroups rotate the query rows themselves.
   const bool q_roles = qsync != nullptr;
@@ -326,7 +347,28 @@ extern "C" int oscar_history_pre(
       history, history_bytes, window, window_elems, qstarts, seq_lens, block_tables,
       table_stride, table_columns, counts, tasks, task_count, n, hq, programs, splits, block_n,
       query_tile, max_query_len, scale, split_tokens, rk_t, rv_t, slots, clip, layout, partials,
-      lse, raw_partials, raw_lse, nullptr, nullptr, stream);
+      lse, raw_partials, raw_lse, nullptr, nullptr, nullptr, stream);
+}
+
+extern "C" int oscar_history_pre_queue(
+    const void* query_rot, int64_t r_s0, int64_t r_s1, int64_t r_s2, const void* query,
+    int64_t q_s0, int64_t q_s1, const void* key, int64_t k_s0, int64_t k_s1, const void* value,
+    int64_t v_s0, int64_t v_s1, void* history, int64_t history_bytes, const void* window,
+    int64_t window_elems, const int32_t* qstarts, const int32_t* seq_lens,
+    const int32_t* block_tables, int64_t table_stride, int64_t table_columns,
+    const int32_t* counts, const int32_t* tasks, const int32_t* task_count, int64_t n,
+    int64_t hq, int64_t programs, int32_t splits, int32_t block_n, int32_t query_tile,
+    int32_t max_query_len, float scale, int32_t split_tokens, const void* rk_t,
+    const void* rv_t, const int64_t* slots, const oscar_clip* clip, const oscar_layout* layout,
+    float* partials, float* lse, float* raw_partials, float* raw_lse, int32_t* queue_counters,
+    void* stream) {
+  if (!queue_counters) return OSCAR_E_NULL;
+  return oscar::history_pre_common(
+      query_rot, r_s0, r_s1, r_s2, query, q_s0, q_s1, key, k_s0, k_s1, value, v_s0, v_s1,
+      history, history_bytes, window, window_elems, qstarts, seq_lens, block_tables,
+      table_stride, table_columns, counts, tasks, task_count, n, hq, programs, splits, block_n,
+      query_tile, max_query_len, scale, split_tokens, rk_t, rv_t, slots, clip, layout, partials,
+      lse, raw_partials, raw_lse, nullptr, nullptr, queue_counters, stream);
 }
 
 extern "C" int oscar_history_pre_q(
@@ -346,7 +388,7 @@ extern "C" int oscar_history_pre_q(
       history_bytes, window, window_elems, qstarts, seq_lens, block_tables, table_stride,
       table_columns, counts, tasks, task_count, n, hq, programs, splits, block_n, query_tile,
       max_query_len, scale, split_tokens, rk_t, rv_t, slots, clip, layout, partials, lse,
-      raw_partials, raw_lse, qrot, qsync, stream);
+      raw_partials, raw_lse, qrot, qsync, nullptr, stream);
 }
 
 namespace oscar {

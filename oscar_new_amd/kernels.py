@@ -569,10 +569,22 @@ def history_post_supported(meta, layout, hq, splits, tokens=None):
     return history_rows(meta, layout, hq) <= 8 and 1 <= splits <= 16 and small
 
 
-def history_pre_supported(meta, layout, hq):
+# Task rows of the four-wavefront history work queue (the MTP step's history launch).
+QUEUE_PRE_TASKS = 512
+
+
+def history_pre_supported(meta, layout, hq, split_tokens=None, tokens=None):
     """Whether ``history_pre`` covers this batch: <= 8 query rows per task (the paired history
-    kernel and a one-tile BF16 branch)."""
-    return history_rows(meta, layout, hq) <= 8
+    kernel and a one-tile BF16 branch), or, given the launch's ``split_tokens`` and query
+    ``tokens``, 17-32 rows per task with token-bounded splits and at most QUEUE_PRE_TASKS task
+    rows (the work queue with the roles as units of its own)."""
+    rows = history_rows(meta, layout, hq)
+    if rows <= 8:
+        return True
+    if not 16 < rows <= 32 or not split_tokens or tokens is None:
+        return False
+    return attention_programs(int(tokens), meta.max_num_reqs,
+                              layout.config.queries_per_tile) <= QUEUE_PRE_TASKS
 
 
 def history_pre(query_rot, query, key, value, history, window, meta, layout, scale, splits,
@@ -590,12 +602,19 @@ def history_pre(query_rot, query, key, value, history, window, meta, layout, sca
     are done; ``q_sync[2]`` is non-zero after a launch in which a workgroup gave up waiting.
     ``query``/``key``/``value``: the step's unrotated rows. Returns ``(partials [n, hq, splits,
     256], lse [n, hq, splits], raw_partials [n, hq, 1, 256], raw_lse [n, hq, 1])``, all fp32.
+    17-32 query rows per task (MTP) run as the history work queue with the BF16 branch and
+    the K/V store as units of the queue (``query_rot`` given, token-bounded ``split_tokens``,
+    ``meta``'s queue counters as for ``attention_partials``).
     """
     _device_check(query_rot, query, key, value, history, window, rk_t, rv_t)
     n, hq, d = query.shape
     cfg = layout.config
-    if not history_pre_supported(meta, layout, hq):
-        raise ValueError("history_pre covers <= 8 query rows per task")
+    if not history_pre_supported(meta, layout, hq, split_tokens, n):
+        raise ValueError("history_pre covers <= 8 query rows per task, or 17-32 with "
+                         "token-bounded splits and at most 512 task rows")
+    queue = history_rows(meta, layout, hq) > 8
+    if queue and (query_rot is None or q_sync is not None):
+        raise ValueError("history_pre with 17-32 rows per task takes the rotated query")
     dev = query.device
     partials = torch.empty((n, hq, splits, d), dtype=torch.float32, device=dev)
     lse = torch.empty((n, hq, splits), dtype=torch.float32, device=dev)
@@ -626,8 +645,12 @@ def history_pre(query_rot, query, key, value, history, window, meta, layout, sca
     table = _int32(meta.block_tables, "block_tables")
     max_query_len = getattr(meta, "max_query_len", None)
     max_query_len = int(max_query_len) if isinstance(max_query_len, int) else 0
+    tail = ()
     if q_sync is not None:
         entry, lead = _ext.library().oscar_history_pre_q, (_ptr(query_rot), _ptr(q_sync))
+    elif queue:
+        entry, lead = _ext.library().oscar_history_pre_queue, (_ptr(query_rot), *rot_strides)
+        tail = (_ptr(queue_counters(meta, dev)),)
     else:
         entry, lead = _ext.library().oscar_history_pre, (_ptr(query_rot), *rot_strides)
     _ext.check(
@@ -642,7 +665,7 @@ def history_pre(query_rot, query, key, value, history, window, meta, layout, sca
             n, hq, programs, splits, cfg.block_n, cfg.queries_per_tile, max_query_len,
             float(scale), int(split_tokens), _ptr(rk_t), _ptr(rv_t), _ptr(meta.slot_mapping),
             clip_struct(cfg), layout_struct(layout), _ptr(partials), _ptr(lse),
-            _ptr(raw_partials), _ptr(raw_lse), _stream(query),
+            _ptr(raw_partials), _ptr(raw_lse), *tail, _stream(query),
         ),
         "history_pre",
     )

@@ -305,6 +305,73 @@ def test_history_pre_matches_single_entry_points(lengths, prefixes, split_tokens
     assert torch.equal(hist_a, hist_b)
 
 
+@pytest.mark.parametrize("lengths,prefixes,split_tokens", [
+    ([69, 263, 1804, 40], [65, 259, 1800, 36], 512),  # 4-token MTP, token-bounded splits
+    ([6000, 300, 4000, 2600], [5996, 296, 3996, 2596], -40),  # the device rule, 40-slot budget
+])
+def test_history_pre_queue_matches_single_entry_points(lengths, prefixes, split_tokens):
+    # 24 rows per task: the history work queue with the BF16 branch and the K/V store as its
+    # units, against pre_attention + attention_partials; two calls (the counters the
+    # first leaves must be zero for the second).
+    print(f"[history_pre queue] {lengths} split_tokens {split_tokens}", flush=True)
+    c = _case(lengths, prefixes, seed=6)
+    meta, layout = c.meta, c.layout
+    n = c.q.shape[0]
+    assert kernels.history_rows(meta, layout, 6) == 24
+    assert kernels.history_pre_supported(meta, layout, 6, split_tokens, n)
+    splits = 8
+    hist_a, win_a = layout.tensor_views(_views(c.raw.clone(), layout))
+    hist_b, win_b = layout.tensor_views(_views(c.raw.clone(), layout))
+    rk_t, rv_t = c.rk.T.contiguous(), c.rv.T.contiguous()
+    qrot = kernels.rotate(c.q, rk_t.T)
+    for _ in range(2):
+        hist_a.copy_(hist_b)
+        hp, hl, rp, rl = kernels.history_pre(qrot, c.q, c.k, c.v, hist_a, win_a, meta, layout,
+                                             1 / 16, splits, rk_t, rv_t,
+                                             split_tokens=split_tokens)
+    with pytest.raises(ValueError):  # the queue form takes the rotated query
+        kernels.history_pre(None, c.q, c.k, c.v, hist_a, win_a, meta, layout, 1 / 16, splits,
+                            rk_t, rv_t, split_tokens=split_tokens)
+    hp_ref, hl_ref = kernels.attention_partials(qrot, c.k, c.v, hist_b, win_b, meta, layout,
+                                                1 / 16, splits, False, split_tokens=split_tokens)
+    _, rp_ref, rl_ref = kernels.pre_attention(c.q, c.k, c.v, hist_b, win_b, meta, layout, 1 / 16,
+                                              rk_t, rv_t)
+    torch.cuda.synchronize()
+    assert kernels.queue_counters(meta, c.q.device)[:2].tolist() == [0, 0]
+    live = hl_ref > -float("inf")
+    assert torch.equal(hl, hl_ref)
+    assert torch.equal(hp[live], hp_ref[live])
+    assert torch.equal(rp, rp_ref)
+    assert torch.equal(rl, rl_ref)
+    assert torch.equal(hist_a, hist_b)
+
+
+def test_mtp_step_with_queue_roles_is_bitwise_the_single_launch_step():
+    # The MTP layer step whose history launch carries the roles (token-bounded splits), and the
+    # same step with the roles in a pre-attention launch, against the reference order.
+    c = _case([69, 263, 1804, 2600], [65, 259, 1800, 2596], seed=7)
+    outs = {}
+    for form in ("single", "fused", "fused_serial"):
+        n = c.q.shape[0]
+        raw = c.raw.clone()
+        k_cache, v_cache = _views(raw, c.layout)
+        impl = OscarAttentionImpl.standalone(6, 256, 1 / 16, 1, c.layout.config,
+                                             fused=form != "single",
+                                             overlap=form != "fused_serial")
+        impl.set_rotations(c.rk, c.rv)
+        impl.partition_for = lambda meta, tokens=None: (8, 512)
+        if form == "fused":
+            assert impl._queue_roles(c.meta, 512, n)
+        c.meta.merged_lse = torch.full((n, 6), 7.0, device=DEV)
+        out = torch.full((n, 6 * 256), 3.0, device=DEV, dtype=torch.bfloat16)
+        impl.forward(None, c.q, c.k, c.v, (k_cache, v_cache), c.meta, out)
+        torch.cuda.synchronize()
+        outs[form] = (out.view(torch.int16).cpu(), c.meta.merged_lse.cpu(), raw.cpu())
+    for form in ("fused", "fused_serial"):
+        for a, b in zip(outs["single"], outs[form]):
+            assert torch.equal(a, b), form
+
+
 def test_post_attention_matches_single_entry_points():
     c = _case([69, 263, 1804], [65, 260, 1800], seed=5)
     meta, layout = c.meta, c.layout
