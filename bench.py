@@ -518,6 +518,7 @@ TRAFFIC_PROFILES = {  # rocprof PMC summaries (FETCH_SIZE / WRITE_SIZE runs) per
     ("history_pair_kernel", "c3"): "history_kernel_c3_traffic.txt",
     ("history_pair_kernel", "c5"): "history_kernel_c5_traffic.txt",
     ("history_queue_kernel", "c4"): "history_queue_kernel_c4_traffic.txt",
+    ("history_queue_pre_kernel", "c4"): "history_queue_pre_kernel_c4_traffic.txt",
 }
 
 

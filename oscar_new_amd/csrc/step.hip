@@ -86,10 +86,12 @@ __global__ __launch_bounds__(kThreads, 2) void post_attention_kernel(const PostA
 // (post_rows_map: the row arithmetic of the other forms, the same bits). A workgroup reads
 // R_v once per 16 rows instead of once per 4, and the launch needs a quarter of the
 // workgroups of the 4-row form, whose rounds of latency set its time at these row counts.
-// One workgroup per CU is allowed its registers: the scanned merge of 16 rows with their
-// rotation operands needs more than 256 (two workgroups per CU spilled).
+// The one-round merge (one split) keeps two workgroups per CU (256 registers, a few spilled);
+// the scanned merge of 16 rows with their rotation operands needs more than 256 and runs one
+// workgroup per CU (two spilled about a hundred registers).
 template <int kMode>
-__global__ __launch_bounds__(kThreads, 1) void post_attention_tile_kernel(const PostArgs p) {
+__global__ __launch_bounds__(kThreads, kMode == kMergeOneRound ? 2 : 1) void
+post_attention_tile_kernel(const PostArgs p) {
   __shared__ __attribute__((aligned(16))) uint16_t s_h[16][kHeadDim];
   __shared__ float s_l[16];
   __shared__ GroupMergeLds group_lds;
