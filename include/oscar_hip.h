@@ -86,6 +86,7 @@ int oscar_rotate(const void* x, int64_t n, int64_t h, int64_t d, int64_t x_s0, i
  * pack key_rot[t, h] to bytes [0, 68) and value_rot[t, h] to bytes [68, 136) of the
  * 160-byte slot at layout slot_offset(slots[t], h). Bytes 136..159 are never written.
  * key_rot/value_rot: contiguous bf16 [n, H, 256]; history: K stripe bytes.
+ * n * H must be below 2^31 (OSCAR_E_SHAPE otherwise).
  */
 int oscar_store_int2(const void* key_rot, const void* value_rot, int64_t n, void* history,
                      int64_t history_bytes, const int64_t* slots, const int32_t* counts,

@@ -34,6 +34,7 @@ int make_layout(const oscar_layout* in, Layout* out) {
   out->ring = in->ring_tokens;
   out->bpp_div = make_fastdiv(static_cast<uint32_t>(out->bpp));
   out->ring_div = make_fastdiv(static_cast<uint32_t>(out->ring));
+  out->bp_div = make_fastdiv(static_cast<uint32_t>(bp));
   return OSCAR_OK;
 }
 

@@ -188,7 +188,19 @@ struct Layout {
   int32_t slot_bytes, vector_bytes, sink, recent, ring;
   FastDiv bpp_div;
   FastDiv ring_div;
+  FastDiv bp_div;  // division by bp (slot -> page)
 };
+
+// Byte offset of slot `slot`, kv head `head` in the paged INT2 history: page slot / bp, token
+// slot mod bp within it (layout.py:9-95 slot geometry). Slots below 2^32 take the
+// multiply-shift division.
+__device__ __forceinline__ int64_t slot_offset(const Layout& L, int64_t slot, int head) {
+  const int64_t page = static_cast<uint64_t>(slot) < (1ull << 32)
+                           ? static_cast<int64_t>(fastdiv(static_cast<uint32_t>(slot), L.bp_div))
+                           : slot / L.bp;
+  const int64_t within = slot - page * L.bp;
+  return page * L.page_bytes + (within * L.kv_heads + head) * L.slot_bytes;
+}
 
 // Returns OSCAR_OK or an argument error code.
 int make_layout(const oscar_layout* in, Layout* out);

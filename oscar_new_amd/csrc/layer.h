@@ -115,9 +115,7 @@ __device__ __forceinline__ void store_int2_row(const AttnArgs& a, const LayerArg
   if (token < 0 || token >= a.counts[1]) return;
   const int64_t slot = l.slots[token];
   if (slot < 0) return;
-  const int64_t page = slot / a.L.bp;
-  const int64_t within = slot - page * a.L.bp;
-  const int64_t base = page * a.L.page_bytes + (within * a.L.kv_heads + head) * a.L.slot_bytes;
+  const int64_t base = slot_offset(a.L, slot, head);
   if (base + 2 * a.L.vector_bytes > a.history_bytes) return;
   quantize_store(x, l.mode, is_v ? l.v_ratio : l.k_ratio, is_v ? l.v_factor : l.k_factor,
                  l.history + base + (is_v ? a.L.vector_bytes : 0));

@@ -95,9 +95,7 @@ __device__ __forceinline__ void kv_store_role(const PreArgs& p, int r, uint8_t* 
   __syncthreads();
   // Same skips as store_int2 (kernels.py:168-169 and the buffer bound).
   if (!live || slot < 0) return;
-  const int64_t page = slot / a.L.bp;
-  const int64_t within = slot - page * a.L.bp;
-  const int64_t base = page * a.L.page_bytes + (within * a.L.kv_heads + head) * a.L.slot_bytes;
+  const int64_t base = slot_offset(a.L, slot, head);
   if (base + 2 * a.L.vector_bytes > p.history_bytes) return;
   const uint2 raw = *reinterpret_cast<const uint2*>(tile_lds + rr * kHeadDim + lane * 4);
   const float x[4] = {bf16_to_float(raw.x & 0xffffu), bf16_to_float(raw.x >> 16),

@@ -18,17 +18,11 @@ namespace oscar {
 // rounded on its own, as numpy and torch do on the CPU).
 
 // BASELINE `search` clip factors: f32(0.6 + 0.4*i/7), evaluated in double then rounded.
+// The same eight values as one FMA: fl(i * f32(0.4/7) + f32(0.6)) for i = 0..7.
+constexpr float kSearchFactorStep = static_cast<float>(0.4 / 7.0);
+constexpr float kSearchFactorBase = static_cast<float>(0.6);
 __device__ __forceinline__ float search_factor(int i) {
-  switch (i) {
-    case 0: return static_cast<float>(0.6 + 0.4 * 0 / 7.0);
-    case 1: return static_cast<float>(0.6 + 0.4 * 1 / 7.0);
-    case 2: return static_cast<float>(0.6 + 0.4 * 2 / 7.0);
-    case 3: return static_cast<float>(0.6 + 0.4 * 3 / 7.0);
-    case 4: return static_cast<float>(0.6 + 0.4 * 4 / 7.0);
-    case 5: return static_cast<float>(0.6 + 0.4 * 5 / 7.0);
-    case 6: return static_cast<float>(0.6 + 0.4 * 6 / 7.0);
-    default: return static_cast<float>(0.6 + 0.4 * 7 / 7.0);
-  }
+  return __builtin_fmaf(static_cast<float>(i), kSearchFactorStep, kSearchFactorBase);
 }
 
 __device__ __forceinline__ int wave_count_ge(const uint32_t key[4], uint32_t t) {
@@ -79,13 +73,27 @@ struct Quantized {
   int code[4];
 };
 
+// x / 3 correctly rounded (fl(x / 3), as IEEE division gives it) for every finite x >= 0:
+// q0 = fl(x * fl(1/3)), the residual x - 3 q0 exact in one FMA, one correction FMA. The
+// identity was checked for all 2^31 non-negative finite floats on the CPU.
+__device__ __forceinline__ float div3(float x) {
+  constexpr float kThird = 1.0f / 3.0f;
+  const float q0 = x * kThird;
+  const float r = __builtin_fmaf(-q0, 3.0f, x);
+  return __builtin_fmaf(r, kThird, q0);
+}
+
+// Reciprocal of a scale (an fp16 value, at least 2^-14) within one ulp (v_rcp_f32).
+__device__ __forceinline__ float scale_rcp(float s) { return __builtin_amdgcn_rcpf(s); }
+
 // Codes, scale and zero of clipped values whose minimum and maximum over the vector are mn and
 // mx (tests/oracle.py:15-17): code = clamp(trunc(fl(fl(x - zero) / scale) + 0.5), 0, 3). The
-// quotient is taken through the correctly rounded reciprocal of the (uniform) scale: within
-// [0.5, 3.5] it differs from the correctly rounded quotient by less than 1.2e-6, so a value of
-// y = q + 0.5 further than 2^-16 from 1, 2 and 3 truncates to the same code. If any lane has a
-// value that close, the wavefront redoes its quotients with IEEE division.
-// The codes of quantize_clipped for q.zf, q.sf and r = 1 / q.sf (correctly rounded).
+// quotient is taken through a reciprocal r of the (uniform) scale within one ulp of 1 / scale:
+// for y in [0.5, 3.5], fl(fl(d r) + 0.5) differs from fl(fl(d / scale) + 0.5) by at most
+// 3 (2^-23 + 2 * 2^-24) + 2^-22 < 1.2e-6, so a value of y = q + 0.5 further than 2^-16 from 1,
+// 2 and 3 truncates to the same code. If any lane has a value that close, the wavefront redoes
+// its quotients with IEEE division.
+// The codes of quantize_clipped for q.zf, q.sf and r = scale_rcp(q.sf).
 __device__ __forceinline__ void quantize_codes(const float xc[4], float r, Quantized& q) {
 #pragma clang fp contract(off)
   float y[4];
@@ -112,13 +120,13 @@ __device__ __forceinline__ void quantize_codes(const float xc[4], float r, Quant
 __device__ __forceinline__ Quantized quantize_clipped(const float xc[4], float mn, float mx) {
 #pragma clang fp contract(off)
   Quantized q;
-  float spread = (mx - mn) / 3.0f;
+  float spread = div3(mx - mn);
   spread = spread < 6.103515625e-05f ? 6.103515625e-05f : spread;
   q.zero = float_to_f16_bits(mn);
   q.scale = float_to_f16_bits(spread);
   q.zf = f16_bits_to_float(q.zero);
   q.sf = f16_bits_to_float(q.scale);
-  quantize_codes(xc, 1.0f / q.sf, q);
+  quantize_codes(xc, scale_rcp(q.sf), q);
   return q;
 }
 
@@ -140,17 +148,18 @@ __device__ __forceinline__ float candidate_sq(const float x[4], float tc, float 
   const float zf = lane_value(zc, i), sf = lane_value(sc, i), r = lane_value(rc, i);
   if constexpr (!kExact) {
     // Fast pass (within search_best's margin of the exact value): no clip (a clipped value's
-    // code is 0 or 3 either way, since z ~ -t or t - z ~ 3 s), and err = (x - z) - c s (c s is
-    // exact: c < 4 and s is an fp16 value) instead of x - fl(c s + z).
-    float sq[4];
+    // code is 0 or 3 either way, since z ~ -t or t - z ~ 3 s), err = (x - z) - c s (c s is
+    // exact: c < 4 and s is an fp16 value) instead of x - fl(c s + z), and the four squares
+    // accumulated by FMA.
+    float acc = 0.f;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const float d = x[e] - zf;
       const float c = __builtin_amdgcn_fmed3f(truncf(__builtin_fmaf(d, r, 0.5f)), 0.0f, 3.0f);
       const float err = __builtin_fmaf(-c, sf, d);
-      sq[e] = err * err;
+      acc = __builtin_fmaf(err, err, acc);
     }
-    return (sq[0] + sq[1]) + (sq[2] + sq[3]);
+    return acc;
   }
   const float t = lane_value(tc, i);
   float xi[4], y[4];
@@ -192,8 +201,8 @@ __device__ __forceinline__ float candidate_sq(const float x[4], float tc, float 
 // A reciprocal-product code differs from the exact one only for a value within about 2^-16 s
 // of a code boundary, i.e. of the midpoint of two decoded values, where the two squared errors
 // differ by at most s (2^-14 s + 2^-21 |z|); the fast error's different rounding moves each
-// squared error by at most 2^-20 m (2 m + 3 s) (m = max |x|); over 256 values and the tree's
-// rounding that bounds each fast MSE within
+// squared error by at most 2^-20 m (2 m + 3 s) (m = max |x|); over 256 values, the per-lane FMA
+// chain and the tree's rounding (at most 9 roundings per term), that bounds each fast MSE within
 // M = 2^-5 s^2 + 2^-12 s |z| + 2^-18 MSE + 2^-10 m (m + s) of the exact one (twice the bound). If no other candidate's interval reaches the fast minimum's, that minimum is
 // the exact one; otherwise the exact pass decides. Same result as the exact pass alone.
 __device__ __forceinline__ int search_best(const float x[4], float tc, float zc, float sc,
@@ -269,17 +278,13 @@ __device__ __forceinline__ void quantize_store(const float x[4], int mode, float
     // The uniform values of candidate i (threshold, fp16 zero and scale, 1 / scale: the
     // arithmetic of quantize_clipped) are computed once, by lane i, and read back per
     // candidate, instead of by every lane for every candidate.
-    const int ci = lane & 7;
-    float fc = search_factor(0);
-#pragma unroll
-    for (int i = 1; i < 8; ++i) fc = ci == i ? search_factor(i) : fc;
-    const float tc = maxabs * fc;
+    const float tc = maxabs * search_factor(lane & 7);
     const float lo = clamp1(mn, tc), hi = clamp1(mx, tc);
-    float spread = (hi - lo) / 3.0f;
+    float spread = div3(hi - lo);
     spread = spread < 6.103515625e-05f ? 6.103515625e-05f : spread;
     const float zc = f16_bits_to_float(float_to_f16_bits(lo));
     const float sc = f16_bits_to_float(float_to_f16_bits(spread));
-    const float rc = 1.0f / sc;
+    const float rc = scale_rcp(sc);
     const int best = search_best(x, tc, zc, sc, rc, maxabs, lane);
     // The winner's threshold, zero and scale are the values its lane computed above (those of
     // quantize_clipped on the clipped extremes), so only its codes are left to compute.

@@ -30,22 +30,22 @@ struct StoreArgs {
   Layout L;
   int32_t mode;
   float k_ratio, v_ratio, k_factor, v_factor;
+  FastDiv h_div;  // division by kv_heads (store_int2_kernel)
 };
 
 // Two rows per workgroup; wavefront 2r+0 handles K of row r, 2r+1 handles V.
 __global__ __launch_bounds__(kThreads) void store_int2_kernel(const StoreArgs a) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  // The row, its token, slot and byte offset are wavefront-uniform (scalar registers).
+  const int lane = threadIdx.x & 63, wave = uniform(static_cast<int>(threadIdx.x >> 6));
   const int64_t row = static_cast<int64_t>(blockIdx.x) * 2 + (wave >> 1);
   const int is_v = wave & 1;
   if (row >= a.rows) return;
-  const int64_t token = row / a.L.kv_heads;
-  const int head = static_cast<int>(row - token * a.L.kv_heads);
-  if (token >= a.counts[1]) return;
+  const uint32_t token = fastdiv(static_cast<uint32_t>(row), a.h_div);  // rows < 2^31
+  const int head = static_cast<int>(row - static_cast<int64_t>(token) * a.L.kv_heads);
+  if (static_cast<int64_t>(token) >= a.counts[1]) return;
   const int64_t slot = a.slots[token];
   if (slot < 0) return;
-  const int64_t page = slot / a.L.bp;
-  const int64_t within = slot - page * a.L.bp;
-  const int64_t base = page * a.L.page_bytes + (within * a.L.kv_heads + head) * a.L.slot_bytes;
+  const int64_t base = slot_offset(a.L, slot, head);
   if (base + 2 * a.L.vector_bytes > a.history_bytes) return;
   const uint16_t* src = (is_v ? a.v : a.k) + row * kHeadDim + lane * 4;
   const uint2 raw = *reinterpret_cast<const uint2*>(src);
@@ -115,9 +115,7 @@ void rotate_store_kernel(const RotateStoreArgs a) {
   __syncthreads();
   // Same skips as store_int2_kernel (kernels.py:168-169 and the buffer bound).
   if (!live || slot < 0) return;
-  const int64_t page = slot / st.L.bp;
-  const int64_t within = slot - page * st.L.bp;
-  const int64_t base = page * st.L.page_bytes + (within * h + head) * st.L.slot_bytes;
+  const int64_t base = slot_offset(st.L, slot, head);
   if (base + 2 * st.L.vector_bytes > st.history_bytes) return;
   const uint2 raw = *reinterpret_cast<const uint2*>(s_rot + wave * kHeadDim + lane * 4);
   const float x[4] = {bf16_to_float(raw.x & 0xffffu), bf16_to_float(raw.x >> 16),
@@ -148,10 +146,7 @@ __global__ __launch_bounds__(kThreads) void unpack_kernel(const UnpackArgs a) {
   const int64_t slot = a.slots[token];
   uint32_t lo = 0, hi = 0;
   if (slot >= 0) {
-    const int64_t page = slot / a.L.bp;
-    const int64_t within = slot - page * a.L.bp;
-    const int64_t base = page * a.L.page_bytes + (within * h + head) * a.L.slot_bytes +
-                         is_v * a.L.vector_bytes;
+    const int64_t base = slot_offset(a.L, slot, head) + is_v * a.L.vector_bytes;
     if (base + a.L.vector_bytes <= a.history_bytes) {
       const uint8_t* p = a.history + base;
       const uint32_t byte = p[lane];
@@ -191,6 +186,8 @@ extern "C" int oscar_store_int2(const void* key_rot, const void* value_rot, int6
   a.k = static_cast<const uint16_t*>(key_rot);
   a.v = static_cast<const uint16_t*>(value_rot);
   a.rows = n * a.L.kv_heads;
+  if (a.rows > 0x7fffffffll) return OSCAR_E_SHAPE;
+  a.h_div = make_fastdiv(static_cast<uint32_t>(a.L.kv_heads));
   a.history = static_cast<uint8_t*>(history);
   a.history_bytes = history_bytes;
   a.slots = slots;
