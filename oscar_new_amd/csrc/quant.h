@@ -25,6 +25,55 @@ __device__ __forceinline__ float search_factor(int i) {
   return __builtin_fmaf(static_cast<float>(i), kSearchFactorStep, kSearchFactorBase);
 }
 
+// Minimum and maximum of the wavefront's 256 finite values through order-preserving unsigned
+// keys (a larger float has a larger key, -0 below +0): integer min / max need no NaN
+// canonicalization, so the lane exchanges fold into them.
+__device__ __forceinline__ uint32_t order_key(float x) {
+  const uint32_t b = __float_as_uint(x);
+  return b ^ (static_cast<uint32_t>(static_cast<int32_t>(b) >> 31) | 0x80000000u);
+}
+__device__ __forceinline__ float key_value(uint32_t k) {
+  return __uint_as_float(k ^ ((k >> 31) ? 0x80000000u : 0xffffffffu));
+}
+__device__ __forceinline__ void wave_min_max(const float x[4], float& mn, float& mx) {
+  uint32_t k[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) k[i] = order_key(x[i]);
+  uint32_t lo = min(min(k[0], k[1]), min(k[2], k[3]));
+  uint32_t hi = max(max(k[0], k[1]), max(k[2], k[3]));
+  auto lo_step = [&](auto ctrl) {
+    lo = min(lo, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(
+                     -1, static_cast<int>(lo), decltype(ctrl)::value, 0xF, 0xF, false)));
+    hi = max(hi, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(
+                     0, static_cast<int>(hi), decltype(ctrl)::value, 0xF, 0xF, false)));
+  };
+  lo_step(std::integral_constant<int, kDppQuadXor1>{});
+  lo_step(std::integral_constant<int, kDppQuadXor2>{});
+  lo_step(std::integral_constant<int, kDppRowHalfMirror>{});
+  lo_step(std::integral_constant<int, kDppRowMirror>{});
+  auto rl = [](uint32_t v, int l) {
+    return static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), l));
+  };
+  lo = min(min(rl(lo, 0), rl(lo, 16)), min(rl(lo, 32), rl(lo, 48)));
+  hi = max(max(rl(hi, 0), rl(hi, 16)), max(rl(hi, 32), rl(hi, 48)));
+  mn = key_value(lo);
+  mx = key_value(hi);
+}
+
+// Lane kLane's value in every lane through the LDS crossbar (ds_bpermute), for values that
+// feed VALU operations anyway: three of them take one VALU move (the byte address) instead of
+// three v_readlane. The address is materialized by asm so that the compiler does not turn a
+// constant-index permute back into v_readlane.
+template <int kLane>
+__device__ __forceinline__ int bcast_addr() {
+  int addr;
+  asm("v_mov_b32 %0, %1" : "=v"(addr) : "n"(4 * kLane));
+  return addr;
+}
+__device__ __forceinline__ float lane_bcast(float v, int addr) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(addr, __builtin_bit_cast(int, v)));
+}
+
 __device__ __forceinline__ int wave_count_ge(const uint32_t key[4], uint32_t t) {
   return __popcll(__ballot(key[0] >= t)) + __popcll(__ballot(key[1] >= t)) +
          __popcll(__ballot(key[2] >= t)) + __popcll(__ballot(key[3] >= t));
@@ -89,10 +138,11 @@ __device__ __forceinline__ float scale_rcp(float s) { return __builtin_amdgcn_rc
 // Codes, scale and zero of clipped values whose minimum and maximum over the vector are mn and
 // mx (tests/oracle.py:15-17): code = clamp(trunc(fl(fl(x - zero) / scale) + 0.5), 0, 3). The
 // quotient is taken through a reciprocal r of the (uniform) scale within one ulp of 1 / scale:
-// for y in [0.5, 3.5], fl(fl(d r) + 0.5) differs from fl(fl(d / scale) + 0.5) by at most
-// 3 (2^-23 + 2 * 2^-24) + 2^-22 < 1.2e-6, so a value of y = q + 0.5 further than 2^-16 from 1,
-// 2 and 3 truncates to the same code. If any lane has a value that close, the wavefront redoes
-// its quotients with IEEE division.
+// for y in [0.5, 3.5], fma(d, r, 0.5) differs from fl(fl(d / scale) + 0.5) by at most
+// 3 (2^-23 + 2^-24) + 2^-22 < 1.2e-6, so a value of y = q + 0.5 further than 2^-16 from every
+// integer truncates to the same code. If any lane has a value that close (a wider test than
+// needed outside [0.5, 3.5], where the code is clamped anyway), the wavefront redoes its
+// quotients with IEEE division.
 // The codes of quantize_clipped for q.zf, q.sf and r = scale_rcp(q.sf).
 __device__ __forceinline__ void quantize_codes(const float xc[4], float r, Quantized& q) {
 #pragma clang fp contract(off)
@@ -100,8 +150,8 @@ __device__ __forceinline__ void quantize_codes(const float xc[4], float r, Quant
   bool near = false;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    y[i] = (xc[i] - q.zf) * r + 0.5f;
-    near |= y[i] > 0.5f && y[i] < 3.5f && fabsf(y[i] - rintf(y[i])) < 1.52587890625e-05f;
+    y[i] = __builtin_fmaf(xc[i] - q.zf, r, 0.5f);
+    near |= fabsf(y[i] - rintf(y[i])) < 1.52587890625e-05f;
   }
   if (__any(near)) {
 #pragma unroll
@@ -130,10 +180,12 @@ __device__ __forceinline__ Quantized quantize_clipped(const float xc[4], float m
   return q;
 }
 
+// Clip to [-thr, thr] (one median-of-three per value: the min/max pair's value for finite
+// inputs; a zero's sign does not reach the codes, which use xc - zero).
 __device__ __forceinline__ void clamp4(const float x[4], float thr, float out[4]) {
 #pragma clang fp contract(off)
 #pragma unroll
-  for (int i = 0; i < 4; ++i) out[i] = fminf(fmaxf(x[i], -thr), thr);
+  for (int i = 0; i < 4; ++i) out[i] = __builtin_amdgcn_fmed3f(x[i], -thr, thr);
 }
 __device__ __forceinline__ float clamp1(float x, float thr) { return fminf(fmaxf(x, -thr), thr); }
 
@@ -143,10 +195,11 @@ __device__ __forceinline__ float clamp1(float x, float thr) { return fminf(fmaxf
 // codes of quantize_clipped); otherwise from the reciprocal product alone.
 template <bool kExact>
 __device__ __forceinline__ float candidate_sq(const float x[4], float tc, float zc, float sc,
-                                              float rc, int i) {
+                                              float rc, int i, int addr = 0) {
 #pragma clang fp contract(off)
-  const float zf = lane_value(zc, i), sf = lane_value(sc, i), r = lane_value(rc, i);
   if constexpr (!kExact) {
+    // addr: bcast_addr<i>().
+    const float zf = lane_bcast(zc, addr), sf = lane_bcast(sc, addr), r = lane_bcast(rc, addr);
     // Fast pass (within search_best's margin of the exact value): no clip (a clipped value's
     // code is 0 or 3 either way, since z ~ -t or t - z ~ 3 s), err = (x - z) - c s (c s is
     // exact: c < 4 and s is an fp16 value) instead of x - fl(c s + z), and the four squares
@@ -161,6 +214,7 @@ __device__ __forceinline__ float candidate_sq(const float x[4], float tc, float 
     }
     return acc;
   }
+  const float zf = lane_value(zc, i), sf = lane_value(sc, i), r = lane_value(rc, i);
   const float t = lane_value(tc, i);
   float xi[4], y[4];
   // Clip (one median-of-three per element: the same value as the min/max pair for the
@@ -208,9 +262,11 @@ __device__ __forceinline__ float candidate_sq(const float x[4], float tc, float 
 __device__ __forceinline__ int search_best(const float x[4], float tc, float zc, float sc,
                                            float rc, float maxabs, int lane) {
 #pragma clang fp contract(off)
+  const int addr[8] = {bcast_addr<0>(), bcast_addr<1>(), bcast_addr<2>(), bcast_addr<3>(),
+                       bcast_addr<4>(), bcast_addr<5>(), bcast_addr<6>(), bcast_addr<7>()};
   float part[8];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) part[i] = candidate_sq<false>(x, tc, zc, sc, rc, i);
+  for (int i = 0; i < 8; ++i) part[i] = candidate_sq<false>(x, tc, zc, sc, rc, i, addr[i]);
   // Levels 3-5 of the tree (lane pairs 1, 2 and 4 apart), keeping half the candidates each.
   const bool b0 = lane & 1, b1 = lane & 2, b2 = lane & 4;
   float q4[4];
@@ -261,15 +317,16 @@ __device__ __forceinline__ int search_best(const float x[4], float tc, float zc,
   return exact;
 }
 
-// Quantize one vector and write codes + scale + zero (68 bytes) at `dst`. Clipping is
+// Quantize one vector and write codes + scale + zero (68 bytes) at `dst` (nothing is written
+// when dst is null: the caller's row is skipped, the arithmetic still runs). Clipping is
 // monotone, so the extremes of the clipped vector are the clipped extremes of the vector: one
 // pair of wavefront reductions serves every candidate threshold.
 __device__ __forceinline__ void quantize_store(const float x[4], int mode, float ratio, float factor,
                                                uint8_t* dst) {
 #pragma clang fp contract(off)
   const int lane = threadIdx.x & 63;
-  const float mn = wave_min_dpp(fminf(fminf(x[0], x[1]), fminf(x[2], x[3])));
-  const float mx = wave_max_dpp(fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3])));
+  float mn, mx;
+  wave_min_max(x, mn, mx);
   const float maxabs = fmaxf(fabsf(mn), fabsf(mx));
   float thr = INFINITY;  // no clipping
   if (mode == OSCAR_CLIP_FACTOR) {
@@ -297,8 +354,10 @@ __device__ __forceinline__ void quantize_store(const float x[4], int mode, float
     float xc[4];
     clamp4(x, t, xc);
     quantize_codes(xc, lane_value(rc, best), q);
-    dst[lane] = static_cast<uint8_t>(q.byte);
-    if (lane == 0) *reinterpret_cast<uint32_t*>(dst + 64) = q.scale | (q.zero << 16);
+    if (dst) {
+      dst[lane] = static_cast<uint8_t>(q.byte);
+      if (lane == 0) *reinterpret_cast<uint32_t*>(dst + 64) = q.scale | (q.zero << 16);
+    }
     return;
   } else if (ratio != 0.0f) {
     thr = percentile_threshold(x, ratio);
@@ -313,8 +372,10 @@ __device__ __forceinline__ void quantize_store(const float x[4], int mode, float
   const Quantized q = thr == INFINITY ? quantize_clipped(xc, mn, mx)
                                       : quantize_clipped(xc, clamp1(mn, thr), clamp1(mx, thr));
   // Lane l owns packed byte l; lane 0 also writes scale | zero (bytes 64..67, 4-aligned).
-  dst[lane] = static_cast<uint8_t>(q.byte);
-  if (lane == 0) *reinterpret_cast<uint32_t*>(dst + 64) = q.scale | (q.zero << 16);
+  if (dst) {
+    dst[lane] = static_cast<uint8_t>(q.byte);
+    if (lane == 0) *reinterpret_cast<uint32_t*>(dst + 64) = q.scale | (q.zero << 16);
+  }
 }
 
 }  // namespace oscar

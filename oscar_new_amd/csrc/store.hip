@@ -42,17 +42,19 @@ __global__ __launch_bounds__(kThreads) void store_int2_kernel(const StoreArgs a)
   if (row >= a.rows) return;
   const uint32_t token = fastdiv(static_cast<uint32_t>(row), a.h_div);  // rows < 2^31
   const int head = static_cast<int>(row - static_cast<int64_t>(token) * a.L.kv_heads);
-  if (static_cast<int64_t>(token) >= a.counts[1]) return;
-  const int64_t slot = a.slots[token];
-  if (slot < 0) return;
-  const int64_t base = slot_offset(a.L, slot, head);
-  if (base + 2 * a.L.vector_bytes > a.history_bytes) return;
+  // The row's values, the token count and the slot are requested together (every address is
+  // in bounds for row < rows); the skips of kernels.py:168-169 and the buffer bound only
+  // decide whether the bytes are written, so nothing waits for the slot before the values.
   const uint16_t* src = (is_v ? a.v : a.k) + row * kHeadDim + lane * 4;
   const uint2 raw = *reinterpret_cast<const uint2*>(src);
+  const int64_t slot = a.slots[token];
+  const bool live = static_cast<int64_t>(token) < a.counts[1] && slot >= 0;
+  const int64_t base = live ? slot_offset(a.L, slot, head) : 0;
+  const bool write = live && base + 2 * a.L.vector_bytes <= a.history_bytes;
   const float x[4] = {bf16_to_float(raw.x & 0xffffu), bf16_to_float(raw.x >> 16),
                       bf16_to_float(raw.y & 0xffffu), bf16_to_float(raw.y >> 16)};
   quantize_store(x, a.mode, is_v ? a.v_ratio : a.k_ratio, is_v ? a.v_factor : a.k_factor,
-                 a.history + base + is_v * a.L.vector_bytes);
+                 write ? a.history + base + is_v * a.L.vector_bytes : nullptr);
 }
 
 // ---- rotate_store_int2: the K/V rotation and the INT2 store of many tokens in one launch.
