@@ -58,12 +58,12 @@ __global__ __launch_bounds__(kThreads) void store_int2_kernel(const StoreArgs a)
 }
 
 // ---- rotate_store_int2: the K/V rotation and the INT2 store of many tokens in one launch.
-// Workgroup (16-row block x, K or V by y) of 16 wavefronts: the block's rows are staged once
-// in LDS (16-byte piece p of row r at slot p ^ r), wavefront w computes output columns
-// 16 w .. 16 w + 15 of the block with the operands, MFMA and k order of rotate_kernel (B from
-// the columns of R, i.e. rows of R^T, through L2), the bf16 block is kept in LDS, and
-// wavefront w then clips, quantizes and stores row w as store_int2_kernel does. The rotated
-// rows never go to HBM.
+// Workgroup (32-row block x: two 16-row tiles, K or V by y) of 16 wavefronts: the block's rows
+// are staged once in LDS (16-byte piece p of row r at slot p ^ r), wavefront w computes output
+// columns 16 w .. 16 w + 15 of both tiles with the operands, MFMA and k order of rotate_kernel
+// (B from the columns of R, i.e. rows of R^T, through L2, read once per 32 rows), the bf16
+// block is kept in LDS, and wavefront w then clips, quantizes and stores rows w and w + 16 as
+// store_int2_kernel does. The rotated rows never go to HBM.
 struct RotateStoreArgs {
   const uint16_t* x[2];  // K, V: row (token, head) at token * s0 + head * s1, contiguous, 16-B aligned
   int64_t s0[2], s1[2];
@@ -76,25 +76,32 @@ constexpr int kRsWaves = 16;
 
 __device__ __forceinline__ int rs_piece(int row, int piece) { return row * kHeadDim + 8 * (piece ^ row); }
 
-__global__ __launch_bounds__(kRsWaves * kWave) __attribute__((amdgpu_waves_per_eu(8)))
+constexpr int kRsTiles = 2;  // 16-row tiles per workgroup
+
+__global__ __launch_bounds__(kRsWaves * kWave) __attribute__((amdgpu_waves_per_eu(4)))
 void rotate_store_kernel(const RotateStoreArgs a) {
-  __shared__ __attribute__((aligned(16))) uint16_t s_x[16 * kHeadDim];
-  __shared__ __attribute__((aligned(16))) uint16_t s_rot[16 * kHeadDim];
+  __shared__ __attribute__((aligned(16))) uint16_t s_x[kRsTiles * 16 * kHeadDim];
+  __shared__ __attribute__((aligned(16))) uint16_t s_rot[kRsTiles * 16 * kHeadDim];
   const StoreArgs& st = a.st;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int n = lane & 15, g = lane >> 4;
   const int is_v = blockIdx.y;
-  const int64_t r0 = static_cast<int64_t>(blockIdx.x) * 16;
+  const int64_t r0 = static_cast<int64_t>(blockIdx.x) * 16 * kRsTiles;
   const int h = st.L.kv_heads;
-  // This wavefront's store row; its token count and slot are requested with the staging loads.
-  const int64_t row = r0 + wave;
-  const bool in = row < st.rows;
-  const uint32_t token = fastdiv(static_cast<uint32_t>(in ? row : 0), a.h_div);
-  const int head = static_cast<int>((in ? row : 0) - static_cast<int64_t>(token) * h);
-  const bool live = in && static_cast<int64_t>(token) < st.counts[1];
-  const int64_t slot = live ? st.slots[token] : -1;
-  if (tid < 16 * 32) {
-    const int rr = tid >> 5, piece = tid & 31;
+  int64_t slot[kRsTiles];
+  int head[kRsTiles];
+  bool live[kRsTiles];
+#pragma unroll
+  for (int t = 0; t < kRsTiles; ++t) {
+    const int64_t row = r0 + 16 * t + wave;
+    const bool in = row < st.rows;
+    const uint32_t token = fastdiv(static_cast<uint32_t>(in ? row : 0), a.h_div);
+    head[t] = static_cast<int>((in ? row : 0) - static_cast<int64_t>(token) * h);
+    live[t] = in && static_cast<int64_t>(token) < st.counts[1];
+    slot[t] = live[t] ? st.slots[token] : -1;
+  }
+  for (int idx = tid; idx < kRsTiles * 16 * 32; idx += kRsWaves * kWave) {
+    const int rr = idx >> 5, piece = idx & 31;
     const int64_t xrow = r0 + rr;
     u32x4 v = u32x4{0u, 0u, 0u, 0u};
     if (xrow < st.rows) {
@@ -109,21 +116,29 @@ void rotate_store_kernel(const RotateStoreArgs a) {
   rotate_load_b<true>(op, a.rt[is_v] + static_cast<int64_t>(16 * wave + n) * kHeadDim, 1, g);
   __syncthreads();
 #pragma unroll
-  for (int m = 0; m < 8; ++m) op.a[m] = *reinterpret_cast<const u32x4*>(s_x + rs_piece(n, 4 * m + g));
-  const f32x4 acc = rotate_mfma(op);
+  for (int t = 0; t < kRsTiles; ++t) {
 #pragma unroll
-  for (int v = 0; v < 4; ++v)
-    s_rot[(4 * g + v) * kHeadDim + 16 * wave + n] = static_cast<uint16_t>(float_to_bf16(acc[v]));
+    for (int m = 0; m < 8; ++m)
+      op.a[m] = *reinterpret_cast<const u32x4*>(s_x + rs_piece(16 * t + n, 4 * m + g));
+    const f32x4 acc = rotate_mfma(op);
+#pragma unroll
+    for (int v = 0; v < 4; ++v)
+      s_rot[(16 * t + 4 * g + v) * kHeadDim + 16 * wave + n] =
+          static_cast<uint16_t>(float_to_bf16(acc[v]));
+  }
   __syncthreads();
-  // Same skips as store_int2_kernel (kernels.py:168-169 and the buffer bound).
-  if (!live || slot < 0) return;
-  const int64_t base = slot_offset(st.L, slot, head);
-  if (base + 2 * st.L.vector_bytes > st.history_bytes) return;
-  const uint2 raw = *reinterpret_cast<const uint2*>(s_rot + wave * kHeadDim + lane * 4);
-  const float x[4] = {bf16_to_float(raw.x & 0xffffu), bf16_to_float(raw.x >> 16),
-                      bf16_to_float(raw.y & 0xffffu), bf16_to_float(raw.y >> 16)};
-  quantize_store(x, st.mode, is_v ? st.v_ratio : st.k_ratio, is_v ? st.v_factor : st.k_factor,
-                 st.history + base + is_v * st.L.vector_bytes);
+#pragma unroll
+  for (int t = 0; t < kRsTiles; ++t) {
+    // Same skips as store_int2_kernel (kernels.py:168-169 and the buffer bound).
+    const int64_t base = live[t] && slot[t] >= 0 ? slot_offset(st.L, slot[t], head[t]) : 0;
+    const bool write = live[t] && slot[t] >= 0 && base + 2 * st.L.vector_bytes <= st.history_bytes;
+    if (!write) continue;
+    const uint2 raw = *reinterpret_cast<const uint2*>(s_rot + (16 * t + wave) * kHeadDim + lane * 4);
+    const float x[4] = {bf16_to_float(raw.x & 0xffffu), bf16_to_float(raw.x >> 16),
+                        bf16_to_float(raw.y & 0xffffu), bf16_to_float(raw.y >> 16)};
+    quantize_store(x, st.mode, is_v ? st.v_ratio : st.k_ratio, is_v ? st.v_factor : st.k_factor,
+                   st.history + base + is_v * st.L.vector_bytes);
+  }
 }
 
 struct UnpackArgs {
@@ -244,7 +259,7 @@ extern "C" int oscar_rotate_store_int2(const void* key, int64_t k_s0, int64_t k_
   st.v_ratio = clip->v_ratio;
   st.k_factor = clip->k_factor;
   st.v_factor = clip->v_factor;
-  const dim3 grid(static_cast<unsigned>((st.rows + 15) / 16), 2);
+  const dim3 grid(static_cast<unsigned>((st.rows + 16 * kRsTiles - 1) / (16 * kRsTiles)), 2);
   hipLaunchKernelGGL(rotate_store_kernel, grid, dim3(kRsWaves * kWave), 0, as_stream(stream), a);
   return static_cast<int>(hipGetLastError());
 }
