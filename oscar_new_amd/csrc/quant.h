@@ -189,31 +189,33 @@ __device__ __forceinline__ void clamp4(const float x[4], float thr, float out[4]
 }
 __device__ __forceinline__ float clamp1(float x, float thr) { return fminf(fmaxf(x, -thr), thr); }
 
+// Fast pass of candidate i over this lane's four values (search_best scales the sum by s^2 and
+// bounds its distance to the exact MSE): u = x / s - z / s as one FMA (bz = -fl(z r), lane i's
+// r and bz read through addr = bcast_addr<i>()), the code by rounding u to nearest (a tie gives
+// the same |u - c| either way), clamped to [0, 3] (a clipped value's code is 0 or 3 either
+// way), and the squares of u - c, the error in units of s, accumulated by FMA.
+__device__ __forceinline__ float candidate_fast(const float x[4], float rc, float bzc, int addr) {
+#pragma clang fp contract(off)
+  const float r = lane_bcast(rc, addr), bz = lane_bcast(bzc, addr);
+  float acc = 0.f;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const float u = __builtin_fmaf(x[e], r, bz);
+    const float d = u - __builtin_amdgcn_fmed3f(rintf(u), 0.0f, 3.0f);
+    acc = __builtin_fmaf(d, d, acc);
+  }
+  return acc;
+}
+
 // Squared error of candidate i (lane i holds its threshold t, zero z, scale s and 1 / s) over
-// this lane's four values, summed in pairs as the oracle's tree does. `exact`: codes from the
-// IEEE quotient wherever the reciprocal product lies within 2^-16 of a code boundary (the
-// codes of quantize_clipped); otherwise from the reciprocal product alone.
+// this lane's four values, summed in pairs as the oracle's tree does: codes from the IEEE
+// quotient wherever the reciprocal product lies within 2^-16 of a code boundary (the codes of
+// quantize_clipped); otherwise from the reciprocal product alone.
 template <bool kExact>
 __device__ __forceinline__ float candidate_sq(const float x[4], float tc, float zc, float sc,
-                                              float rc, int i, int addr = 0) {
+                                              float rc, int i) {
 #pragma clang fp contract(off)
-  if constexpr (!kExact) {
-    // addr: bcast_addr<i>().
-    const float zf = lane_bcast(zc, addr), sf = lane_bcast(sc, addr), r = lane_bcast(rc, addr);
-    // Fast pass (within search_best's margin of the exact value): no clip (a clipped value's
-    // code is 0 or 3 either way, since z ~ -t or t - z ~ 3 s), err = (x - z) - c s (c s is
-    // exact: c < 4 and s is an fp16 value) instead of x - fl(c s + z), and the four squares
-    // accumulated by FMA.
-    float acc = 0.f;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const float d = x[e] - zf;
-      const float c = __builtin_amdgcn_fmed3f(truncf(__builtin_fmaf(d, r, 0.5f)), 0.0f, 3.0f);
-      const float err = __builtin_fmaf(-c, sf, d);
-      acc = __builtin_fmaf(err, err, acc);
-    }
-    return acc;
-  }
+  static_assert(kExact, "the fast pass is candidate_fast");
   const float zf = lane_value(zc, i), sf = lane_value(sc, i), r = lane_value(rc, i);
   const float t = lane_value(tc, i);
   float xi[4], y[4];
@@ -249,24 +251,35 @@ __device__ __forceinline__ float candidate_sq(const float x[4], float tc, float 
 }
 
 // The clip search's argmin (tests/oracle.py extension: the first of the 8 factors with the
-// least float32 MSE, summed as a pairwise tree over the 256 values). Fast pass: every
-// candidate's MSE from reciprocal-product codes, the 8 sums reduced together (each tree level
-// halves the candidates a lane keeps until lane l holds candidate (l&1)*4 + (l&2) + (l>>2&1)).
-// A reciprocal-product code differs from the exact one only for a value within about 2^-16 s
-// of a code boundary, i.e. of the midpoint of two decoded values, where the two squared errors
-// differ by at most s (2^-14 s + 2^-21 |z|); the fast error's different rounding moves each
-// squared error by at most 2^-20 m (2 m + 3 s) (m = max |x|); over 256 values, the per-lane FMA
-// chain and the tree's rounding (at most 9 roundings per term), that bounds each fast MSE within
-// M = 2^-5 s^2 + 2^-12 s |z| + 2^-18 MSE + 2^-10 m (m + s) of the exact one (twice the bound). If no other candidate's interval reaches the fast minimum's, that minimum is
-// the exact one; otherwise the exact pass decides. Same result as the exact pass alone.
+// least float32 MSE, summed as a pairwise tree over the 256 values). Fast pass
+// (candidate_fast): every candidate's MSE as s^2 sum (u - c)^2, the 8 sums reduced together
+// (each tree level halves the candidates a lane keeps until lane l holds candidate
+// (l&1)*4 + (l&2) + (l>>2&1)). Error bound (eps = 2^-24, m = max |x| >= |z|, r within one ulp
+// of 1/s): u differs from q = (x - z)/s by at most 7.3 m eps / s; the exact code is that of
+// fl(fl(x - z)/s) + 0.5, within (4 m / s + 4) eps of q + 0.5. Where the codes agree, s (u - c)
+// and the oracle's x - fl(c s + z) differ by at most eps (10.3 m + 3 s + 2|D|), D = x - z - c s,
+// |D| <= 2 m + 3 s, so the squares differ by at most eps (57.2 m^2 + 121.8 m s + 54 s^2);
+// where they differ (q within (11.3 m / s + 4) eps of a code boundary) the two squares differ by
+// at most eps (22.6 m s + 8 s^2). Per value at most 2^7 eps (m + s)^2, over 256 values
+// 2^-9 (m + s)^2, and the two summations' rounding (at most 20 eps relative) 2^-19 MSE: each
+// fast MSE lies within M = 2^-8 (m + s)^2 + 2^-18 MSE of the exact one (twice the bound;
+// checked against the oracle on the CPU in tests/test_store_arith.py). If no other candidate's
+// interval reaches the fast minimum's, that minimum is the exact one; otherwise the exact pass
+// decides. Same result as the exact pass alone. The fast pass codes unclipped values, which
+// is the clipped value's code (0 below the range, 3 above) only when the clipped range spans
+// about three steps: `fast_ok` (lanes 0..7, candidate = lane) says the spread was not raised to
+// 2^-14 and fp16 rounding moved the zero by at most s / 4 (then the top of the range sits at
+// least 2.74 steps above the zero and the bottom at most 0.25); a candidate without it sends
+// the vector to the exact pass.
 __device__ __forceinline__ int search_best(const float x[4], float tc, float zc, float sc,
-                                           float rc, float maxabs, int lane) {
+                                           float rc, float maxabs, bool fast_ok, int lane) {
 #pragma clang fp contract(off)
   const int addr[8] = {bcast_addr<0>(), bcast_addr<1>(), bcast_addr<2>(), bcast_addr<3>(),
                        bcast_addr<4>(), bcast_addr<5>(), bcast_addr<6>(), bcast_addr<7>()};
+  const float bzc = -(zc * rc);
   float part[8];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) part[i] = candidate_sq<false>(x, tc, zc, sc, rc, i, addr[i]);
+  for (int i = 0; i < 8; ++i) part[i] = candidate_fast(x, rc, bzc, addr[i]);
   // Levels 3-5 of the tree (lane pairs 1, 2 and 4 apart), keeping half the candidates each.
   const bool b0 = lane & 1, b1 = lane & 2, b2 = lane & 4;
   float q4[4];
@@ -289,17 +302,22 @@ __device__ __forceinline__ int search_best(const float x[4], float tc, float zc,
   v = sum_xor32(v);
   // Lane c (< 8) takes candidate c's sum, its margin and the decision.
   const int c = lane & 7;
-  const float fv = __shfl(v, ((c >> 2) & 1) | (c & 2) | ((c & 1) << 2), kWave);
-  const float margin = 0.03125f * sc * sc + 2.44140625e-04f * sc * fabsf(zc) +
-                       3.814697265625e-06f * fv + 9.765625e-04f * maxabs * (maxabs + sc);
-  float m8 = fv;
-  m8 = fminf(m8, dpp<kDppQuadXor1>(m8));
-  m8 = fminf(m8, dpp<kDppQuadXor2>(m8));
-  m8 = fminf(m8, dpp<kDppRowHalfMirror>(m8));
-  const float fmin = lane_value(m8, 0);
+  const float fv = __shfl(v, ((c >> 2) & 1) | (c & 2) | ((c & 1) << 2), kWave) * (sc * sc);
+  const float ms = maxabs + sc;
+  const float margin = 0.00390625f * ms * ms + 3.814697265625e-06f * fv;
+  // Lanes 0..7 hold the non-negative sums: their bit patterns order like the values.
+  uint32_t m8 = __float_as_uint(fv);
+  m8 = min(m8, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(-1, static_cast<int>(m8),
+                                                                 kDppQuadXor1, 0xF, 0xF, false)));
+  m8 = min(m8, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(-1, static_cast<int>(m8),
+                                                                 kDppQuadXor2, 0xF, 0xF, false)));
+  m8 = min(m8, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(
+                   -1, static_cast<int>(m8), kDppRowHalfMirror, 0xF, 0xF, false)));
+  const float fmin = __uint_as_float(static_cast<uint32_t>(
+      __builtin_amdgcn_readlane(static_cast<int>(m8), 0)));
   const uint64_t at_min = __ballot(lane < 8 && fv == fmin);
   const int best = __ffsll(static_cast<long long>(at_min)) - 1;
-  if (best >= 0) {
+  if (best >= 0 && !__any(lane < 8 && !fast_ok)) {
     const float reach = lane_value(fv + margin, best);
     if (!__any(lane < 8 && lane != best && fv - margin <= reach)) return best;
   }
@@ -337,12 +355,13 @@ __device__ __forceinline__ void quantize_store(const float x[4], int mode, float
     // candidate, instead of by every lane for every candidate.
     const float tc = maxabs * search_factor(lane & 7);
     const float lo = clamp1(mn, tc), hi = clamp1(mx, tc);
-    float spread = div3(hi - lo);
-    spread = spread < 6.103515625e-05f ? 6.103515625e-05f : spread;
+    const float spread_raw = div3(hi - lo);
+    const float spread = spread_raw < 6.103515625e-05f ? 6.103515625e-05f : spread_raw;
     const float zc = f16_bits_to_float(float_to_f16_bits(lo));
     const float sc = f16_bits_to_float(float_to_f16_bits(spread));
     const float rc = scale_rcp(sc);
-    const int best = search_best(x, tc, zc, sc, rc, maxabs, lane);
+    const bool fast_ok = spread_raw >= 6.103515625e-05f && fabsf(lo - zc) <= 0.25f * sc;
+    const int best = search_best(x, tc, zc, sc, rc, maxabs, fast_ok, lane);
     // The winner's threshold, zero and scale are the values its lane computed above (those of
     // quantize_clipped on the clipped extremes), so only its codes are left to compute.
     const float t = lane_value(tc, best), zf = lane_value(zc, best), sf = lane_value(sc, best);

@@ -218,6 +218,32 @@ def test_store_c2_scale_rotated_outliers_permuted_pages():
         _check_slots(history.cpu().numpy(), slots.tolist(), expected, lay)
 
 
+def test_store_search_degenerate_ranges_bit_exact():
+    """Search clip mode on vectors whose clipped range spans under three steps (spreads below
+    3 * 2^-14, large offsets against small spreads): the fast candidate pass does not apply
+    and the exact pass decides; bytes as the oracle's."""
+    g = torch.Generator().manual_seed(31)
+    n = 2048
+    cfg = OscarConfig(sink_tokens=4, recent_tokens=128, clip_mode="search")
+    layout = __import__("oscar_new_amd.layout", fromlist=["CacheLayout"]).CacheLayout(768, config=cfg)
+    pages = 6
+    history = torch.full((pages * layout.stripe_page_bytes,), 0x5A, dtype=torch.uint8, device=DEV)
+    blocks = torch.randperm(pages * 6, generator=g)[: n // 128]
+    slots = (blocks[:, None] * 128 + torch.arange(128)[None]).reshape(-1).to(torch.int64)
+    parts = [1e-5 * torch.randn(512, 1, 256, generator=g),
+             3e-5 * torch.randn(512, 1, 256, generator=g),
+             100 + 0.02 * torch.randn(256, 1, 256, generator=g),
+             37 + 0.05 * torch.randn(256, 1, 256, generator=g),
+             -50 + torch.rand(256, 1, 256, generator=g),
+             torch.full((256, 1, 256), 3.25)]
+    k = torch.cat(parts).bfloat16()
+    v = torch.cat(parts[::-1]).bfloat16()
+    counts = torch.tensor([1, n], dtype=torch.int32, device=DEV)
+    kernels.store_int2(k.to(DEV), v.to(DEV), history, slots.to(DEV), counts, layout)
+    expected = O.packed_slots(bits(k), bits(v), cfg)
+    _check_slots(history.cpu().numpy(), slots.tolist(), expected, layout)
+
+
 # ------------------------------------------------------------------ prepare_tasks
 
 
