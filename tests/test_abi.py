@@ -39,6 +39,10 @@ def test_host_side_argument_errors():
     assert lib.oscar_store_int2(None, None, 4, None, 0, None, None, bad, clip, None) == -3
     good = _ext.OscarLayout(256, 1, 768, 128, 160, 68, 4, 128, 132, 0, 393216)
     assert lib.oscar_store_int2(None, None, 4, None, 0, None, None, good, clip, None) == -1
+    # n * H must stay below 2^31 (the kernel divides 32-bit row indices); fake, aligned,
+    # never dereferenced addresses.
+    a = 1 << 20
+    assert lib.oscar_store_int2(a, a, 1 << 31, a, 1 << 24, a, a, good, clip, None) == -2
     assert lib.oscar_merge_splits(None, None, None, 3, 6, 4, 128, None, None, None) == -5
     assert lib.oscar_unpack(None, 0, None, 5000, good, None, None, None) == -2
     with pytest.raises(ValueError):
