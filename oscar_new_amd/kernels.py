@@ -368,11 +368,20 @@ def pre_attention(query, key, value, history, window, meta, layout, scale, rk_t,
     (backend.py:171-173, 195, 211-222). ``rk_t``/``rv_t`` are R^T as contiguous bf16 [256, 256].
     Returns ``(qrot bf16 [n, hq, 256], raw_partials fp32 [n, hq, 1, 256], raw_lse [n, hq, 1])``.
     ``raw=False``: the launch leaves the BF16 branch out and the partials come from
-    ``chunk_raw_attention`` (a launch of its own, for long chunks), with the same bits.
+    ``chunk_raw_attention`` (a launch of its own, for long chunks), with the same bits. From
+    SPLIT_PRE_ROWS query rows on, the q rotation and the K/V store run as ``rotate`` (the
+    tiled form: R staged once per workgroup) and ``rotate_store_int2`` (32-row workgroups)
+    instead of role workgroups that each read R from L2 for one 16-row tile: the same bits.
     """
     _device_check(query, key, value, history, window, rk_t, rv_t)
     n, hq, d = query.shape
     cfg = layout.config
+    if not raw and n * hq >= SPLIT_PRE_ROWS and n > 0:
+        qrot = rotate(query, rk_t.t())
+        rotate_store_int2(key, value, rk_t, rv_t, history, meta.slot_mapping, meta.counts,
+                          layout)
+        partials, lse = chunk_raw_attention(query, key, value, window, meta, layout, scale)
+        return qrot, partials, lse
     qrot = torch.empty((n, hq, d), dtype=torch.bfloat16, device=query.device)
     partials = torch.empty((n, hq, 1, d), dtype=torch.float32, device=query.device)
     lse = torch.empty((n, hq, 1), dtype=torch.float32, device=query.device)
@@ -416,6 +425,11 @@ def pre_attention(query, key, value, history, window, meta, layout, scale, rk_t,
 # Query tokens per request from which a step's BF16 branch runs as the chunk flash launch
 # (chunk_raw_attention) instead of decode-shaped roles of the pre-attention launch.
 CHUNK_RAW_FROM = 64
+
+
+# Query rows from which a long chunk's q rotation and K/V store leave the pre-attention launch
+# for the tiled rotation and the fused rotate + store (pre_attention(raw=False)).
+SPLIT_PRE_ROWS = 4096
 
 
 def chunk_raw_preferred(meta):
