@@ -129,6 +129,39 @@ __device__ __forceinline__ void post_rows_map(const PostArgs& p, RowOf row_of, i
       *reinterpret_cast<uint2*>(&s_h[0][lane * 4]) = merge_splits_out(m);
       if (lane == 0) s_l[0] = merge_splits_lse(m);
     }
+  } else if (kMode == kMergeOneRound && R > 4 && live_splits == 1) {
+    // One split (long chunks): every row's partial and LSE requested before any is merged
+    // (one round of latency instead of one per row), then merge_splits_row's arithmetic.
+    constexpr int kPer = R / (kThreads / kWave);
+    float l0[kPer];
+    float4 v0[kPer];
+    bool live[kPer];
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      const int64_t row = row_of(wave + (kThreads / kWave) * i);
+      const bool in = row >= 0;
+      live[i] = in && row / p.hq < active;
+      l0[i] = p.hl[(in ? row : 0) * p.splits];
+      v0[i] = *reinterpret_cast<const float4*>(p.hp + (in ? row : 0) * p.splits * kHeadDim +
+                                               lane * 4);
+    }
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      const int r = wave + (kThreads / kWave) * i;
+      float l[16];
+      float4 v[16];
+#pragma unroll
+      for (int k = 0; k < 16; ++k) {
+        l[k] = k == 0 && live[i] ? l0[i] : -INFINITY;
+        v[k] = k == 0 ? v0[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+      }
+      SplitMerge m = empty_merge();
+#pragma unroll
+      for (int k = 0; k < 16; ++k) m.mx = fmaxf(m.mx, l[k]);
+      merge_group(m, l, v, m.mx == -INFINITY ? 0.f : m.mx);
+      *reinterpret_cast<uint2*>(&s_h[r][lane * 4]) = merge_splits_out(m);
+      if (lane == 0) s_l[r] = merge_splits_lse(m);
+    }
   } else {
     for (int r = wave; r < R; r += kThreads / kWave) {
       const int64_t row = row_of(r);

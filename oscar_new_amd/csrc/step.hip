@@ -95,15 +95,18 @@ post_attention_tile_kernel(const PostArgs p) {
   __shared__ __attribute__((aligned(16))) uint16_t s_h[16][kHeadDim];
   __shared__ float s_l[16];
   __shared__ GroupMergeLds group_lds;
-  if (static_cast<int>(blockIdx.x) < p.merge_wgs) {
-    const int64_t row0 = static_cast<int64_t>(blockIdx.x) * 16;
+  // The window-store workgroups come first: each walks its request's writers in sequence, so
+  // started last they would end the launch.
+  const int64_t win = p.win_requests;
+  if (static_cast<int64_t>(blockIdx.x) >= win) {
+    const int64_t row0 = (static_cast<int64_t>(blockIdx.x) - win) * 16;
     const int64_t rows = p.rows;
     post_rows_map<16, kMode>(
         p, [row0, rows](int r) -> int64_t { return row0 + r < rows ? row0 + r : -1; },
         p.splits, s_h, s_l, &group_lds);
     return;
   }
-  const int req = static_cast<int>(blockIdx.x) - p.merge_wgs;
+  const int req = static_cast<int>(blockIdx.x);
   for (int head = 0; head < p.win.L.kv_heads; ++head) store_window_request(p.win, req, head);
 }
 

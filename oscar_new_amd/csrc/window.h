@@ -54,6 +54,11 @@ __device__ __forceinline__ void store_window_request(const WindowArgs& a, int re
   const int s0 = max(prefix, 0), s1 = max(s0, min(sink, seq));  // sink writers
   const int r0 = max(max(prefix, sink), seq - ring), r1 = max(r0, seq);  // ring writers
   const int nsink = s1 - s0, total = nsink + (r1 - r0);
+  const bool vec = a.ks2 == 1 && a.vs2 == 1 && a.ks0 % 4 == 0 && a.ks1 % 4 == 0 &&
+                   a.vs0 % 4 == 0 && a.vs1 % 4 == 0 &&
+                   reinterpret_cast<uintptr_t>(a.k) % 8 == 0 &&
+                   reinterpret_cast<uintptr_t>(a.v) % 8 == 0;
+  const bool vst = reinterpret_cast<uintptr_t>(a.window) % 8 == 0;
   for (int base = wave * kBatch; base < total; base += (kThreads / kWave) * kBatch) {
     uint16_t kx[kBatch][4], vx[kBatch][4];
     int64_t dst[kBatch];
@@ -75,6 +80,13 @@ __device__ __forceinline__ void store_window_request(const WindowArgs& a, int re
       dst[b] = d;
       const uint16_t* ks = a.k + current * a.ks0 + head * a.ks1;
       const uint16_t* vs = a.v + current * a.vs0 + head * a.vs1;
+      if (vec) {  // contiguous, 8-byte aligned rows: one 8-byte load per lane and row
+        const uint2 kw = *reinterpret_cast<const uint2*>(ks + lane * 4);
+        const uint2 vw = *reinterpret_cast<const uint2*>(vs + lane * 4);
+        kx[b][0] = kw.x & 0xffffu, kx[b][1] = kw.x >> 16, kx[b][2] = kw.y & 0xffffu, kx[b][3] = kw.y >> 16;
+        vx[b][0] = vw.x & 0xffffu, vx[b][1] = vw.x >> 16, vx[b][2] = vw.y & 0xffffu, vx[b][3] = vw.y >> 16;
+        continue;
+      }
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int e = lane * 4 + i;
@@ -87,6 +99,15 @@ __device__ __forceinline__ void store_window_request(const WindowArgs& a, int re
       if (dst[b] < 0) continue;
       uint16_t* kd = a.window + dst[b];
       uint16_t* vd = kd + static_cast<int64_t>(h) * kHeadDim;
+      if (vst) {  // window rows start 512 bytes apart from an 8-byte aligned base
+        *reinterpret_cast<uint2*>(kd + lane * 4) =
+            make_uint2(kx[b][0] | (static_cast<uint32_t>(kx[b][1]) << 16),
+                       kx[b][2] | (static_cast<uint32_t>(kx[b][3]) << 16));
+        *reinterpret_cast<uint2*>(vd + lane * 4) =
+            make_uint2(vx[b][0] | (static_cast<uint32_t>(vx[b][1]) << 16),
+                       vx[b][2] | (static_cast<uint32_t>(vx[b][3]) << 16));
+        continue;
+      }
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         kd[lane * 4 + i] = kx[b][i];
