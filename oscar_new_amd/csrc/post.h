@@ -98,12 +98,15 @@ __device__ __forceinline__ void rotate_merge(const PostArgs& p, const PathRows& 
 // The reads that do not depend on the merge (the BF16-branch values and LSEs, and the R_v
 // operands of the first kEarly column tiles) are requested before it, the other R_v tiles
 // after it (fewer registers live across the merge); none waits for the token count.
-template <int R, int kMode, int kEarly = 4, class RowOf>
+// kTiles 2 (R = 16): rows row_of(0 .. 31), the two groups of 16 one after the other, R_v's
+// operands read once for both.
+template <int R, int kMode, int kEarly = 4, int kTiles = 1, class RowOf>
 __device__ __forceinline__ void post_rows_map(const PostArgs& p, RowOf row_of, int live_splits,
                                               uint16_t (*s_h)[kHeadDim], float* s_l,
                                               GroupMergeLds* group_lds) {
   static_assert(R == 1 || R == 4 || R == 8 || R == 16, "row groups of 1, 4, 8 or 16");
   static_assert(kEarly >= 0 && kEarly <= 4, "four column tiles per wavefront");
+  static_assert(kTiles == 1 || (kTiles == 2 && R == 16), "two tiles of 16 rows");
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int n = lane & 15, g = lane >> 4;
   const int active = p.counts[1];
@@ -116,77 +119,85 @@ __device__ __forceinline__ void post_rows_map(const PostArgs& p, RowOf row_of, i
   };
 #pragma unroll
   for (int ct = 0; ct < kEarly; ++ct) load_rv(ct);
-  PathRows pr;
-  load_path_rows<R>(p, row_of, active, pr);
-  if (R == 1) {
-    const int64_t row0 = row_of(0);
-    const bool in = row0 >= 0;
-    const int64_t lrow = in ? row0 : 0;
-    const SplitMerge m = merge_splits_row_group(p.hp + lrow * p.splits * kHeadDim,
-                                                p.hl + lrow * p.splits, live_splits,
-                                                in && row0 / p.hq < active, group_lds);
-    if (wave == 0) {
-      *reinterpret_cast<uint2*>(&s_h[0][lane * 4]) = merge_splits_out(m);
-      if (lane == 0) s_l[0] = merge_splits_lse(m);
-    }
-  } else if (kMode == kMergeOneRound && R > 4 && live_splits == 1) {
-    // One split (long chunks): every row's partial and LSE requested before any is merged
-    // (one round of latency instead of one per row), then merge_splits_row's arithmetic.
-    constexpr int kPer = R / (kThreads / kWave);
-    float l0[kPer];
-    float4 v0[kPer];
-    bool live[kPer];
-#pragma unroll
-    for (int i = 0; i < kPer; ++i) {
-      const int64_t row = row_of(wave + (kThreads / kWave) * i);
-      const bool in = row >= 0;
-      live[i] = in && row / p.hq < active;
-      l0[i] = p.hl[(in ? row : 0) * p.splits];
-      v0[i] = *reinterpret_cast<const float4*>(p.hp + (in ? row : 0) * p.splits * kHeadDim +
-                                               lane * 4);
-    }
-#pragma unroll
-    for (int i = 0; i < kPer; ++i) {
-      const int r = wave + (kThreads / kWave) * i;
-      float l[16];
-      float4 v[16];
-#pragma unroll
-      for (int k = 0; k < 16; ++k) {
-        l[k] = k == 0 && live[i] ? l0[i] : -INFINITY;
-        v[k] = k == 0 ? v0[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+  // kTiles 2: rows row_of(0 .. 2R-1) as two groups of R, one after the other, with R_v's
+  // operands read once (the group barrier ends the first group's reads of s_h and s_l).
+  for (int t = 0; t < kTiles; ++t) {
+    if (t > 0) __syncthreads();
+    auto rof = [&](int r) -> int64_t { return row_of(R * t + r); };
+    PathRows pr;
+    load_path_rows<R>(p, rof, active, pr);
+    if (R == 1) {
+      const int64_t row0 = rof(0);
+      const bool in = row0 >= 0;
+      const int64_t lrow = in ? row0 : 0;
+      const SplitMerge m = merge_splits_row_group(p.hp + lrow * p.splits * kHeadDim,
+                                                  p.hl + lrow * p.splits, live_splits,
+                                                  in && row0 / p.hq < active, group_lds);
+      if (wave == 0) {
+        *reinterpret_cast<uint2*>(&s_h[0][lane * 4]) = merge_splits_out(m);
+        if (lane == 0) s_l[0] = merge_splits_lse(m);
       }
-      SplitMerge m = empty_merge();
+    } else if (kMode == kMergeOneRound && R > 4 && live_splits == 1) {
+      // One split (long chunks): every row's partial and LSE requested before any is merged
+      // (one round of latency instead of one per row), then merge_splits_row's arithmetic.
+      constexpr int kPer = R / (kThreads / kWave);
+      float l0[kPer];
+      float4 v0[kPer];
+      bool live[kPer];
 #pragma unroll
-      for (int k = 0; k < 16; ++k) m.mx = fmaxf(m.mx, l[k]);
-      merge_group(m, l, v, m.mx == -INFINITY ? 0.f : m.mx);
-      *reinterpret_cast<uint2*>(&s_h[r][lane * 4]) = merge_splits_out(m);
-      if (lane == 0) s_l[r] = merge_splits_lse(m);
+      for (int i = 0; i < kPer; ++i) {
+        const int64_t row = rof(wave + (kThreads / kWave) * i);
+        const bool in = row >= 0;
+        live[i] = in && row / p.hq < active;
+        l0[i] = p.hl[(in ? row : 0) * p.splits];
+        v0[i] = *reinterpret_cast<const float4*>(p.hp + (in ? row : 0) * p.splits * kHeadDim +
+                                                 lane * 4);
+      }
+#pragma unroll
+      for (int i = 0; i < kPer; ++i) {
+        const int r = wave + (kThreads / kWave) * i;
+        float l[16];
+        float4 v[16];
+#pragma unroll
+        for (int k = 0; k < 16; ++k) {
+          l[k] = k == 0 && live[i] ? l0[i] : -INFINITY;
+          v[k] = k == 0 ? v0[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+        SplitMerge m = empty_merge();
+#pragma unroll
+        for (int k = 0; k < 16; ++k) m.mx = fmaxf(m.mx, l[k]);
+        merge_group(m, l, v, m.mx == -INFINITY ? 0.f : m.mx);
+        *reinterpret_cast<uint2*>(&s_h[r][lane * 4]) = merge_splits_out(m);
+        if (lane == 0) s_l[r] = merge_splits_lse(m);
+      }
+    } else {
+      for (int r = wave; r < R; r += kThreads / kWave) {
+        const int64_t row = rof(r);
+        const bool in = row >= 0;
+        const float* part = p.hp + (in ? row : 0) * p.splits * kHeadDim;
+        const float* ls = p.hl + (in ? row : 0) * p.splits;
+        const bool live = in && row / p.hq < active;
+        const SplitMerge m = kMode == kMergeOneRound
+                                 ? merge_splits_row(part, ls, live_splits, live, lane)
+                                 : merge_splits_row_scan(part, ls, live_splits, live, lane);
+        *reinterpret_cast<uint2*>(&s_h[r][lane * 4]) = merge_splits_out(m);
+        if (lane == 0) s_l[r] = merge_splits_lse(m);
+      }
     }
-  } else {
-    for (int r = wave; r < R; r += kThreads / kWave) {
-      const int64_t row = row_of(r);
-      const bool in = row >= 0;
-      const float* part = p.hp + (in ? row : 0) * p.splits * kHeadDim;
-      const float* ls = p.hl + (in ? row : 0) * p.splits;
-      const bool live = in && row / p.hq < active;
-      const SplitMerge m = kMode == kMergeOneRound
-                               ? merge_splits_row(part, ls, live_splits, live, lane)
-                               : merge_splits_row_scan(part, ls, live_splits, live, lane);
-      *reinterpret_cast<uint2*>(&s_h[r][lane * 4]) = merge_splits_out(m);
-      if (lane == 0) s_l[r] = merge_splits_lse(m);
+    if (t == 0) {
+#pragma unroll
+      for (int ct = kEarly; ct < 4; ++ct) load_rv(ct);
     }
+    __syncthreads();
+    rotate_merge<R>(
+        p, pr,
+        [&](int ct, u32x4(&b)[8]) {
+#pragma unroll
+          for (int m = 0; m < 8; ++m) b[m] = rb[ct][m];
+        },
+        s_h, s_l,
+        [&](int, int64_t row, int col, uint16_t bits) { p.out[row * kHeadDim + col] = bits; });
   }
-#pragma unroll
-  for (int ct = kEarly; ct < 4; ++ct) load_rv(ct);
-  __syncthreads();
-  rotate_merge<R>(
-      p, pr,
-      [&](int ct, u32x4(&b)[8]) {
-#pragma unroll
-        for (int m = 0; m < 8; ++m) b[m] = rb[ct][m];
-      },
-      s_h, s_l,
-      [&](int, int64_t row, int col, uint16_t bits) { p.out[row * kHeadDim + col] = bits; });
 }
 
 // Rows [row0, min(row0 + R, p.rows)) (R <= 4, one per wavefront) for kQuarters quarters of

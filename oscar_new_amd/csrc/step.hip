@@ -89,7 +89,9 @@ __global__ __launch_bounds__(kThreads, 2) void post_attention_kernel(const PostA
 // The one-round merge (one split) keeps two workgroups per CU (256 registers, a few spilled);
 // the scanned merge of 16 rows with their rotation operands needs more than 256 and runs one
 // workgroup per CU (two spilled about a hundred registers).
-template <int kMode>
+// kTiles 2 (one split): a workgroup walks two 16-row tiles with one read of R_v (per tile
+// the rows take one round of loads, and R_v's 128 KB from L2 set the first tile's wait).
+template <int kMode, int kTiles>
 __global__ __launch_bounds__(kThreads, kMode == kMergeOneRound ? 2 : 1) void
 post_attention_tile_kernel(const PostArgs p) {
   __shared__ __attribute__((aligned(16))) uint16_t s_h[16][kHeadDim];
@@ -99,9 +101,9 @@ post_attention_tile_kernel(const PostArgs p) {
   // started last they would end the launch.
   const int64_t win = p.win_requests;
   if (static_cast<int64_t>(blockIdx.x) >= win) {
-    const int64_t row0 = (static_cast<int64_t>(blockIdx.x) - win) * 16;
+    const int64_t row0 = (static_cast<int64_t>(blockIdx.x) - win) * 16 * kTiles;
     const int64_t rows = p.rows;
-    post_rows_map<16, kMode>(
+    post_rows_map<16, kMode, 4, kTiles>(
         p, [row0, rows](int r) -> int64_t { return row0 + r < rows ? row0 + r : -1; },
         p.splits, s_h, s_l, &group_lds);
     return;
@@ -473,14 +475,21 @@ extern "C" int oscar_post_attention(
   const int mode = merge_mode(p.rows, splits);
   hipStream_t s = as_stream(stream);
   if (mode != kMergeScanGroup && p.rows >= kPostTileFrom) {
-    const int64_t tiles = (p.rows + 15) / 16;
+    const bool two = mode == kMergeOneRound && splits == 1;  // 32 rows per workgroup
+    const int64_t span = two ? 32 : 16;
+    const int64_t tiles = (p.rows + span - 1) / span;
     if (tiles + p.win_requests > 0x7fffffffll) return OSCAR_E_SHAPE;
     p.merge_wgs = static_cast<int32_t>(tiles);
     const dim3 grid(static_cast<unsigned>(tiles + p.win_requests));
-    if (mode == kMergeOneRound)
-      hipLaunchKernelGGL(post_attention_tile_kernel<kMergeOneRound>, grid, dim3(kThreads), 0, s, p);
+    if (two)
+      hipLaunchKernelGGL((post_attention_tile_kernel<kMergeOneRound, 2>), grid, dim3(kThreads), 0,
+                         s, p);
+    else if (mode == kMergeOneRound)
+      hipLaunchKernelGGL((post_attention_tile_kernel<kMergeOneRound, 1>), grid, dim3(kThreads), 0,
+                         s, p);
     else
-      hipLaunchKernelGGL(post_attention_tile_kernel<kMergeScanWave>, grid, dim3(kThreads), 0, s, p);
+      hipLaunchKernelGGL((post_attention_tile_kernel<kMergeScanWave, 1>), grid, dim3(kThreads), 0,
+                         s, p);
     return static_cast<int>(hipGetLastError());
   }
   const bool wide = mode != kMergeScanGroup && p.rows >= kPostWideFrom;
