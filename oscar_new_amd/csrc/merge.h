@@ -118,13 +118,40 @@ __device__ __forceinline__ void merge_range(SplitMerge& r, const float* p, const
   }
 }
 
-// More than 16 splits, one wavefront per row (batches with many rows).
+// merge_range with its first round (splits [s_begin, s_begin + 16)) already loaded for every
+// slot below `splits`, before the LSE scan that sets s_end was complete: slots at or past
+// s_end are dropped here, and the rest is merge_range's arithmetic in the same order.
+__device__ __forceinline__ void merge_range_pre(SplitMerge& r, const float* p, const float* ls,
+                                                int s_begin, int s_end, float (&l)[16],
+                                                float4 (&v)[16]) {
+  const float safe = r.mx == -INFINITY ? 0.f : r.mx;
+#pragma unroll
+  for (int k = 0; k < 16; ++k) l[k] = s_begin + k < s_end ? l[k] : -INFINITY;
+  for (int s0 = s_begin; s0 < s_end; s0 += 16) {
+    float ln[16];
+    float4 vn[16];
+    load_group(p, ls, s0 + 16, s_end, true, ln, vn);  // empty past the range
+    merge_group(r, l, v, safe);
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      l[k] = ln[k];
+      v[k] = vn[k];
+    }
+  }
+}
+
+// More than 16 splits, one wavefront per row (batches with many rows). The first round's
+// loads are requested with the LSE scan's (every slot is inside the row's buffers), so the
+// row takes one round of latency less.
 __device__ __forceinline__ SplitMerge merge_splits_row_scan(const float* part, const float* ls,
                                                             int splits, bool valid, int lane) {
   SplitMerge r = empty_merge();
+  float l[16];
+  float4 v[16];
+  load_group(part + lane * 4, ls, 0, splits, true, l, v);
   const LseScan sc = scan_lse(ls, splits, valid);
   r.mx = sc.mx;
-  merge_range(r, part + lane * 4, ls, 0, sc.end);
+  merge_range_pre(r, part + lane * 4, ls, 0, sc.end, l, v);
   return r;
 }
 
@@ -142,11 +169,14 @@ __device__ __forceinline__ SplitMerge merge_splits_row_group(const float* part, 
                                                              GroupMergeLds* lds) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   SplitMerge r = empty_merge();
+  const int q = (splits + 3) >> 2;
+  float l[16];
+  float4 v[16];
+  load_group(part + lane * 4, ls, min(wave * q, splits), splits, true, l, v);
   const LseScan sc = scan_lse(ls, splits, valid);
   r.mx = sc.mx;
-  const int q = (splits + 3) >> 2;
   const int s_begin = min(wave * q, sc.end), s_end = min(s_begin + q, sc.end);
-  merge_range(r, part + lane * 4, ls, s_begin, s_end);
+  merge_range_pre(r, part + lane * 4, ls, s_begin, s_end, l, v);
 #pragma unroll
   for (int i = 0; i < 4; ++i) lds->acc[wave][lane * 4 + i] = r.acc[i];
   if (lane == 0) lds->den[wave] = r.den;
